@@ -1,0 +1,181 @@
+/*
+ * sdfoam_hip.h -- C ABI of libsdfoam_hip.so, the MI355X (gfx950) build of
+ * SDFoam's Voronoi-foam tracer.
+ *
+ * Plain pointers and sizes only.  Every pointer argument named as device
+ * memory must point to memory the calling process allocated on the current
+ * HIP device; `stream` is a hipStream_t passed as void* (NULL = the legacy
+ * default stream).  Calls are asynchronous on `stream` unless stated.  Every
+ * call returns 0 on success or a nonzero SDF_E_* code; sdf_last_error()
+ * returns the calling thread's last message.
+ *
+ * The library allocates no device memory: callers pass the scratch the
+ * tracer needs (size from sdf_trace_scratch_bytes).
+ *
+ * Each entry point names the reference interface it replaces
+ * (paths are into mmlab-cv/SDFoam).
+ */
+#ifndef SDFOAM_HIP_H
+#define SDFOAM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SDF_OK 0
+#define SDF_E_INVALID 1 /* bad argument (size, degree, null pointer) */
+#define SDF_E_HIP 2     /* a HIP runtime call failed */
+
+/* alpha_mode values (src/tracing/pipeline.h:10) */
+#define SDF_ALPHA_STANDARD 0u
+#define SDF_ALPHA_NEUS 1u
+
+/* The TraceSettings fields the forward/backward kernels read
+ * (src/tracing/pipeline.h:12-27; defaults src/tracing/pipeline.h:29-40:
+ * weight_threshold 1e-7, max_intersections 1024, alpha_mode standard,
+ * sdf_channel -1).  inv_s, eps and the viewer fields are not read by the
+ * reference's kernels and are not part of this struct. */
+typedef struct sdf_trace_settings {
+    float weight_threshold;
+    uint32_t max_intersections;
+    uint32_t alpha_mode;
+    int32_t sdf_channel;
+} sdf_trace_settings;
+
+/* Library version string. */
+const char *sdf_version(void);
+
+/* Thread-local description of the last failure. */
+const char *sdf_last_error(void);
+
+/* 1 + 3 (L+1)^2, or -1 for an unsupported degree.
+ * Replaces Pipeline::attribute_dim (src/tracing/pipeline.h:158,
+ * src/tracing/pipeline.cu:1467-1469). */
+int sdf_attribute_dim(int sh_degree);
+
+/* Bytes of scratch sdf_trace_forward / sdf_trace_backward need for a scene
+ * with `adjacency_size` CSR entries (the fp16 neighbour-offset table,
+ * (E + 32) x 8 bytes, as src/tracing/pipeline.cu:1270, 1328). */
+size_t sdf_trace_scratch_bytes(uint32_t num_points, uint32_t adjacency_size);
+
+/* adjacent_diff[k] = fp16(points[adjacency[k]] - points[i]) for every CSR
+ * entry k of row i, 4 halves per entry (w = 0); rows with out-of-range
+ * neighbours get NaN planes.  `adjacent_diff` holds (E + 32) x 4 halves.
+ * Replaces prefetch_adjacent_diff (src/tracing/pipeline.h:70-77,
+ * src/tracing/pipeline.cu:1202-1242). */
+int sdf_prefetch_adjacent_diff(const float *points, uint32_t num_points,
+                               uint32_t adjacency_size,
+                               const uint32_t *point_adjacency,
+                               const uint32_t *point_adjacency_offsets,
+                               uint16_t *adjacent_diff, void *stream);
+
+/* Forward trace: per ray rgba [R,4], depth [R,Q] and depth_indices [R,Q]
+ * (both NULL when Q = 0), num_intersections [R]; per point contribution
+ * [N] (+= weights; NULL to skip) and alpha [N] (a visiting ray's alpha).
+ * Attributes are fp32 AoS [N, D], D = sdf_attribute_dim(sh_degree); rays are
+ * [R, 6] (origin, direction); sharpness is read at element 0.
+ * Outputs contribution and alpha must be zeroed by the caller.
+ * Replaces Pipeline::trace_forward (src/tracing/pipeline.h:83-101,
+ * src/tracing/pipeline.cu:1251-1303). */
+int sdf_trace_forward(int sh_degree, const sdf_trace_settings *settings,
+                      uint32_t num_points, const float *points,
+                      const float *attributes, uint32_t adjacency_size,
+                      const uint32_t *point_adjacency,
+                      const uint32_t *point_adjacency_offsets,
+                      uint32_t num_rays, const float *rays,
+                      const uint32_t *start_point_index,
+                      uint32_t num_depth_quantiles,
+                      const float *depth_quantiles, float *ray_rgba,
+                      float *quantile_depths, uint32_t *quantile_point_indices,
+                      uint32_t *num_intersections, float *point_contribution,
+                      const float *sharpness, float *alpha_output,
+                      void *scratch, size_t scratch_bytes, void *stream);
+
+/* Backward trace: accumulates points_grad [N,3], attribute_grad [N,D],
+ * sharpness_grad [1] (NULL to skip) and point_error [N] (NULL to skip; then
+ * ray_error is ignored).  Gradient buffers must be zeroed by the caller.
+ * alpha_mode NEUS runs backward_sdf, STANDARD runs the density backward.
+ * ray_rgba is the forward's rgba; quantile_point_indices is read in
+ * standard mode only.
+ * Replaces Pipeline::trace_backward (src/tracing/pipeline.h:104-126,
+ * src/tracing/pipeline.cu:1305-1391). */
+int sdf_trace_backward(int sh_degree, const sdf_trace_settings *settings,
+                       uint32_t num_points, const float *points,
+                       const float *attributes, uint32_t adjacency_size,
+                       const uint32_t *point_adjacency,
+                       const uint32_t *point_adjacency_offsets,
+                       uint32_t num_rays, const float *rays,
+                       const uint32_t *start_point_index,
+                       uint32_t num_depth_quantiles,
+                       const float *depth_quantiles,
+                       const uint32_t *quantile_point_indices,
+                       const float *ray_rgba, const float *ray_rgba_grad,
+                       const float *depth_grad, const float *ray_error,
+                       float *points_grad, float *attribute_grad,
+                       float *point_error, const float *sharpness,
+                       float *sharpness_grad, void *scratch,
+                       size_t scratch_bytes, void *stream);
+
+/* Implicit AABB tree over consecutive point pairs, tree [pow2(N), 2, 3]
+ * (node (d, i) at 2^td - 2^(d+1) + i; the last entry is zeroed).
+ * Replaces build_aabb_tree (src/aabb_tree/aabb_tree.h:10-13,
+ * src/aabb_tree/aabb_tree.cu:294-341). */
+int sdf_build_aabb_tree(const float *points, uint32_t num_points,
+                        float *aabb_tree, void *stream);
+
+/* Exact nearest point of each query by fp32 distance (ties: smallest
+ * index); num_points >= 32 as in the reference.
+ * Replaces nn (src/aabb_tree/aabb_tree.h:16-23,
+ * src/aabb_tree/aabb_tree.cu:343-415). */
+int sdf_nn(const float *points, const float *aabb_tree, const float *queries,
+           uint32_t num_points, uint32_t num_queries, uint32_t *indices,
+           void *stream);
+
+/* ---- measurement and test hooks (no counterpart in the reference) ----- */
+
+/* Per-ray walk statistics of the forward (backward = 0) or backward
+ * (backward = 1) walk with the same settings: FNV-1a-64 hash of the cell
+ * sequence of the steps, number of steps, faces scanned in all loop
+ * iterations and faces of the stepped cells.  Any output may be NULL.
+ * Used by the parity tests (visit sequences) and the bench (byte model). */
+int sdf_trace_walk_stats(int sh_degree, const sdf_trace_settings *settings,
+                         int backward, uint32_t num_points, const float *points,
+                         const float *attributes, uint32_t adjacency_size,
+                         const uint32_t *point_adjacency,
+                         const uint32_t *point_adjacency_offsets,
+                         uint32_t num_rays, const float *rays,
+                         const uint32_t *start_point_index,
+                         const float *sharpness, uint64_t *visit_hash,
+                         uint32_t *steps, uint64_t *faces,
+                         uint64_t *faces_stepped, uint32_t *cells,
+                         uint32_t cells_stride, void *scratch,
+                         size_t scratch_bytes, void *stream);
+
+/* Evaluate the fp-math contract on the device, n elements:
+ * op 0: out_f32 = sdf_expf(in); op 1: out_u16 = fp16 bits of in (RNE);
+ * op 2: out_f32 = sdf_sigmoidf(in). */
+int sdf_debug_fpmath(int op, const float *in, void *out, uint64_t n,
+                     void *stream);
+
+/* Kernel timing.  While enabled, every kernel launch of the entry points
+ * above is bracketed by two HIP events recorded on its stream (up to 512
+ * launches are kept).  sdf_timing_collect waits for them, writes each
+ * launch's kind (SDF_KERNEL_*) and duration in milliseconds, in launch
+ * order, sets *n_out, and empties the record.  sdf_set_timing also empties
+ * it.  Not for use under stream capture. */
+#define SDF_KERNEL_PREFETCH 0
+#define SDF_KERNEL_FORWARD 1
+#define SDF_KERNEL_BACKWARD 2
+#define SDF_KERNEL_AABB_TREE 3
+#define SDF_KERNEL_NN 4
+int sdf_set_timing(int enable);
+int sdf_timing_collect(int *kinds, float *ms, int max_n, int *n_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SDFOAM_HIP_H */

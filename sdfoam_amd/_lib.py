@@ -1,0 +1,139 @@
+"""ctypes binding of libsdfoam_hip.so (the C ABI in include/sdfoam_hip.h).
+
+The library is built in-tree by ``python -m sdfoam_amd.build``.  There is no
+fallback: if it is missing, loading raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+from .build import LIB_PATH
+
+SDF_OK = 0
+SDF_ALPHA_STANDARD = 0
+SDF_ALPHA_NEUS = 1
+
+# every symbol include/sdfoam_hip.h declares
+EXPORTS = (
+    "sdf_version",
+    "sdf_last_error",
+    "sdf_attribute_dim",
+    "sdf_trace_scratch_bytes",
+    "sdf_prefetch_adjacent_diff",
+    "sdf_trace_forward",
+    "sdf_trace_backward",
+    "sdf_build_aabb_tree",
+    "sdf_nn",
+    "sdf_trace_walk_stats",
+    "sdf_debug_fpmath",
+    "sdf_set_timing",
+    "sdf_timing_collect",
+)
+
+KERNEL_NAMES = {0: "prefetch_adjacent_diff", 1: "forward", 2: "backward", 3: "build_aabb_tree", 4: "nn"}
+
+
+class TraceSettings(C.Structure):
+    """sdf_trace_settings (mirrors the fields of the reference's TraceSettings
+    that its kernels read, src/tracing/pipeline.h:12-27)."""
+
+    _fields_ = [
+        ("weight_threshold", C.c_float),
+        ("max_intersections", C.c_uint32),
+        ("alpha_mode", C.c_uint32),
+        ("sdf_channel", C.c_int32),
+    ]
+
+
+_lib = None
+
+P = C.c_void_p
+U32 = C.c_uint32
+SZ = C.c_size_t
+
+
+class LibraryError(RuntimeError):
+    pass
+
+
+def lib() -> C.CDLL:
+    """Load libsdfoam_hip.so (once)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise LibraryError(
+            f"{LIB_PATH} is not built; run `python -m sdfoam_amd.build` "
+            "(the HIP library is required, there is no CPU fallback)"
+        )
+    L = C.CDLL(LIB_PATH)
+    L.sdf_version.restype = C.c_char_p
+    L.sdf_version.argtypes = []
+    L.sdf_last_error.restype = C.c_char_p
+    L.sdf_last_error.argtypes = []
+    L.sdf_attribute_dim.restype = C.c_int
+    L.sdf_attribute_dim.argtypes = [C.c_int]
+    L.sdf_trace_scratch_bytes.restype = SZ
+    L.sdf_trace_scratch_bytes.argtypes = [U32, U32]
+    L.sdf_prefetch_adjacent_diff.restype = C.c_int
+    L.sdf_prefetch_adjacent_diff.argtypes = [P, U32, U32, P, P, P, P]
+    L.sdf_trace_forward.restype = C.c_int
+    L.sdf_trace_forward.argtypes = [
+        C.c_int, C.POINTER(TraceSettings), U32, P, P, U32, P, P, U32, P, P, U32, P,
+        P, P, P, P, P, P, P, P, SZ, P]
+    L.sdf_trace_backward.restype = C.c_int
+    L.sdf_trace_backward.argtypes = [
+        C.c_int, C.POINTER(TraceSettings), U32, P, P, U32, P, P, U32, P, P, U32, P, P,
+        P, P, P, P, P, P, P, P, P, P, SZ, P]
+    L.sdf_build_aabb_tree.restype = C.c_int
+    L.sdf_build_aabb_tree.argtypes = [P, U32, P, P]
+    L.sdf_nn.restype = C.c_int
+    L.sdf_nn.argtypes = [P, P, P, U32, U32, P, P]
+    L.sdf_trace_walk_stats.restype = C.c_int
+    L.sdf_trace_walk_stats.argtypes = [
+        C.c_int, C.POINTER(TraceSettings), C.c_int, U32, P, P, U32, P, P, U32, P, P, P,
+        P, P, P, P, P, U32, P, SZ, P]
+    L.sdf_debug_fpmath.restype = C.c_int
+    L.sdf_debug_fpmath.argtypes = [C.c_int, P, P, C.c_uint64, P]
+    L.sdf_set_timing.restype = C.c_int
+    L.sdf_set_timing.argtypes = [C.c_int]
+    L.sdf_timing_collect.restype = C.c_int
+    L.sdf_timing_collect.argtypes = [P, P, C.c_int, C.POINTER(C.c_int)]
+    _lib = L
+    return L
+
+
+def check(rc: int) -> None:
+    """Raise RuntimeError with the library's message for a nonzero status."""
+    if rc != SDF_OK:
+        msg = lib().sdf_last_error()
+        raise RuntimeError(msg.decode() if msg else f"sdfoam_hip error {rc}")
+
+
+def ptr(t) -> int | None:
+    """Raw device pointer of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device) -> int:
+    """hipStream_t of torch's current stream on `device`."""
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def set_timing(enable: bool) -> None:
+    """Record HIP events around every kernel launch (see sdf_set_timing)."""
+    check(lib().sdf_set_timing(1 if enable else 0))
+
+
+def collect_timings(max_n: int = 512) -> list[tuple[str, float]]:
+    """(kernel name, milliseconds) of every launch recorded since the last
+    collect, in launch order."""
+    kinds = (C.c_int * max_n)()
+    ms = (C.c_float * max_n)()
+    n = C.c_int()
+    check(lib().sdf_timing_collect(kinds, ms, max_n, C.byref(n)))
+    return [(KERNEL_NAMES.get(kinds[i], str(kinds[i])), float(ms[i])) for i in range(n.value)]

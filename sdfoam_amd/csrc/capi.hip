@@ -1,0 +1,357 @@
+// extern "C" entry points of libsdfoam_hip.so (declared in
+// include/sdfoam_hip.h).  Argument checks, stream plumbing, optional kernel
+// timing; no device allocation.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "trace_kernels.h"
+
+using namespace sdfoam_hip;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *where) {
+    return fail(SDF_E_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+// ---- optional kernel timing ----------------------------------------------
+// When enabled, every kernel launch is bracketed by two HIP events recorded
+// on its stream, kept in a ring until sdf_timing_collect reads them.
+constexpr int kRing = 512;
+struct TimedLaunch {
+    hipEvent_t begin;
+    hipEvent_t end;
+    int kind;
+};
+bool g_timing = false;
+TimedLaunch g_ring[kRing] = {};
+int g_ring_n = 0;
+int g_open = -1;
+
+void tbegin(int kind, hipStream_t s) {
+    g_open = -1;
+    if (!g_timing || g_ring_n >= kRing) return;
+    TimedLaunch &t = g_ring[g_ring_n];
+    if (!t.begin && hipEventCreate(&t.begin) != hipSuccess) return;
+    if (!t.end && hipEventCreate(&t.end) != hipSuccess) return;
+    t.kind = kind;
+    if (hipEventRecord(t.begin, s) != hipSuccess) return;
+    g_open = g_ring_n;
+}
+
+void tend(hipStream_t s) {
+    if (g_open < 0) return;
+    if (hipEventRecord(g_ring[g_open].end, s) == hipSuccess) g_ring_n = g_open + 1;
+    g_open = -1;
+}
+
+int check_scene(int sh_degree, const sdf_trace_settings *settings, uint32_t num_points,
+                const float *points, const float *attributes, uint32_t adjacency_size,
+                const uint32_t *adj, const uint32_t *offs, uint32_t num_rays, const float *rays,
+                const uint32_t *start, const float *sharpness, void *scratch,
+                size_t scratch_bytes) {
+    if (sh_degree < 0 || sh_degree > 3) return fail(SDF_E_INVALID, "Unsupported SH degree");
+    if (!settings) return fail(SDF_E_INVALID, "settings must not be NULL");
+    if (settings->alpha_mode != SDF_ALPHA_STANDARD && settings->alpha_mode != SDF_ALPHA_NEUS)
+        return fail(SDF_E_INVALID, "alpha_mode must be 0 (standard) or 1 (sdfoam)");
+    const int D = 1 + 3 * (sh_degree + 1) * (sh_degree + 1);
+    if (settings->sdf_channel >= D)
+        return fail(SDF_E_INVALID, "sdf_channel %d out of range for attribute dim %d",
+                    settings->sdf_channel, D);
+    if (num_points == 0) return fail(SDF_E_INVALID, "num_points must be positive");
+    if (!points || !attributes || !offs || (!adj && adjacency_size > 0))
+        return fail(SDF_E_INVALID, "scene pointers must not be NULL");
+    if (num_rays > 0 && (!rays || !start))
+        return fail(SDF_E_INVALID, "rays and start_point_index must not be NULL");
+    if (!sharpness) return fail(SDF_E_INVALID, "sharpness must not be NULL");
+    const size_t need = sdf_trace_scratch_bytes(num_points, adjacency_size);
+    if (!scratch || scratch_bytes < need)
+        return fail(SDF_E_INVALID, "scratch must hold %zu bytes (got %zu)", need, scratch_bytes);
+    if ((reinterpret_cast<uintptr_t>(scratch) & 7u) != 0)
+        return fail(SDF_E_INVALID, "scratch must be 8-byte aligned");
+    return SDF_OK;
+}
+
+SceneView make_scene(uint32_t num_points, const float *points, const float *attributes,
+                     uint32_t adjacency_size, const uint32_t *adj, const uint32_t *offs,
+                     void *scratch) {
+    SceneView sc;
+    sc.points = points;
+    sc.attrs = attributes;
+    sc.adj = adj;
+    sc.offs = offs;
+    sc.diff = static_cast<const uint2 *>(scratch);
+    sc.num_points = num_points;
+    sc.num_adj = adjacency_size;
+    return sc;
+}
+
+} // namespace
+
+extern "C" {
+
+const char *sdf_version(void) { return "sdfoam_hip 0.1 (gfx950)"; }
+
+const char *sdf_last_error(void) { return g_err; }
+
+int sdf_attribute_dim(int sh_degree) {
+    if (sh_degree < 0 || sh_degree > 3) return -1;
+    return 1 + 3 * (sh_degree + 1) * (sh_degree + 1);
+}
+
+size_t sdf_trace_scratch_bytes(uint32_t num_points, uint32_t adjacency_size) {
+    (void)num_points;
+    return ((size_t)adjacency_size + kDiffPad) * 8u;
+}
+
+int sdf_prefetch_adjacent_diff(const float *points, uint32_t num_points, uint32_t adjacency_size,
+                               const uint32_t *point_adjacency,
+                               const uint32_t *point_adjacency_offsets, uint16_t *adjacent_diff,
+                               void *stream) {
+    if (!points || !point_adjacency_offsets || !adjacent_diff ||
+        (!point_adjacency && adjacency_size > 0))
+        return fail(SDF_E_INVALID, "NULL pointer argument");
+    if (num_points == 0) return fail(SDF_E_INVALID, "num_points must be positive");
+    if ((reinterpret_cast<uintptr_t>(adjacent_diff) & 7u) != 0)
+        return fail(SDF_E_INVALID, "adjacent_diff must be 8-byte aligned");
+    hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
+                                        point_adjacency_offsets,
+                                        reinterpret_cast<uint2 *>(adjacent_diff),
+                                        static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
+    return SDF_OK;
+}
+
+int sdf_trace_forward(int sh_degree, const sdf_trace_settings *settings, uint32_t num_points,
+                      const float *points, const float *attributes, uint32_t adjacency_size,
+                      const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
+                      uint32_t num_rays, const float *rays, const uint32_t *start_point_index,
+                      uint32_t num_depth_quantiles, const float *depth_quantiles, float *ray_rgba,
+                      float *quantile_depths, uint32_t *quantile_point_indices,
+                      uint32_t *num_intersections, float *point_contribution,
+                      const float *sharpness, float *alpha_output, void *scratch,
+                      size_t scratch_bytes, void *stream) {
+    int rc = check_scene(sh_degree, settings, num_points, points, attributes, adjacency_size,
+                         point_adjacency, point_adjacency_offsets, num_rays, rays,
+                         start_point_index, sharpness, scratch, scratch_bytes);
+    if (rc != SDF_OK) return rc;
+    if (num_rays > 0 && !ray_rgba) return fail(SDF_E_INVALID, "ray_rgba must not be NULL");
+    if (num_depth_quantiles > 0 && (!depth_quantiles || !quantile_depths || !quantile_point_indices))
+        return fail(SDF_E_INVALID, "depth buffers must not be NULL when num_depth_quantiles > 0");
+    if ((reinterpret_cast<uintptr_t>(ray_rgba) & 15u) != 0)
+        return fail(SDF_E_INVALID, "ray_rgba must be 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    tbegin(SDF_KERNEL_PREFETCH, s);
+    hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
+                                        point_adjacency_offsets, static_cast<uint2 *>(scratch), s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
+    if (num_rays == 0) return SDF_OK;
+    FwdArgs a = {};
+    a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
+                         point_adjacency_offsets, scratch);
+    a.settings = *settings;
+    a.rays = rays;
+    a.num_rays = num_rays;
+    a.start = start_point_index;
+    a.num_quantiles = num_depth_quantiles;
+    a.quantiles = num_depth_quantiles ? depth_quantiles : nullptr;
+    a.sharpness = sharpness;
+    a.rgba = ray_rgba;
+    a.depth = quantile_depths;
+    a.depth_indices = quantile_point_indices;
+    a.num_intersections = num_intersections;
+    a.contribution = point_contribution;
+    a.alpha_out = alpha_output;
+    tbegin(SDF_KERNEL_FORWARD, s);
+    e = launch_forward(sh_degree, a, settings->alpha_mode == SDF_ALPHA_NEUS, false, s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "forward");
+    return SDF_OK;
+}
+
+int sdf_trace_backward(int sh_degree, const sdf_trace_settings *settings, uint32_t num_points,
+                       const float *points, const float *attributes, uint32_t adjacency_size,
+                       const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
+                       uint32_t num_rays, const float *rays, const uint32_t *start_point_index,
+                       uint32_t num_depth_quantiles, const float *depth_quantiles,
+                       const uint32_t *quantile_point_indices, const float *ray_rgba,
+                       const float *ray_rgba_grad, const float *depth_grad,
+                       const float *ray_error, float *points_grad, float *attribute_grad,
+                       float *point_error, const float *sharpness, float *sharpness_grad,
+                       void *scratch, size_t scratch_bytes, void *stream) {
+    int rc = check_scene(sh_degree, settings, num_points, points, attributes, adjacency_size,
+                         point_adjacency, point_adjacency_offsets, num_rays, rays,
+                         start_point_index, sharpness, scratch, scratch_bytes);
+    if (rc != SDF_OK) return rc;
+    const bool neus = settings->alpha_mode == SDF_ALPHA_NEUS;
+    if (!points_grad || !attribute_grad)
+        return fail(SDF_E_INVALID, "points_grad and attribute_grad must not be NULL");
+    if (num_rays > 0 && (!ray_rgba || !ray_rgba_grad))
+        return fail(SDF_E_INVALID, "ray_rgba and ray_rgba_grad must not be NULL");
+    if (num_depth_quantiles > 0 && (!depth_quantiles || !depth_grad))
+        return fail(SDF_E_INVALID, "depth_grad must be provided if depth_quantiles is provided");
+    if (!neus && num_depth_quantiles > 0 && !quantile_point_indices)
+        return fail(SDF_E_INVALID, "depth_indices must be provided in standard mode");
+    if (((reinterpret_cast<uintptr_t>(ray_rgba) | reinterpret_cast<uintptr_t>(ray_rgba_grad)) &
+         15u) != 0)
+        return fail(SDF_E_INVALID, "ray_rgba and ray_rgba_grad must be 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    tbegin(SDF_KERNEL_PREFETCH, s);
+    hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
+                                        point_adjacency_offsets, static_cast<uint2 *>(scratch), s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
+    if (num_rays == 0) return SDF_OK;
+    BwdArgs a = {};
+    a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
+                         point_adjacency_offsets, scratch);
+    a.settings = *settings;
+    a.rays = rays;
+    a.num_rays = num_rays;
+    a.start = start_point_index;
+    a.num_quantiles = num_depth_quantiles;
+    a.quantiles = num_depth_quantiles ? depth_quantiles : nullptr;
+    a.depth_indices = quantile_point_indices;
+    a.rgba = ray_rgba;
+    a.rgba_grad = ray_rgba_grad;
+    a.depth_grad = num_depth_quantiles ? depth_grad : nullptr;
+    a.ray_error = point_error ? ray_error : nullptr;
+    a.sharpness = sharpness;
+    a.points_grad = points_grad;
+    a.attr_grad = attribute_grad;
+    a.point_error = ray_error ? point_error : nullptr;
+    a.sharpness_grad = sharpness_grad;
+    tbegin(SDF_KERNEL_BACKWARD, s);
+    e = launch_backward(sh_degree, a, neus, false, s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "backward");
+    return SDF_OK;
+}
+
+int sdf_build_aabb_tree(const float *points, uint32_t num_points, float *aabb_tree,
+                        void *stream) {
+    if (!points || !aabb_tree) return fail(SDF_E_INVALID, "NULL pointer argument");
+    if (num_points == 0) return fail(SDF_E_INVALID, "num_points must be positive");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    tbegin(SDF_KERNEL_AABB_TREE, s);
+    hipError_t e = launch_build_aabb_tree(points, num_points, aabb_tree, s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "build_aabb_tree");
+    return SDF_OK;
+}
+
+int sdf_nn(const float *points, const float *aabb_tree, const float *queries, uint32_t num_points,
+           uint32_t num_queries, uint32_t *indices, void *stream) {
+    if (num_points < 32) return fail(SDF_E_INVALID, "number of points must be at least 32");
+    if (!points || !aabb_tree || (num_queries > 0 && (!queries || !indices)))
+        return fail(SDF_E_INVALID, "NULL pointer argument");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    tbegin(SDF_KERNEL_NN, s);
+    hipError_t e = launch_nn(points, aabb_tree, queries, num_points, num_queries, indices, s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "nn");
+    return SDF_OK;
+}
+
+int sdf_trace_walk_stats(int sh_degree, const sdf_trace_settings *settings, int backward,
+                         uint32_t num_points, const float *points, const float *attributes,
+                         uint32_t adjacency_size, const uint32_t *point_adjacency,
+                         const uint32_t *point_adjacency_offsets, uint32_t num_rays,
+                         const float *rays, const uint32_t *start_point_index,
+                         const float *sharpness, uint64_t *visit_hash, uint32_t *steps,
+                         uint64_t *faces, uint64_t *faces_stepped, uint32_t *cells,
+                         uint32_t cells_stride, void *scratch, size_t scratch_bytes,
+                         void *stream) {
+    int rc = check_scene(sh_degree, settings, num_points, points, attributes, adjacency_size,
+                         point_adjacency, point_adjacency_offsets, num_rays, rays,
+                         start_point_index, sharpness, scratch, scratch_bytes);
+    if (rc != SDF_OK) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
+                                        point_adjacency_offsets, static_cast<uint2 *>(scratch), s);
+    if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
+    if (num_rays == 0) return SDF_OK;
+    const bool neus = settings->alpha_mode == SDF_ALPHA_NEUS;
+    const SceneView sc = make_scene(num_points, points, attributes, adjacency_size,
+                                    point_adjacency, point_adjacency_offsets, scratch);
+    if (!backward) {
+        FwdArgs a = {};
+        a.scene = sc;
+        a.settings = *settings;
+        a.rays = rays;
+        a.num_rays = num_rays;
+        a.start = start_point_index;
+        a.sharpness = sharpness;
+        a.visit_hash = visit_hash;
+        a.steps = steps;
+        a.faces = faces;
+        a.faces_stepped = faces_stepped;
+        a.cells = cells;
+        a.cells_stride = cells ? cells_stride : 0;
+        e = launch_forward(sh_degree, a, neus, true, s);
+    } else {
+        BwdArgs a = {};
+        a.scene = sc;
+        a.settings = *settings;
+        a.rays = rays;
+        a.num_rays = num_rays;
+        a.start = start_point_index;
+        a.sharpness = sharpness;
+        a.visit_hash = visit_hash;
+        a.steps = steps;
+        a.faces = faces;
+        a.faces_stepped = faces_stepped;
+        a.cells = cells;
+        a.cells_stride = cells ? cells_stride : 0;
+        e = launch_backward(sh_degree, a, neus, true, s);
+    }
+    if (e != hipSuccess) return hip_fail(e, "walk_stats");
+    return SDF_OK;
+}
+
+int sdf_debug_fpmath(int op, const float *in, void *out, uint64_t n, void *stream) {
+    if (op < 0 || op > 2) return fail(SDF_E_INVALID, "op must be 0, 1 or 2");
+    if (n == 0) return SDF_OK;
+    if (!in || !out) return fail(SDF_E_INVALID, "NULL pointer argument");
+    hipError_t e = launch_fpmath(op, in, out, n, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "fpmath");
+    return SDF_OK;
+}
+
+int sdf_set_timing(int enable) {
+    g_timing = enable != 0;
+    g_ring_n = 0;
+    g_open = -1;
+    return SDF_OK;
+}
+
+int sdf_timing_collect(int *kinds, float *ms, int max_n, int *n_out) {
+    if (!n_out) return fail(SDF_E_INVALID, "n_out must not be NULL");
+    const int n = g_ring_n < max_n ? g_ring_n : max_n;
+    for (int i = 0; i < n; ++i) {
+        hipError_t e = hipEventSynchronize(g_ring[i].end);
+        if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+        float t = 0.0f;
+        e = hipEventElapsedTime(&t, g_ring[i].begin, g_ring[i].end);
+        if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+        if (kinds) kinds[i] = g_ring[i].kind;
+        if (ms) ms[i] = t;
+    }
+    *n_out = n;
+    g_ring_n = 0;
+    return SDF_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,223 @@
+// Device-side building blocks of the Voronoi-foam walk for gfx950.
+//
+// Floating-point contract: this code is compiled with -ffp-contract=off; the
+// only fused multiply-adds are the explicit fmaf calls, placed where the
+// reference accumulates `a += b * c`, plus the dot of include/sdfoam_fpmath.h.
+// exp / sigmoid / fp16 rounding come from that header, so the per-step
+// alpha, the transmittance and therefore the visit sequence are bit-identical
+// to the host oracle's.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sdfoam_fpmath.h"
+#include "../../include/sdfoam_hip.h"
+
+namespace sdfoam_hip {
+
+constexpr uint32_t kNoIndex = 0xffffffffu;
+constexpr int kBlock = 256;
+// entries past E in the fp16 offset table, so a face batch can over-read
+constexpr uint32_t kDiffPad = 32;
+
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xffffu));
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+struct RayF {
+    float ox, oy, oz;
+    float dx, dy, dz;
+};
+
+// ray.direction /= ray.direction.norm()  (src/tracing/pipeline.cu:76-77)
+__device__ __forceinline__ RayF load_ray(const float *__restrict__ rays, uint32_t i) {
+    const float *r = rays + 6ull * i;
+    RayF ray;
+    ray.ox = r[0];
+    ray.oy = r[1];
+    ray.oz = r[2];
+    const float x = r[3], y = r[4], z = r[5];
+    const float n = sqrtf(sdf_dot3(x, y, z, x, y, z));
+    ray.dx = x / n;
+    ray.dy = y / n;
+    ray.dz = z / n;
+    return ray;
+}
+
+// Real SH basis up to degree L, 3DGS sign convention
+// (src/tracing/sh_utils.cuh:8-62).
+template <int L>
+__device__ __forceinline__ void sh_basis(float x, float y, float z, float *sh) {
+    constexpr float C0 = 0.28209479177387814f;
+    constexpr float C1 = 0.4886025119029199f;
+    sh[0] = C0;
+    if constexpr (L > 0) {
+        sh[1] = -C1 * y;
+        sh[2] = C1 * z;
+        sh[3] = -C1 * x;
+    }
+    const float xx = x * x, yy = y * y, zz = z * z;
+    const float xy = x * y, yz = y * z, xz = x * z;
+    if constexpr (L > 1) {
+        sh[4] = 1.0925484305920792f * xy;
+        sh[5] = -1.0925484305920792f * yz;
+        sh[6] = 0.31539156525252005f * (2.0f * zz - xx - yy);
+        sh[7] = -1.0925484305920792f * xz;
+        sh[8] = 0.5462742152960396f * (xx - yy);
+    }
+    if constexpr (L > 2) {
+        sh[9] = -0.5900435899266435f * y * (3.0f * xx - yy);
+        sh[10] = 2.890611442640554f * xy * z;
+        sh[11] = -0.4570457994644658f * y * (4.0f * zz - xx - yy);
+        sh[12] = 0.3731763325901154f * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+        sh[13] = -0.4570457994644658f * x * (4.0f * zz - xx - yy);
+        sh[14] = 1.445305721320277f * z * (xx - yy);
+        sh[15] = -0.5900435899266435f * x * (xx - 3.0f * yy);
+    }
+}
+
+// rgb = max(0, 0.5 + sum_j Y_j * row[3j + c])  (src/tracing/sh_utils.cuh:64-75)
+template <int L>
+__device__ __forceinline__ void sh_rgb(const float *sh, const float *__restrict__ row,
+                                       float &r, float &g, float &b) {
+    constexpr int nsh = (L + 1) * (L + 1);
+    float a0 = 0.5f, a1 = 0.5f, a2 = 0.5f;
+#pragma unroll
+    for (int j = 0; j < nsh; ++j) {
+        a0 = fmaf(sh[j], row[3 * j + 0], a0);
+        a1 = fmaf(sh[j], row[3 * j + 1], a1);
+        a2 = fmaf(sh[j], row[3 * j + 2], a2);
+    }
+    r = fmaxf(a0, 0.0f);
+    g = fmaxf(a1, 0.0f);
+    b = fmaxf(a2, 0.0f);
+}
+
+struct SceneView {
+    const float *__restrict__ points;
+    const float *__restrict__ attrs;
+    const uint32_t *__restrict__ adj;
+    const uint32_t *__restrict__ offs;
+    const uint2 *__restrict__ diff; // fp16 x, y | z, 0 per CSR entry
+    uint32_t num_points;
+    uint32_t num_adj;
+};
+
+struct WalkCounters {
+    uint32_t n;             // loop iterations (the reference's return value)
+    uint32_t steps;         // step-functor calls
+    uint64_t faces;         // faces scanned
+    uint64_t faces_stepped; // faces of the cells that got a step
+};
+
+// The walk of src/tracing/tracing_utils.cuh:15-109.  Exit face: the first
+// minimum t over the cell's CSR row with dp > 0 (and t > t0 in safe mode).
+// The reference passes UINT32_MAX for the index bounds; the real bounds are
+// used here, which is the same walk for a well-formed scene and stops instead
+// of reading out of bounds otherwise.
+//
+// step(cell, next, t0, t1, xc[3], xn[3]) -> keep going?
+template <bool SAFE, bool COUNT, typename Step>
+__device__ __forceinline__ void walk(const SceneView &sc, const RayF &ray, uint32_t start,
+                                     uint32_t max_steps, Step &&step, WalkCounters &wc) {
+    wc.n = 0;
+    wc.steps = 0;
+    wc.faces = 0;
+    wc.faces_stepped = 0;
+    if (start >= sc.num_points) return;
+    uint32_t cell = start;
+    float xc[3] = {sc.points[3ull * cell], sc.points[3ull * cell + 1], sc.points[3ull * cell + 2]};
+    float t0 = 0.0f;
+    uint32_t n = 0;
+    for (;;) {
+        ++n;
+        if (n > max_steps) break;
+        const uint32_t beg = sc.offs[cell];
+        const uint32_t end = sc.offs[cell + 1];
+        if (beg > end || end > sc.num_adj) break;
+        const uint32_t nf = end - beg;
+        if constexpr (COUNT) wc.faces += nf;
+        float t1 = __builtin_bit_cast(float, 0x7f800000u);
+        uint32_t best = kNoIndex;
+        const uint2 *__restrict__ row = sc.diff + beg;
+        // batches of 4: the table is padded, so the last batch may over-read
+        for (uint32_t k0 = 0; k0 < nf; k0 += 4) {
+            uint2 h[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) h[u] = row[k0 + u];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t k = k0 + u;
+                const float dx = f16_to_f32(h[u].x);
+                const float dy = f16_to_f32(h[u].x >> 16);
+                const float dz = f16_to_f32(h[u].y);
+                const float fx = xc[0] + dx * 0.5f;
+                const float fy = xc[1] + dy * 0.5f;
+                const float fz = xc[2] + dz * 0.5f;
+                const float dp = sdf_dot3(dx, dy, dz, ray.dx, ray.dy, ray.dz);
+                const float t = sdf_dot3(fx - ray.ox, fy - ray.oy, fz - ray.oz, dx, dy, dz) / dp;
+                bool take;
+                if constexpr (SAFE) {
+                    take = dp > 0.0f && t > t0 && t < t1;
+                } else {
+                    take = dp > 0.0f && t < t1;
+                }
+                if (take && k < nf) {
+                    t1 = t;
+                    best = k;
+                }
+            }
+        }
+        if (best == kNoIndex) break;
+        const uint32_t next = sc.adj[beg + best];
+        if (next >= sc.num_points) break;
+        const float xn[3] = {sc.points[3ull * next], sc.points[3ull * next + 1],
+                             sc.points[3ull * next + 2]};
+        if (t1 > t0) {
+            if constexpr (COUNT) {
+                wc.steps++;
+                wc.faces_stepped += nf;
+            }
+            if (!step(cell, next, t0, t1, xc, xn)) break;
+        }
+        t0 = fmaxf(t0, t1);
+        cell = next;
+        xc[0] = xn[0];
+        xc[1] = xn[1];
+        xc[2] = xn[2];
+    }
+    wc.n = n;
+}
+
+// cell_intersection_grad (src/tracing/tracing_utils.cuh:112-124):
+// d t / d p for t = ((p + q) / 2 - o) . (q - p) / ((q - p) . d)
+__device__ __forceinline__ void cell_isect_grad(const float *p, const float *q, const RayF &ray,
+                                                float *g) {
+    const float fo0 = (p[0] + q[0]) / 2.0f, fo1 = (p[1] + q[1]) / 2.0f, fo2 = (p[2] + q[2]) / 2.0f;
+    const float fn0 = q[0] - p[0], fn1 = q[1] - p[1], fn2 = q[2] - p[2];
+    const float num = sdf_dot3(fo0 - ray.ox, fo1 - ray.oy, fo2 - ray.oz, fn0, fn1, fn2);
+    const float dp = sdf_dot3(fn0, fn1, fn2, ray.dx, ray.dy, ray.dz);
+    const float dp2 = dp * dp;
+    g[0] = (num * ray.dx + dp * (ray.ox - p[0])) / dp2;
+    g[1] = (num * ray.dy + dp * (ray.oy - p[1])) / dp2;
+    g[2] = (num * ray.dz + dp * (ray.oz - p[2])) / dp2;
+}
+
+__device__ __forceinline__ uint64_t fnv_step(uint64_t h, uint32_t cell) {
+    return (h ^ (uint64_t)cell) * 0x100000001b3ull;
+}
+
+constexpr uint64_t kFnvOffset = 0xcbf29ce484222325ull;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+} // namespace sdfoam_hip

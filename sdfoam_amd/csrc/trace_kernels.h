@@ -1,0 +1,73 @@
+// Kernel argument blocks and launchers shared by the C ABI (capi.hip) and
+// the kernels (trace_kernels.hip, aabb_kernels.hip).
+#pragma once
+
+#include "trace_device.h"
+
+namespace sdfoam_hip {
+
+struct FwdArgs {
+    SceneView scene;
+    sdf_trace_settings settings;
+    const float *rays;
+    uint32_t num_rays;
+    const uint32_t *start;
+    uint32_t num_quantiles;
+    const float *quantiles;
+    const float *sharpness;
+    float *rgba;
+    float *depth;
+    uint32_t *depth_indices;
+    uint32_t *num_intersections;
+    float *contribution;
+    float *alpha_out;
+    // walk statistics (STATS instantiation only)
+    uint64_t *visit_hash;
+    uint32_t *steps;
+    uint64_t *faces;
+    uint64_t *faces_stepped;
+    uint32_t *cells;
+    uint32_t cells_stride;
+};
+
+struct BwdArgs {
+    SceneView scene;
+    sdf_trace_settings settings;
+    const float *rays;
+    uint32_t num_rays;
+    const uint32_t *start;
+    uint32_t num_quantiles;
+    const float *quantiles;
+    const uint32_t *depth_indices;
+    const float *rgba;
+    const float *rgba_grad;
+    const float *depth_grad;
+    const float *ray_error;
+    const float *sharpness;
+    float *points_grad;
+    float *attr_grad;
+    float *point_error;
+    float *sharpness_grad;
+    // walk statistics (STATS instantiation only)
+    uint64_t *visit_hash;
+    uint32_t *steps;
+    uint64_t *faces;
+    uint64_t *faces_stepped;
+    uint32_t *cells;
+    uint32_t cells_stride;
+};
+
+hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32_t num_adj,
+                                const uint32_t *adj, const uint32_t *offs, uint2 *diff,
+                                hipStream_t stream);
+hipError_t launch_forward(int L, const FwdArgs &a, bool neus, bool stats, hipStream_t stream);
+hipError_t launch_backward(int L, const BwdArgs &a, bool neus, bool stats, hipStream_t stream);
+hipError_t launch_fpmath(int op, const float *in, void *out, uint64_t n, hipStream_t stream);
+
+hipError_t launch_build_aabb_tree(const float *points, uint32_t num_points, float *tree,
+                                  hipStream_t stream);
+hipError_t launch_nn(const float *points, const float *tree, const float *queries,
+                     uint32_t num_points, uint32_t num_queries, uint32_t *indices,
+                     hipStream_t stream);
+
+} // namespace sdfoam_hip

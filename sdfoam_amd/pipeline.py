@@ -1,0 +1,431 @@
+"""The ``Pipeline`` operator surface of the reference's ``sdfoam`` module.
+
+``create_pipeline`` / ``Pipeline.trace_forward`` / ``Pipeline.trace_backward``
+take the same arguments, apply the same checks with the same messages, and
+return the same dicts of tensors as the reference's pybind11 bindings
+(torch_bindings/pipeline_bindings.cpp:12-75, 124-607, 744-837).  The work is
+done by libsdfoam_hip.so through its C ABI, on torch's current stream.
+
+Deliberate differences, all on paths where the reference's behaviour is
+undefined or wasteful:
+* no ``.item()`` host sync for ``inv_s`` (the kernels read the tensor);
+* ``ray_grad`` is returned zeroed instead of uninitialised;
+* an ``sdf_channel`` beyond the attribute row raises instead of reading out
+  of bounds; start points or neighbours out of range end the walk;
+* ``inv_s`` may also be a Python number.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+from ._lib import TraceSettings, check, ptr
+
+# torch dtype -> c10::toString name, as printed in the reference's messages
+_C10_NAMES = {
+    torch.float32: "Float",
+    torch.float64: "Double",
+    torch.float16: "Half",
+    torch.bfloat16: "BFloat16",
+    torch.int64: "Long",
+    torch.int32: "Int",
+    torch.int16: "Short",
+    torch.int8: "Char",
+    torch.uint8: "Byte",
+    torch.bool: "Bool",
+}
+for _name in ("uint16", "uint32", "uint64"):
+    if hasattr(torch, _name):
+        _C10_NAMES[getattr(torch, _name)] = _name.replace("uint", "UInt")
+
+_SCALAR_NAMES = {torch.float32: "float32", torch.float64: "float64", torch.float16: "float16"}
+
+
+def _c10(dtype) -> str:
+    return _C10_NAMES.get(dtype, str(dtype).replace("torch.", ""))
+
+
+def _scalar_type(dtype) -> str:
+    """dtype_to_scalar_type (torch_bindings/bindings.h:44-54)."""
+    if dtype in _SCALAR_NAMES:
+        return _SCALAR_NAMES[dtype]
+    raise RuntimeError(f"unsupported dtype '{_c10(dtype)}'")
+
+
+def _is_cuda(t: torch.Tensor) -> bool:
+    return t.device.type == "cuda"
+
+
+def _dtype_string_to_scalar_type(dtype: str) -> str:
+    """torch_bindings/pipeline_bindings.cpp:734-745."""
+    if dtype in ("float32", "torch.float32"):
+        return "float32"
+    if dtype in ("float64", "torch.float64"):
+        return "float64"
+    if dtype in ("float16", "torch.float16"):
+        return "float16"
+    raise RuntimeError(f"unsupported dtype '{dtype}'")
+
+
+def _parse_alpha_mode(alpha_mode) -> int:
+    """torch_bindings/pipeline_bindings.cpp:221-229."""
+    if alpha_mode is None:
+        return _lib.SDF_ALPHA_STANDARD
+    mode = str(alpha_mode).lower()
+    if mode in ("sdfoam", "sdf", "alpha_neus"):
+        return _lib.SDF_ALPHA_NEUS
+    return _lib.SDF_ALPHA_STANDARD
+
+
+def _inv_s_to_tensor(inv_s, like: torch.Tensor) -> torch.Tensor:
+    """torch_bindings/pipeline_bindings.cpp:124-136."""
+    if inv_s is None:
+        return torch.ones(1, dtype=torch.float32, device=like.device)
+    if not isinstance(inv_s, torch.Tensor):
+        return torch.tensor([float(inv_s)], dtype=torch.float32, device=like.device)
+    s = inv_s.contiguous()
+    if s.device != like.device or s.dtype != torch.float32:
+        s = s.to(like.device, torch.float32).contiguous()
+    return s
+
+
+class Pipeline:
+    """A tracing pipeline for one SH degree and attribute dtype
+    (src/tracing/pipeline.h:79-161)."""
+
+    def __init__(self, sh_degree: int, attr_dtype: torch.dtype):
+        self._sh_degree = int(sh_degree)
+        self._attr_dtype = attr_dtype
+
+    # -- src/tracing/pipeline.h:158-160 -------------------------------------
+    def attribute_dim(self) -> int:
+        return 1 + 3 * (self._sh_degree + 1) ** 2
+
+    def attribute_type(self) -> torch.dtype:
+        return self._attr_dtype
+
+    @property
+    def sh_degree(self) -> int:
+        return self._sh_degree
+
+    # -- validation (torch_bindings/pipeline_bindings.cpp:12-75) -------------
+    def _validate_scene_data(self, points, attributes, point_adjacency, point_adjacency_offsets):
+        if points.size(-1) != 3:
+            raise RuntimeError(f"points had dimension {points.size(-1)} along axis -1, expected 3")
+        if _scalar_type(points.dtype) != "float32":
+            raise RuntimeError(f"points had dtype {_c10(points.dtype)}, expected float32")
+        if not _is_cuda(points):
+            raise RuntimeError("points must be on CUDA device")
+        num_points = points.numel() // 3
+        D = self.attribute_dim()
+        if attributes.size(-1) != D:
+            raise RuntimeError(
+                f"attributes had dimension {attributes.size(-1)} along axis -1, expected {D}")
+        if attributes.numel() // D != num_points:
+            raise RuntimeError("attributes must have the same number of rows as points")
+        if attributes.dtype != self._attr_dtype:
+            _scalar_type(attributes.dtype)
+            raise RuntimeError(
+                f"attributes had dtype {_c10(attributes.dtype)}, expected "
+                f"{_SCALAR_NAMES[self._attr_dtype]}")
+        if not _is_cuda(attributes):
+            raise RuntimeError("attributes must be on CUDA device")
+        if point_adjacency_offsets.dtype != torch.uint32:
+            raise RuntimeError("point_adjacency_offsets must have uint32 dtype")
+        if not _is_cuda(point_adjacency_offsets):
+            raise RuntimeError("point_adjacency_offsets must be on CUDA device")
+        if point_adjacency_offsets.numel() != num_points + 1:
+            raise RuntimeError("point_adjacency_offsets must have num_points + 1 elements")
+        if point_adjacency.dtype != torch.uint32:
+            raise RuntimeError("point_adjacency must have uint32 dtype")
+        if not _is_cuda(point_adjacency):
+            raise RuntimeError("point_adjacency must be on CUDA device")
+
+    def _validate_rays(self, rays, start_point, num_rays):
+        if rays.size(-1) != 6:
+            raise RuntimeError("rays must have 6 as the last dimension")
+        if rays.dtype != torch.float32:
+            raise RuntimeError("rays must have float32 dtype")
+        if not _is_cuda(rays):
+            raise RuntimeError("rays must be on CUDA device")
+        if start_point.numel() != num_rays:
+            raise RuntimeError("start_point must have the same batch size as rays")
+        if start_point.dtype != torch.uint32:
+            raise RuntimeError("start_point must have uint32 dtype")
+        if not _is_cuda(start_point):
+            raise RuntimeError("start_point must be on CUDA device")
+
+    def _settings(self, weight_threshold, max_intersections, alpha_mode, sdf_channel):
+        """default_trace_settings + kwargs (src/tracing/pipeline.h:29-40;
+        torch_bindings/pipeline_bindings.cpp:212-242)."""
+        mode = _parse_alpha_mode(alpha_mode)
+        if sdf_channel is not None:
+            ch = int(sdf_channel)
+        elif mode == _lib.SDF_ALPHA_NEUS:
+            ch = self.attribute_dim() - 1
+        else:
+            ch = -1
+        return TraceSettings(
+            1e-7 if weight_threshold is None else float(weight_threshold),
+            1024 if max_intersections is None else int(max_intersections),
+            mode,
+            ch,
+        )
+
+    def _require_native(self):
+        if self._attr_dtype != torch.float32:
+            raise RuntimeError(
+                "float16 attribute pipelines are not available in this build "
+                "(only float32 attributes are traced)")
+
+    @staticmethod
+    def _scratch(num_points: int, num_adj: int, device) -> tuple[torch.Tensor, int]:
+        nbytes = int(_lib.lib().sdf_trace_scratch_bytes(num_points, num_adj))
+        buf = torch.empty((nbytes + 7) // 8, dtype=torch.int64, device=device)
+        return buf, nbytes
+
+    # -- trace_forward (torch_bindings/pipeline_bindings.cpp:138-334) -------
+    def trace_forward(self, points, attributes, point_adjacency, point_adjacency_offsets, rays,
+                      start_point, depth_quantiles=None, weight_threshold=None,
+                      max_intersections=None, return_contribution=False, alpha_mode=None,
+                      inv_s=None, eps=None, sdf_channel=None):
+        points_c = points.contiguous()
+        attributes_c = attributes.contiguous()
+        adj_c = point_adjacency.contiguous()
+        offs_c = point_adjacency_offsets.contiguous()
+        rays_c = rays.contiguous()
+        start_c = start_point.contiguous()
+        sharpness = _inv_s_to_tensor(inv_s, rays_c)
+
+        self._validate_scene_data(points, attributes, point_adjacency, point_adjacency_offsets)
+        return_depth = depth_quantiles is not None
+        num_points = points_c.size(0)
+        num_adj = adj_c.size(0)
+        num_rays = rays_c.numel() // 6
+        self._validate_rays(rays_c, start_c, num_rays)
+        num_q = 0
+        dq = None
+        if return_depth:
+            dq = depth_quantiles.contiguous()
+            num_q = dq.size(-1)
+            if dq.dtype != torch.float32:
+                raise RuntimeError("depth_quantiles must have float32 dtype")
+            if not _is_cuda(dq):
+                raise RuntimeError("depth_quantiles must be on CUDA device")
+            if num_q == 0 or dq.numel() // num_q != num_rays:
+                raise RuntimeError("depth_quantiles must have the same batch size as rays")
+        settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel)
+        self._require_native()
+
+        dev = rays_c.device
+        lead = tuple(rays_c.shape[:-1])
+        rgba = torch.empty(lead + (4,), dtype=self._attr_dtype, device=dev)
+        nisect = torch.empty(lead + (1,), dtype=torch.uint32, device=dev)
+        contribution = (torch.zeros((num_points, 1), dtype=self._attr_dtype, device=dev)
+                        if return_contribution else None)
+        depth = didx = None
+        if return_depth:
+            depth = torch.zeros(lead + (num_q,), dtype=torch.float32, device=dev)
+            didx = torch.zeros(lead + (num_q,), dtype=torch.uint32, device=dev)
+        alpha = torch.zeros((num_points, 1), dtype=torch.float32, device=dev)
+        scratch, nbytes = self._scratch(num_points, num_adj, dev)
+        with torch.cuda.device(dev):
+            check(_lib.lib().sdf_trace_forward(
+                self._sh_degree, C.byref(settings), num_points, ptr(points_c), ptr(attributes_c),
+                num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c), ptr(start_c), num_q,
+                ptr(dq), ptr(rgba), ptr(depth), ptr(didx), ptr(nisect), ptr(contribution),
+                ptr(sharpness), ptr(alpha), ptr(scratch), nbytes, _lib.stream_handle(dev)))
+        out = {"rgba": rgba}
+        if return_depth:
+            out["depth"] = depth
+            out["depth_indices"] = didx
+        if return_contribution:
+            out["contribution"] = contribution
+        out["num_intersections"] = nisect
+        out["alpha"] = alpha
+        return out
+
+    # -- trace_backward (torch_bindings/pipeline_bindings.cpp:336-607) ------
+    def trace_backward(self, points, attributes, point_adjacency, point_adjacency_offsets, rays,
+                       start_point, rgb_out, grad_in, depth_quantiles=None, depth_indices=None,
+                       depth_grad_in=None, ray_error=None, weight_threshold=None,
+                       max_intersections=None, alpha_mode=None, inv_s=None, eps=None,
+                       sdf_channel=None):
+        points_c = points.contiguous()
+        attributes_c = attributes.contiguous()
+        adj_c = point_adjacency.contiguous()
+        offs_c = point_adjacency_offsets.contiguous()
+        rays_c = rays.contiguous()
+        start_c = start_point.contiguous()
+        sharpness = _inv_s_to_tensor(inv_s, rays_c)
+
+        self._validate_scene_data(points, attributes, point_adjacency, point_adjacency_offsets)
+        return_depth = depth_quantiles is not None
+        return_error = ray_error is not None
+        num_points = points_c.size(0)
+        num_adj = adj_c.size(0)
+        num_rays = rays_c.numel() // 6
+        self._validate_rays(rays_c, start_c, num_rays)
+
+        g = grad_in.contiguous()
+        if g.size(-1) != 4:
+            raise RuntimeError("rgb_grad_in must have 4 as the last dimension")
+        if g.dtype != self._attr_dtype:
+            _scalar_type(g.dtype)
+            raise RuntimeError(
+                f"rgb_grad_in had dtype {_c10(g.dtype)}, expected {_SCALAR_NAMES[self._attr_dtype]}")
+        if not _is_cuda(g):
+            raise RuntimeError("rgb_grad_in must be on CUDA device")
+        if g.numel() // 4 != num_rays:
+            raise RuntimeError("rgb_grad_in must have the same batch size as rays")
+
+        num_q = 0
+        dq = didx = dgrad = None
+        if return_depth:
+            dq = depth_quantiles.contiguous()
+            num_q = dq.size(-1)
+            if dq.dtype != torch.float32:
+                raise RuntimeError("depth_quantiles must have float32 dtype")
+            if not _is_cuda(dq):
+                raise RuntimeError("depth_quantiles must be on CUDA device")
+            if dq.numel() != num_rays * num_q:
+                raise RuntimeError("depth_quantiles must have the same batch size as rays")
+            if depth_grad_in is None:
+                raise RuntimeError("depth_grad must be provided if depth_quantiles is provided")
+            if depth_indices is None:
+                raise RuntimeError("bad optional access")
+            didx = depth_indices.contiguous()
+            if didx.dtype != torch.uint32:
+                raise RuntimeError("depth_indices must have uint32 dtype")
+            if not _is_cuda(didx):
+                raise RuntimeError("depth_indices must be on CUDA device")
+            if didx.numel() != num_rays * num_q:
+                raise RuntimeError("depth_indices must have the same batch size as rays")
+            dgrad = depth_grad_in.contiguous()
+            if dgrad.size(-1) != num_q:
+                raise RuntimeError(
+                    "depth_grad must have the same number of depth quantiles as depth_quantiles")
+            if dgrad.dtype != torch.float32:
+                _scalar_type(dgrad.dtype)
+                raise RuntimeError(f"depth_grad had dtype {_c10(dgrad.dtype)}, expected float32")
+            if not _is_cuda(dgrad):
+                raise RuntimeError("depth_grad must be on CUDA device")
+            if dgrad.numel() != num_rays * num_q:
+                raise RuntimeError("depth_grad must have the same batch size as rays")
+
+        rerr = None
+        point_error = None
+        dev = rays_c.device
+        if return_error:
+            rerr = ray_error.contiguous()
+            if rerr.dtype != self._attr_dtype:
+                _scalar_type(rerr.dtype)
+                raise RuntimeError(
+                    f"ray_error had dtype {_c10(rerr.dtype)}, expected {_SCALAR_NAMES[self._attr_dtype]}")
+            if not _is_cuda(rerr):
+                raise RuntimeError("ray_error must be on CUDA device")
+            if rerr.numel() != num_rays:
+                raise RuntimeError("ray_error must have the same batch size as rays")
+            point_error = torch.zeros((num_points, 1), dtype=self._attr_dtype, device=dev)
+
+        settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel)
+        self._require_native()
+        rgba = rgb_out.contiguous()
+        if rgba.dtype != self._attr_dtype or rgba.numel() != 4 * num_rays or not _is_cuda(rgba):
+            raise RuntimeError("rgb_out must be the forward's rgba output")
+
+        num_attr = attributes_c.size(0)
+        attr_grad = torch.zeros((num_attr, self.attribute_dim()), dtype=self._attr_dtype, device=dev)
+        points_grad = torch.zeros((num_points, 3), dtype=rays_c.dtype, device=dev)
+        ray_grad = torch.zeros_like(rays_c)
+        sharpness_grad = torch.zeros_like(sharpness, dtype=torch.float32)
+        scratch, nbytes = self._scratch(num_points, num_adj, dev)
+        with torch.cuda.device(dev):
+            check(_lib.lib().sdf_trace_backward(
+                self._sh_degree, C.byref(settings), num_points, ptr(points_c), ptr(attributes_c),
+                num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c), ptr(start_c), num_q,
+                ptr(dq), ptr(didx), ptr(rgba), ptr(g), ptr(dgrad), ptr(rerr), ptr(points_grad),
+                ptr(attr_grad), ptr(point_error), ptr(sharpness), ptr(sharpness_grad),
+                ptr(scratch), nbytes, _lib.stream_handle(dev)))
+        out = {
+            "points_grad": points_grad,
+            "attr_grad": attr_grad,
+            "ray_grad": ray_grad,
+            "sharpness_grad": sharpness_grad,
+        }
+        if return_error:
+            out["point_error"] = point_error
+        return out
+
+    # -- walk statistics (measurement / parity hook) -------------------------
+    def walk_stats(self, points, attributes, point_adjacency, point_adjacency_offsets, rays,
+                   start_point, *, backward=False, alpha_mode=None, inv_s=None,
+                   weight_threshold=None, max_intersections=None, sdf_channel=None,
+                   record_cells: int = 0):
+        """Per-ray visit hash, step count, faces scanned and faces of stepped
+        cells of the forward (or backward) walk, plus the first
+        ``record_cells`` visited cells of each ray."""
+        points_c = points.contiguous()
+        attributes_c = attributes.contiguous()
+        adj_c = point_adjacency.contiguous()
+        offs_c = point_adjacency_offsets.contiguous()
+        rays_c = rays.contiguous()
+        start_c = start_point.contiguous()
+        self._validate_scene_data(points, attributes, point_adjacency, point_adjacency_offsets)
+        num_rays = rays_c.numel() // 6
+        self._validate_rays(rays_c, start_c, num_rays)
+        self._require_native()
+        sharpness = _inv_s_to_tensor(inv_s, rays_c)
+        settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel)
+        dev = rays_c.device
+        n = points_c.size(0)
+        num_adj = adj_c.size(0)
+        vh = torch.zeros(num_rays, dtype=torch.int64, device=dev)
+        steps = torch.zeros(num_rays, dtype=torch.int32, device=dev)
+        faces = torch.zeros(num_rays, dtype=torch.int64, device=dev)
+        faces_st = torch.zeros(num_rays, dtype=torch.int64, device=dev)
+        cells = (torch.full((num_rays, record_cells), -1, dtype=torch.int32, device=dev)
+                 if record_cells else None)
+        scratch, nbytes = self._scratch(n, num_adj, dev)
+        with torch.cuda.device(dev):
+            check(_lib.lib().sdf_trace_walk_stats(
+                self._sh_degree, C.byref(settings), 1 if backward else 0, n, ptr(points_c),
+                ptr(attributes_c), num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c),
+                ptr(start_c), ptr(sharpness), ptr(vh), ptr(steps), ptr(faces), ptr(faces_st),
+                ptr(cells), record_cells, ptr(scratch), nbytes, _lib.stream_handle(dev)))
+        return {"visit_hash": vh, "steps": steps, "faces": faces, "faces_stepped": faces_st,
+                "cells": cells}
+
+
+_registry: list[Pipeline] = []
+
+
+def create_pipeline(sh_degree: int, attr_dtype: str = "float32") -> Pipeline:
+    """torch_bindings/pipeline_bindings.cpp:747-751 and src/tracing/pipeline.cu:1476-1506.
+    Pipelines are kept in a process-wide registry, as the reference does."""
+    st = _dtype_string_to_scalar_type(str(attr_dtype))
+    if st == "float64":
+        raise RuntimeError("Unsupported attribute type")
+    if int(sh_degree) not in (0, 1, 2, 3):
+        raise RuntimeError("Unsupported SH degree")
+    p = Pipeline(int(sh_degree), torch.float32 if st == "float32" else torch.float16)
+    _registry.append(p)
+    return p
+
+
+def prefetch_adjacent_diff(points, point_adjacency, point_adjacency_offsets) -> torch.Tensor:
+    """fp16 neighbour offsets [E + 32, 4] (src/tracing/pipeline.cu:1202-1242)."""
+    points_c = points.contiguous()
+    adj_c = point_adjacency.contiguous()
+    offs_c = point_adjacency_offsets.contiguous()
+    n = points_c.size(0)
+    e = adj_c.size(0)
+    out = torch.empty((e + 32, 4), dtype=torch.float16, device=points_c.device)
+    with torch.cuda.device(points_c.device):
+        check(_lib.lib().sdf_prefetch_adjacent_diff(
+            ptr(points_c), n, e, ptr(adj_c), ptr(offs_c), ptr(out),
+            _lib.stream_handle(points_c.device)))
+    return out

@@ -1,0 +1,373 @@
+"""GPU parity: libsdfoam_hip.so (through its C ABI, via the sdfoam_amd host
+mirror) against the scalar host oracle on the same seeded inputs.
+
+Bars (the contract of the port):
+* visit sequences (hash + step count + full sequences on C1),
+  num_intersections, depth_indices, fp16 offset table, AABB tree, nn:
+  bit-exact;
+* rgba, depth: |d| <= 1e-5 + 1e-4 |ref|;
+* gradients and contribution (fp32 atomics in any order against the
+  oracle's fp64 sum): |d| <= 1e-5 + 1e-4 |ref| + gamma_{K-1} A, with
+  A = sum |c_k| over the element's K contributions and
+  gamma_n = n u / (1 - n u), u = 2^-24 (the order-independent bound for
+  recursive summation, Higham 2002, section 4.2);
+* alpha: the value some visiting step of that point wrote (the reference
+  stores it racily, src/tracing/pipeline.cu:159); untouched points stay 0.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+from conftest import scene
+
+pytestmark = pytest.mark.gpu
+
+U = 2.0 ** -24
+
+
+def _threads():
+    try:
+        return max(1, min(16, len(os.sched_getaffinity(0))))
+    except AttributeError:
+        return 4
+
+
+def gamma(k):
+    k = np.maximum(np.asarray(k, dtype=np.float64) - 1.0, 0.0)
+    ku = k * U
+    return ku / (1.0 - ku)
+
+
+def assert_close_model(name, got, ref, abs_sum, k):
+    got = np.asarray(got, dtype=np.float64)
+    tol = 1e-5 + 1e-4 * np.abs(ref) + gamma(k) * abs_sum
+    err = np.abs(got - ref)
+    bad = ~(err <= tol)
+    if bad.any():
+        i = np.argmax(np.where(bad, err / np.maximum(tol, 1e-30), 0))
+        raise AssertionError(
+            f"{name}: {int(bad.sum())} of {bad.size} elements out of tolerance; worst at "
+            f"{np.unravel_index(i, np.shape(ref))}: got {got.ravel()[i]!r} ref {np.ravel(ref)[i]!r} "
+            f"tol {tol.ravel()[i]!r}")
+
+
+def assert_close(name, got, ref, rtol=1e-4, atol=1e-5):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    err = np.abs(got - ref)
+    tol = atol + rtol * np.abs(ref)
+    bad = ~(err <= tol)
+    if bad.any():
+        i = np.argmax(np.where(bad, err, 0))
+        raise AssertionError(f"{name}: {int(bad.sum())} of {bad.size} out of tolerance; worst "
+                             f"got {got.ravel()[i]!r} ref {ref.ravel()[i]!r}")
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def to_dev(a, dev, dtype=None):
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.to(dev)
+
+
+def u32(a, dev):
+    import torch
+
+    return to_dev(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32), dev).view(torch.uint32)
+
+
+def np_u32(t):
+    import torch
+
+    return t.view(torch.int32).cpu().numpy().view(np.uint32)
+
+
+def gpu_scene(w, dev):
+    return dict(
+        points=to_dev(w.points, dev),
+        attributes=to_dev(w.attributes, dev),
+        point_adjacency=u32(w.adjacency, dev),
+        point_adjacency_offsets=u32(w.offsets, dev),
+        rays=to_dev(w.rays, dev),
+        start_point=u32(w.extra["start"], dev),
+    )
+
+
+# ---------------------------------------------------------------------------
+
+
+def test_fpmath_device_bitexact(torch_dev, oracle_lib):
+    import torch
+
+    from sdfoam_amd import _lib
+
+    rng = np.random.default_rng(7)
+    x = np.concatenate([
+        rng.uniform(-110, 100, 400_000),
+        rng.uniform(-1, 1, 400_000),
+        rng.normal(0, 1e-3, 100_000),
+        np.array([0.0, -0.0, 88.72, 88.73, -87.33, -87.34, -103.0, 1e-30, -1e-30, np.inf, -np.inf]),
+    ]).astype(np.float32)
+    xd = to_dev(x, torch_dev)
+    out = torch.empty_like(xd)
+    _lib.check(_lib.lib().sdf_debug_fpmath(0, xd.data_ptr(), out.data_ptr(), x.size, None))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ref = oracle_lib.expf(x)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "device exp differs from host"
+
+    # fp16 rounding: wide range incl. halfway points, subnormals and overflow
+    y = np.concatenate([
+        rng.uniform(-70000, 70000, 200_000),
+        rng.uniform(-2, 2, 400_000),
+        rng.uniform(-1e-4, 1e-4, 200_000),
+        (np.arange(1, 2048, dtype=np.float64) * 2.0 ** -25),
+        (np.arange(1, 4096, dtype=np.float64) * 2.0 ** -12 + 0.5 * 2.0 ** -11),
+    ]).astype(np.float32)
+    yd = to_dev(y, torch_dev)
+    h = torch.empty(y.size, dtype=torch.int16, device=torch_dev)
+    _lib.check(_lib.lib().sdf_debug_fpmath(1, yd.data_ptr(), h.data_ptr(), y.size, None))
+    torch.cuda.synchronize()
+    got_h = h.cpu().numpy().view(np.uint16)
+    assert np.array_equal(got_h, oracle_lib.f32_to_f16_bits(y))
+    assert np.array_equal(got_h, y.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("cfg", [1, 2])
+def test_prefetch_diff_bitexact(torch_dev, oracle_lib, cfg):
+    import torch
+
+    from sdfoam_amd import prefetch_adjacent_diff
+
+    w = scene(cfg)
+    g = gpu_scene(w, torch_dev)
+    d = prefetch_adjacent_diff(g["points"], g["point_adjacency"], g["point_adjacency_offsets"])
+    torch.cuda.synchronize()
+    got = d.cpu().numpy().view(np.uint16)[: w.adjacency.size]
+    ref = oracle_lib.prefetch_adjacent_diff(w.points, w.adjacency, w.offsets)
+    assert np.array_equal(got, ref)
+
+
+def _forward_both(w, dev, oracle_lib, mode, record=0, inv_s=None):
+    import torch
+
+    import sdfoam_amd
+
+    inv = w.inv_s if inv_s is None else inv_s
+    g = gpu_scene(w, dev)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    q = to_dev(w.quantiles, dev)
+    out = pipe.trace_forward(**g, depth_quantiles=q, return_contribution=True, alpha_mode=mode,
+                             inv_s=torch.tensor([inv], device=dev))
+    st = pipe.walk_stats(**g, alpha_mode=mode, inv_s=torch.tensor([inv], device=dev),
+                         record_cells=record)
+    torch.cuda.synchronize()
+    ref = oracle_lib.trace_forward(
+        w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, w.rays, w.extra["start"],
+        w.quantiles, alpha_mode=mode, inv_s=inv, record=record, threads=_threads())
+    return out, st, ref
+
+
+def _check_forward(out, st, ref, w, record):
+    R = w.num_rays
+    ni = np_u32(out["num_intersections"]).reshape(R)
+    assert np.array_equal(ni, ref.num_intersections.reshape(R)), "num_intersections"
+    vh = st["visit_hash"].cpu().numpy().view(np.uint64)
+    assert np.array_equal(vh, ref.visit_hash.reshape(R)), "visit hash"
+    assert np.array_equal(st["steps"].cpu().numpy().astype(np.uint32), ref.steps.reshape(R))
+    assert np.array_equal(st["faces"].cpu().numpy().astype(np.uint64), ref.faces.reshape(R))
+    if record:
+        cells = st["cells"].cpu().numpy().view(np.uint32)
+        n = np.minimum(ref.steps.reshape(R), record)
+        mask = np.arange(record)[None, :] < n[:, None]
+        assert np.array_equal(np.where(mask, cells, 0), np.where(mask, ref.cells, 0)), "cells"
+    assert np.array_equal(np_u32(out["depth_indices"]).reshape(R, -1),
+                          ref.depth_indices.reshape(R, -1)), "depth_indices"
+    rgba = out["rgba"].cpu().numpy().reshape(R, 4)
+    assert_close("rgba", rgba, ref.rgba.reshape(R, 4))
+    assert_close("depth", out["depth"].cpu().numpy().reshape(R, -1), ref.depth.reshape(R, -1))
+    contrib = out["contribution"].cpu().numpy().reshape(-1)
+    cref = ref.contribution.reshape(-1)
+    assert_close_model("contribution", contrib, cref, np.abs(cref), R)
+    # alpha: some visiting step's value; unvisited points untouched
+    alpha = out["alpha"].cpu().numpy().reshape(-1)
+    visited = np.zeros(w.num_points, dtype=bool)
+    if record:
+        cells = ref.cells
+        n = np.minimum(ref.steps.reshape(R), record)
+        mask = np.arange(record)[None, :] < n[:, None]
+        vc = cells[mask]
+        va = ref.cell_alphas[mask]
+        visited[vc] = True
+        pairs = set(zip(vc.tolist(), va.view(np.uint32).tolist()))
+        for p in np.nonzero(visited)[0]:
+            assert (int(p), int(alpha[p:p + 1].view(np.uint32)[0])) in pairs, f"alpha of point {p}"
+        assert np.all(alpha[~visited] == 0.0)
+    return rgba
+
+
+@pytest.mark.parametrize("mode", ["sdfoam", "standard"])
+def test_forward_parity_c1(torch_dev, oracle_lib, mode):
+    w = scene(1, mode=mode)
+    out, st, ref = _forward_both(w, torch_dev, oracle_lib, mode, record=1100)
+    rgba = _check_forward(out, st, ref, w, 1100)
+    print(f"C1 {mode}: rgba bit-exact fraction "
+          f"{np.mean(rgba.view(np.uint32) == ref.rgba.reshape(-1, 4).view(np.uint32)):.4f}")
+
+
+def test_forward_parity_c2(torch_dev, oracle_lib):
+    w = scene(2)
+    out, st, ref = _forward_both(w, torch_dev, oracle_lib, "sdfoam", record=0)
+    _check_forward(out, st, ref, w, 0)
+
+
+def test_forward_parity_c2_sharp(torch_dev, oracle_lib):
+    """inv_s = 50: opaque surfaces, walks end early on the weight threshold."""
+    w = scene(2)
+    out, st, ref = _forward_both(w, torch_dev, oracle_lib, "sdfoam", record=0, inv_s=50.0)
+    _check_forward(out, st, ref, w, 0)
+
+
+def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False):
+    import torch
+
+    import sdfoam_amd
+
+    inv = w.inv_s if inv_s is None else inv_s
+    g = gpu_scene(w, dev)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    q = to_dev(w.quantiles, dev)
+    inv_t = torch.tensor([inv], device=dev)
+    fwd = pipe.trace_forward(**g, depth_quantiles=q, alpha_mode=mode, inv_s=inv_t)
+    rerr = None
+    if ray_error:
+        rerr_np = np.random.default_rng(11).uniform(0, 1, w.rays.shape[:-1]).astype(np.float32)
+        rerr = to_dev(rerr_np, dev)
+    bwd = pipe.trace_backward(**g, rgb_out=fwd["rgba"], grad_in=to_dev(w.grad_rgba, dev),
+                              depth_quantiles=q, depth_indices=fwd["depth_indices"],
+                              depth_grad_in=to_dev(w.depth_grad, dev), ray_error=rerr,
+                              alpha_mode=mode, inv_s=inv_t)
+    st = pipe.walk_stats(**g, backward=True, alpha_mode=mode, inv_s=inv_t)
+    torch.cuda.synchronize()
+    rgba = fwd["rgba"].cpu().numpy()
+    didx = np_u32(fwd["depth_indices"])
+    ref = oracle_lib.trace_backward(
+        w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, w.rays, w.extra["start"],
+        rgba, w.grad_rgba, w.quantiles, didx, w.depth_grad,
+        None if rerr is None else rerr.cpu().numpy(), alpha_mode=mode, inv_s=inv,
+        threads=_threads())
+    return bwd, st, ref
+
+
+def _check_backward(bwd, st, ref, w):
+    R = w.num_rays
+    vh = st["visit_hash"].cpu().numpy().view(np.uint64)
+    assert np.array_equal(vh, ref.visit_hash.reshape(R)), "backward visit hash"
+    assert_close_model("points_grad", bwd["points_grad"].cpu().numpy(), ref.points_grad,
+                       ref.points_grad_abs, ref.points_grad_k)
+    assert_close_model("attr_grad", bwd["attr_grad"].cpu().numpy(), ref.attr_grad,
+                       ref.attr_grad_abs, ref.attr_grad_k)
+    sg = float(bwd["sharpness_grad"].cpu().numpy().reshape(-1)[0])
+    assert_close_model("sharpness_grad", np.array([sg]), np.array([ref.sharpness_grad]),
+                       np.array([ref.sharpness_abs]), np.array([ref.sharpness_k]))
+    print(f"sharpness: gpu {sg!r} ref {ref.sharpness_grad!r} |d| {abs(sg - ref.sharpness_grad):.3e} "
+          f"sqrt(K) u A {np.sqrt(max(ref.sharpness_k, 1)) * U * ref.sharpness_abs:.3e}")
+    if "point_error" in bwd:
+        assert_close_model("point_error", bwd["point_error"].cpu().numpy().reshape(-1),
+                           ref.point_error.reshape(-1), np.abs(ref.point_error.reshape(-1)), R)
+    assert np.all(bwd["ray_grad"].cpu().numpy() == 0)
+
+
+@pytest.mark.parametrize("mode", ["sdfoam", "standard"])
+def test_backward_parity_c1(torch_dev, oracle_lib, mode):
+    w = scene(1, mode=mode)
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, mode, ray_error=True)
+    _check_backward(bwd, st, ref, w)
+
+
+def test_backward_parity_c2(torch_dev, oracle_lib):
+    w = scene(2)
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "sdfoam")
+    _check_backward(bwd, st, ref, w)
+
+
+def test_aabb_tree_and_nn_exact(torch_dev, oracle_lib):
+    import torch
+
+    import sdfoam_amd
+
+    w = scene(2)
+    pts = to_dev(w.points, torch_dev)
+    tree = sdfoam_amd.build_aabb_tree(pts)
+    torch.cuda.synchronize()
+    ref_tree = oracle_lib.build_aabb_tree(w.points)
+    got = tree.cpu().numpy()
+    n2 = got.shape[0]
+    assert np.array_equal(got[: n2 - 1], ref_tree[: n2 - 1])
+    rng = np.random.default_rng(5)
+    queries = np.concatenate([
+        rng.uniform(-1.6, 1.6, (3000, 3)),
+        rng.normal(0, 3, (500, 3)),
+        w.points[rng.integers(0, w.num_points, 200)],  # exact hits
+        w.rays.reshape(-1, 6)[:1, :3],
+    ]).astype(np.float32)
+    idx = sdfoam_amd.nn(pts, tree, to_dev(queries, torch_dev))
+    torch.cuda.synchronize()
+    ref = oracle_lib.nn(w.points, queries, threads=_threads())
+    assert np.array_equal(np_u32(idx), ref)
+
+
+def test_get_starting_point_matches_nn(torch_dev, oracle_lib):
+    import torch
+
+    import sdfoam_amd
+
+    w = scene(1)
+    pts = to_dev(w.points, torch_dev)
+    tree = sdfoam_amd.build_aabb_tree(pts)
+    rays = to_dev(w.rays, torch_dev)
+    sp = sdfoam_amd.get_starting_point(rays, pts, tree)
+    torch.cuda.synchronize()
+    assert sp.dtype == torch.uint32 and tuple(sp.shape) == w.rays.shape[:-1]
+    assert np.array_equal(np_u32(sp), w.extra["start"])
+
+
+def test_trace_rays_autograd(torch_dev):
+    import torch
+
+    import sdfoam_amd
+
+    w = scene(1)
+    g = gpu_scene(w, torch_dev)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    pts = g["points"].clone().requires_grad_(True)
+    attrs = g["attributes"].clone().requires_grad_(True)
+    inv = torch.full((w.num_points, 1), w.inv_s, device=torch_dev, requires_grad=True)
+    q = to_dev(w.quantiles, torch_dev)
+    rgba, depth, contrib, nis, errbox, alpha = sdfoam_amd.TraceRays.apply(
+        pipe, pts, attrs, g["point_adjacency"], g["point_adjacency_offsets"], g["rays"],
+        g["start_point"], q, True, True, inv, 1e-6, w.attributes.shape[-1] - 1)
+    gr = to_dev(w.grad_rgba, torch_dev)
+    gd = to_dev(w.depth_grad, torch_dev)
+    loss = (rgba * gr).sum() + (depth * gd).sum()
+    loss.backward()
+    assert pts.grad is not None and attrs.grad is not None and inv.grad is not None
+    assert torch.isfinite(pts.grad).all() and torch.isfinite(attrs.grad).all()
+    assert inv.grad.shape == inv.shape
+    # only element 0 of the sharpness gradient is written (the reference reads sharpness[0])
+    assert torch.count_nonzero(inv.grad[1:]) == 0
+    assert float(rgba.detach()[..., 3].max()) <= 1.0
+    del contrib, nis, errbox, alpha
