@@ -1,0 +1,260 @@
+#!/usr/bin/env python
+"""Throughput of the Voronoi-foam tracer, forward + backward, on one MI355X.
+
+Workload (default): config C3 -- 1M points (superquadric surface + uniform
+box), SH degree 3, sdfoam alpha, inv_s = exp(0.3), 1600x1200 pinhole rays,
+one depth quantile, upstream gradients N(0,1); all synthetic and seeded.
+Inputs are resident in HBM before the timed region.
+
+A step is one training pass of the path through the drop-in API:
+``Pipeline.trace_forward`` (with contribution and depth) then
+``Pipeline.trace_backward`` -- each runs the fp16 offset prepass and its
+kernel, as the reference does.
+
+Output: one JSON line on stdout.  ``roofline`` prices the dominant kernel's
+algorithmic bytes (the gather model below) against MI355X's 8 TB/s, with the
+kernel's average duration measured live by HIP events recorded on its launch
+stream.  ``cpu_baseline`` is the scalar host oracle (a port of the
+reference's algorithm) on a strided sample of the same rays, on this host's
+cores.
+
+Byte model (per launch; D = attribute width, deg = CSR row length of the
+stepped cell, Q = quantiles):
+  forward : per ray 48 + 12Q; per step 28 + 4D + 4 (contribution) + 8 deg
+  backward: per ray 60 + 12Q; per step 36 + 8D + 8 deg
+  prepass : 12 E + 16 N
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Mrays/s fwd+bwd at 1M pts/1600x1200 rays; % HBM roofline"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3])
+    ap.add_argument("--cpu-stride", type=int, default=8,
+                    help="CPU baseline traces every n-th ray (0 skips it)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py runs on one GPU only: this build has no multi-GPU path "
+              "(rays would shard across GPUs with one gradient all-reduce; not built)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import _lib, scenes
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    _lib.lib()
+
+    t0 = time.time()
+    log(f"generating config C{args.config} (Delaunay via Qhull)")
+    w = scenes.make_config(args.config)
+    log(f"scene ready in {time.time() - t0:.1f}s: N={w.num_points} E={w.adjacency.size} R={w.num_rays}")
+
+    def u32(a):
+        return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(dev).view(torch.uint32)
+
+    pts = torch.from_numpy(w.points).to(dev)
+    attrs = torch.from_numpy(w.attributes).to(dev)
+    adj, offs = u32(w.adjacency), u32(w.offsets)
+    rays = torch.from_numpy(w.rays).to(dev)
+    q = torch.from_numpy(w.quantiles).to(dev)
+    grad_rgba = torch.from_numpy(w.grad_rgba).to(dev)
+    depth_grad = torch.from_numpy(w.depth_grad).to(dev)
+    inv = torch.tensor([w.inv_s], dtype=torch.float32, device=dev)
+    tree = sdfoam_amd.build_aabb_tree(pts)
+    start = sdfoam_amd.get_starting_point(rays, pts, tree)
+    torch.cuda.synchronize()
+    host_start = scenes.start_points_for(w.points, w.rays)
+    if not np.array_equal(start.view(torch.int32).cpu().numpy().view(np.uint32), host_start):
+        raise RuntimeError("GPU start cells differ from the host nearest neighbour")
+
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    D = pipe.attribute_dim()
+    Q = int(w.quantiles.shape[-1])
+
+    def step():
+        out = pipe.trace_forward(pts, attrs, adj, offs, rays, start, depth_quantiles=q,
+                                 return_contribution=True, alpha_mode="sdfoam", inv_s=inv)
+        bwd = pipe.trace_backward(pts, attrs, adj, offs, rays, start, out["rgba"], grad_rgba, q,
+                                  out["depth_indices"], depth_grad, alpha_mode="sdfoam", inv_s=inv)
+        return out, bwd
+
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    log(f"timing {args.steps} steps")
+    _lib.set_timing(True)
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t_end = time.perf_counter()
+    launches = _lib.collect_timings()
+    _lib.set_timing(False)
+    ms_per_step = (t_end - t_start) * 1e3 / args.steps
+    log(f"{ms_per_step:.3f} ms/step")
+
+    per_kernel: dict[str, list[float]] = {}
+    for name, ms in launches:
+        per_kernel.setdefault(name, []).append(ms)
+    avg = {k: float(np.mean(v)) for k, v in per_kernel.items()}
+
+    # walk statistics for the byte model (untimed)
+    st = pipe.walk_stats(pts, attrs, adj, offs, rays, start, alpha_mode="sdfoam", inv_s=inv)
+    torch.cuda.synchronize()
+    S = int(st["steps"].sum().item())
+    F_st = int(st["faces_stepped"].sum().item())
+    F_all = int(st["faces"].sum().item())
+    R = w.num_rays
+    N = w.num_points
+    E = int(w.adjacency.size)
+    bytes_fwd = R * (48 + 12 * Q) + S * (28 + 4 * D + 4) + 8 * F_st
+    bytes_bwd = R * (60 + 12 * Q) + S * (36 + 8 * D) + 8 * F_st
+    bytes_pre = 12 * E + 16 * N
+    bytes_step = bytes_fwd + bytes_bwd + 2 * bytes_pre
+
+    kernel_bytes = {"forward": bytes_fwd, "backward": bytes_bwd, "prefetch_adjacent_diff": bytes_pre}
+    dominant = max((k for k in avg if k in kernel_bytes), key=lambda k: avg[k] * len(per_kernel[k]))
+    achieved = kernel_bytes[dominant] / (avg[dominant] * 1e-3) / 1e9
+
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", f"traffic_{dominant}_C{args.config}.json")
+    if os.path.exists(prof):
+        with open(prof) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": R / (ms_per_step * 1e-3) / 1e6,
+        "unit": "Mrays/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"C{args.config}: {N} points, SH degree {w.sh_degree}, sdfoam alpha, "
+                        f"inv_s={w.inv_s:.4f}, {w.rays.shape[1]}x{w.rays.shape[0]} rays, Q={Q}, "
+                        "trace_forward(contribution, depth) + trace_backward",
+            "points": N,
+            "adjacency": E,
+            "rays": R,
+            "sh_degree": w.sh_degree,
+        },
+        "rays_per_s": R / (ms_per_step * 1e-3),
+        "cell_steps_per_s": S / (ms_per_step * 1e-3),
+        "cell_steps_per_ray": S / R,
+        "faces_per_step": F_st / max(S, 1),
+        "faces_scanned": F_all,
+        "kernel_ms": avg,
+        "algorithmic_bytes": {"forward": bytes_fwd, "backward": bytes_bwd, "prefetch": bytes_pre,
+                              "step": bytes_step},
+        "step_algorithmic_GBps": bytes_step / (ms_per_step * 1e-3) / 1e9,
+        "roofline": {
+            "kernel": dominant,
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic,
+        },
+    }
+
+    if args.cpu_stride > 0:
+        result["cpu_baseline"] = cpu_baseline(w, host_start, args.cpu_stride)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline(w, start, stride: int) -> dict:
+    """Scalar host oracle, forward + backward, every `stride`-th ray."""
+    import numpy as np
+
+    from oracle import oracle
+
+    oracle.build()
+    threads = cpu_threads()
+    rays = w.rays.reshape(-1, 6)[::stride]
+    sp = start.reshape(-1)[::stride]
+    qv = w.quantiles.reshape(-1, w.quantiles.shape[-1])[::stride]
+    g = w.grad_rgba.reshape(-1, 4)[::stride]
+    dg = w.depth_grad.reshape(-1, w.depth_grad.shape[-1])[::stride]
+    log(f"CPU baseline: {rays.shape[0]} rays on {threads} threads")
+    t0 = time.perf_counter()
+    f = oracle.trace_forward(w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, rays, sp,
+                             qv, alpha_mode="sdfoam", inv_s=w.inv_s, threads=threads)
+    oracle.trace_backward(w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, rays, sp,
+                          f.rgba, g, qv, f.depth_indices, dg, alpha_mode="sdfoam", inv_s=w.inv_s,
+                          threads=threads, side_buffers=False)
+    dt = time.perf_counter() - t0
+    log(f"CPU baseline: {dt:.1f}s")
+    return {
+        "value": rays.shape[0] / dt / 1e6,
+        "unit": "Mrays/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"every {stride}th ray of the same workload ({rays.shape[0]} rays, "
+                  f"{int(np.sum(f.steps))} cell steps), forward + backward, {dt:.1f}s on "
+                  f"{threads} threads of {cpu_model()}",
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -46,6 +46,7 @@ class _Visits(C.Structure):
         ("steps", C.c_void_p),
         ("faces", C.c_void_p),
         ("faces_stepped", C.c_void_p),
+        ("t_exit", C.c_void_p),
     ]
 
 
@@ -98,6 +99,7 @@ def lib():
             C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p,
             C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
             C.c_void_p, C.c_void_p, C.POINTER(_Grads), C.POINTER(_Visits), C.c_int]
+        L.oracle_cell_intersection_grad.argtypes = [C.c_void_p] * 5
         L.oracle_build_aabb_tree.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p]
         L.oracle_nn.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p, C.c_int]
         _lib = L
@@ -142,6 +144,13 @@ def prefetch_adjacent_diff(points, adjacency, offsets) -> np.ndarray:
     return out
 
 
+def cell_intersection_grad(p, q, o, d) -> np.ndarray:
+    args = [np.ascontiguousarray(v, dtype=np.float32) for v in (p, q, o, d)]
+    g = np.zeros(3, dtype=np.float32)
+    lib().oracle_cell_intersection_grad(*[_p(a) for a in args], _p(g))
+    return g
+
+
 def build_aabb_tree(points) -> np.ndarray:
     from sdfoam_amd.scenes import pow2_round_up
 
@@ -174,6 +183,7 @@ class ForwardResult:
     faces_stepped: np.ndarray
     cells: np.ndarray | None
     cell_alphas: np.ndarray | None
+    t_exit: np.ndarray | None
 
 
 def _settings(alpha_mode, weight_threshold, max_intersections, sdf_channel, D):
@@ -218,7 +228,9 @@ def trace_forward(sh_degree, points, attributes, adjacency, offsets, rays, start
     faces_st = np.zeros(R, dtype=np.uint64)
     cells = np.zeros((R, record), dtype=np.uint32) if record else None
     calpha = np.zeros((R, record), dtype=np.float32) if record else None
-    vis = _Visits(_p(vh), _p(cells), _p(calpha), record, _p(steps), _p(faces), _p(faces_st))
+    texit = np.zeros((R, record), dtype=np.float32) if record else None
+    vis = _Visits(_p(vh), _p(cells), _p(calpha), record, _p(steps), _p(faces), _p(faces_st),
+                  _p(texit))
     rc = lib().oracle_trace_forward(
         C.byref(st), sh_degree, N, _p(points), _p(attributes), adjacency.size, _p(adjacency),
         _p(offsets), R, _p(rays), _p(start), Q, _p(quant), _p(sharp), _p(rgba), _p(depth),
@@ -233,7 +245,7 @@ def trace_forward(sh_degree, points, attributes, adjacency, offsets, rays, start
         None if contrib is None else contrib.reshape(N, 1),
         alpha.reshape(N, 1),
         vh.reshape(lead), steps.reshape(lead), faces.reshape(lead), faces_st.reshape(lead),
-        cells, calpha)
+        cells, calpha, texit)
 
 
 @dataclass
@@ -255,7 +267,10 @@ class BackwardResult:
 def trace_backward(sh_degree, points, attributes, adjacency, offsets, rays, start_point,
                    rgba, grad_rgba, depth_quantiles=None, depth_indices=None, depth_grad=None,
                    ray_error=None, *, alpha_mode="sdfoam", inv_s=1.0, weight_threshold=None,
-                   max_intersections=None, sdf_channel=None, threads=1) -> BackwardResult:
+                   max_intersections=None, sdf_channel=None, threads=1,
+                   side_buffers=True) -> BackwardResult:
+    """side_buffers=False skips the sum|c| / count buffers of the tolerance
+    model (the plain algorithm, as timed for the CPU baseline)."""
     points = _c(points, np.float32)
     attributes = _c(attributes, np.float32)
     adjacency = _c(adjacency, np.uint32)
@@ -277,13 +292,16 @@ def trace_backward(sh_degree, points, attributes, adjacency, offsets, rays, star
     sharp = np.array([inv_s], dtype=np.float32).ravel()[:1] if np.ndim(inv_s) == 0 else _c(inv_s, np.float32).ravel()
     pg = np.zeros((N, 3)); ag = np.zeros((N, D)); sg = np.zeros(1)
     pe = np.zeros(N) if rerr is not None else None
-    pga = np.zeros((N, 3)); aga = np.zeros((N, D)); sga = np.zeros(1)
-    pgk = np.zeros((N, 3), dtype=np.uint32); agk = np.zeros((N, D), dtype=np.uint32)
-    sgk = np.zeros(1, dtype=np.uint64)
+    if side_buffers:
+        pga = np.zeros((N, 3)); aga = np.zeros((N, D)); sga = np.zeros(1)
+        pgk = np.zeros((N, 3), dtype=np.uint32); agk = np.zeros((N, D), dtype=np.uint32)
+        sgk = np.zeros(1, dtype=np.uint64)
+    else:
+        pga = aga = sga = pgk = agk = sgk = None
     g = _Grads(_p(pg), _p(ag), _p(sg), _p(pe), _p(pga), _p(aga), _p(sga), _p(pgk), _p(agk), _p(sgk))
     vh = np.zeros(R, dtype=np.uint64)
     steps = np.zeros(R, dtype=np.uint32)
-    vis = _Visits(_p(vh), None, None, 0, _p(steps), None, None)
+    vis = _Visits(_p(vh), None, None, 0, _p(steps), None, None, None)
     rc = lib().oracle_trace_backward(
         C.byref(st), sh_degree, N, _p(points), _p(attributes), adjacency.size, _p(adjacency),
         _p(offsets), R, _p(rays), _p(start), Q, _p(quant), _p(didx), _p(rgba), _p(grad_rgba),
@@ -291,5 +309,6 @@ def trace_backward(sh_degree, points, attributes, adjacency, offsets, rays, star
     if rc != 0:
         raise RuntimeError("oracle_trace_backward failed")
     return BackwardResult(pg, ag, float(sg[0]), None if pe is None else pe.reshape(N, 1),
-                          pga, aga, float(sga[0]), pgk, agk, int(sgk[0]),
+                          pga, aga, None if sga is None else float(sga[0]), pgk, agk,
+                          None if sgk is None else int(sgk[0]),
                           vh.reshape(lead), steps.reshape(lead))

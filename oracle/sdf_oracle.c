@@ -269,12 +269,13 @@ typedef struct {
     uint32_t count;
 } visit_rec;
 
-static void visit_push(visit_rec *vr, uint32_t cell, float alpha) {
+static void visit_push(visit_rec *vr, uint32_t cell, float alpha, float t1) {
     vr->hash ^= (uint64_t)cell;
     vr->hash *= 0x100000001b3ull;
     if (vr->v && vr->count < vr->v->stride) {
         if (vr->v->cells) vr->v->cells[vr->ray * vr->v->stride + vr->count] = cell;
         if (vr->v->alphas) vr->v->alphas[vr->ray * vr->v->stride + vr->count] = alpha;
+        if (vr->v->t_exit) vr->v->t_exit[vr->ray * vr->v->stride + vr->count] = t1;
     }
     vr->count++;
 }
@@ -434,7 +435,7 @@ static int fwd_step(void *ctx, uint32_t cell, uint32_t next, float t0,
             if (r->qi < j->Q) r->q = r->rq[r->qi];
         }
     }
-    visit_push(&r->vr, cell, alpha);
+    visit_push(&r->vr, cell, alpha, t1);
     r->T = Tn;
     return r->T > j->st->weight_threshold;
 }
@@ -540,6 +541,17 @@ static void cell_isect_grad(const float *p, const float *q, const ray_t *ray,
         const float v = num * ray->d[i] + dp * (ray->o[i] - p[i]);
         g[i] = v / dp2;
     }
+}
+
+/* exported for the tests: origin o, unit direction d */
+void oracle_cell_intersection_grad(const float *p, const float *q, const float *o,
+                                   const float *d, float *g) {
+    ray_t ray;
+    for (int i = 0; i < 3; ++i) {
+        ray.o[i] = o[i];
+        ray.d[i] = d[i];
+    }
+    cell_isect_grad(p, q, &ray, g);
 }
 
 typedef struct {
@@ -701,7 +713,7 @@ static int bwd_step_sdf(void *ctx, uint32_t cell, uint32_t next, float t0,
         if (j->g->sharpness_k) add_u64(j->g->sharpness_k, j->shared);
     }
     bwd_sh(r, cell, rgb, dL_drgb);
-    visit_push(&r->vr, cell, alpha);
+    visit_push(&r->vr, cell, alpha, t1);
     r->T = Tn;
     return r->T > j->st->weight_threshold;
 }
@@ -755,7 +767,7 @@ static int bwd_step_density(void *ctx, uint32_t cell, uint32_t next, float t0,
     dL_dt0 = dL_dt0 + -dL_ddt;
     const float dL_dt1 = dL_ddt;
     bwd_geometry(r, cell, xc, xn, dL_dt0, dL_dt1);
-    visit_push(&r->vr, cell, alpha);
+    visit_push(&r->vr, cell, alpha, t1);
     r->T = Tn;
     bwd_sh(r, cell, rgb, dL_drgb);
     grad_add(j->g->attr_grad, j->g->attr_grad_abs, j->g->attr_grad_k,

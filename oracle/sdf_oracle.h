@@ -54,6 +54,7 @@ typedef struct {
     uint32_t *steps;
     uint64_t *faces;
     uint64_t *faces_stepped; /* faces of the cells that got a functor call */
+    float *t_exit;           /* [R, stride]: t1 of each recorded step */
 } oracle_visits;
 
 const char *oracle_version(void);
@@ -122,6 +123,11 @@ int oracle_trace_backward(const oracle_settings *settings, uint32_t sh_degree,
                           const float *ray_error, const float *sharpness,
                           oracle_grads *grads, oracle_visits *visits,
                           int num_threads);
+
+/* d t / d p of the bisector-plane crossing between p and q for the ray
+ * (o, unit d)  (src/tracing/tracing_utils.cuh:112-124). */
+void oracle_cell_intersection_grad(const float *p, const float *q, const float *o,
+                                   const float *d, float *g);
 
 /* AABB tree over consecutive point pairs, layout [pow2(N), 2, 3]
  * (src/aabb_tree/aabb_tree.cu:192-341, src/aabb_tree/aabb_tree.cuh:35-43). */
