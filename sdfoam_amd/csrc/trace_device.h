@@ -115,83 +115,123 @@ struct WalkCounters {
     uint64_t faces_stepped; // faces of the cells that got a step
 };
 
-// The walk of src/tracing/tracing_utils.cuh:15-109.  Exit face: the first
-// minimum t over the cell's CSR row with dp > 0 (and t > t0 in safe mode).
-// The reference passes UINT32_MAX for the index bounds; the real bounds are
-// used here, which is the same walk for a well-formed scene and stops instead
-// of reading out of bounds otherwise.
-//
-// step(cell, next, t0, t1, xc[3], xn[3]) -> keep going?
-template <bool SAFE, bool COUNT, typename Step>
-__device__ __forceinline__ void walk(const SceneView &sc, const RayF &ray, uint32_t start,
-                                     uint32_t max_steps, Step &&step, WalkCounters &wc) {
-    wc.n = 0;
-    wc.steps = 0;
-    wc.faces = 0;
-    wc.faces_stepped = 0;
-    if (start >= sc.num_points) return;
-    uint32_t cell = start;
-    float xc[3] = {sc.points[3ull * cell], sc.points[3ull * cell + 1], sc.points[3ull * cell + 2]};
-    float t0 = 0.0f;
-    uint32_t n = 0;
-    for (;;) {
-        ++n;
-        if (n > max_steps) break;
-        const uint32_t beg = sc.offs[cell];
-        const uint32_t end = sc.offs[cell + 1];
-        if (beg > end || end > sc.num_adj) break;
-        const uint32_t nf = end - beg;
-        if constexpr (COUNT) wc.faces += nf;
-        float t1 = __builtin_bit_cast(float, 0x7f800000u);
-        uint32_t best = kNoIndex;
-        const uint2 *__restrict__ row = sc.diff + beg;
-        // batches of 4: the table is padded, so the last batch may over-read
-        for (uint32_t k0 = 0; k0 < nf; k0 += 4) {
-            uint2 h[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) h[u] = row[k0 + u];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t k = k0 + u;
-                const float dx = f16_to_f32(h[u].x);
-                const float dy = f16_to_f32(h[u].x >> 16);
-                const float dz = f16_to_f32(h[u].y);
-                const float fx = xc[0] + dx * 0.5f;
-                const float fy = xc[1] + dy * 0.5f;
-                const float fz = xc[2] + dz * 0.5f;
-                const float dp = sdf_dot3(dx, dy, dz, ray.dx, ray.dy, ray.dz);
-                const float t = sdf_dot3(fx - ray.ox, fy - ray.oy, fz - ray.oz, dx, dy, dz) / dp;
-                bool take;
-                if constexpr (SAFE) {
-                    take = dp > 0.0f && t > t0 && t < t1;
-                } else {
-                    take = dp > 0.0f && t < t1;
-                }
-                if (take && k < nf) {
-                    t1 = t;
-                    best = k;
-                }
-            }
-        }
-        if (best == kNoIndex) break;
-        const uint32_t next = sc.adj[beg + best];
-        if (next >= sc.num_points) break;
-        const float xn[3] = {sc.points[3ull * next], sc.points[3ull * next + 1],
-                             sc.points[3ull * next + 2]};
-        if (t1 > t0) {
-            if constexpr (COUNT) {
-                wc.steps++;
-                wc.faces_stepped += nf;
-            }
-            if (!step(cell, next, t0, t1, xc, xn)) break;
-        }
-        t0 = fmaxf(t0, t1);
-        cell = next;
-        xc[0] = xn[0];
-        xc[1] = xn[1];
-        xc[2] = xn[2];
+// Per-lane state of the walk of src/tracing/tracing_utils.cuh:15-109.
+struct WalkState {
+    uint32_t cell;
+    float xc[3];   // position of `cell`
+    float t0;      // entry distance into `cell`
+    uint32_t n;    // loop iterations so far (the reference's return value)
+    bool alive;
+};
+
+// Outcome of one loop iteration of the walk.
+struct StepInfo {
+    bool found;    // an exit face was found: the walk moves to `next`
+    bool stepped;  // ... and t1 > t0: the step functor runs for `cell`
+    uint32_t next;
+    float t1;
+    float xn[3];
+};
+
+__device__ __forceinline__ void walk_init(const SceneView &sc, uint32_t start, WalkState &ws) {
+    ws.cell = start;
+    ws.t0 = 0.0f;
+    ws.n = 0;
+    ws.alive = start < sc.num_points;
+    ws.xc[0] = ws.xc[1] = ws.xc[2] = 0.0f;
+    if (ws.alive) {
+        ws.xc[0] = sc.points[3ull * start];
+        ws.xc[1] = sc.points[3ull * start + 1];
+        ws.xc[2] = sc.points[3ull * start + 2];
     }
-    wc.n = n;
+}
+
+// One iteration of the walk: exit face = the first minimum t over the cell's
+// CSR row with dp > 0 (and t > t0 in safe mode).  The reference passes
+// UINT32_MAX for the index bounds; the real bounds are used here, which is
+// the same walk for a well-formed scene and ends it instead of reading out
+// of bounds otherwise.  Clears ws.alive when the walk ends.
+template <bool SAFE, bool COUNT>
+__device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ray,
+                                             uint32_t max_steps, WalkState &ws, StepInfo &si,
+                                             WalkCounters &wc) {
+    si.found = false;
+    si.stepped = false;
+    ++ws.n;
+    if (ws.n > max_steps) {
+        ws.alive = false;
+        return;
+    }
+    const uint32_t beg = sc.offs[ws.cell];
+    const uint32_t end = sc.offs[ws.cell + 1];
+    if (beg > end || end > sc.num_adj) {
+        ws.alive = false;
+        return;
+    }
+    const uint32_t nf = end - beg;
+    const float t0 = ws.t0;
+    float t1 = __builtin_bit_cast(float, 0x7f800000u);
+    uint32_t best = kNoIndex;
+    const uint2 *__restrict__ row = sc.diff + beg;
+    // batches of 4: the table is padded, so the last batch may over-read
+    for (uint32_t k0 = 0; k0 < nf; k0 += 4) {
+        uint2 h[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) h[u] = row[k0 + u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t k = k0 + u;
+            const float dx = f16_to_f32(h[u].x);
+            const float dy = f16_to_f32(h[u].x >> 16);
+            const float dz = f16_to_f32(h[u].y);
+            const float fx = ws.xc[0] + dx * 0.5f;
+            const float fy = ws.xc[1] + dy * 0.5f;
+            const float fz = ws.xc[2] + dz * 0.5f;
+            const float dp = sdf_dot3(dx, dy, dz, ray.dx, ray.dy, ray.dz);
+            const float t = sdf_dot3(fx - ray.ox, fy - ray.oy, fz - ray.oz, dx, dy, dz) / dp;
+            bool take;
+            if constexpr (SAFE) {
+                take = dp > 0.0f && t > t0 && t < t1;
+            } else {
+                take = dp > 0.0f && t < t1;
+            }
+            if (take && k < nf) {
+                t1 = t;
+                best = k;
+            }
+        }
+    }
+    if constexpr (COUNT) wc.faces += nf;
+    if (best == kNoIndex) {
+        ws.alive = false;
+        return;
+    }
+    const uint32_t next = sc.adj[beg + best];
+    if (next >= sc.num_points) {
+        ws.alive = false;
+        return;
+    }
+    si.found = true;
+    si.next = next;
+    si.t1 = t1;
+    si.xn[0] = sc.points[3ull * next];
+    si.xn[1] = sc.points[3ull * next + 1];
+    si.xn[2] = sc.points[3ull * next + 2];
+    si.stepped = t1 > t0;
+    if constexpr (COUNT) {
+        if (si.stepped) {
+            wc.steps++;
+            wc.faces_stepped += nf;
+        }
+    }
+}
+
+__device__ __forceinline__ void walk_move(WalkState &ws, const StepInfo &si) {
+    ws.t0 = fmaxf(ws.t0, si.t1);
+    ws.cell = si.next;
+    ws.xc[0] = si.xn[0];
+    ws.xc[1] = si.xn[1];
+    ws.xc[2] = si.xn[2];
 }
 
 // cell_intersection_grad (src/tracing/tracing_utils.cuh:112-124):

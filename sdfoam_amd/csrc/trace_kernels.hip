@@ -1,11 +1,19 @@
 // Forward / backward kernels of the Voronoi-foam tracer for gfx950, and the
 // fp16 neighbour-offset prepass.
 //
-// One lane per ray (wave64), 256 lanes per block.  Each lane walks its ray
-// through the cells of the foam (trace_device.h), compositing in registers.
-// The backward pass replays the same walk and accumulates per-point
-// gradients with fp32 atomics; the sharpness gradient, a single address in
-// the reference, is summed per lane and reduced per wave before one atomic.
+// One lane per ray, wave64, 256 lanes per block.  The walk is wave
+// synchronous: every trip of the kernel's loop advances each live lane by one
+// cell (the divergent part: face scan and the step's arithmetic), then the
+// whole wave reconverges and applies the step's scattered updates grouped by
+// cell.  Coherent rays of a wave sit in the same few cells at a time, so the
+// lanes of a wave that stepped into one cell are summed first (ballot +
+// readlane), and the sum goes out as one coalesced atomic instruction: lane i
+// of the wave owns component i of the cell's gradient row.  The reference
+// issues ~52 single-word atomics per step per ray instead
+// (src/tracing/pipeline.cu:500-533).
+//
+// Each per-element contribution is the same fp32 product the reference
+// forms; only the order of the sums differs (fp32 atomics have no order).
 #include "trace_kernels.h"
 
 namespace sdfoam_hip {
@@ -49,24 +57,42 @@ __global__ __launch_bounds__(kBlock) void prefetch_diff_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// wave helpers
+
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ __forceinline__ uint32_t readlane_u(uint32_t v, int lane) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
+}
+
+__device__ __forceinline__ int first_lane(uint64_t mask) { return __builtin_ctzll(mask); }
+
+// ---------------------------------------------------------------------------
 // forward (src/tracing/pipeline.cu:36-264)
 
 template <int L, bool NEUS, bool STATS>
 __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     const uint32_t ray_idx = blockIdx.x * kBlock + threadIdx.x;
-    if (ray_idx >= a.num_rays) return;
+    const bool valid = ray_idx < a.num_rays;
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
+    const uint32_t lane = lane_id();
 
-    const RayF ray = load_ray(a.rays, ray_idx);
+    RayF ray = {};
     float sh[nsh];
+    if (valid) ray = load_ray(a.rays, ray_idx);
     sh_basis<L>(ray.dx, ray.dy, ray.dz, sh);
     const float sha = a.sharpness[0];
     const int32_t sdf_ch = a.settings.sdf_channel;
     const bool neus_alpha = NEUS && sdf_ch >= 0;
     const float thr = a.settings.weight_threshold;
     const uint32_t Q = a.num_quantiles;
-    const float *rq = a.quantiles ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
+    const float *rq = (valid && a.quantiles) ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
+    const uint32_t max_steps = a.settings.max_intersections;
 
     float T = 1.0f;
     float C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
@@ -75,66 +101,96 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     uint64_t hash = kFnvOffset;
     uint32_t rec = 0;
 
-    auto step = [&](uint32_t cell, uint32_t next, float t0, float t1, const float *xc,
-                    const float *xn) -> bool {
-        const float *__restrict__ row = a.scene.attrs + (uint64_t)cell * D;
-        float s = row[D - 1];
-        float r, g, b;
-        if (NEUS || s > 1e-6f) {
-            sh_rgb<L>(sh, row, r, g, b);
-        } else {
-            r = g = b = 0.0f;
-        }
-        float alpha;
-        const float dt = fmaxf(t1 - t0, 0.0f);
-        if (neus_alpha) {
-            const float d = row[sdf_ch];
-            const float phi = sdf_sigmoidf(-sha * d);
-            s = sha * phi * (1.0f - phi);
+    WalkState ws;
+    walk_init(a.scene, valid ? a.start[ray_idx] : kNoIndex, ws);
+    WalkCounters wc = {0u, 0u, 0ull, 0ull};
+
+    while (__ballot(ws.alive) != 0ull) {
+        StepInfo si;
+        si.stepped = false;
+        si.found = false;
+        if (ws.alive) walk_advance<true, STATS>(a.scene, ray, max_steps, ws, si, wc);
+
+        float alpha = 0.0f, w = 0.0f;
+        bool keep = true;
+        if (si.stepped) {
+            const uint32_t cell = ws.cell;
+            const float t0 = ws.t0, t1 = si.t1;
+            const float *__restrict__ row = a.scene.attrs + (uint64_t)cell * D;
+            float s = row[D - 1];
+            const float dt = fmaxf(t1 - t0, 0.0f);
+            if (neus_alpha) {
+                const float d = row[sdf_ch];
+                const float phi = sdf_sigmoidf(-sha * d);
+                s = sha * phi * (1.0f - phi);
+            }
             alpha = 1.0f - sdf_expf(-s * dt);
-        } else {
-            alpha = 1.0f - sdf_expf(-s * dt);
+            w = T * alpha;
+            const float Tn = T * (1.0f - alpha);
+            if constexpr (!STATS) {
+                float r, g, b;
+                if (NEUS || row[D - 1] > 1e-6f) {
+                    sh_rgb<L>(sh, row, r, g, b);
+                } else {
+                    r = g = b = 0.0f;
+                }
+                C0 = fmaf(w, r, C0);
+                C1 = fmaf(w, g, C1);
+                C2 = fmaf(w, b, C2);
+                const uint64_t qbase = (uint64_t)ray_idx * Q;
+                if (NEUS) {
+                    const float drop = T - Tn;
+                    if (drop > 1e-12f) {
+                        while (qi < Q && Tn < q) {
+                            float frac = (T - q) / drop;
+                            frac = fminf(1.0f, fmaxf(0.0f, frac));
+                            a.depth[qbase + qi] = fmaf(frac, t1 - t0, t0);
+                            a.depth_indices[qbase + qi] = cell;
+                            ++qi;
+                            if (qi < Q) q = rq[qi];
+                        }
+                    }
+                } else {
+                    while (qi < Q && Tn < q) {
+                        a.depth[qbase + qi] = t0 + logf(T / q) / s;
+                        a.depth_indices[qbase + qi] = cell;
+                        ++qi;
+                        if (qi < Q) q = rq[qi];
+                    }
+                }
+            } else {
+                hash = fnv_step(hash, cell);
+                if (a.cells && rec < a.cells_stride) a.cells[(uint64_t)ray_idx * a.cells_stride + rec] = cell;
+                ++rec;
+            }
+            T = Tn;
+            keep = T > thr;
         }
-        const float w = T * alpha;
-        if (a.alpha_out) a.alpha_out[cell] = alpha; // racy last writer, as the reference
-        if (a.contribution) atomicAdd(a.contribution + cell, w);
-        C0 = fmaf(w, r, C0);
-        C1 = fmaf(w, g, C1);
-        C2 = fmaf(w, b, C2);
-        const float Tn = T * (1.0f - alpha);
-        const uint64_t qbase = (uint64_t)ray_idx * Q;
-        if (NEUS) {
-            const float drop = T - Tn;
-            if (drop > 1e-12f) {
-                while (qi < Q && Tn < q) {
-                    float frac = (T - q) / drop;
-                    frac = fminf(1.0f, fmaxf(0.0f, frac));
-                    a.depth[qbase + qi] = fmaf(frac, t1 - t0, t0);
-                    a.depth_indices[qbase + qi] = cell;
-                    ++qi;
-                    if (qi < Q) q = rq[qi];
+
+        if constexpr (!STATS) {
+            // per cell: contribution += sum of the weights; alpha = one
+            // visiting step's alpha (the reference's last-writer store,
+            // src/tracing/pipeline.cu:159-163)
+            if (a.contribution || a.alpha_out) {
+                uint64_t todo = __ballot(si.stepped);
+                while (todo) {
+                    const int leader = first_lane(todo);
+                    const uint32_t c = readlane_u(ws.cell, leader);
+                    const uint64_t grp = __ballot(si.stepped && ws.cell == c);
+                    todo &= ~grp;
+                    float sum = 0.0f;
+                    for (uint64_t mm = grp; mm; mm &= mm - 1) sum += readlane_f(w, first_lane(mm));
+                    const float al = readlane_f(alpha, leader);
+                    if (lane == 0 && a.contribution) atomicAdd(a.contribution + c, sum);
+                    if (lane == 1 && a.alpha_out) a.alpha_out[c] = al;
                 }
             }
-        } else {
-            while (qi < Q && Tn < q) {
-                a.depth[qbase + qi] = t0 + logf(T / q) / s;
-                a.depth_indices[qbase + qi] = cell;
-                ++qi;
-                if (qi < Q) q = rq[qi];
-            }
         }
-        if constexpr (STATS) {
-            hash = fnv_step(hash, cell);
-            if (a.cells && rec < a.cells_stride) a.cells[(uint64_t)ray_idx * a.cells_stride + rec] = cell;
-            ++rec;
-        }
-        T = Tn;
-        return T > thr;
-    };
+        if (si.stepped && !keep) ws.alive = false;
+        if (ws.alive && si.found) walk_move(ws, si);
+    }
 
-    WalkCounters wc;
-    walk<true, STATS>(a.scene, ray, a.start[ray_idx], a.settings.max_intersections, step, wc);
-
+    if (!valid) return;
     if constexpr (STATS) {
         if (a.visit_hash) a.visit_hash[ray_idx] = hash;
         if (a.steps) a.steps[ray_idx] = wc.steps;
@@ -148,24 +204,35 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     }
     float4 out = make_float4(C0, C1, C2, 1.0f - T);
     *reinterpret_cast<float4 *>(a.rgba + 4ull * ray_idx) = out;
-    if (a.num_intersections) a.num_intersections[ray_idx] = wc.n;
+    if (a.num_intersections) a.num_intersections[ray_idx] = ws.n;
 }
 
 // ---------------------------------------------------------------------------
-// backward, shared geometry bookkeeping (src/tracing/pipeline.cu:452-474 and
-// :731-760): the position gradient of a cell is flushed one step late, the
-// first cell gets a face against the world origin (prev = 0) and the last
-// two pending gradients are never flushed -- all as the reference does.
+// backward, shared pieces
 
+// Position-gradient bookkeeping of src/tracing/pipeline.cu:452-474 and
+// :731-760: the gradient of a cell is flushed one step late, the first cell
+// gets a face against the world origin (prev = 0) and the last two pending
+// gradients are never flushed -- all as the reference does.  Returns whether
+// a flush of (flush_idx, flush_g) is due.
 struct GeomState {
     uint32_t prev_idx;
     float prev_pt[3];
     float prev_g[3], cur_g[3], next_g[3];
 };
 
-__device__ __forceinline__ void geom_step(GeomState &gs, uint32_t cell, const float *xc,
+__device__ __forceinline__ void geom_init(GeomState &gs) {
+    gs.prev_idx = kNoIndex;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        gs.prev_pt[i] = 0.0f;
+        gs.prev_g[i] = gs.cur_g[i] = gs.next_g[i] = 0.0f;
+    }
+}
+
+__device__ __forceinline__ bool geom_step(GeomState &gs, uint32_t cell, const float *xc,
                                           const float *xn, float dL_dt0, float dL_dt1,
-                                          const RayF &ray, float *__restrict__ points_grad) {
+                                          const RayF &ray, uint32_t &flush_idx, float *flush_g) {
     float dprev[3] = {0.0f, 0.0f, 0.0f};
     if (gs.prev_idx != kNoIndex) cell_isect_grad(gs.prev_pt, xc, ray, dprev);
     float dt1_cur[3], dt0_cur[3], dt1_next[3];
@@ -178,162 +245,234 @@ __device__ __forceinline__ void geom_step(GeomState &gs, uint32_t cell, const fl
         gs.cur_g[i] = gs.cur_g[i] + (dL_dt0 * dt0_cur[i] + dL_dt1 * dt1_cur[i]);
         gs.next_g[i] = fmaf(dL_dt1, dt1_next[i], gs.next_g[i]);
     }
-    if (gs.prev_idx != kNoIndex) {
-        float *dst = points_grad + 3ull * gs.prev_idx;
-        atomicAdd(dst + 0, gs.prev_g[0]);
-        atomicAdd(dst + 1, gs.prev_g[1]);
-        atomicAdd(dst + 2, gs.prev_g[2]);
-    }
+    const bool flush = gs.prev_idx != kNoIndex;
+    flush_idx = gs.prev_idx;
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
+        flush_g[i] = gs.prev_g[i];
         gs.prev_pt[i] = xc[i];
         gs.prev_g[i] = gs.cur_g[i];
         gs.cur_g[i] = gs.next_g[i];
         gs.next_g[i] = 0.0f;
     }
     gs.prev_idx = cell;
+    return flush;
 }
 
-// SH colour gradients, zeroed where the colour clamped to 0
-// (src/tracing/pipeline.cu:528-533, src/tracing/sh_utils.cuh:85-92)
+// Grouped gradient updates of one wave-synchronous step (all 64 lanes
+// active).  For every cell some lanes stepped into, lane i < D adds
+//   sum over those lanes of  Y_{i/3} * g_{i%3}      (i < 3 nsh; SH, sh_utils.cuh:85-92)
+//   + sum of g_last                                 (i == last_ch)
+// to row `cell` of attr_grad, lane 63 adds the point-error sum; then for
+// every flushed cell lanes 0..2 add the flushed position gradients.
+// Y of every lane of the wave sits in LDS (ylds[lane * nsh + j]).
 template <int L>
-__device__ __forceinline__ void sh_grad(const float *sh, float r, float g, float b, float gr,
-                                        float gg, float gb, float *__restrict__ grow) {
+__device__ __forceinline__ void grouped_backward_updates(
+    bool stepped, uint32_t cell, float gr, float gg, float gb, float g_last, int last_ch,
+    float pe, bool flush, uint32_t flush_idx, const float *flush_g, const float *ylds,
+    float *__restrict__ attr_grad, float *__restrict__ point_error,
+    float *__restrict__ points_grad) {
     constexpr int nsh = (L + 1) * (L + 1);
-    if (r == 0.0f) gr = 0.0f;
-    if (g == 0.0f) gg = 0.0f;
-    if (b == 0.0f) gb = 0.0f;
-#pragma unroll
-    for (int j = 0; j < nsh; ++j) {
-        atomicAdd(grow + 3 * j + 0, sh[j] * gr);
-        atomicAdd(grow + 3 * j + 1, sh[j] * gg);
-        atomicAdd(grow + 3 * j + 2, sh[j] * gb);
+    constexpr int D = 1 + 3 * nsh;
+    const uint32_t lane = lane_id();
+    const int j = (int)lane / 3;
+    const int ch = (int)lane % 3;
+    const bool sh_lane = lane < 3u * nsh;
+    uint64_t todo = __ballot(stepped);
+    while (todo) {
+        const int leader = first_lane(todo);
+        const uint32_t c = readlane_u(cell, leader);
+        const uint64_t grp = __ballot(stepped && cell == c);
+        todo &= ~grp;
+        float acc = 0.0f;
+        float pacc = 0.0f;
+        for (uint64_t mm = grp; mm; mm &= mm - 1) {
+            const int m = first_lane(mm);
+            const float vr = readlane_f(gr, m);
+            const float vg = readlane_f(gg, m);
+            const float vb = readlane_f(gb, m);
+            const float vl = readlane_f(g_last, m);
+            if (sh_lane) {
+                const float y = ylds[m * nsh + j];
+                const float gsel = ch == 0 ? vr : (ch == 1 ? vg : vb);
+                acc = acc + y * gsel;
+            }
+            if ((int)lane == last_ch) acc = acc + vl;
+            if (point_error) pacc = pacc + readlane_f(pe, m);
+        }
+        if (lane < (uint32_t)D) atomicAdd(attr_grad + (uint64_t)c * D + lane, acc);
+        if (point_error && lane == 63u) atomicAdd(point_error + c, pacc);
+    }
+    todo = __ballot(flush);
+    while (todo) {
+        const int leader = first_lane(todo);
+        const uint32_t c = readlane_u(flush_idx, leader);
+        const uint64_t grp = __ballot(flush && flush_idx == c);
+        todo &= ~grp;
+        float acc = 0.0f;
+        for (uint64_t mm = grp; mm; mm &= mm - 1) {
+            const int m = first_lane(mm);
+            const float vx = readlane_f(flush_g[0], m);
+            const float vy = readlane_f(flush_g[1], m);
+            const float vz = readlane_f(flush_g[2], m);
+            acc = acc + (lane == 0u ? vx : (lane == 1u ? vy : vz));
+        }
+        if (lane < 3u) atomicAdd(points_grad + 3ull * c + lane, acc);
     }
 }
 
+// ---------------------------------------------------------------------------
 // backward_sdf (src/tracing/pipeline.cu:267-550)
+
 template <int L, bool STATS>
 __global__ __launch_bounds__(kBlock) void backward_sdf_kernel(BwdArgs a) {
-    const uint32_t ray_idx = blockIdx.x * kBlock + threadIdx.x;
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
-    float sharp_acc = 0.0f;
-    if (ray_idx < a.num_rays) {
-        const RayF ray = load_ray(a.rays, ray_idx);
-        float sh[nsh];
-        sh_basis<L>(ray.dx, ray.dy, ray.dz, sh);
-        const float sha = a.sharpness[0];
-        const int32_t sdf_ch = a.settings.sdf_channel >= 0 ? a.settings.sdf_channel : D - 1;
-        const bool write_sdf = a.settings.sdf_channel >= 0;
-        const float thr = a.settings.weight_threshold;
-        const uint32_t Q = a.num_quantiles;
-        const float *rq = a.quantiles ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
-        const float *rdg = a.depth_grad ? a.depth_grad + (uint64_t)ray_idx * Q : nullptr;
-        // the statistics instantiation gets no rgba / gradient buffers
-        const float4 g4 = STATS ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-                                : *reinterpret_cast<const float4 *>(a.rgba_grad + 4ull * ray_idx);
-        const float4 c4 = STATS ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-                                : *reinterpret_cast<const float4 *>(a.rgba + 4ull * ray_idx);
-        const float err = a.ray_error ? a.ray_error[ray_idx] : 0.0f;
+    __shared__ float ylds_all[kBlock / 64][64 * nsh];
+    const uint32_t ray_idx = blockIdx.x * kBlock + threadIdx.x;
+    const bool valid = ray_idx < a.num_rays;
+    const uint32_t lane = lane_id();
+    float *ylds = ylds_all[threadIdx.x >> 6];
 
-        float T = 1.0f;
-        float C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
-        uint32_t qi = 0;
-        float q = (rq && Q > 0) ? rq[0] : 0.0f;
-        float g_logT = 0.0f;
-        GeomState gs;
-        gs.prev_idx = kNoIndex;
+    RayF ray = {};
+    if (valid) ray = load_ray(a.rays, ray_idx);
+    float sh[nsh];
+    sh_basis<L>(ray.dx, ray.dy, ray.dz, sh);
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            gs.prev_pt[i] = 0.0f;
-            gs.prev_g[i] = gs.cur_g[i] = gs.next_g[i] = 0.0f;
-        }
-        uint64_t hash = kFnvOffset;
-        uint32_t rec = 0;
+    for (int k = 0; k < nsh; ++k) ylds[lane * nsh + k] = sh[k];
+    __builtin_amdgcn_wave_barrier();
 
-        auto step = [&](uint32_t cell, uint32_t next, float t0, float t1, const float *xc,
-                        const float *xn) -> bool {
+    const float sha = a.sharpness[0];
+    const int32_t sdf_ch = a.settings.sdf_channel >= 0 ? a.settings.sdf_channel : D - 1;
+    const bool write_sdf = a.settings.sdf_channel >= 0;
+    const float thr = a.settings.weight_threshold;
+    const uint32_t Q = a.num_quantiles;
+    const float *rq = (valid && a.quantiles) ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
+    const float *rdg = (valid && a.depth_grad) ? a.depth_grad + (uint64_t)ray_idx * Q : nullptr;
+    // the statistics instantiation gets no rgba / gradient buffers
+    float4 g4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 c4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (!STATS && valid) {
+        g4 = *reinterpret_cast<const float4 *>(a.rgba_grad + 4ull * ray_idx);
+        c4 = *reinterpret_cast<const float4 *>(a.rgba + 4ull * ray_idx);
+    }
+    const float err = (valid && a.ray_error) ? a.ray_error[ray_idx] : 0.0f;
+
+    float T = 1.0f;
+    float C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
+    uint32_t qi = 0;
+    float q = (rq && Q > 0) ? rq[0] : 0.0f;
+    float g_logT = 0.0f;
+    float sharp_acc = 0.0f;
+    GeomState gs;
+    geom_init(gs);
+    uint64_t hash = kFnvOffset;
+    uint32_t rec = 0;
+
+    WalkState ws;
+    walk_init(a.scene, valid ? a.start[ray_idx] : kNoIndex, ws);
+    WalkCounters wc = {0u, 0u, 0ull, 0ull};
+
+    while (__ballot(ws.alive) != 0ull) {
+        StepInfo si;
+        si.stepped = false;
+        si.found = false;
+        if (ws.alive) walk_advance<true, STATS>(a.scene, ray, a.settings.max_intersections, ws, si, wc);
+
+        bool keep = true;
+        float dr = 0.0f, dg = 0.0f, db = 0.0f, dsdf = 0.0f, pe = 0.0f;
+        bool flush = false;
+        uint32_t flush_idx = kNoIndex;
+        float flush_g[3] = {0.0f, 0.0f, 0.0f};
+        if (si.stepped) {
+            const uint32_t cell = ws.cell;
+            const float t0 = ws.t0, t1 = si.t1;
             if constexpr (STATS) {
                 hash = fnv_step(hash, cell);
                 if (a.cells && rec < a.cells_stride) a.cells[(uint64_t)ray_idx * a.cells_stride + rec] = cell;
                 ++rec;
             }
             const float *__restrict__ row = a.scene.attrs + (uint64_t)cell * D;
-            float r, g, b;
-            sh_rgb<L>(sh, row, r, g, b);
             const float dt = fmaxf(t1 - t0, 0.0f);
             const float d = row[sdf_ch];
             const float phi = sdf_sigmoidf(-sha * d);
             const float s = sha * phi * (1.0f - phi);
             const float alpha = 1.0f - sdf_expf(-s * dt);
-            const float w = T * alpha;
-            C0 = fmaf(w, r, C0);
-            C1 = fmaf(w, g, C1);
-            C2 = fmaf(w, b, C2);
-            if (STATS) {
-                const float Tn = T * (1.0f - alpha);
-                T = Tn;
-                return T > thr;
-            }
-            if (a.point_error) atomicAdd(a.point_error + cell, w * err);
-
-            const float dr = g4.x * w, dg = g4.y * w, db = g4.z * w;
-            const float den = T * (1.0f - alpha) + 1e-6f;
-            const float rest0 = (c4.x - C0) / den;
-            const float rest1 = (c4.y - C1) / den;
-            const float rest2 = (c4.z - C2) / den;
-            float dL_dalpha = T * sdf_dot3(r - rest0, g - rest1, b - rest2, g4.x, g4.y, g4.z);
-            dL_dalpha = dL_dalpha + (1.0f - c4.w) * g4.w / (1.0f - alpha + 1e-6f);
-            dL_dalpha = dL_dalpha + -g_logT / fmaxf(1.0f - alpha, 1e-12f);
-            const float oma = 1.0f - alpha;
-            const float dL_ds = dL_dalpha * (dt * oma);
-            float dL_ddelta = dL_dalpha * (s * oma);
             const float Tn = T * (1.0f - alpha);
-            float units = 0.0f;
-            if (rq && Q > 0) {
-                const float T0 = T;
-                const float drop = T0 - Tn;
-                if (drop > 1e-12f) {
-                    while (qi < Q && Tn < q) {
-                        const float gq = rdg[qi];
-                        float frac = (T0 - q) / drop;
-                        frac = fminf(1.0f, fmaxf(0.0f, frac));
-                        units = units + gq;
-                        dL_ddelta = fmaf(gq, frac, dL_ddelta);
-                        if (alpha > 1e-12f && T0 > 1e-20f) {
-                            g_logT = fmaf(gq, dt * q / (alpha * T0), g_logT);
+            if constexpr (!STATS) {
+                float r, g, b;
+                sh_rgb<L>(sh, row, r, g, b);
+                const float w = T * alpha;
+                C0 = fmaf(w, r, C0);
+                C1 = fmaf(w, g, C1);
+                C2 = fmaf(w, b, C2);
+                pe = w * err;
+                dr = g4.x * w;
+                dg = g4.y * w;
+                db = g4.z * w;
+                const float den = T * (1.0f - alpha) + 1e-6f;
+                const float rest0 = (c4.x - C0) / den;
+                const float rest1 = (c4.y - C1) / den;
+                const float rest2 = (c4.z - C2) / den;
+                float dL_dalpha = T * sdf_dot3(r - rest0, g - rest1, b - rest2, g4.x, g4.y, g4.z);
+                dL_dalpha = dL_dalpha + (1.0f - c4.w) * g4.w / (1.0f - alpha + 1e-6f);
+                dL_dalpha = dL_dalpha + -g_logT / fmaxf(1.0f - alpha, 1e-12f);
+                const float oma = 1.0f - alpha;
+                const float dL_ds = dL_dalpha * (dt * oma);
+                float dL_ddelta = dL_dalpha * (s * oma);
+                float units = 0.0f;
+                if (rq && Q > 0) {
+                    const float T0 = T;
+                    const float drop = T0 - Tn;
+                    if (drop > 1e-12f) {
+                        while (qi < Q && Tn < q) {
+                            const float gq = rdg[qi];
+                            float frac = (T0 - q) / drop;
+                            frac = fminf(1.0f, fmaxf(0.0f, frac));
+                            units = units + gq;
+                            dL_ddelta = fmaf(gq, frac, dL_ddelta);
+                            if (alpha > 1e-12f && T0 > 1e-20f) {
+                                g_logT = fmaf(gq, dt * q / (alpha * T0), g_logT);
+                            }
+                            ++qi;
+                            if (qi < Q) q = rq[qi];
                         }
-                        ++qi;
-                        if (qi < Q) q = rq[qi];
                     }
                 }
+                flush = geom_step(gs, cell, ws.xc, si.xn, units - dL_ddelta, dL_ddelta, ray,
+                                  flush_idx, flush_g);
+                const float dphi_dd = -sha * phi * (1.0f - phi);
+                const float ds_dd = sha * (1.0f - 2.0f * phi) * dphi_dd;
+                const float ds_dsha = phi * (1.0f - phi) * (1.0f - sha * d * (1.0f - 2.0f * phi));
+                dsdf = dL_ds * ds_dd;
+                sharp_acc += dL_ds * ds_dsha;
+                if (r == 0.0f) dr = 0.0f;
+                if (g == 0.0f) dg = 0.0f;
+                if (b == 0.0f) db = 0.0f;
             }
-            geom_step(gs, cell, xc, xn, units - dL_ddelta, dL_ddelta, ray, a.points_grad);
-
-            const float dphi_dd = -sha * phi * (1.0f - phi);
-            const float ds_dd = sha * (1.0f - 2.0f * phi) * dphi_dd;
-            const float ds_dsha = phi * (1.0f - phi) * (1.0f - sha * d * (1.0f - 2.0f * phi));
-            float *__restrict__ grow = a.attr_grad + (uint64_t)cell * D;
-            if (write_sdf) atomicAdd(grow + sdf_ch, dL_ds * ds_dd);
-            sharp_acc += dL_ds * ds_dsha;
-            sh_grad<L>(sh, r, g, b, dr, dg, db, grow);
             T = Tn;
-            return T > thr;
-        };
+            keep = T > thr;
+        }
+        if constexpr (!STATS) {
+            grouped_backward_updates<L>(si.stepped, ws.cell, dr, dg, db, dsdf,
+                                        write_sdf ? sdf_ch : -1, pe, flush, flush_idx, flush_g,
+                                        ylds, a.attr_grad, a.point_error, a.points_grad);
+        }
+        if (si.stepped && !keep) ws.alive = false;
+        if (ws.alive && si.found) walk_move(ws, si);
+    }
 
-        WalkCounters wc;
-        walk<true, STATS>(a.scene, ray, a.start[ray_idx], a.settings.max_intersections, step, wc);
-        if constexpr (STATS) {
+    if constexpr (STATS) {
+        if (valid) {
             if (a.visit_hash) a.visit_hash[ray_idx] = hash;
             if (a.steps) a.steps[ray_idx] = wc.steps;
             if (a.faces) a.faces[ray_idx] = wc.faces;
             if (a.faces_stepped) a.faces_stepped[ray_idx] = wc.faces_stepped;
         }
-    }
-    if constexpr (!STATS) {
+    } else {
         if (a.sharpness_grad) {
             const float v = wave_sum(sharp_acc);
-            if ((threadIdx.x & 63) == 0 && v != 0.0f) atomicAdd(a.sharpness_grad, v);
+            if (lane == 0 && v != 0.0f) atomicAdd(a.sharpness_grad, v);
         }
     }
 }
@@ -342,113 +481,143 @@ __global__ __launch_bounds__(kBlock) void backward_sdf_kernel(BwdArgs a) {
 // the reference's unsafe mode (no t > t0 test, :782-790).
 template <int L, bool STATS>
 __global__ __launch_bounds__(kBlock) void backward_density_kernel(BwdArgs a) {
-    const uint32_t ray_idx = blockIdx.x * kBlock + threadIdx.x;
-    if (ray_idx >= a.num_rays) return;
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
-    const RayF ray = load_ray(a.rays, ray_idx);
+    __shared__ float ylds_all[kBlock / 64][64 * nsh];
+    const uint32_t ray_idx = blockIdx.x * kBlock + threadIdx.x;
+    const bool valid = ray_idx < a.num_rays;
+    const uint32_t lane = lane_id();
+    float *ylds = ylds_all[threadIdx.x >> 6];
+
+    RayF ray = {};
+    if (valid) ray = load_ray(a.rays, ray_idx);
     float sh[nsh];
     sh_basis<L>(ray.dx, ray.dy, ray.dz, sh);
+#pragma unroll
+    for (int k = 0; k < nsh; ++k) ylds[lane * nsh + k] = sh[k];
+    __builtin_amdgcn_wave_barrier();
+
     const float thr = a.settings.weight_threshold;
     const uint32_t Q = a.num_quantiles;
-    const float *rq = a.quantiles ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
-    const float *rdg = a.depth_grad ? a.depth_grad + (uint64_t)ray_idx * Q : nullptr;
-    // the statistics instantiation gets no rgba / gradient / depth buffers
-    const float4 g4 = STATS ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-                            : *reinterpret_cast<const float4 *>(a.rgba_grad + 4ull * ray_idx);
-    const float4 c4 = STATS ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-                            : *reinterpret_cast<const float4 *>(a.rgba + 4ull * ray_idx);
-    const float err = a.ray_error ? a.ray_error[ray_idx] : 0.0f;
-
+    const float *rq = (valid && a.quantiles) ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
+    const float *rdg = (valid && a.depth_grad) ? a.depth_grad + (uint64_t)ray_idx * Q : nullptr;
+    float4 g4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 c4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float cur_dg = 0.0f; // src/tracing/pipeline.cu:620-629
-    for (uint32_t k = 0; k < (STATS ? 0u : Q); ++k) {
-        const uint32_t pi = a.depth_indices[(uint64_t)ray_idx * Q + k];
-        if (pi != kNoIndex && pi < a.scene.num_points) {
-            cur_dg = cur_dg + rdg[k] / a.scene.attrs[(uint64_t)pi * D + D - 1];
+    if (!STATS && valid) {
+        g4 = *reinterpret_cast<const float4 *>(a.rgba_grad + 4ull * ray_idx);
+        c4 = *reinterpret_cast<const float4 *>(a.rgba + 4ull * ray_idx);
+        for (uint32_t k = 0; k < Q; ++k) {
+            const uint32_t pi = a.depth_indices[(uint64_t)ray_idx * Q + k];
+            if (pi != kNoIndex && pi < a.scene.num_points) {
+                cur_dg = cur_dg + rdg[k] / a.scene.attrs[(uint64_t)pi * D + D - 1];
+            }
         }
     }
+    const float err = (valid && a.ray_error) ? a.ray_error[ray_idx] : 0.0f;
+
     float T = 1.0f;
     float C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
     uint32_t qi = 0;
     float q = (rq && Q > 0) ? rq[0] : 0.0f;
     GeomState gs;
-    gs.prev_idx = kNoIndex;
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        gs.prev_pt[i] = 0.0f;
-        gs.prev_g[i] = gs.cur_g[i] = gs.next_g[i] = 0.0f;
-    }
+    geom_init(gs);
     uint64_t hash = kFnvOffset;
     uint32_t rec = 0;
 
-    auto step = [&](uint32_t cell, uint32_t next, float t0, float t1, const float *xc,
-                    const float *xn) -> bool {
-        if constexpr (STATS) {
-            hash = fnv_step(hash, cell);
-            if (a.cells && rec < a.cells_stride) a.cells[(uint64_t)ray_idx * a.cells_stride + rec] = cell;
-            ++rec;
-        }
-        const float *__restrict__ row = a.scene.attrs + (uint64_t)cell * D;
-        const float s = row[D - 1];
-        float r, g, b;
-        if (s > 1e-6f) {
-            sh_rgb<L>(sh, row, r, g, b);
-        } else {
-            r = g = b = 0.0f;
-        }
-        const float dt = fmaxf(t1 - t0, 0.0f);
-        const float alpha = 1.0f - sdf_expf(-s * dt);
-        const float w = T * alpha;
-        const float dalpha_ds = dt * (1.0f - alpha);
-        float dalpha_ddt = 0.0f;
-        if (dt > 0.0f) dalpha_ddt = s * (1.0f - alpha);
-        C0 = fmaf(w, r, C0);
-        C1 = fmaf(w, g, C1);
-        C2 = fmaf(w, b, C2);
-        if (STATS) {
-            T = T * (1.0f - alpha);
-            return T > thr;
-        }
-        if (a.point_error) atomicAdd(a.point_error + cell, w * err);
-        const float dr = g4.x * w, dg = g4.y * w, db = g4.z * w;
-        const float den = T * (1.0f - alpha + 1e-6f);
-        const float rest0 = (c4.x - C0) / den;
-        const float rest1 = (c4.y - C1) / den;
-        const float rest2 = (c4.z - C2) / den;
-        float dL_dalpha = T * sdf_dot3(r - rest0, g - rest1, b - rest2, g4.x, g4.y, g4.z);
-        dL_dalpha = dL_dalpha + (1.0f - c4.w) * g4.w / (1.0f - alpha + 1e-6f);
-        float dL_ds = dL_dalpha * dalpha_ds;
-        float dL_ddt = dL_dalpha * dalpha_ddt;
-        float dL_dt0 = 0.0f;
-        const float Tn = T * (1.0f - alpha);
-        while (qi < Q && Tn < q) {
-            const float dgi = rdg[qi] / s;
-            dL_dt0 = dL_dt0 + dgi;
-            dL_ds = dL_ds + -dgi * logf(T / q) / s;
-            cur_dg = cur_dg - dgi;
-            ++qi;
-            if (qi < Q) q = rq[qi];
-        }
-        if (qi < Q) {
-            dL_ds = fmaf(-dt, cur_dg, dL_ds);
-            dL_ddt = fmaf(-s, cur_dg, dL_ddt);
-        }
-        dL_dt0 = dL_dt0 + -dL_ddt;
-        geom_step(gs, cell, xc, xn, dL_dt0, dL_ddt, ray, a.points_grad);
-        T = Tn;
-        float *__restrict__ grow = a.attr_grad + (uint64_t)cell * D;
-        sh_grad<L>(sh, r, g, b, dr, dg, db, grow);
-        atomicAdd(grow + (D - 1), dL_ds);
-        return T > thr;
-    };
+    WalkState ws;
+    walk_init(a.scene, valid ? a.start[ray_idx] : kNoIndex, ws);
+    WalkCounters wc = {0u, 0u, 0ull, 0ull};
 
-    WalkCounters wc;
-    walk<false, STATS>(a.scene, ray, a.start[ray_idx], a.settings.max_intersections, step, wc);
+    while (__ballot(ws.alive) != 0ull) {
+        StepInfo si;
+        si.stepped = false;
+        si.found = false;
+        if (ws.alive) walk_advance<false, STATS>(a.scene, ray, a.settings.max_intersections, ws, si, wc);
+
+        bool keep = true;
+        float dr = 0.0f, dg = 0.0f, db = 0.0f, dds = 0.0f, pe = 0.0f;
+        bool flush = false;
+        uint32_t flush_idx = kNoIndex;
+        float flush_g[3] = {0.0f, 0.0f, 0.0f};
+        if (si.stepped) {
+            const uint32_t cell = ws.cell;
+            const float t0 = ws.t0, t1 = si.t1;
+            if constexpr (STATS) {
+                hash = fnv_step(hash, cell);
+                if (a.cells && rec < a.cells_stride) a.cells[(uint64_t)ray_idx * a.cells_stride + rec] = cell;
+                ++rec;
+            }
+            const float *__restrict__ row = a.scene.attrs + (uint64_t)cell * D;
+            const float s = row[D - 1];
+            const float dt = fmaxf(t1 - t0, 0.0f);
+            const float alpha = 1.0f - sdf_expf(-s * dt);
+            const float Tn = T * (1.0f - alpha);
+            if constexpr (!STATS) {
+                float r, g, b;
+                if (s > 1e-6f) {
+                    sh_rgb<L>(sh, row, r, g, b);
+                } else {
+                    r = g = b = 0.0f;
+                }
+                const float w = T * alpha;
+                const float dalpha_ds = dt * (1.0f - alpha);
+                float dalpha_ddt = 0.0f;
+                if (dt > 0.0f) dalpha_ddt = s * (1.0f - alpha);
+                C0 = fmaf(w, r, C0);
+                C1 = fmaf(w, g, C1);
+                C2 = fmaf(w, b, C2);
+                pe = w * err;
+                dr = g4.x * w;
+                dg = g4.y * w;
+                db = g4.z * w;
+                const float den = T * (1.0f - alpha + 1e-6f);
+                const float rest0 = (c4.x - C0) / den;
+                const float rest1 = (c4.y - C1) / den;
+                const float rest2 = (c4.z - C2) / den;
+                float dL_dalpha = T * sdf_dot3(r - rest0, g - rest1, b - rest2, g4.x, g4.y, g4.z);
+                dL_dalpha = dL_dalpha + (1.0f - c4.w) * g4.w / (1.0f - alpha + 1e-6f);
+                float dL_ds = dL_dalpha * dalpha_ds;
+                float dL_ddt = dL_dalpha * dalpha_ddt;
+                float dL_dt0 = 0.0f;
+                while (qi < Q && Tn < q) {
+                    const float dgi = rdg[qi] / s;
+                    dL_dt0 = dL_dt0 + dgi;
+                    dL_ds = dL_ds + -dgi * logf(T / q) / s;
+                    cur_dg = cur_dg - dgi;
+                    ++qi;
+                    if (qi < Q) q = rq[qi];
+                }
+                if (qi < Q) {
+                    dL_ds = fmaf(-dt, cur_dg, dL_ds);
+                    dL_ddt = fmaf(-s, cur_dg, dL_ddt);
+                }
+                dL_dt0 = dL_dt0 + -dL_ddt;
+                flush = geom_step(gs, cell, ws.xc, si.xn, dL_dt0, dL_ddt, ray, flush_idx, flush_g);
+                dds = dL_ds;
+                if (r == 0.0f) dr = 0.0f;
+                if (g == 0.0f) dg = 0.0f;
+                if (b == 0.0f) db = 0.0f;
+            }
+            T = Tn;
+            keep = T > thr;
+        }
+        if constexpr (!STATS) {
+            grouped_backward_updates<L>(si.stepped, ws.cell, dr, dg, db, dds, D - 1, pe, flush,
+                                        flush_idx, flush_g, ylds, a.attr_grad, a.point_error,
+                                        a.points_grad);
+        }
+        if (si.stepped && !keep) ws.alive = false;
+        if (ws.alive && si.found) walk_move(ws, si);
+    }
+
     if constexpr (STATS) {
-        if (a.visit_hash) a.visit_hash[ray_idx] = hash;
-        if (a.steps) a.steps[ray_idx] = wc.steps;
-        if (a.faces) a.faces[ray_idx] = wc.faces;
-        if (a.faces_stepped) a.faces_stepped[ray_idx] = wc.faces_stepped;
+        if (valid) {
+            if (a.visit_hash) a.visit_hash[ray_idx] = hash;
+            if (a.steps) a.steps[ray_idx] = wc.steps;
+            if (a.faces) a.faces[ray_idx] = wc.faces;
+            if (a.faces_stepped) a.faces_stepped[ray_idx] = wc.faces_stepped;
+        }
     }
 }
 
