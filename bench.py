@@ -73,6 +73,11 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3])
     ap.add_argument("--cpu-stride", type=int, default=8,
                     help="CPU baseline traces every n-th ray (0 skips it)")
+    ap.add_argument("--scene-cache", default="",
+                    help="npz file to load the generated scene from / save it to")
+    ap.add_argument("--calibrate-copy-gib", type=float, default=0.0,
+                    help="only run a device-to-device copy of this many GiB (a kernel of known "
+                         "traffic, to scale rocprof FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
@@ -92,9 +97,25 @@ def main() -> int:
     dev = torch.device("cuda:0")
     _lib.lib()
 
+    if args.calibrate_copy_gib > 0:
+        n = int(args.calibrate_copy_gib * (1 << 30)) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration_copy_bytes": 4 * n, "launches": 3}), flush=True)
+        return 0
+
     t0 = time.time()
-    log(f"generating config C{args.config} (Delaunay via Qhull)")
-    w = scenes.make_config(args.config)
+    if args.scene_cache and os.path.exists(args.scene_cache):
+        log(f"loading scene from {args.scene_cache}")
+        w = scenes.load_workload(args.scene_cache)
+    else:
+        log(f"generating config C{args.config} (Delaunay via Qhull)")
+        w = scenes.make_config(args.config)
+        if args.scene_cache:
+            scenes.save_workload(w, args.scene_cache)
     log(f"scene ready in {time.time() - t0:.1f}s: N={w.num_points} E={w.adjacency.size} R={w.num_rays}")
 
     def u32(a):

@@ -37,12 +37,17 @@ extern "C" {
  * (src/tracing/pipeline.h:12-27; defaults src/tracing/pipeline.h:29-40:
  * weight_threshold 1e-7, max_intersections 1024, alpha_mode standard,
  * sdf_channel -1).  inv_s, eps and the viewer fields are not read by the
- * reference's kernels and are not part of this struct. */
+ * reference's kernels and are not part of this struct.
+ * ray_image_width is a layout hint with no counterpart in the reference: 0
+ * for rays in any order, or W when the rays are image rows of W pixels
+ * ([..., H, W, 6]); the kernels then give each wavefront an 8x8 pixel tile.
+ * Results do not depend on it. */
 typedef struct sdf_trace_settings {
     float weight_threshold;
     uint32_t max_intersections;
     uint32_t alpha_mode;
     int32_t sdf_channel;
+    uint32_t ray_image_width;
 } sdf_trace_settings;
 
 /* Library version string. */

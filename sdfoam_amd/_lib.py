@@ -44,6 +44,7 @@ class TraceSettings(C.Structure):
         ("max_intersections", C.c_uint32),
         ("alpha_mode", C.c_uint32),
         ("sdf_channel", C.c_int32),
+        ("ray_image_width", C.c_uint32),
     ]
 
 

@@ -69,6 +69,9 @@ int check_scene(int sh_degree, const sdf_trace_settings *settings, uint32_t num_
     if (settings->sdf_channel >= D)
         return fail(SDF_E_INVALID, "sdf_channel %d out of range for attribute dim %d",
                     settings->sdf_channel, D);
+    if (settings->ray_image_width != 0 && num_rays % settings->ray_image_width != 0)
+        return fail(SDF_E_INVALID, "ray_image_width %u does not divide the %u rays",
+                    settings->ray_image_width, num_rays);
     if (num_points == 0) return fail(SDF_E_INVALID, "num_points must be positive");
     if (!points || !attributes || !offs || (!adj && adjacency_size > 0))
         return fail(SDF_E_INVALID, "scene pointers must not be NULL");
@@ -164,6 +167,7 @@ int sdf_trace_forward(int sh_degree, const sdf_trace_settings *settings, uint32_
     a.settings = *settings;
     a.rays = rays;
     a.num_rays = num_rays;
+    a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
     a.start = start_point_index;
     a.num_quantiles = num_depth_quantiles;
     a.quantiles = num_depth_quantiles ? depth_quantiles : nullptr;
@@ -220,6 +224,7 @@ int sdf_trace_backward(int sh_degree, const sdf_trace_settings *settings, uint32
     a.settings = *settings;
     a.rays = rays;
     a.num_rays = num_rays;
+    a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
     a.start = start_point_index;
     a.num_quantiles = num_depth_quantiles;
     a.quantiles = num_depth_quantiles ? depth_quantiles : nullptr;
@@ -292,6 +297,7 @@ int sdf_trace_walk_stats(int sh_degree, const sdf_trace_settings *settings, int 
         a.settings = *settings;
         a.rays = rays;
         a.num_rays = num_rays;
+    a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
         a.start = start_point_index;
         a.sharpness = sharpness;
         a.visit_hash = visit_hash;
@@ -307,6 +313,7 @@ int sdf_trace_walk_stats(int sh_degree, const sdf_trace_settings *settings, int 
         a.settings = *settings;
         a.rays = rays;
         a.num_rays = num_rays;
+    a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
         a.start = start_point_index;
         a.sharpness = sharpness;
         a.visit_hash = visit_hash;

@@ -34,6 +34,47 @@ struct RayF {
     float dx, dy, dz;
 };
 
+// Work decomposition.  A block is one tile of rays: 16x16 pixels (an 8x8
+// tile per wavefront) when the rays are image rows of `width` pixels, else
+// 256 consecutive rays.  Blocks are dealt round-robin to the 8 XCDs, each
+// with its own L2, so block b is given tile (b % 8) * per + b / 8: every XCD
+// walks a contiguous band of tiles whose rays cross the same cells.  The
+// grid has 8 * per blocks, per = ceil(num_tiles / 8); surplus blocks idle.
+constexpr uint32_t kXcds = 8;
+constexpr uint32_t kTile = 16;
+
+__host__ __device__ inline uint32_t num_ray_tiles(uint32_t num_rays, uint32_t width) {
+    if (width == 0) return (num_rays + kBlock - 1) / kBlock;
+    const uint32_t height = num_rays / width;
+    return ((width + kTile - 1) / kTile) * ((height + kTile - 1) / kTile);
+}
+
+__host__ inline uint32_t grid_blocks_for_tiles(uint32_t num_tiles) {
+    return kXcds * ((num_tiles + kXcds - 1) / kXcds);
+}
+
+__device__ __forceinline__ uint32_t ray_for_lane(uint32_t num_rays, uint32_t width,
+                                                 uint32_t num_tiles, bool &valid) {
+    const uint32_t per = gridDim.x / kXcds;
+    const uint32_t t = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+    if (t >= num_tiles) {
+        valid = false;
+        return 0;
+    }
+    if (width == 0) {
+        const uint32_t i = t * kBlock + threadIdx.x;
+        valid = i < num_rays;
+        return i;
+    }
+    const uint32_t height = num_rays / width;
+    const uint32_t tiles_x = (width + kTile - 1) / kTile;
+    const uint32_t w = threadIdx.x >> 6, l = threadIdx.x & 63u;
+    const uint32_t x = (t % tiles_x) * kTile + (w & 1u) * 8u + (l & 7u);
+    const uint32_t y = (t / tiles_x) * kTile + (w >> 1) * 8u + (l >> 3);
+    valid = x < width && y < height;
+    return valid ? y * width + x : 0u;
+}
+
 // ray.direction /= ray.direction.norm()  (src/tracing/pipeline.cu:76-77)
 __device__ __forceinline__ RayF load_ray(const float *__restrict__ rays, uint32_t i) {
     const float *r = rays + 6ull * i;

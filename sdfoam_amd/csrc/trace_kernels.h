@@ -11,6 +11,7 @@ struct FwdArgs {
     sdf_trace_settings settings;
     const float *rays;
     uint32_t num_rays;
+    uint32_t num_tiles; // num_ray_tiles(num_rays, settings.ray_image_width)
     const uint32_t *start;
     uint32_t num_quantiles;
     const float *quantiles;
@@ -35,6 +36,7 @@ struct BwdArgs {
     sdf_trace_settings settings;
     const float *rays;
     uint32_t num_rays;
+    uint32_t num_tiles; // num_ray_tiles(num_rays, settings.ray_image_width)
     const uint32_t *start;
     uint32_t num_quantiles;
     const float *quantiles;

@@ -76,8 +76,9 @@ __device__ __forceinline__ int first_lane(uint64_t mask) { return __builtin_ctzl
 
 template <int L, bool NEUS, bool STATS>
 __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
-    const uint32_t ray_idx = blockIdx.x * kBlock + threadIdx.x;
-    const bool valid = ray_idx < a.num_rays;
+    bool valid;
+    const uint32_t ray_idx =
+        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid);
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
     const uint32_t lane = lane_id();
@@ -259,25 +260,52 @@ __device__ __forceinline__ bool geom_step(GeomState &gs, uint32_t cell, const fl
     return flush;
 }
 
+// Per-wave LDS tables of the grouped updates.  Row 64 of each is zero: it
+// pads a batch of members, so padded slots add exact zeros.
+template <int L>
+struct WaveTables {
+    static constexpr int nsh = (L + 1) * (L + 1);
+    float y[65 * nsh]; // SH basis of each lane's ray, written once
+    float4 g[65];      // per step: d L / d rgb (r, g, b), d L / d last channel
+    float4 p[65];      // per step: flushed position gradient (x, y, z), point error
+};
+
+// Next member of a lane mask (64 = padding once the mask is empty).
+__device__ __forceinline__ int pop_member(uint64_t &mm) {
+    if (!mm) return 64;
+    const int m = first_lane(mm);
+    mm &= mm - 1;
+    return m;
+}
+
 // Grouped gradient updates of one wave-synchronous step (all 64 lanes
 // active).  For every cell some lanes stepped into, lane i < D adds
 //   sum over those lanes of  Y_{i/3} * g_{i%3}      (i < 3 nsh; SH, sh_utils.cuh:85-92)
 //   + sum of g_last                                 (i == last_ch)
 // to row `cell` of attr_grad, lane 63 adds the point-error sum; then for
-// every flushed cell lanes 0..2 add the flushed position gradients.
-// Y of every lane of the wave sits in LDS (ylds[lane * nsh + j]).
+// every flushed cell lanes 0..2 add the flushed position gradients.  The
+// stepping lanes publish their values in the wave's LDS tables; the owner
+// lane of each component reads the members four at a time.
 template <int L>
 __device__ __forceinline__ void grouped_backward_updates(
     bool stepped, uint32_t cell, float gr, float gg, float gb, float g_last, int last_ch,
-    float pe, bool flush, uint32_t flush_idx, const float *flush_g, const float *ylds,
+    float pe, bool flush, uint32_t flush_idx, const float *flush_g, WaveTables<L> &tb,
     float *__restrict__ attr_grad, float *__restrict__ point_error,
     float *__restrict__ points_grad) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
     const uint32_t lane = lane_id();
-    const int j = (int)lane / 3;
-    const int ch = (int)lane % 3;
+    if (stepped) {
+        tb.g[lane] = make_float4(gr, gg, gb, g_last);
+        tb.p[lane] = make_float4(flush_g[0], flush_g[1], flush_g[2], pe);
+    }
+    __builtin_amdgcn_wave_barrier();
     const bool sh_lane = lane < 3u * nsh;
+    const int j = sh_lane ? (int)lane / 3 : 0;
+    const int ch = sh_lane ? (int)lane % 3 : 0;
+    const bool last_lane = (int)lane == last_ch;
+    const float *gf = reinterpret_cast<const float *>(tb.g);
+    const float *pf = reinterpret_cast<const float *>(tb.p);
     uint64_t todo = __ballot(stepped);
     while (todo) {
         const int leader = first_lane(todo);
@@ -286,39 +314,65 @@ __device__ __forceinline__ void grouped_backward_updates(
         todo &= ~grp;
         float acc = 0.0f;
         float pacc = 0.0f;
-        for (uint64_t mm = grp; mm; mm &= mm - 1) {
-            const int m = first_lane(mm);
-            const float vr = readlane_f(gr, m);
-            const float vg = readlane_f(gg, m);
-            const float vb = readlane_f(gb, m);
-            const float vl = readlane_f(g_last, m);
-            if (sh_lane) {
-                const float y = ylds[m * nsh + j];
-                const float gsel = ch == 0 ? vr : (ch == 1 ? vg : vb);
-                acc = acc + y * gsel;
+        uint64_t mm = grp;
+        while (mm) {
+            int m[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) m[u] = pop_member(mm);
+            float y[4], g[4], l[4], e[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                y[u] = tb.y[m[u] * nsh + j];
+                g[u] = gf[m[u] * 4 + ch];
+                l[u] = gf[m[u] * 4 + 3];
+                e[u] = pf[m[u] * 4 + 3];
             }
-            if ((int)lane == last_ch) acc = acc + vl;
-            if (point_error) pacc = pacc + readlane_f(pe, m);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (sh_lane) acc = acc + y[u] * g[u];
+                if (last_lane) acc = acc + l[u];
+                pacc = pacc + e[u];
+            }
         }
         if (lane < (uint32_t)D) atomicAdd(attr_grad + (uint64_t)c * D + lane, acc);
         if (point_error && lane == 63u) atomicAdd(point_error + c, pacc);
     }
     todo = __ballot(flush);
+    const int pl = lane < 3u ? (int)lane : 0;
     while (todo) {
         const int leader = first_lane(todo);
         const uint32_t c = readlane_u(flush_idx, leader);
         const uint64_t grp = __ballot(flush && flush_idx == c);
         todo &= ~grp;
         float acc = 0.0f;
-        for (uint64_t mm = grp; mm; mm &= mm - 1) {
-            const int m = first_lane(mm);
-            const float vx = readlane_f(flush_g[0], m);
-            const float vy = readlane_f(flush_g[1], m);
-            const float vz = readlane_f(flush_g[2], m);
-            acc = acc + (lane == 0u ? vx : (lane == 1u ? vy : vz));
+        uint64_t mm = grp;
+        while (mm) {
+            int m[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) m[u] = pop_member(mm);
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = pf[m[u] * 4 + pl];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc = acc + v[u];
         }
         if (lane < 3u) atomicAdd(points_grad + 3ull * c + lane, acc);
     }
+    __builtin_amdgcn_wave_barrier();
+}
+
+template <int L>
+__device__ __forceinline__ void tables_init(WaveTables<L> &tb, const float *sh) {
+    constexpr int nsh = (L + 1) * (L + 1);
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (int k = 0; k < nsh; ++k) tb.y[lane * nsh + k] = sh[k];
+    if (lane < (uint32_t)nsh) tb.y[64 * nsh + lane] = 0.0f;
+    if (lane == 0) {
+        tb.g[64] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        tb.p[64] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    __builtin_amdgcn_wave_barrier();
 }
 
 // ---------------------------------------------------------------------------
@@ -328,19 +382,21 @@ template <int L, bool STATS>
 __global__ __launch_bounds__(kBlock) void backward_sdf_kernel(BwdArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
-    __shared__ float ylds_all[kBlock / 64][64 * nsh];
-    const uint32_t ray_idx = blockIdx.x * kBlock + threadIdx.x;
-    const bool valid = ray_idx < a.num_rays;
+    __shared__ WaveTables<L> tables[kBlock / 64];
+    bool valid;
+    const uint32_t ray_idx =
+        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid);
     const uint32_t lane = lane_id();
-    float *ylds = ylds_all[threadIdx.x >> 6];
+    WaveTables<L> &tb = tables[threadIdx.x >> 6];
 
     RayF ray = {};
     if (valid) ray = load_ray(a.rays, ray_idx);
-    float sh[nsh];
-    sh_basis<L>(ray.dx, ray.dy, ray.dz, sh);
-#pragma unroll
-    for (int k = 0; k < nsh; ++k) ylds[lane * nsh + k] = sh[k];
-    __builtin_amdgcn_wave_barrier();
+    {
+        float sh0[nsh];
+        sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
+        tables_init<L>(tb, sh0);
+    }
+    const float *sh = tb.y + lane * nsh; // this ray's SH basis, in LDS
 
     const float sha = a.sharpness[0];
     const int32_t sdf_ch = a.settings.sdf_channel >= 0 ? a.settings.sdf_channel : D - 1;
@@ -456,7 +512,7 @@ __global__ __launch_bounds__(kBlock) void backward_sdf_kernel(BwdArgs a) {
         if constexpr (!STATS) {
             grouped_backward_updates<L>(si.stepped, ws.cell, dr, dg, db, dsdf,
                                         write_sdf ? sdf_ch : -1, pe, flush, flush_idx, flush_g,
-                                        ylds, a.attr_grad, a.point_error, a.points_grad);
+                                        tb, a.attr_grad, a.point_error, a.points_grad);
         }
         if (si.stepped && !keep) ws.alive = false;
         if (ws.alive && si.found) walk_move(ws, si);
@@ -483,19 +539,21 @@ template <int L, bool STATS>
 __global__ __launch_bounds__(kBlock) void backward_density_kernel(BwdArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
-    __shared__ float ylds_all[kBlock / 64][64 * nsh];
-    const uint32_t ray_idx = blockIdx.x * kBlock + threadIdx.x;
-    const bool valid = ray_idx < a.num_rays;
+    __shared__ WaveTables<L> tables[kBlock / 64];
+    bool valid;
+    const uint32_t ray_idx =
+        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid);
     const uint32_t lane = lane_id();
-    float *ylds = ylds_all[threadIdx.x >> 6];
+    WaveTables<L> &tb = tables[threadIdx.x >> 6];
 
     RayF ray = {};
     if (valid) ray = load_ray(a.rays, ray_idx);
-    float sh[nsh];
-    sh_basis<L>(ray.dx, ray.dy, ray.dz, sh);
-#pragma unroll
-    for (int k = 0; k < nsh; ++k) ylds[lane * nsh + k] = sh[k];
-    __builtin_amdgcn_wave_barrier();
+    {
+        float sh0[nsh];
+        sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
+        tables_init<L>(tb, sh0);
+    }
+    const float *sh = tb.y + lane * nsh; // this ray's SH basis, in LDS
 
     const float thr = a.settings.weight_threshold;
     const uint32_t Q = a.num_quantiles;
@@ -604,7 +662,7 @@ __global__ __launch_bounds__(kBlock) void backward_density_kernel(BwdArgs a) {
         }
         if constexpr (!STATS) {
             grouped_backward_updates<L>(si.stepped, ws.cell, dr, dg, db, dds, D - 1, pe, flush,
-                                        flush_idx, flush_g, ylds, a.attr_grad, a.point_error,
+                                        flush_idx, flush_g, tb, a.attr_grad, a.point_error,
                                         a.points_grad);
         }
         if (si.stepped && !keep) ws.alive = false;
@@ -636,7 +694,7 @@ hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32
 
 template <int L>
 static hipError_t launch_forward_L(const FwdArgs &a, bool neus, bool stats, hipStream_t stream) {
-    const dim3 grid = grid_for(a.num_rays);
+    const dim3 grid(grid_blocks_for_tiles(a.num_tiles));
     if (neus) {
         if (stats) {
             hipLaunchKernelGGL((forward_kernel<L, true, true>), grid, dim3(kBlock), 0, stream, a);
@@ -665,7 +723,7 @@ hipError_t launch_forward(int L, const FwdArgs &a, bool neus, bool stats, hipStr
 
 template <int L>
 static hipError_t launch_backward_L(const BwdArgs &a, bool neus, bool stats, hipStream_t stream) {
-    const dim3 grid = grid_for(a.num_rays);
+    const dim3 grid(grid_blocks_for_tiles(a.num_tiles));
     if (neus) {
         if (stats) {
             hipLaunchKernelGGL((backward_sdf_kernel<L, true>), grid, dim3(kBlock), 0, stream, a);

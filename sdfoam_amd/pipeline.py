@@ -158,9 +158,10 @@ class Pipeline:
         if not _is_cuda(start_point):
             raise RuntimeError("start_point must be on CUDA device")
 
-    def _settings(self, weight_threshold, max_intersections, alpha_mode, sdf_channel):
+    def _settings(self, weight_threshold, max_intersections, alpha_mode, sdf_channel, rays=None):
         """default_trace_settings + kwargs (src/tracing/pipeline.h:29-40;
-        torch_bindings/pipeline_bindings.cpp:212-242)."""
+        torch_bindings/pipeline_bindings.cpp:212-242), plus the image-width
+        layout hint for rays shaped [..., H, W, 6]."""
         mode = _parse_alpha_mode(alpha_mode)
         if sdf_channel is not None:
             ch = int(sdf_channel)
@@ -168,11 +169,13 @@ class Pipeline:
             ch = self.attribute_dim() - 1
         else:
             ch = -1
+        width = int(rays.shape[-2]) if rays is not None and rays.dim() >= 3 else 0
         return TraceSettings(
             1e-7 if weight_threshold is None else float(weight_threshold),
             1024 if max_intersections is None else int(max_intersections),
             mode,
             ch,
+            width,
         )
 
     def _require_native(self):
@@ -217,7 +220,7 @@ class Pipeline:
                 raise RuntimeError("depth_quantiles must be on CUDA device")
             if num_q == 0 or dq.numel() // num_q != num_rays:
                 raise RuntimeError("depth_quantiles must have the same batch size as rays")
-        settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel)
+        settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel, rays_c)
         self._require_native()
 
         dev = rays_c.device
@@ -331,7 +334,7 @@ class Pipeline:
                 raise RuntimeError("ray_error must have the same batch size as rays")
             point_error = torch.zeros((num_points, 1), dtype=self._attr_dtype, device=dev)
 
-        settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel)
+        settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel, rays_c)
         self._require_native()
         rgba = rgb_out.contiguous()
         if rgba.dtype != self._attr_dtype or rgba.numel() != 4 * num_rays or not _is_cuda(rgba):
@@ -379,7 +382,7 @@ class Pipeline:
         self._validate_rays(rays_c, start_c, num_rays)
         self._require_native()
         sharpness = _inv_s_to_tensor(inv_s, rays_c)
-        settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel)
+        settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel, rays_c)
         dev = rays_c.device
         n = points_c.size(0)
         num_adj = adj_c.size(0)

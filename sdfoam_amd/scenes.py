@@ -324,6 +324,28 @@ def make_config(index: int, *, mode: str = "sdfoam", inv_s: float | None = None,
     )
 
 
+def save_workload(w: Workload, path: str) -> None:
+    """Write a workload to an .npz file (arrays only; no pickled objects)."""
+    cam = w.extra.get("camera")
+    np.savez(
+        path, name=np.array(w.name), sh_degree=np.array(w.sh_degree), points=w.points,
+        attributes=w.attributes, adjacency=w.adjacency, offsets=w.offsets, rays=w.rays,
+        quantiles=w.quantiles, grad_rgba=w.grad_rgba, depth_grad=w.depth_grad,
+        inv_s=np.array(w.inv_s), alpha_mode=np.array(w.alpha_mode),
+    )
+
+
+def load_workload(path: str) -> Workload:
+    """Read a workload written by save_workload (allow_pickle stays off)."""
+    z = np.load(path)
+    return Workload(
+        name=str(z["name"]), sh_degree=int(z["sh_degree"]), points=z["points"],
+        attributes=z["attributes"], adjacency=z["adjacency"], offsets=z["offsets"],
+        rays=z["rays"], quantiles=z["quantiles"], grad_rgba=z["grad_rgba"],
+        depth_grad=z["depth_grad"], inv_s=float(z["inv_s"]), alpha_mode=str(z["alpha_mode"]),
+    )
+
+
 def nearest_point_bruteforce(points: np.ndarray, queries: np.ndarray) -> np.ndarray:
     """Exact nearest neighbour by float32 distance (host helper for building
     start points; ties go to the smallest index)."""
