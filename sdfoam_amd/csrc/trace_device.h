@@ -128,7 +128,9 @@ __device__ __forceinline__ void sh_rgb(const float *sh, const float *__restrict_
                                        float &r, float &g, float &b) {
     constexpr int nsh = (L + 1) * (L + 1);
     float a0 = 0.5f, a1 = 0.5f, a2 = 0.5f;
-#pragma unroll
+    // partial unroll: 12 row values in flight at a time instead of 48 keeps
+    // the kernels' register count low (same FMA order per channel)
+#pragma unroll 4
     for (int j = 0; j < nsh; ++j) {
         a0 = fmaf(sh[j], row[3 * j + 0], a0);
         a1 = fmaf(sh[j], row[3 * j + 1], a1);

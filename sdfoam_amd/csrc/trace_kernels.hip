@@ -76,17 +76,24 @@ __device__ __forceinline__ int first_lane(uint64_t mask) { return __builtin_ctzl
 
 template <int L, bool NEUS, bool STATS>
 __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
+    constexpr int nsh = (L + 1) * (L + 1);
+    constexpr int D = 1 + 3 * nsh;
+    // SH basis of each lane's ray, in LDS (frees nsh VGPRs)
+    __shared__ float sh_all[kBlock * nsh];
     bool valid;
     const uint32_t ray_idx =
         ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid);
-    constexpr int nsh = (L + 1) * (L + 1);
-    constexpr int D = 1 + 3 * nsh;
     const uint32_t lane = lane_id();
 
     RayF ray = {};
-    float sh[nsh];
     if (valid) ray = load_ray(a.rays, ray_idx);
-    sh_basis<L>(ray.dx, ray.dy, ray.dz, sh);
+    float *sh = sh_all + threadIdx.x * nsh;
+    {
+        float sh0[nsh];
+        sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
+#pragma unroll
+        for (int k = 0; k < nsh; ++k) sh[k] = sh0[k];
+    }
     const float sha = a.sharpness[0];
     const int32_t sdf_ch = a.settings.sdf_channel;
     const bool neus_alpha = NEUS && sdf_ch >= 0;
@@ -379,7 +386,8 @@ __device__ __forceinline__ void tables_init(WaveTables<L> &tb, const float *sh) 
 // backward_sdf (src/tracing/pipeline.cu:267-550)
 
 template <int L, bool STATS>
-__global__ __launch_bounds__(kBlock) void backward_sdf_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(5, 8))) void
+backward_sdf_kernel(BwdArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
     __shared__ WaveTables<L> tables[kBlock / 64];
@@ -536,7 +544,8 @@ __global__ __launch_bounds__(kBlock) void backward_sdf_kernel(BwdArgs a) {
 // backward, density mode (src/tracing/pipeline.cu:553-791); the walk runs in
 // the reference's unsafe mode (no t > t0 test, :782-790).
 template <int L, bool STATS>
-__global__ __launch_bounds__(kBlock) void backward_density_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(5, 8))) void
+backward_density_kernel(BwdArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
     __shared__ WaveTables<L> tables[kBlock / 64];
