@@ -1,0 +1,97 @@
+"""The C ABI without a GPU: libsdfoam_hip.so loads, exports every symbol the
+headers under include/ declare, and rejects bad arguments with its own
+messages before any HIP call."""
+
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    with open(os.path.join(ROOT, "include", "sdfoam_hip.h")) as f:
+        text = f.read()
+    for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b(sdf_\w+)\s*\(", text, re.M):
+        names.add(m.group(1))
+    return names
+
+
+def test_every_declared_symbol_is_exported():
+    from sdfoam_amd import _lib
+
+    names = declared_functions()
+    assert len(names) >= 12
+    assert names == set(_lib.EXPORTS)
+    L = C.CDLL(_lib.LIB_PATH)
+    for n in names:
+        assert hasattr(L, n), n
+
+
+def test_pure_queries():
+    from sdfoam_amd import _lib
+
+    L = _lib.lib()
+    assert L.sdf_version().startswith(b"sdfoam_hip")
+    assert [L.sdf_attribute_dim(d) for d in range(4)] == [4, 13, 28, 49]
+    assert L.sdf_attribute_dim(4) == -1 and L.sdf_attribute_dim(-1) == -1
+    assert L.sdf_trace_scratch_bytes(10, 100) == (100 + 32) * 8
+
+
+def _settings(mode=1, ch=48, width=0):
+    from sdfoam_amd._lib import TraceSettings
+
+    return TraceSettings(1e-7, 1024, mode, ch, width)
+
+
+def _fwd(L, degree=3, settings=None, num_points=10, scratch=True, scratch_bytes=None, rays=1,
+         width=0):
+    s = settings or _settings(width=width)
+    buf = (C.c_uint64 * 64)()
+    p = C.cast(buf, C.c_void_p)
+    nb = L.sdf_trace_scratch_bytes(num_points, 4) if scratch_bytes is None else scratch_bytes
+    return L.sdf_trace_forward(degree, C.byref(s), num_points, p, p, 4, p, p, rays, p, p, 0,
+                               None, p, None, None, p, None, p, p, p if scratch else None, nb,
+                               None)
+
+
+def test_forward_argument_errors():
+    from sdfoam_amd import _lib
+
+    L = _lib.lib()
+    assert _fwd(L, degree=4) == 1
+    assert L.sdf_last_error() == b"Unsupported SH degree"
+    assert _fwd(L, settings=_settings(mode=7)) == 1
+    assert b"alpha_mode" in L.sdf_last_error()
+    assert _fwd(L, settings=_settings(ch=49)) == 1
+    assert b"sdf_channel 49 out of range" in L.sdf_last_error()
+    assert _fwd(L, num_points=0) == 1
+    assert _fwd(L, scratch=False) == 1
+    assert b"scratch must hold" in L.sdf_last_error()
+    assert _fwd(L, scratch_bytes=8) == 1
+    assert _fwd(L, rays=10, width=3) == 1
+    assert b"ray_image_width 3 does not divide" in L.sdf_last_error()
+
+
+def test_nn_and_tree_argument_errors():
+    from sdfoam_amd import _lib
+
+    L = _lib.lib()
+    buf = (C.c_uint64 * 8)()
+    p = C.cast(buf, C.c_void_p)
+    assert L.sdf_nn(p, p, p, 31, 1, p, None) == 1
+    assert L.sdf_last_error() == b"number of points must be at least 32"
+    assert L.sdf_build_aabb_tree(None, 10, p, None) == 1
+    assert L.sdf_debug_fpmath(5, p, p, 1, None) == 1
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from sdfoam_amd import _lib
+
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
+    with pytest.raises(_lib.LibraryError, match="not built"):
+        _lib.lib()

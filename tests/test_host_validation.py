@@ -1,0 +1,79 @@
+"""The host mirror's argument checks, without a GPU: the same messages, in
+the same order, as the reference's bindings
+(torch_bindings/pipeline_bindings.cpp:12-75, 176-210, 734-751;
+torch_bindings/triangulation_bindings.cpp:117-181).  Checks that come
+before the device checks are reachable with CPU tensors."""
+
+import pytest
+import torch
+
+import sdfoam_amd
+
+
+def scene(n=40, D=49):
+    pts = torch.zeros(n, 3)
+    attrs = torch.zeros(n, D)
+    adj = torch.zeros(8, dtype=torch.uint32)
+    offs = torch.zeros(n + 1, dtype=torch.uint32)
+    rays = torch.zeros(5, 6)
+    start = torch.zeros(5, dtype=torch.uint32)
+    return pts, attrs, adj, offs, rays, start
+
+
+def test_create_pipeline():
+    p = sdfoam_amd.create_pipeline(3)
+    assert p.attribute_dim() == 49 and p.attribute_type() == torch.float32
+    assert sdfoam_amd.create_pipeline(0, "torch.float32").attribute_dim() == 4
+    assert sdfoam_amd.create_pipeline(1, "float16").attribute_type() == torch.float16
+    with pytest.raises(RuntimeError, match="Unsupported SH degree"):
+        sdfoam_amd.create_pipeline(4)
+    with pytest.raises(RuntimeError, match="Unsupported attribute type"):
+        sdfoam_amd.create_pipeline(0, "float64")
+    with pytest.raises(RuntimeError, match="unsupported dtype 'int8'"):
+        sdfoam_amd.create_pipeline(0, "int8")
+
+
+def test_scene_checks_in_order():
+    pipe = sdfoam_amd.create_pipeline(3)
+    pts, attrs, adj, offs, rays, start = scene()
+    with pytest.raises(RuntimeError, match=r"points had dimension 4 along axis -1, expected 3"):
+        pipe.trace_forward(torch.zeros(40, 4), attrs, adj, offs, rays, start)
+    with pytest.raises(RuntimeError, match=r"points had dtype Double, expected float32"):
+        pipe.trace_forward(pts.double(), attrs, adj, offs, rays, start)
+    with pytest.raises(RuntimeError, match=r"unsupported dtype 'Int'"):
+        pipe.trace_forward(pts.int(), attrs, adj, offs, rays, start)
+    with pytest.raises(RuntimeError, match="points must be on CUDA device"):
+        pipe.trace_forward(pts, attrs, adj, offs, rays, start)
+
+
+def test_backward_checks():
+    pipe = sdfoam_amd.create_pipeline(3)
+    pts, attrs, adj, offs, rays, start = scene()
+    with pytest.raises(RuntimeError, match="points must be on CUDA device"):
+        pipe.trace_backward(pts, attrs, adj, offs, rays, start, torch.zeros(5, 4), torch.zeros(5, 4))
+
+
+def test_spatial_checks():
+    with pytest.raises(RuntimeError, match="points must have 3 as the last dimension"):
+        sdfoam_amd.build_aabb_tree(torch.zeros(40, 4))
+    with pytest.raises(RuntimeError, match="points must have 2 dimensions"):
+        sdfoam_amd.build_aabb_tree(torch.zeros(2, 40, 3))
+    with pytest.raises(RuntimeError, match="points must be on CUDA device"):
+        sdfoam_amd.build_aabb_tree(torch.zeros(40, 3))
+    with pytest.raises(RuntimeError, match="points and queries must have the same dtype"):
+        sdfoam_amd.nn(torch.zeros(40, 3), torch.zeros(64, 2, 3), torch.zeros(5, 3).double())
+    with pytest.raises(RuntimeError, match="points and tree must have the same dtype"):
+        sdfoam_amd.nn(torch.zeros(40, 3), torch.zeros(64, 2, 3).double(), torch.zeros(5, 3))
+    with pytest.raises(RuntimeError, match="points must be on CUDA device"):
+        sdfoam_amd.nn(torch.zeros(40, 3), torch.zeros(64, 2, 3), torch.zeros(5, 3))
+
+
+def test_trace_rays_signature():
+    """TraceRays.forward takes the reference's arguments in the reference's
+    order (sdfoam_model/render.py:12-29)."""
+    import inspect
+
+    params = list(inspect.signature(sdfoam_amd.TraceRays.forward).parameters)
+    assert params == ["ctx", "pipeline", "_points", "_attributes", "_point_adjacency",
+                      "_point_adjacency_offsets", "rays", "start_point", "depth_quantiles",
+                      "return_contribution", "use_sdfoam", "inv_s", "eps", "sdf_channel"]
