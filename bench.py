@@ -23,6 +23,8 @@ stepped cell, Q = quantiles):
   forward : per ray 48 + 12Q; per step 28 + 4D + 4 (contribution) + 8 deg
   backward: per ray 60 + 12Q; per step 36 + 8D + 8 deg
   prepass : 12 E + 16 N
+With the walk record (default, as TraceRays runs it) the forward writes 8 B
+per step more and the backward reads those 8 B instead of 8 deg.
 """
 
 from __future__ import annotations
@@ -73,6 +75,9 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3])
     ap.add_argument("--cpu-stride", type=int, default=8,
                     help="CPU baseline traces every n-th ray (0 skips it)")
+    ap.add_argument("--walk-record", type=int, default=1, choices=[0, 1],
+                    help="1: the forward records each ray's steps and the backward replays "
+                         "them (TraceRays does this); 0: the backward scans the faces again")
     ap.add_argument("--scene-cache", default="",
                     help="npz file to load the generated scene from / save it to")
     ap.add_argument("--calibrate-copy-gib", type=float, default=0.0,
@@ -140,11 +145,15 @@ def main() -> int:
     D = pipe.attribute_dim()
     Q = int(w.quantiles.shape[-1])
 
+    use_record = bool(args.walk_record)
+
     def step():
         out = pipe.trace_forward(pts, attrs, adj, offs, rays, start, depth_quantiles=q,
-                                 return_contribution=True, alpha_mode="sdfoam", inv_s=inv)
+                                 return_contribution=True, alpha_mode="sdfoam", inv_s=inv,
+                                 record_walk=use_record)
         bwd = pipe.trace_backward(pts, attrs, adj, offs, rays, start, out["rgba"], grad_rgba, q,
-                                  out["depth_indices"], depth_grad, alpha_mode="sdfoam", inv_s=inv)
+                                  out["depth_indices"], depth_grad, alpha_mode="sdfoam", inv_s=inv,
+                                  walk_record=out.get("walk_record"))
         return out, bwd
 
     log(f"warmup {args.warmup}")
@@ -179,8 +188,14 @@ def main() -> int:
     R = w.num_rays
     N = w.num_points
     E = int(w.adjacency.size)
-    bytes_fwd = R * (48 + 12 * Q) + S * (28 + 4 * D + 4) + 8 * F_st
-    bytes_bwd = R * (60 + 12 * Q) + S * (36 + 8 * D) + 8 * F_st
+    if use_record:
+        # the forward also writes 8 B per step; the backward reads them
+        # instead of the stepped cells' face rows
+        bytes_fwd = R * (48 + 12 * Q) + S * (28 + 4 * D + 4 + 8) + 8 * F_st
+        bytes_bwd = R * (60 + 12 * Q) + S * (36 + 8 * D + 8)
+    else:
+        bytes_fwd = R * (48 + 12 * Q) + S * (28 + 4 * D + 4) + 8 * F_st
+        bytes_bwd = R * (60 + 12 * Q) + S * (36 + 8 * D) + 8 * F_st
     bytes_pre = 12 * E + 16 * N
     bytes_step = bytes_fwd + bytes_bwd + 2 * bytes_pre
 
@@ -189,7 +204,8 @@ def main() -> int:
     achieved = kernel_bytes[dominant] / (avg[dominant] * 1e-3) / 1e9
 
     traffic = None
-    prof = os.path.join(ROOT, "profiles", f"traffic_{dominant}_C{args.config}.json")
+    variant = "" if use_record else "_scan"
+    prof = os.path.join(ROOT, "profiles", f"traffic_{dominant}{variant}_C{args.config}.json")
     if os.path.exists(prof):
         with open(prof) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
@@ -210,7 +226,8 @@ def main() -> int:
         "config": {
             "workload": f"C{args.config}: {N} points, SH degree {w.sh_degree}, sdfoam alpha, "
                         f"inv_s={w.inv_s:.4f}, {w.rays.shape[1]}x{w.rays.shape[0]} rays, Q={Q}, "
-                        "trace_forward(contribution, depth) + trace_backward",
+                        "trace_forward(contribution, depth) + trace_backward"
+                        + (" replaying the forward's walk record" if use_record else ""),
             "points": N,
             "adjacency": E,
             "rays": R,

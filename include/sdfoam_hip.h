@@ -124,6 +124,50 @@ int sdf_trace_backward(int sh_degree, const sdf_trace_settings *settings,
                        float *sharpness_grad, void *scratch,
                        size_t scratch_bytes, void *stream);
 
+/* ---- walk record (no counterpart in the reference) --------------------- *
+ * The forward of an sdfoam-mode trace can record each ray's steps (next
+ * cell and exit distance, 8 bytes a step, `budget` steps per wavefront of
+ * 64 rays); the backward over the same rays, start points, scene and
+ * settings then reads the steps instead of scanning the cell faces again.
+ * Results are identical with and without the record.  A standard-mode
+ * trace ignores it.  entries == NULL means no record.  Rays past `budget`
+ * trips, or that walk further in the backward, scan as usual. */
+typedef struct sdf_walk_record {
+    void *entries;  /* device memory, 8-byte aligned */
+    size_t bytes;   /* >= sdf_walk_record_bytes(num_rays, ray_image_width, budget) */
+    uint32_t budget;
+} sdf_walk_record;
+
+size_t sdf_walk_record_bytes(uint32_t num_rays, uint32_t ray_image_width,
+                             uint32_t budget);
+
+/* sdf_trace_forward that also writes the walk record. */
+int sdf_trace_forward_recorded(
+    const sdf_walk_record *record, int sh_degree,
+    const sdf_trace_settings *settings, uint32_t num_points,
+    const float *points, const float *attributes, uint32_t adjacency_size,
+    const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
+    uint32_t num_rays, const float *rays, const uint32_t *start_point_index,
+    uint32_t num_depth_quantiles, const float *depth_quantiles,
+    float *ray_rgba, float *quantile_depths, uint32_t *quantile_point_indices,
+    uint32_t *num_intersections, float *point_contribution,
+    const float *sharpness, float *alpha_output, void *scratch,
+    size_t scratch_bytes, void *stream);
+
+/* sdf_trace_backward that replays the forward's walk record. */
+int sdf_trace_backward_recorded(
+    const sdf_walk_record *record, int sh_degree,
+    const sdf_trace_settings *settings, uint32_t num_points,
+    const float *points, const float *attributes, uint32_t adjacency_size,
+    const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
+    uint32_t num_rays, const float *rays, const uint32_t *start_point_index,
+    uint32_t num_depth_quantiles, const float *depth_quantiles,
+    const uint32_t *quantile_point_indices, const float *ray_rgba,
+    const float *ray_rgba_grad, const float *depth_grad,
+    const float *ray_error, float *points_grad, float *attribute_grad,
+    float *point_error, const float *sharpness, float *sharpness_grad,
+    void *scratch, size_t scratch_bytes, void *stream);
+
 /* Implicit AABB tree over consecutive point pairs, tree [pow2(N), 2, 3]
  * (node (d, i) at 2^td - 2^(d+1) + i; the last entry is zeroed).
  * Replaces build_aabb_tree (src/aabb_tree/aabb_tree.h:10-13,

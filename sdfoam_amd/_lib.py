@@ -24,6 +24,9 @@ EXPORTS = (
     "sdf_prefetch_adjacent_diff",
     "sdf_trace_forward",
     "sdf_trace_backward",
+    "sdf_walk_record_bytes",
+    "sdf_trace_forward_recorded",
+    "sdf_trace_backward_recorded",
     "sdf_build_aabb_tree",
     "sdf_nn",
     "sdf_trace_walk_stats",
@@ -45,6 +48,16 @@ class TraceSettings(C.Structure):
         ("alpha_mode", C.c_uint32),
         ("sdf_channel", C.c_int32),
         ("ray_image_width", C.c_uint32),
+    ]
+
+
+class WalkRecordDesc(C.Structure):
+    """sdf_walk_record: device buffer of the forward's walk steps."""
+
+    _fields_ = [
+        ("entries", C.c_void_p),
+        ("bytes", C.c_size_t),
+        ("budget", C.c_uint32),
     ]
 
 
@@ -88,6 +101,12 @@ def lib() -> C.CDLL:
     L.sdf_trace_backward.argtypes = [
         C.c_int, C.POINTER(TraceSettings), U32, P, P, U32, P, P, U32, P, P, U32, P, P,
         P, P, P, P, P, P, P, P, P, P, SZ, P]
+    L.sdf_walk_record_bytes.restype = SZ
+    L.sdf_walk_record_bytes.argtypes = [U32, U32, U32]
+    L.sdf_trace_forward_recorded.restype = C.c_int
+    L.sdf_trace_forward_recorded.argtypes = [C.POINTER(WalkRecordDesc)] + L.sdf_trace_forward.argtypes
+    L.sdf_trace_backward_recorded.restype = C.c_int
+    L.sdf_trace_backward_recorded.argtypes = [C.POINTER(WalkRecordDesc)] + L.sdf_trace_backward.argtypes
     L.sdf_build_aabb_tree.restype = C.c_int
     L.sdf_build_aabb_tree.argtypes = [P, U32, P, P]
     L.sdf_nn.restype = C.c_int

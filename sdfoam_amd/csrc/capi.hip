@@ -100,6 +100,145 @@ SceneView make_scene(uint32_t num_points, const float *points, const float *attr
     return sc;
 }
 
+// record == NULL or record->entries == NULL: no record.  Otherwise it
+// must hold sdf_walk_record_bytes(num_rays, ray_image_width, budget) bytes.
+int check_record(const sdf_walk_record *record, uint32_t num_rays, uint32_t ray_image_width,
+                 WalkRecordArgs &out) {
+    out.entries = nullptr;
+    out.budget = 0;
+    if (!record || !record->entries) return SDF_OK;
+    if (record->budget == 0) return fail(SDF_E_INVALID, "walk record budget must be positive");
+    const uint64_t need =
+        walk_record_entries(num_ray_tiles(num_rays, ray_image_width), record->budget) * 8u;
+    if (record->bytes < need)
+        return fail(SDF_E_INVALID, "walk record must hold %llu bytes (got %zu)",
+                    (unsigned long long)need, record->bytes);
+    if ((reinterpret_cast<uintptr_t>(record->entries) & 7u) != 0)
+        return fail(SDF_E_INVALID, "walk record must be 8-byte aligned");
+    out.entries = static_cast<uint2 *>(record->entries);
+    out.budget = record->budget;
+    return SDF_OK;
+}
+
+int trace_forward_impl(const sdf_walk_record *record, int sh_degree,
+                       const sdf_trace_settings *settings, uint32_t num_points,
+                       const float *points, const float *attributes, uint32_t adjacency_size,
+                       const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
+                       uint32_t num_rays, const float *rays, const uint32_t *start_point_index,
+                       uint32_t num_depth_quantiles, const float *depth_quantiles,
+                       float *ray_rgba, float *quantile_depths,
+                       uint32_t *quantile_point_indices, uint32_t *num_intersections,
+                       float *point_contribution, const float *sharpness, float *alpha_output,
+                       void *scratch, size_t scratch_bytes, void *stream) {
+    int rc = check_scene(sh_degree, settings, num_points, points, attributes, adjacency_size,
+                         point_adjacency, point_adjacency_offsets, num_rays, rays,
+                         start_point_index, sharpness, scratch, scratch_bytes);
+    if (rc != SDF_OK) return rc;
+    if (num_rays > 0 && !ray_rgba) return fail(SDF_E_INVALID, "ray_rgba must not be NULL");
+    if (num_depth_quantiles > 0 && (!depth_quantiles || !quantile_depths || !quantile_point_indices))
+        return fail(SDF_E_INVALID, "depth buffers must not be NULL when num_depth_quantiles > 0");
+    if ((reinterpret_cast<uintptr_t>(ray_rgba) & 15u) != 0)
+        return fail(SDF_E_INVALID, "ray_rgba must be 16-byte aligned");
+    WalkRecordArgs rec = {};
+    rc = check_record(record, num_rays, settings->ray_image_width, rec);
+    if (rc != SDF_OK) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    tbegin(SDF_KERNEL_PREFETCH, s);
+    hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
+                                        point_adjacency_offsets, static_cast<uint2 *>(scratch), s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
+    if (num_rays == 0) return SDF_OK;
+    FwdArgs a = {};
+    a.record = rec;
+    a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
+                         point_adjacency_offsets, scratch);
+    a.settings = *settings;
+    a.rays = rays;
+    a.num_rays = num_rays;
+    a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
+    a.start = start_point_index;
+    a.num_quantiles = num_depth_quantiles;
+    a.quantiles = num_depth_quantiles ? depth_quantiles : nullptr;
+    a.sharpness = sharpness;
+    a.rgba = ray_rgba;
+    a.depth = quantile_depths;
+    a.depth_indices = quantile_point_indices;
+    a.num_intersections = num_intersections;
+    a.contribution = point_contribution;
+    a.alpha_out = alpha_output;
+    tbegin(SDF_KERNEL_FORWARD, s);
+    e = launch_forward(sh_degree, a, settings->alpha_mode == SDF_ALPHA_NEUS, false, s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "forward");
+    return SDF_OK;
+}
+
+int trace_backward_impl(const sdf_walk_record *record, int sh_degree,
+                        const sdf_trace_settings *settings, uint32_t num_points,
+                        const float *points, const float *attributes, uint32_t adjacency_size,
+                        const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
+                        uint32_t num_rays, const float *rays, const uint32_t *start_point_index,
+                        uint32_t num_depth_quantiles, const float *depth_quantiles,
+                        const uint32_t *quantile_point_indices, const float *ray_rgba,
+                        const float *ray_rgba_grad, const float *depth_grad,
+                        const float *ray_error, float *points_grad, float *attribute_grad,
+                        float *point_error, const float *sharpness, float *sharpness_grad,
+                        void *scratch, size_t scratch_bytes, void *stream) {
+    int rc = check_scene(sh_degree, settings, num_points, points, attributes, adjacency_size,
+                         point_adjacency, point_adjacency_offsets, num_rays, rays,
+                         start_point_index, sharpness, scratch, scratch_bytes);
+    if (rc != SDF_OK) return rc;
+    const bool neus = settings->alpha_mode == SDF_ALPHA_NEUS;
+    if (!points_grad || !attribute_grad)
+        return fail(SDF_E_INVALID, "points_grad and attribute_grad must not be NULL");
+    if (num_rays > 0 && (!ray_rgba || !ray_rgba_grad))
+        return fail(SDF_E_INVALID, "ray_rgba and ray_rgba_grad must not be NULL");
+    if (num_depth_quantiles > 0 && (!depth_quantiles || !depth_grad))
+        return fail(SDF_E_INVALID, "depth_grad must be provided if depth_quantiles is provided");
+    if (!neus && num_depth_quantiles > 0 && !quantile_point_indices)
+        return fail(SDF_E_INVALID, "depth_indices must be provided in standard mode");
+    if (((reinterpret_cast<uintptr_t>(ray_rgba) | reinterpret_cast<uintptr_t>(ray_rgba_grad)) &
+         15u) != 0)
+        return fail(SDF_E_INVALID, "ray_rgba and ray_rgba_grad must be 16-byte aligned");
+    WalkRecordArgs rec = {};
+    rc = check_record(record, num_rays, settings->ray_image_width, rec);
+    if (rc != SDF_OK) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    tbegin(SDF_KERNEL_PREFETCH, s);
+    hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
+                                        point_adjacency_offsets, static_cast<uint2 *>(scratch), s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
+    if (num_rays == 0) return SDF_OK;
+    BwdArgs a = {};
+    a.record = rec;
+    a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
+                         point_adjacency_offsets, scratch);
+    a.settings = *settings;
+    a.rays = rays;
+    a.num_rays = num_rays;
+    a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
+    a.start = start_point_index;
+    a.num_quantiles = num_depth_quantiles;
+    a.quantiles = num_depth_quantiles ? depth_quantiles : nullptr;
+    a.depth_indices = quantile_point_indices;
+    a.rgba = ray_rgba;
+    a.rgba_grad = ray_rgba_grad;
+    a.depth_grad = num_depth_quantiles ? depth_grad : nullptr;
+    a.ray_error = point_error ? ray_error : nullptr;
+    a.sharpness = sharpness;
+    a.points_grad = points_grad;
+    a.attr_grad = attribute_grad;
+    a.point_error = ray_error ? point_error : nullptr;
+    a.sharpness_grad = sharpness_grad;
+    tbegin(SDF_KERNEL_BACKWARD, s);
+    e = launch_backward(sh_degree, a, neus, false, s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "backward");
+    return SDF_OK;
+}
+
 } // namespace
 
 extern "C" {
@@ -145,44 +284,12 @@ int sdf_trace_forward(int sh_degree, const sdf_trace_settings *settings, uint32_
                       uint32_t *num_intersections, float *point_contribution,
                       const float *sharpness, float *alpha_output, void *scratch,
                       size_t scratch_bytes, void *stream) {
-    int rc = check_scene(sh_degree, settings, num_points, points, attributes, adjacency_size,
-                         point_adjacency, point_adjacency_offsets, num_rays, rays,
-                         start_point_index, sharpness, scratch, scratch_bytes);
-    if (rc != SDF_OK) return rc;
-    if (num_rays > 0 && !ray_rgba) return fail(SDF_E_INVALID, "ray_rgba must not be NULL");
-    if (num_depth_quantiles > 0 && (!depth_quantiles || !quantile_depths || !quantile_point_indices))
-        return fail(SDF_E_INVALID, "depth buffers must not be NULL when num_depth_quantiles > 0");
-    if ((reinterpret_cast<uintptr_t>(ray_rgba) & 15u) != 0)
-        return fail(SDF_E_INVALID, "ray_rgba must be 16-byte aligned");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    tbegin(SDF_KERNEL_PREFETCH, s);
-    hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
-                                        point_adjacency_offsets, static_cast<uint2 *>(scratch), s);
-    tend(s);
-    if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
-    if (num_rays == 0) return SDF_OK;
-    FwdArgs a = {};
-    a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
-                         point_adjacency_offsets, scratch);
-    a.settings = *settings;
-    a.rays = rays;
-    a.num_rays = num_rays;
-    a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
-    a.start = start_point_index;
-    a.num_quantiles = num_depth_quantiles;
-    a.quantiles = num_depth_quantiles ? depth_quantiles : nullptr;
-    a.sharpness = sharpness;
-    a.rgba = ray_rgba;
-    a.depth = quantile_depths;
-    a.depth_indices = quantile_point_indices;
-    a.num_intersections = num_intersections;
-    a.contribution = point_contribution;
-    a.alpha_out = alpha_output;
-    tbegin(SDF_KERNEL_FORWARD, s);
-    e = launch_forward(sh_degree, a, settings->alpha_mode == SDF_ALPHA_NEUS, false, s);
-    tend(s);
-    if (e != hipSuccess) return hip_fail(e, "forward");
-    return SDF_OK;
+    return trace_forward_impl(nullptr, sh_degree, settings, num_points, points, attributes,
+                              adjacency_size, point_adjacency, point_adjacency_offsets, num_rays,
+                              rays, start_point_index, num_depth_quantiles, depth_quantiles,
+                              ray_rgba, quantile_depths, quantile_point_indices,
+                              num_intersections, point_contribution, sharpness, alpha_output,
+                              scratch, scratch_bytes, stream);
 }
 
 int sdf_trace_backward(int sh_degree, const sdf_trace_settings *settings, uint32_t num_points,
@@ -195,54 +302,50 @@ int sdf_trace_backward(int sh_degree, const sdf_trace_settings *settings, uint32
                        const float *ray_error, float *points_grad, float *attribute_grad,
                        float *point_error, const float *sharpness, float *sharpness_grad,
                        void *scratch, size_t scratch_bytes, void *stream) {
-    int rc = check_scene(sh_degree, settings, num_points, points, attributes, adjacency_size,
-                         point_adjacency, point_adjacency_offsets, num_rays, rays,
-                         start_point_index, sharpness, scratch, scratch_bytes);
-    if (rc != SDF_OK) return rc;
-    const bool neus = settings->alpha_mode == SDF_ALPHA_NEUS;
-    if (!points_grad || !attribute_grad)
-        return fail(SDF_E_INVALID, "points_grad and attribute_grad must not be NULL");
-    if (num_rays > 0 && (!ray_rgba || !ray_rgba_grad))
-        return fail(SDF_E_INVALID, "ray_rgba and ray_rgba_grad must not be NULL");
-    if (num_depth_quantiles > 0 && (!depth_quantiles || !depth_grad))
-        return fail(SDF_E_INVALID, "depth_grad must be provided if depth_quantiles is provided");
-    if (!neus && num_depth_quantiles > 0 && !quantile_point_indices)
-        return fail(SDF_E_INVALID, "depth_indices must be provided in standard mode");
-    if (((reinterpret_cast<uintptr_t>(ray_rgba) | reinterpret_cast<uintptr_t>(ray_rgba_grad)) &
-         15u) != 0)
-        return fail(SDF_E_INVALID, "ray_rgba and ray_rgba_grad must be 16-byte aligned");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    tbegin(SDF_KERNEL_PREFETCH, s);
-    hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
-                                        point_adjacency_offsets, static_cast<uint2 *>(scratch), s);
-    tend(s);
-    if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
-    if (num_rays == 0) return SDF_OK;
-    BwdArgs a = {};
-    a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
-                         point_adjacency_offsets, scratch);
-    a.settings = *settings;
-    a.rays = rays;
-    a.num_rays = num_rays;
-    a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
-    a.start = start_point_index;
-    a.num_quantiles = num_depth_quantiles;
-    a.quantiles = num_depth_quantiles ? depth_quantiles : nullptr;
-    a.depth_indices = quantile_point_indices;
-    a.rgba = ray_rgba;
-    a.rgba_grad = ray_rgba_grad;
-    a.depth_grad = num_depth_quantiles ? depth_grad : nullptr;
-    a.ray_error = point_error ? ray_error : nullptr;
-    a.sharpness = sharpness;
-    a.points_grad = points_grad;
-    a.attr_grad = attribute_grad;
-    a.point_error = ray_error ? point_error : nullptr;
-    a.sharpness_grad = sharpness_grad;
-    tbegin(SDF_KERNEL_BACKWARD, s);
-    e = launch_backward(sh_degree, a, neus, false, s);
-    tend(s);
-    if (e != hipSuccess) return hip_fail(e, "backward");
-    return SDF_OK;
+    return trace_backward_impl(nullptr, sh_degree, settings, num_points, points, attributes,
+                               adjacency_size, point_adjacency, point_adjacency_offsets,
+                               num_rays, rays, start_point_index, num_depth_quantiles,
+                               depth_quantiles, quantile_point_indices, ray_rgba, ray_rgba_grad,
+                               depth_grad, ray_error, points_grad, attribute_grad, point_error,
+                               sharpness, sharpness_grad, scratch, scratch_bytes, stream);
+}
+
+size_t sdf_walk_record_bytes(uint32_t num_rays, uint32_t ray_image_width, uint32_t budget) {
+    return (size_t)walk_record_entries(num_ray_tiles(num_rays, ray_image_width), budget) * 8u;
+}
+
+int sdf_trace_forward_recorded(
+    const sdf_walk_record *record, int sh_degree, const sdf_trace_settings *settings,
+    uint32_t num_points, const float *points, const float *attributes, uint32_t adjacency_size,
+    const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets, uint32_t num_rays,
+    const float *rays, const uint32_t *start_point_index, uint32_t num_depth_quantiles,
+    const float *depth_quantiles, float *ray_rgba, float *quantile_depths,
+    uint32_t *quantile_point_indices, uint32_t *num_intersections, float *point_contribution,
+    const float *sharpness, float *alpha_output, void *scratch, size_t scratch_bytes,
+    void *stream) {
+    return trace_forward_impl(record, sh_degree, settings, num_points, points, attributes,
+                              adjacency_size, point_adjacency, point_adjacency_offsets, num_rays,
+                              rays, start_point_index, num_depth_quantiles, depth_quantiles,
+                              ray_rgba, quantile_depths, quantile_point_indices,
+                              num_intersections, point_contribution, sharpness, alpha_output,
+                              scratch, scratch_bytes, stream);
+}
+
+int sdf_trace_backward_recorded(
+    const sdf_walk_record *record, int sh_degree, const sdf_trace_settings *settings,
+    uint32_t num_points, const float *points, const float *attributes, uint32_t adjacency_size,
+    const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets, uint32_t num_rays,
+    const float *rays, const uint32_t *start_point_index, uint32_t num_depth_quantiles,
+    const float *depth_quantiles, const uint32_t *quantile_point_indices, const float *ray_rgba,
+    const float *ray_rgba_grad, const float *depth_grad, const float *ray_error,
+    float *points_grad, float *attribute_grad, float *point_error, const float *sharpness,
+    float *sharpness_grad, void *scratch, size_t scratch_bytes, void *stream) {
+    return trace_backward_impl(record, sh_degree, settings, num_points, points, attributes,
+                               adjacency_size, point_adjacency, point_adjacency_offsets,
+                               num_rays, rays, start_point_index, num_depth_quantiles,
+                               depth_quantiles, quantile_point_indices, ray_rgba, ray_rgba_grad,
+                               depth_grad, ray_error, points_grad, attribute_grad, point_error,
+                               sharpness, sharpness_grad, scratch, scratch_bytes, stream);
 }
 
 int sdf_build_aabb_tree(const float *points, uint32_t num_points, float *aabb_tree,
@@ -297,7 +400,7 @@ int sdf_trace_walk_stats(int sh_degree, const sdf_trace_settings *settings, int 
         a.settings = *settings;
         a.rays = rays;
         a.num_rays = num_rays;
-    a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
+        a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
         a.start = start_point_index;
         a.sharpness = sharpness;
         a.visit_hash = visit_hash;
@@ -313,7 +416,7 @@ int sdf_trace_walk_stats(int sh_degree, const sdf_trace_settings *settings, int 
         a.settings = *settings;
         a.rays = rays;
         a.num_rays = num_rays;
-    a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
+        a.num_tiles = num_ray_tiles(num_rays, settings->ray_image_width);
         a.start = start_point_index;
         a.sharpness = sharpness;
         a.visit_hash = visit_hash;

@@ -53,10 +53,14 @@ __host__ inline uint32_t grid_blocks_for_tiles(uint32_t num_tiles) {
     return kXcds * ((num_tiles + kXcds - 1) / kXcds);
 }
 
+__device__ __forceinline__ uint32_t block_tile() {
+    const uint32_t per = gridDim.x / kXcds;
+    return (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+}
+
 __device__ __forceinline__ uint32_t ray_for_lane(uint32_t num_rays, uint32_t width,
                                                  uint32_t num_tiles, bool &valid) {
-    const uint32_t per = gridDim.x / kXcds;
-    const uint32_t t = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+    const uint32_t t = block_tile();
     if (t >= num_tiles) {
         valid = false;
         return 0;

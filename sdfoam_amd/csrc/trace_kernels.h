@@ -6,7 +6,34 @@
 
 namespace sdfoam_hip {
 
+// Walk record: for every wavefront, `budget` trips of 64 entries (one per
+// lane) of {next cell, bits of t1}, with next = kNoIndex where the lane's
+// walk ended on that trip and kWalkUnrecorded where the lane was not
+// walking.  Written by the forward of the sdfoam (safe) walk, replayed by
+// its backward, which then skips the face scans; a lane scans again from
+// its first unrecorded trip (past `budget`, or where it outlives the
+// forward's walk).
+constexpr uint32_t kWalkUnrecorded = 0xfffffffeu;
+
+struct WalkRecordArgs {
+    uint2 *entries;  // NULL: no record
+    uint32_t budget; // trips recorded per wavefront
+};
+
+// entries for every block of the launch grid, the padding blocks included
+// (they write their "unrecorded" row)
+__host__ inline uint64_t walk_record_entries(uint32_t num_tiles, uint32_t budget) {
+    return (uint64_t)grid_blocks_for_tiles(num_tiles) * (kBlock / 64) * budget * 64;
+}
+
+// this lane's entry of trip 0; trip k is 64 * k entries further
+__device__ inline uint2 *walk_record_lane(const WalkRecordArgs &r, uint32_t lane) {
+    const uint64_t wave = (uint64_t)block_tile() * (kBlock / 64) + (threadIdx.x >> 6);
+    return r.entries + wave * r.budget * 64 + lane;
+}
+
 struct FwdArgs {
+    WalkRecordArgs record;
     SceneView scene;
     sdf_trace_settings settings;
     const float *rays;
@@ -32,6 +59,7 @@ struct FwdArgs {
 };
 
 struct BwdArgs {
+    WalkRecordArgs record;
     SceneView scene;
     sdf_trace_settings settings;
     const float *rays;

@@ -112,12 +112,23 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     WalkState ws;
     walk_init(a.scene, valid ? a.start[ray_idx] : kNoIndex, ws);
     WalkCounters wc = {0u, 0u, 0ull, 0ull};
+    // walk record of this wavefront (sdfoam walks only; the density
+    // backward walks differently): one row of 64 entries per trip
+    uint2 *wrec = nullptr;
+    if (!STATS && NEUS && a.record.entries) wrec = walk_record_lane(a.record, lane);
+    uint32_t trip = 0;
 
     while (__ballot(ws.alive) != 0ull) {
         StepInfo si;
         si.stepped = false;
         si.found = false;
-        if (ws.alive) walk_advance<true, STATS>(a.scene, ray, max_steps, ws, si, wc);
+        uint2 entry = make_uint2(kWalkUnrecorded, 0u);
+        if (ws.alive) {
+            walk_advance<true, STATS>(a.scene, ray, max_steps, ws, si, wc);
+            entry = make_uint2(si.found ? si.next : kNoIndex, __builtin_bit_cast(uint32_t, si.t1));
+        }
+        if (wrec && trip < a.record.budget) wrec[(uint64_t)trip * 64] = entry;
+        ++trip;
 
         float alpha = 0.0f, w = 0.0f;
         bool keep = true;
@@ -197,6 +208,8 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         if (si.stepped && !keep) ws.alive = false;
         if (ws.alive && si.found) walk_move(ws, si);
     }
+    // a backward lane that outlives this wave's walk reads "unrecorded"
+    if (wrec && trip < a.record.budget) wrec[(uint64_t)trip * 64] = make_uint2(kWalkUnrecorded, 0u);
 
     if (!valid) return;
     if constexpr (STATS) {
@@ -436,12 +449,38 @@ backward_sdf_kernel(BwdArgs a) {
     WalkState ws;
     walk_init(a.scene, valid ? a.start[ray_idx] : kNoIndex, ws);
     WalkCounters wc = {0u, 0u, 0ull, 0ull};
+    // replay of the forward's walk record: while this lane's entries are
+    // recorded, the step is read instead of scanned; from the first
+    // unrecorded (or out-of-range) entry on, the lane scans.
+    const uint2 *wrec = nullptr;
+    if (!STATS && a.record.entries) wrec = walk_record_lane(a.record, lane);
+    uint32_t trip = 0;
 
     while (__ballot(ws.alive) != 0ull) {
         StepInfo si;
         si.stepped = false;
         si.found = false;
-        if (ws.alive) walk_advance<true, STATS>(a.scene, ray, a.settings.max_intersections, ws, si, wc);
+        if (ws.alive) {
+            uint2 e = make_uint2(kWalkUnrecorded, 0u);
+            if (wrec && trip < a.record.budget) e = wrec[(uint64_t)trip * 64];
+            if (e.x == kNoIndex) {
+                ++ws.n;
+                ws.alive = false;
+            } else if (e.x < a.scene.num_points) {
+                ++ws.n;
+                si.found = true;
+                si.next = e.x;
+                si.t1 = __builtin_bit_cast(float, e.y);
+                si.xn[0] = a.scene.points[3ull * e.x];
+                si.xn[1] = a.scene.points[3ull * e.x + 1];
+                si.xn[2] = a.scene.points[3ull * e.x + 2];
+                si.stepped = si.t1 > ws.t0;
+            } else {
+                wrec = nullptr;
+                walk_advance<true, STATS>(a.scene, ray, a.settings.max_intersections, ws, si, wc);
+            }
+        }
+        ++trip;
 
         bool keep = true;
         float dr = 0.0f, dg = 0.0f, db = 0.0f, dsdf = 0.0f, pe = 0.0f;

@@ -92,6 +92,49 @@ def _inv_s_to_tensor(inv_s, like: torch.Tensor) -> torch.Tensor:
     return s
 
 
+
+DEFAULT_WALK_BUDGET = 512
+
+
+class WalkRecord:
+    """Device buffer of a forward trace's walk steps (8 bytes per step and
+    ray, ``budget`` trips per wavefront of 64 rays; sdf_walk_record in the C
+    ABI).  Valid for a backward over the same rays, start points, scene and
+    settings; the tracer checks the ray count, image width and walk limit."""
+
+    def __init__(self, entries: torch.Tensor, nbytes: int, budget: int, num_rays: int,
+                 ray_image_width: int, max_intersections: int):
+        self.entries = entries
+        self.nbytes = nbytes
+        self.budget = budget
+        self.num_rays = num_rays
+        self.ray_image_width = ray_image_width
+        self.max_intersections = max_intersections
+
+    @classmethod
+    def allocate(cls, num_rays: int, settings, budget, device) -> "WalkRecord":
+        if budget is None:
+            # a wavefront walks at most max_intersections + 1 trips, plus the
+            # terminating row
+            budget = min(int(settings.max_intersections) + 2, DEFAULT_WALK_BUDGET)
+        budget = int(budget)
+        if budget <= 0:
+            raise RuntimeError("walk_budget must be positive")
+        nbytes = int(_lib.lib().sdf_walk_record_bytes(num_rays, settings.ray_image_width, budget))
+        entries = torch.empty(max(1, nbytes // 8), dtype=torch.int64, device=device)
+        return cls(entries, nbytes, budget, num_rays, int(settings.ray_image_width),
+                   int(settings.max_intersections))
+
+    def desc(self):
+        return _lib.WalkRecordDesc(self.entries.data_ptr(), self.nbytes, self.budget)
+
+    def check_matches(self, num_rays: int, settings, device) -> None:
+        if (num_rays != self.num_rays or int(settings.ray_image_width) != self.ray_image_width
+                or int(settings.max_intersections) != self.max_intersections
+                or self.entries.device != torch.device(device)):
+            raise RuntimeError("walk_record does not belong to these rays and settings")
+
+
 class Pipeline:
     """A tracing pipeline for one SH degree and attribute dtype
     (src/tracing/pipeline.h:79-161)."""
@@ -194,7 +237,13 @@ class Pipeline:
     def trace_forward(self, points, attributes, point_adjacency, point_adjacency_offsets, rays,
                       start_point, depth_quantiles=None, weight_threshold=None,
                       max_intersections=None, return_contribution=False, alpha_mode=None,
-                      inv_s=None, eps=None, sdf_channel=None):
+                      inv_s=None, eps=None, sdf_channel=None, record_walk=False,
+                      walk_budget=None):
+        """Reference arguments and outputs, plus (no counterpart in the
+        reference): ``record_walk=True`` in sdfoam mode also returns
+        ``"walk_record"``, the rays' steps, which ``trace_backward`` over the
+        same rays and settings takes as ``walk_record=`` to skip its face
+        scans.  ``walk_budget`` bounds the recorded trips per wavefront."""
         points_c = points.contiguous()
         attributes_c = attributes.contiguous()
         adj_c = point_adjacency.contiguous()
@@ -235,12 +284,19 @@ class Pipeline:
             didx = torch.zeros(lead + (num_q,), dtype=torch.uint32, device=dev)
         alpha = torch.zeros((num_points, 1), dtype=torch.float32, device=dev)
         scratch, nbytes = self._scratch(num_points, num_adj, dev)
+        record = None
+        if record_walk and settings.alpha_mode == _lib.SDF_ALPHA_NEUS:
+            record = WalkRecord.allocate(num_rays, settings, walk_budget, dev)
+        args = (
+            self._sh_degree, C.byref(settings), num_points, ptr(points_c), ptr(attributes_c),
+            num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c), ptr(start_c), num_q,
+            ptr(dq), ptr(rgba), ptr(depth), ptr(didx), ptr(nisect), ptr(contribution),
+            ptr(sharpness), ptr(alpha), ptr(scratch), nbytes, _lib.stream_handle(dev))
         with torch.cuda.device(dev):
-            check(_lib.lib().sdf_trace_forward(
-                self._sh_degree, C.byref(settings), num_points, ptr(points_c), ptr(attributes_c),
-                num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c), ptr(start_c), num_q,
-                ptr(dq), ptr(rgba), ptr(depth), ptr(didx), ptr(nisect), ptr(contribution),
-                ptr(sharpness), ptr(alpha), ptr(scratch), nbytes, _lib.stream_handle(dev)))
+            if record is None:
+                check(_lib.lib().sdf_trace_forward(*args))
+            else:
+                check(_lib.lib().sdf_trace_forward_recorded(C.byref(record.desc()), *args))
         out = {"rgba": rgba}
         if return_depth:
             out["depth"] = depth
@@ -249,6 +305,8 @@ class Pipeline:
             out["contribution"] = contribution
         out["num_intersections"] = nisect
         out["alpha"] = alpha
+        if record is not None:
+            out["walk_record"] = record
         return out
 
     # -- trace_backward (torch_bindings/pipeline_bindings.cpp:336-607) ------
@@ -256,7 +314,7 @@ class Pipeline:
                        start_point, rgb_out, grad_in, depth_quantiles=None, depth_indices=None,
                        depth_grad_in=None, ray_error=None, weight_threshold=None,
                        max_intersections=None, alpha_mode=None, inv_s=None, eps=None,
-                       sdf_channel=None):
+                       sdf_channel=None, walk_record=None):
         points_c = points.contiguous()
         attributes_c = attributes.contiguous()
         adj_c = point_adjacency.contiguous()
@@ -346,13 +404,19 @@ class Pipeline:
         ray_grad = torch.zeros_like(rays_c)
         sharpness_grad = torch.zeros_like(sharpness, dtype=torch.float32)
         scratch, nbytes = self._scratch(num_points, num_adj, dev)
+        if walk_record is not None:
+            walk_record.check_matches(num_rays, settings, dev)
+        args = (
+            self._sh_degree, C.byref(settings), num_points, ptr(points_c), ptr(attributes_c),
+            num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c), ptr(start_c), num_q,
+            ptr(dq), ptr(didx), ptr(rgba), ptr(g), ptr(dgrad), ptr(rerr), ptr(points_grad),
+            ptr(attr_grad), ptr(point_error), ptr(sharpness), ptr(sharpness_grad),
+            ptr(scratch), nbytes, _lib.stream_handle(dev))
         with torch.cuda.device(dev):
-            check(_lib.lib().sdf_trace_backward(
-                self._sh_degree, C.byref(settings), num_points, ptr(points_c), ptr(attributes_c),
-                num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c), ptr(start_c), num_q,
-                ptr(dq), ptr(didx), ptr(rgba), ptr(g), ptr(dgrad), ptr(rerr), ptr(points_grad),
-                ptr(attr_grad), ptr(point_error), ptr(sharpness), ptr(sharpness_grad),
-                ptr(scratch), nbytes, _lib.stream_handle(dev)))
+            if walk_record is None:
+                check(_lib.lib().sdf_trace_backward(*args))
+            else:
+                check(_lib.lib().sdf_trace_backward_recorded(C.byref(walk_record.desc()), *args))
         out = {
             "points_grad": points_grad,
             "attr_grad": attr_grad,

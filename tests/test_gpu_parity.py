@@ -241,7 +241,11 @@ def test_forward_parity_c2_sharp(torch_dev, oracle_lib):
     _check_forward(out, st, ref, w, 0)
 
 
-def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False):
+def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False, walk=False,
+                   walk_budget=None):
+    """GPU forward + backward (with walk=True: the backward replays the
+    forward's walk record, `walk_budget` trips per wavefront) and the
+    oracle's backward on the same inputs."""
     import torch
 
     import sdfoam_amd
@@ -251,7 +255,10 @@ def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False):
     pipe = sdfoam_amd.create_pipeline(w.sh_degree)
     q = to_dev(w.quantiles, dev)
     inv_t = torch.tensor([inv], device=dev)
-    fwd = pipe.trace_forward(**g, depth_quantiles=q, alpha_mode=mode, inv_s=inv_t)
+    fwd = pipe.trace_forward(**g, depth_quantiles=q, alpha_mode=mode, inv_s=inv_t,
+                             record_walk=walk, walk_budget=walk_budget)
+    if walk and mode == "sdfoam":
+        assert fwd["walk_record"].budget == (walk_budget or min(1024 + 2, 512))
     rerr = None
     if ray_error:
         rerr_np = np.random.default_rng(11).uniform(0, 1, w.rays.shape[:-1]).astype(np.float32)
@@ -259,7 +266,8 @@ def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False):
     bwd = pipe.trace_backward(**g, rgb_out=fwd["rgba"], grad_in=to_dev(w.grad_rgba, dev),
                               depth_quantiles=q, depth_indices=fwd["depth_indices"],
                               depth_grad_in=to_dev(w.depth_grad, dev), ray_error=rerr,
-                              alpha_mode=mode, inv_s=inv_t)
+                              alpha_mode=mode, inv_s=inv_t,
+                              walk_record=fwd.get("walk_record"))
     st = pipe.walk_stats(**g, backward=True, alpha_mode=mode, inv_s=inv_t)
     torch.cuda.synchronize()
     rgba = fwd["rgba"].cpu().numpy()
@@ -302,6 +310,53 @@ def test_backward_parity_c2(torch_dev, oracle_lib):
     w = scene(2)
     bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "sdfoam")
     _check_backward(bwd, st, ref, w)
+
+
+@pytest.mark.parametrize("budget", [None, 2, 7])
+def test_backward_walk_record_c1(torch_dev, oracle_lib, budget):
+    """Backward replaying the forward's walk record: full record, and budgets
+    so small that every wavefront goes back to scanning mid-walk."""
+    w = scene(1)
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "sdfoam", ray_error=True, walk=True,
+                                  walk_budget=budget)
+    _check_backward(bwd, st, ref, w)
+
+
+def test_backward_walk_record_c2(torch_dev, oracle_lib):
+    w = scene(2)
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "sdfoam", walk=True)
+    _check_backward(bwd, st, ref, w)
+
+
+def test_backward_walk_record_c2_sharp(torch_dev, oracle_lib):
+    """inv_s = 50: walks end on the weight threshold, lanes of a wavefront
+    stop at different trips."""
+    w = scene(2)
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "sdfoam", inv_s=50.0, walk=True)
+    _check_backward(bwd, st, ref, w)
+
+
+def test_walk_record_standard_mode_ignored(torch_dev, oracle_lib):
+    """Standard mode records nothing; its backward runs as without a record."""
+    w = scene(1, mode="standard")
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "standard", walk=True)
+    _check_backward(bwd, st, ref, w)
+
+
+def test_walk_record_mismatch_raises(torch_dev):
+    import torch
+
+    import sdfoam_amd
+
+    w = scene(1)
+    g = gpu_scene(w, torch_dev)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    inv_t = torch.tensor([w.inv_s], device=torch_dev)
+    fwd = pipe.trace_forward(**g, alpha_mode="sdfoam", inv_s=inv_t, record_walk=True)
+    with pytest.raises(RuntimeError, match="walk_record does not belong"):
+        pipe.trace_backward(**g, rgb_out=fwd["rgba"], grad_in=to_dev(w.grad_rgba, torch_dev),
+                            alpha_mode="sdfoam", inv_s=inv_t, max_intersections=100,
+                            walk_record=fwd["walk_record"])
 
 
 def test_aabb_tree_and_nn_exact(torch_dev, oracle_lib):
