@@ -124,6 +124,49 @@ int sdf_trace_backward(int sh_degree, const sdf_trace_settings *settings,
                        float *sharpness_grad, void *scratch,
                        size_t scratch_bytes, void *stream);
 
+/* Camera of the inference render (src/tracing/camera.h:17-27). */
+#define SDF_CAMERA_PINHOLE 0
+#define SDF_CAMERA_FISHEYE 1
+typedef struct sdf_camera {
+    float position[3];
+    float forward[3];
+    float right[3];
+    float up[3];
+    float fov; /* vertical, radians */
+    uint32_t width;
+    uint32_t height;
+    uint32_t model; /* SDF_CAMERA_* */
+} sdf_camera;
+
+/* Background of the inference render (the fields of VisualizationSettings
+ * the render reads, src/tracing/pipeline.h:50-68). */
+typedef struct sdf_visualization {
+    float bg_color[3];
+    int32_t checker_bg;
+} sdf_visualization;
+
+/* Inference render: one ray per pixel cast in the kernel, all starting in
+ * cell *start_point_index (device pointer, one element), composited as the
+ * forward and packed as RGBA8 (colour + T * background, alpha 255) into
+ * output_rgba[(height - 1 - j) * width + i].  adjacent_diff is the caller's
+ * fp16 offset table, adjacent_diff_entries >= adjacency_size rows of 4
+ * halves (as prefetch_adjacent_diff writes them).  vis NULL: white, no
+ * checker (default_visualization_settings).  settings->ray_image_width is
+ * ignored.
+ * Replaces Pipeline::trace_benchmark (src/tracing/pipeline.h:144-156,
+ * src/tracing/pipeline.cu:1067-1199, 1432-1466). */
+int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
+                        uint32_t num_points, const float *points,
+                        const float *attributes, uint32_t adjacency_size,
+                        const uint32_t *point_adjacency,
+                        const uint32_t *point_adjacency_offsets,
+                        const uint16_t *adjacent_diff,
+                        size_t adjacent_diff_entries, const sdf_camera *camera,
+                        const sdf_visualization *vis,
+                        const uint32_t *start_point_index,
+                        uint32_t *output_rgba, const float *sharpness,
+                        void *stream);
+
 /* ---- walk record (no counterpart in the reference) --------------------- *
  * The forward of an sdfoam-mode trace can record each ray's steps (next
  * cell and exit distance, 8 bytes a step, `budget` steps per wavefront of
@@ -220,6 +263,7 @@ int sdf_debug_fpmath(int op, const float *in, void *out, uint64_t n,
 #define SDF_KERNEL_BACKWARD 2
 #define SDF_KERNEL_AABB_TREE 3
 #define SDF_KERNEL_NN 4
+#define SDF_KERNEL_RENDER 5
 int sdf_set_timing(int enable);
 int sdf_timing_collect(int *kinds, float *ms, int max_n, int *n_out);
 

@@ -65,6 +65,28 @@ class _Grads(C.Structure):
     ]
 
 
+class _Camera(C.Structure):
+    _fields_ = [
+        ("position", C.c_float * 3),
+        ("forward", C.c_float * 3),
+        ("right", C.c_float * 3),
+        ("up", C.c_float * 3),
+        ("fov", C.c_float),
+        ("width", C.c_uint32),
+        ("height", C.c_uint32),
+        ("model", C.c_uint32),
+    ]
+
+
+def make_camera(cam: dict) -> _Camera:
+    """camera dict of Pipeline.trace_benchmark (position, forward, right, up,
+    fov, width, height, model 'pinhole' | 'fisheye')."""
+    model = {"pinhole": 0, "fisheye": 1}[cam.get("model", "pinhole")]
+    vec = [np.asarray(cam[k], dtype=np.float32).reshape(3) for k in ("position", "forward", "right", "up")]
+    return _Camera(*[(C.c_float * 3)(*v.tolist()) for v in vec], float(cam["fov"]),
+                   int(cam["width"]), int(cam["height"]), model)
+
+
 _lib = None
 
 
@@ -102,6 +124,18 @@ def lib():
         L.oracle_cell_intersection_grad.argtypes = [C.c_void_p] * 5
         L.oracle_build_aabb_tree.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p]
         L.oracle_nn.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p, C.c_int]
+        L.oracle_trace_benchmark.restype = C.c_int
+        L.oracle_trace_benchmark.argtypes = [
+            C.POINTER(_Settings), C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p,
+            C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(_Camera), C.c_uint32,
+            C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+        L.oracle_camera_focal.restype = C.c_float
+        L.oracle_camera_focal.argtypes = [C.c_float]
+        L.oracle_cast_ray.argtypes = [C.POINTER(_Camera), C.c_uint32, C.c_uint32, C.c_void_p]
+        L.oracle_sincosf_n.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64]
+        L.oracle_atan2f_n.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64]
+        L.oracle_make_rgba8.restype = C.c_uint32
+        L.oracle_make_rgba8.argtypes = [C.c_float] * 4
         _lib = L
     return _lib
 
@@ -312,3 +346,66 @@ def trace_backward(sh_degree, points, attributes, adjacency, offsets, rays, star
                           pga, aga, None if sga is None else float(sga[0]), pgk, agk,
                           None if sgk is None else int(sgk[0]),
                           vh.reshape(lead), steps.reshape(lead))
+
+
+def sincosf(x):
+    x = _c(x, np.float32).ravel()
+    sn = np.empty_like(x)
+    cs = np.empty_like(x)
+    lib().oracle_sincosf_n(_p(x), _p(sn), _p(cs), x.size)
+    return sn, cs
+
+
+def atan2f(y, x):
+    y = _c(y, np.float32).ravel()
+    x = _c(x, np.float32).ravel()
+    out = np.empty_like(x)
+    lib().oracle_atan2f_n(_p(y), _p(x), _p(out), x.size)
+    return out
+
+
+def make_rgba8(r, g, b, a) -> int:
+    return int(lib().oracle_make_rgba8(float(r), float(g), float(b), float(a)))
+
+
+def cast_ray(cam: dict, i: int, j: int) -> np.ndarray:
+    d = np.zeros(3, dtype=np.float32)
+    c = make_camera(cam)
+    lib().oracle_cast_ray(C.byref(c), i, j, _p(d))
+    return d
+
+
+@dataclass
+class RenderResult:
+    rgba8: np.ndarray            # [H, W] uint32, row H-1-j holds pixel row j
+    rgbt: np.ndarray             # [H*W, 4]: C, T per pixel (j * W + i); -1 where masked
+    num_intersections: np.ndarray  # [H*W]
+
+
+def trace_benchmark(sh_degree, points, attributes, adjacency, offsets, adjacent_diff, camera,
+                    start_point, *, alpha_mode="sdfoam", inv_s=1.0, weight_threshold=None,
+                    max_intersections=None, sdf_channel=None, bg_color=None, checker_bg=False,
+                    threads=1) -> RenderResult:
+    points = _c(points, np.float32)
+    attributes = _c(attributes, np.float32)
+    adjacency = _c(adjacency, np.uint32)
+    offsets = _c(offsets, np.uint32)
+    diff = _c(adjacent_diff, np.uint16).reshape(-1, 4)
+    if diff.shape[0] < adjacency.size:
+        raise ValueError("adjacent_diff must have one row per adjacency entry")
+    D = attributes.shape[-1]
+    st, _ = _settings(alpha_mode, weight_threshold, max_intersections, sdf_channel, D)
+    sharp = np.array([inv_s], dtype=np.float32).ravel()[:1] if np.ndim(inv_s) == 0 else _c(inv_s, np.float32).ravel()
+    cam = make_camera(camera)
+    W, H = cam.width, cam.height
+    out = np.zeros((H, W), dtype=np.uint32)
+    rgbt = np.zeros((H * W, 4), dtype=np.float32)
+    nis = np.zeros(H * W, dtype=np.uint32)
+    bg = None if bg_color is None else _c(bg_color, np.float32).ravel()
+    rc = lib().oracle_trace_benchmark(
+        C.byref(st), sh_degree, points.shape[0], _p(points), _p(attributes), adjacency.size,
+        _p(adjacency), _p(offsets), _p(diff), C.byref(cam), int(np.asarray(start_point).ravel()[0]),
+        _p(sharp), _p(bg), int(bool(checker_bg)), _p(out), _p(rgbt), _p(nis), threads)
+    if rc != 0:
+        raise RuntimeError("oracle_trace_benchmark failed")
+    return RenderResult(out, rgbt, nis)

@@ -524,6 +524,126 @@ int oracle_trace_forward(const oracle_settings *settings, uint32_t sh_degree,
 }
 
 /* ------------------------------------------------------------------------ */
+/* inference render (src/tracing/pipeline.cu:1067-1199, the `benchmark`      */
+/* kernel behind Pipeline::trace_benchmark)                                  */
+
+typedef struct {
+    fwd_job fj;
+    const oracle_camera *cam;
+    float focal;
+    float bg[3];
+    int checker_bg;
+    uint32_t *out;
+    float *rgbt;  /* optional [H*W, 4]: C, T per pixel, in pixel order j * W + i */
+    uint32_t *num_isect_px; /* optional [H*W] */
+} bench_job;
+
+static void bench_range(void *p, uint32_t lo, uint32_t hi) {
+    const bench_job *b = (const bench_job *)p;
+    const oracle_camera *cam = b->cam;
+    for (uint32_t px = lo; px < hi; ++px) {
+        const uint32_t i = px % cam->width, jj = px / cam->width;
+        const uint32_t out_idx = (cam->height - 1 - jj) * cam->width + i;
+        float dir[3];
+        sdf_cast_ray(cam->forward, cam->right, cam->up, cam->fov, b->focal, cam->width,
+                     cam->height, cam->model, i, jj, dir);
+        const float n = sqrtf(sdf_dot3(dir[0], dir[1], dir[2], dir[0], dir[1], dir[2]));
+        if (n < 0.1f) {
+            /* masked fisheye pixel: the settings' background colour */
+            b->out[out_idx] = sdf_make_rgba8(b->bg[0], b->bg[1], b->bg[2], 1.0f);
+            if (b->rgbt) for (int c = 0; c < 4; ++c) b->rgbt[4ull * px + c] = -1.0f;
+            if (b->num_isect_px) b->num_isect_px[px] = 0;
+            continue;
+        }
+        const float r6[6] = {cam->position[0], cam->position[1], cam->position[2],
+                             dir[0], dir[1], dir[2]};
+        const ray_t ray = load_ray(r6); /* ray.direction /= ray.direction.norm() */
+        fwd_ray r;
+        memset(&r, 0, sizeof(r));
+        r.job = &b->fj;
+        r.ray = px;
+        oracle_sh_basis(b->fj.sh_degree, ray.d[0], ray.d[1], ray.d[2], r.sh);
+        r.T = 1.0f;
+        /* the benchmark functor is the forward's step without its outputs
+         * (no alpha / contribution / quantiles: those pointers are NULL) */
+        const walk_stats st = walk(&b->fj.sc, &ray, b->fj.start[0],
+                                   b->fj.st->max_intersections, 1, fwd_step, &r);
+        float bg[3] = {b->bg[0], b->bg[1], b->bg[2]};
+        if (b->checker_bg) {
+            const int is = 2 * (int)((i / 20) % 2) - 1;
+            const int js = 2 * (int)((jj / 20) % 2) - 1;
+            const float g = (is * js > 0) ? 0.3f : 0.5f;
+            bg[0] = bg[1] = bg[2] = g;
+        }
+        float col[3];
+        for (int c = 0; c < 3; ++c) col[c] = fmaf(r.T, bg[c], r.C[c]);
+        b->out[out_idx] = sdf_make_rgba8(col[0], col[1], col[2], 1.0f);
+        if (b->rgbt) {
+            for (int c = 0; c < 3; ++c) b->rgbt[4ull * px + c] = r.C[c];
+            b->rgbt[4ull * px + 3] = r.T;
+        }
+        if (b->num_isect_px) b->num_isect_px[px] = st.n;
+    }
+}
+
+float oracle_camera_focal(float fov) { return 1.0f / tanf(fov * 0.5f); }
+
+void oracle_cast_ray(const oracle_camera *cam, uint32_t i, uint32_t j, float *dir) {
+    sdf_cast_ray(cam->forward, cam->right, cam->up, cam->fov, oracle_camera_focal(cam->fov),
+                 cam->width, cam->height, cam->model, i, j, dir);
+}
+
+void oracle_sincosf_n(const float *x, float *s, float *c, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) sdf_sincosf(x[i], &s[i], &c[i]);
+}
+
+void oracle_atan2f_n(const float *y, const float *x, float *out, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = sdf_atan2f(y[i], x[i]);
+}
+
+uint32_t oracle_make_rgba8(float r, float g, float b, float a) {
+    return sdf_make_rgba8(r, g, b, a);
+}
+
+int oracle_trace_benchmark(const oracle_settings *settings, uint32_t sh_degree,
+                           uint32_t num_points, const float *points,
+                           const float *attributes, uint32_t adjacency_size,
+                           const uint32_t *adjacency, const uint32_t *offsets,
+                           const uint16_t *adjacent_diff, const oracle_camera *camera,
+                           uint32_t start_point, const float *sharpness,
+                           const float *bg_color, int checker_bg, uint32_t *output_rgba,
+                           float *rgbt, uint32_t *num_intersections, int num_threads) {
+    if (sh_degree > 3 || !settings || !camera || !output_rgba || !adjacent_diff) return -1;
+    if (camera->width == 0 || camera->height == 0) return -1;
+    bench_job b;
+    memset(&b, 0, sizeof(b));
+    fwd_job *j = &b.fj;
+    j->st = settings;
+    j->sh_degree = sh_degree;
+    j->nsh = (sh_degree + 1) * (sh_degree + 1);
+    j->D = 1 + 3 * j->nsh;
+    j->sc.points = points;
+    j->sc.adjacency = adjacency;
+    j->sc.offsets = offsets;
+    j->sc.num_points = num_points;
+    j->sc.adjacency_size = adjacency_size;
+    j->sc.diff = adjacent_diff;
+    j->attributes = attributes;
+    j->start = &start_point;
+    j->sharp = sharpness ? sharpness[0] : 1.0f;
+    b.cam = camera;
+    b.focal = oracle_camera_focal(camera->fov);
+    /* default_visualization_settings (src/tracing/pipeline.h:59-68): white */
+    for (int c = 0; c < 3; ++c) b.bg[c] = bg_color ? bg_color[c] : 1.0f;
+    b.checker_bg = checker_bg;
+    b.out = output_rgba;
+    b.rgbt = rgbt;
+    b.num_isect_px = num_intersections;
+    run_rays(bench_range, &b, camera->width * camera->height, num_threads);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* backward                                                                  */
 
 /* cell_intersection_grad (src/tracing/tracing_utils.cuh:112-124):

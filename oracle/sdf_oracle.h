@@ -92,6 +92,39 @@ int oracle_trace_forward(const oracle_settings *settings, uint32_t sh_degree,
                          float *alpha_out, oracle_visits *visits,
                          int num_threads);
 
+/* Camera of Pipeline::trace_benchmark (src/tracing/camera.h:17-27); model
+ * 0 = pinhole, 1 = fisheye. */
+typedef struct {
+    float position[3];
+    float forward[3];
+    float right[3];
+    float up[3];
+    float fov;
+    uint32_t width;
+    uint32_t height;
+    uint32_t model;
+} oracle_camera;
+
+/* Inference render (src/tracing/pipeline.cu:1067-1199): one ray per pixel
+ * cast in-kernel (src/tracing/camera.h:56-85), one start cell for all,
+ * the forward's compositing, colour + T * background packed as RGBA8 into
+ * row (height - 1 - j).  adjacent_diff is the caller's fp16 offset table
+ * [E, 4].  bg_color NULL = white.  rgbt (optional, [H*W, 4], pixel order
+ * j * W + i) receives C and T; num_intersections (optional) the loop count. */
+int oracle_trace_benchmark(const oracle_settings *settings, uint32_t sh_degree,
+                           uint32_t num_points, const float *points,
+                           const float *attributes, uint32_t adjacency_size,
+                           const uint32_t *adjacency, const uint32_t *offsets,
+                           const uint16_t *adjacent_diff, const oracle_camera *camera,
+                           uint32_t start_point, const float *sharpness,
+                           const float *bg_color, int checker_bg, uint32_t *output_rgba,
+                           float *rgbt, uint32_t *num_intersections, int num_threads);
+float oracle_camera_focal(float fov);
+void oracle_cast_ray(const oracle_camera *cam, uint32_t i, uint32_t j, float *dir);
+void oracle_sincosf_n(const float *x, float *s, float *c, uint64_t n);
+void oracle_atan2f_n(const float *y, const float *x, float *out, uint64_t n);
+uint32_t oracle_make_rgba8(float r, float g, float b, float a);
+
 /* Gradient buffers of the backward pass.  Any of the *_abs / *_k buffers may
  * be NULL. */
 typedef struct {

@@ -24,6 +24,7 @@ EXPORTS = (
     "sdf_prefetch_adjacent_diff",
     "sdf_trace_forward",
     "sdf_trace_backward",
+    "sdf_trace_benchmark",
     "sdf_walk_record_bytes",
     "sdf_trace_forward_recorded",
     "sdf_trace_backward_recorded",
@@ -35,7 +36,11 @@ EXPORTS = (
     "sdf_timing_collect",
 )
 
-KERNEL_NAMES = {0: "prefetch_adjacent_diff", 1: "forward", 2: "backward", 3: "build_aabb_tree", 4: "nn"}
+KERNEL_NAMES = {0: "prefetch_adjacent_diff", 1: "forward", 2: "backward", 3: "build_aabb_tree", 4: "nn",
+                5: "render"}
+
+SDF_CAMERA_PINHOLE = 0
+SDF_CAMERA_FISHEYE = 1
 
 
 class TraceSettings(C.Structure):
@@ -49,6 +54,27 @@ class TraceSettings(C.Structure):
         ("sdf_channel", C.c_int32),
         ("ray_image_width", C.c_uint32),
     ]
+
+
+class Camera(C.Structure):
+    """sdf_camera (src/tracing/camera.h:17-27)."""
+
+    _fields_ = [
+        ("position", C.c_float * 3),
+        ("forward", C.c_float * 3),
+        ("right", C.c_float * 3),
+        ("up", C.c_float * 3),
+        ("fov", C.c_float),
+        ("width", C.c_uint32),
+        ("height", C.c_uint32),
+        ("model", C.c_uint32),
+    ]
+
+
+class Visualization(C.Structure):
+    """sdf_visualization (src/tracing/pipeline.h:50-68)."""
+
+    _fields_ = [("bg_color", C.c_float * 3), ("checker_bg", C.c_int32)]
 
 
 class WalkRecordDesc(C.Structure):
@@ -101,6 +127,10 @@ def lib() -> C.CDLL:
     L.sdf_trace_backward.argtypes = [
         C.c_int, C.POINTER(TraceSettings), U32, P, P, U32, P, P, U32, P, P, U32, P, P,
         P, P, P, P, P, P, P, P, P, P, SZ, P]
+    L.sdf_trace_benchmark.restype = C.c_int
+    L.sdf_trace_benchmark.argtypes = [
+        C.c_int, C.POINTER(TraceSettings), U32, P, P, U32, P, P, P, SZ, C.POINTER(Camera),
+        C.POINTER(Visualization), P, P, P, P]
     L.sdf_walk_record_bytes.restype = SZ
     L.sdf_walk_record_bytes.argtypes = [U32, U32, U32]
     L.sdf_trace_forward_recorded.restype = C.c_int

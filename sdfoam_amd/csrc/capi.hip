@@ -310,6 +310,73 @@ int sdf_trace_backward(int sh_degree, const sdf_trace_settings *settings, uint32
                                sharpness, sharpness_grad, scratch, scratch_bytes, stream);
 }
 
+int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings, uint32_t num_points,
+                        const float *points, const float *attributes, uint32_t adjacency_size,
+                        const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
+                        const uint16_t *adjacent_diff, size_t adjacent_diff_entries,
+                        const sdf_camera *camera, const sdf_visualization *vis,
+                        const uint32_t *start_point_index, uint32_t *output_rgba,
+                        const float *sharpness, void *stream) {
+    if (sh_degree < 0 || sh_degree > 3) return fail(SDF_E_INVALID, "Unsupported SH degree");
+    if (!settings) return fail(SDF_E_INVALID, "settings must not be NULL");
+    if (settings->alpha_mode != SDF_ALPHA_STANDARD && settings->alpha_mode != SDF_ALPHA_NEUS)
+        return fail(SDF_E_INVALID, "alpha_mode must be 0 (standard) or 1 (sdfoam)");
+    const int D = 1 + 3 * (sh_degree + 1) * (sh_degree + 1);
+    if (settings->sdf_channel >= D)
+        return fail(SDF_E_INVALID, "sdf_channel %d out of range for attribute dim %d",
+                    settings->sdf_channel, D);
+    if (num_points == 0) return fail(SDF_E_INVALID, "num_points must be positive");
+    if (!points || !attributes || !point_adjacency_offsets ||
+        (!point_adjacency && adjacency_size > 0))
+        return fail(SDF_E_INVALID, "scene pointers must not be NULL");
+    if (!adjacent_diff || adjacent_diff_entries < adjacency_size)
+        return fail(SDF_E_INVALID, "adjacent_diff must hold one row of 4 halves per adjacency "
+                                   "entry (%u rows, got %zu)",
+                    adjacency_size, adjacent_diff_entries);
+    if ((reinterpret_cast<uintptr_t>(adjacent_diff) & 7u) != 0)
+        return fail(SDF_E_INVALID, "adjacent_diff must be 8-byte aligned");
+    if (!camera) return fail(SDF_E_INVALID, "camera must not be NULL");
+    if (camera->model != SDF_CAMERA_PINHOLE && camera->model != SDF_CAMERA_FISHEYE)
+        return fail(SDF_E_INVALID, "Invalid camera model");
+    if (camera->width == 0 || camera->height == 0 ||
+        (uint64_t)camera->width * camera->height > 0xffffffffull)
+        return fail(SDF_E_INVALID, "camera width and height must be positive and "
+                                   "width * height < 2^32");
+    if (!start_point_index) return fail(SDF_E_INVALID, "start_point must not be NULL");
+    if (!output_rgba) return fail(SDF_E_INVALID, "output_rgba must not be NULL");
+    if (!sharpness) return fail(SDF_E_INVALID, "sharpness must not be NULL");
+
+    RenderArgs a = {};
+    a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
+                         point_adjacency_offsets, const_cast<uint16_t *>(adjacent_diff));
+    a.settings = *settings;
+    for (int k = 0; k < 3; ++k) {
+        a.position[k] = camera->position[k];
+        a.forward[k] = camera->forward[k];
+        a.right[k] = camera->right[k];
+        a.up[k] = camera->up[k];
+        // default_visualization_settings: white background
+        a.bg[k] = vis ? vis->bg_color[k] : 1.0f;
+    }
+    a.checker_bg = vis ? vis->checker_bg : 0;
+    a.fov = camera->fov;
+    // pinhole focal factor, once per launch (cast_ray evaluates it per ray)
+    a.focal = 1.0f / tanf(camera->fov * 0.5f);
+    a.width = camera->width;
+    a.height = camera->height;
+    a.model = camera->model;
+    a.num_tiles = num_ray_tiles(camera->width * camera->height, camera->width);
+    a.start = start_point_index;
+    a.sharpness = sharpness;
+    a.out = output_rgba;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    tbegin(SDF_KERNEL_RENDER, s);
+    hipError_t e = launch_render(sh_degree, a, settings->alpha_mode == SDF_ALPHA_NEUS, s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "trace_benchmark");
+    return SDF_OK;
+}
+
 size_t sdf_walk_record_bytes(uint32_t num_rays, uint32_t ray_image_width, uint32_t budget) {
     return (size_t)walk_record_entries(num_ray_tiles(num_rays, ray_image_width), budget) * 8u;
 }

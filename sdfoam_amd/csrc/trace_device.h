@@ -198,7 +198,9 @@ __device__ __forceinline__ void walk_init(const SceneView &sc, uint32_t start, W
 // UINT32_MAX for the index bounds; the real bounds are used here, which is
 // the same walk for a well-formed scene and ends it instead of reading out
 // of bounds otherwise.  Clears ws.alive when the walk ends.
-template <bool SAFE, bool COUNT>
+// GUARD: the offset table has no padding past E (a caller's table), so the
+// last batch of a row re-reads the row's last entry instead of over-reading.
+template <bool SAFE, bool COUNT, bool GUARD = false>
 __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ray,
                                              uint32_t max_steps, WalkState &ws, StepInfo &si,
                                              WalkCounters &wc) {
@@ -224,7 +226,7 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
     for (uint32_t k0 = 0; k0 < nf; k0 += 4) {
         uint2 h[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) h[u] = row[k0 + u];
+        for (int u = 0; u < 4; ++u) h[u] = row[GUARD ? min(k0 + u, nf - 1) : k0 + u];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const uint32_t k = k0 + u;

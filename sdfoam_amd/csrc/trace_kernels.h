@@ -87,6 +87,23 @@ struct BwdArgs {
     uint32_t cells_stride;
 };
 
+// Inference render (Pipeline::trace_benchmark): rays cast per pixel.
+struct RenderArgs {
+    SceneView scene; // diff: the caller's table, no padding
+    sdf_trace_settings settings;
+    float position[3], forward[3], right[3], up[3];
+    float fov, focal; // focal = 1 / tan(fov / 2)
+    uint32_t width, height, model;
+    uint32_t num_tiles; // num_ray_tiles(width * height, width)
+    float bg[3];
+    int32_t checker_bg;
+    const uint32_t *start; // one element
+    const float *sharpness;
+    uint32_t *out;
+};
+
+hipError_t launch_render(int L, const RenderArgs &a, bool neus, hipStream_t stream);
+
 hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32_t num_adj,
                                 const uint32_t *adj, const uint32_t *offs, uint2 *diff,
                                 hipStream_t stream);

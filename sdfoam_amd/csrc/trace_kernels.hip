@@ -799,6 +799,129 @@ hipError_t launch_backward(int L, const BwdArgs &a, bool neus, bool stats, hipSt
 }
 
 // ---------------------------------------------------------------------------
+// inference render (the reference's `benchmark` kernel,
+// src/tracing/pipeline.cu:1067-1199)
+
+// One lane per pixel, 16x16 pixel tiles per block as the traced kernels.  The
+// step is the forward's compositing without its per-point outputs; the walk
+// reads the caller's unpadded offset table with guarded loads.
+template <int L, bool NEUS>
+__global__ __launch_bounds__(kBlock) void render_kernel(RenderArgs a) {
+    constexpr int nsh = (L + 1) * (L + 1);
+    constexpr int D = 1 + 3 * nsh;
+    __shared__ float sh_all[kBlock * nsh];
+    bool valid;
+    const uint32_t px = ray_for_lane(a.width * a.height, a.width, a.num_tiles, valid);
+    const uint32_t pi = valid ? px % a.width : 0u, pj = valid ? px / a.width : 0u;
+
+    RayF ray = {};
+    bool masked = false;
+    if (valid) {
+        float dir[3];
+        sdf_cast_ray(a.forward, a.right, a.up, a.fov, a.focal, a.width, a.height, a.model, pi,
+                     pj, dir);
+        const float n = sqrtf(sdf_dot3(dir[0], dir[1], dir[2], dir[0], dir[1], dir[2]));
+        masked = n < 0.1f;
+        ray.ox = a.position[0];
+        ray.oy = a.position[1];
+        ray.oz = a.position[2];
+        if (!masked) {
+            // ray.direction /= ray.direction.norm()
+            ray.dx = dir[0] / n;
+            ray.dy = dir[1] / n;
+            ray.dz = dir[2] / n;
+        }
+    }
+    float *sh = sh_all + threadIdx.x * nsh;
+    {
+        float sh0[nsh];
+        sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
+#pragma unroll
+        for (int k = 0; k < nsh; ++k) sh[k] = sh0[k];
+    }
+    const float sha = a.sharpness[0];
+    const int32_t sdf_ch = a.settings.sdf_channel;
+    const bool neus_alpha = NEUS && sdf_ch >= 0;
+    const float thr = a.settings.weight_threshold;
+
+    float T = 1.0f;
+    float C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
+    WalkState ws;
+    walk_init(a.scene, (valid && !masked) ? a.start[0] : kNoIndex, ws);
+    WalkCounters wc = {0u, 0u, 0ull, 0ull};
+
+    while (__ballot(ws.alive) != 0ull) {
+        StepInfo si;
+        si.stepped = false;
+        si.found = false;
+        if (ws.alive)
+            walk_advance<true, false, true>(a.scene, ray, a.settings.max_intersections, ws, si,
+                                            wc);
+        bool keep = true;
+        if (si.stepped) {
+            const float *__restrict__ row = a.scene.attrs + (uint64_t)ws.cell * D;
+            float s = row[D - 1];
+            const float dt = fmaxf(si.t1 - ws.t0, 0.0f);
+            if (neus_alpha) {
+                const float d = row[sdf_ch];
+                const float phi = sdf_sigmoidf(-sha * d);
+                s = sha * phi * (1.0f - phi);
+            }
+            const float alpha = 1.0f - sdf_expf(-s * dt);
+            const float w = T * alpha;
+            float r, g, b;
+            if (NEUS || row[D - 1] > 1e-6f) {
+                sh_rgb<L>(sh, row, r, g, b);
+            } else {
+                r = g = b = 0.0f;
+            }
+            C0 = fmaf(w, r, C0);
+            C1 = fmaf(w, g, C1);
+            C2 = fmaf(w, b, C2);
+            T = T * (1.0f - alpha);
+            keep = T > thr;
+        }
+        if (si.stepped && !keep) ws.alive = false;
+        if (ws.alive && si.found) walk_move(ws, si);
+    }
+
+    if (!valid) return;
+    const uint64_t out_idx = (uint64_t)(a.height - 1u - pj) * a.width + pi;
+    if (masked) {
+        a.out[out_idx] = sdf_make_rgba8(a.bg[0], a.bg[1], a.bg[2], 1.0f);
+        return;
+    }
+    float bg0 = a.bg[0], bg1 = a.bg[1], bg2 = a.bg[2];
+    if (a.checker_bg) {
+        const int is = 2 * (int)((pi / 20u) % 2u) - 1;
+        const int js = 2 * (int)((pj / 20u) % 2u) - 1;
+        bg0 = bg1 = bg2 = (is * js > 0) ? 0.3f : 0.5f;
+    }
+    a.out[out_idx] = sdf_make_rgba8(fmaf(T, bg0, C0), fmaf(T, bg1, C1), fmaf(T, bg2, C2), 1.0f);
+}
+
+template <int L>
+static hipError_t launch_render_L(const RenderArgs &a, bool neus, hipStream_t stream) {
+    const dim3 grid(grid_blocks_for_tiles(a.num_tiles));
+    if (neus) {
+        hipLaunchKernelGGL((render_kernel<L, true>), grid, dim3(kBlock), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((render_kernel<L, false>), grid, dim3(kBlock), 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_render(int L, const RenderArgs &a, bool neus, hipStream_t stream) {
+    switch (L) {
+    case 0: return launch_render_L<0>(a, neus, stream);
+    case 1: return launch_render_L<1>(a, neus, stream);
+    case 2: return launch_render_L<2>(a, neus, stream);
+    case 3: return launch_render_L<3>(a, neus, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // fp-math contract on the device (test hook)
 
 __global__ __launch_bounds__(kBlock) void fpmath_kernel(int op, const float *__restrict__ in,

@@ -92,7 +92,6 @@ def _inv_s_to_tensor(inv_s, like: torch.Tensor) -> torch.Tensor:
     return s
 
 
-
 DEFAULT_WALK_BUDGET = 512
 
 
@@ -426,6 +425,80 @@ class Pipeline:
         if return_error:
             out["point_error"] = point_error
         return out
+
+    # -- trace_benchmark (torch_bindings/pipeline_bindings.cpp:609-732) -------
+    def trace_benchmark(self, points, attributes, point_adjacency, point_adjacency_offsets,
+                        adjacent_diff, camera, start_point, output_rgba, weight_threshold=None,
+                        max_intersections=None, alpha_mode=None, inv_s=None, eps=None,
+                        sdf_channel=None, *, bg_color=None, checker_bg=False):
+        """Render one camera into ``output_rgba`` (uint32 RGBA8, ``height x
+        width`` elements, row ``height - 1 - j`` holds pixel row j).
+
+        ``camera`` is the reference's dict: ``position``, ``forward``,
+        ``right``, ``up`` (3 floats each), ``fov`` (vertical, radians),
+        ``width``, ``height``, ``model`` ("pinhole" | "fisheye").
+        ``adjacent_diff`` is the fp16 offset table ``[E, 4]`` (as
+        ``prefetch_adjacent_diff`` returns it, or ``(x_adj - x_self)`` cast to
+        half with a zero 4th column).  ``start_point`` is one uint32 cell.
+        ``bg_color`` / ``checker_bg`` (no counterpart in the reference's
+        binding, which always uses the white default) set the background."""
+        points_c = points.contiguous()
+        attributes_c = attributes.contiguous()
+        adj_c = point_adjacency.contiguous()
+        offs_c = point_adjacency_offsets.contiguous()
+        diff_c = adjacent_diff.contiguous()
+        sharpness = _inv_s_to_tensor(inv_s, output_rgba)
+        self._validate_scene_data(points, attributes, point_adjacency, point_adjacency_offsets)
+        num_points = points_c.size(0)
+        num_adj = adj_c.size(0)
+
+        cam = _lib.Camera()
+        for key in ("position", "forward", "up", "right"):
+            v = torch.as_tensor(camera[key]).detach().to("cpu", torch.float32).reshape(-1)
+            if v.numel() < 3:
+                raise RuntimeError(f"camera {key} must have 3 elements")
+            getattr(cam, key)[:] = [float(x) for x in v[:3]]
+        cam.fov = float(camera["fov"])
+        cam.width = int(camera["width"])
+        cam.height = int(camera["height"])
+        model = str(camera["model"])
+        if model == "pinhole":
+            cam.model = _lib.SDF_CAMERA_PINHOLE
+        elif model == "fisheye":
+            cam.model = _lib.SDF_CAMERA_FISHEYE
+        else:
+            raise RuntimeError("Invalid camera model")
+
+        if start_point.numel() != 1:
+            raise RuntimeError("start_point must have a single element")
+        if start_point.dtype != torch.uint32:
+            raise RuntimeError("start_point must have uint32 dtype")
+        if not _is_cuda(start_point):
+            raise RuntimeError("start_point must be on CUDA device")
+        if output_rgba.numel() != cam.width * cam.height:
+            raise RuntimeError("output_rgba must have width * height elements")
+        if output_rgba.dtype != torch.uint32:
+            raise RuntimeError("output_rgba must have uint32 dtype")
+        if not _is_cuda(output_rgba):
+            raise RuntimeError("output_rgba must be on CUDA device")
+        if not output_rgba.is_contiguous():
+            raise RuntimeError("output_rgba must be contiguous")
+        if diff_c.element_size() != 2 or diff_c.numel() < 4 * num_adj or not _is_cuda(diff_c):
+            raise RuntimeError("adjacent_diff must be a CUDA tensor of 4 halves per adjacency entry")
+
+        settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel)
+        self._require_native()
+        vis = _lib.Visualization()
+        bg = [1.0, 1.0, 1.0] if bg_color is None else [float(x) for x in bg_color]
+        vis.bg_color[:] = bg
+        vis.checker_bg = 1 if checker_bg else 0
+        dev = output_rgba.device
+        with torch.cuda.device(dev):
+            check(_lib.lib().sdf_trace_benchmark(
+                self._sh_degree, C.byref(settings), num_points, ptr(points_c),
+                ptr(attributes_c), num_adj, ptr(adj_c), ptr(offs_c), ptr(diff_c),
+                diff_c.numel() // 4, C.byref(cam), C.byref(vis), ptr(start_point),
+                ptr(output_rgba), ptr(sharpness), _lib.stream_handle(dev)))
 
     # -- walk statistics (measurement / parity hook) -------------------------
     def walk_stats(self, points, attributes, point_adjacency, point_adjacency_offsets, rays,

@@ -134,6 +134,22 @@ def look_at(position, target, up, fov: float, width: int, height: int) -> Camera
     return Camera(position, fwd, right, cup, float(fov), int(width), int(height))
 
 
+def camera_dict(cam: Camera, model: str = "pinhole", width: int | None = None,
+                height: int | None = None, fov: float | None = None) -> dict:
+    """The camera dict of ``Pipeline.trace_benchmark`` (benchmark.py:63-82 of
+    the reference builds the same keys)."""
+    return {
+        "position": np.asarray(cam.position, dtype=np.float32),
+        "forward": np.asarray(cam.forward, dtype=np.float32),
+        "right": np.asarray(cam.right, dtype=np.float32),
+        "up": np.asarray(cam.up, dtype=np.float32),
+        "fov": float(cam.fov if fov is None else fov),
+        "width": int(cam.width if width is None else width),
+        "height": int(cam.height if height is None else height),
+        "model": model,
+    }
+
+
 def default_up(position) -> np.ndarray:
     """World up is +z, or +y for a camera on the z axis."""
     p = np.asarray(position, dtype=np.float64)

@@ -102,6 +102,32 @@ def test_walk_record_sizes_and_errors():
         assert rc == 1 and msg in L.sdf_last_error()
 
 
+def test_trace_benchmark_argument_errors():
+    from sdfoam_amd import _lib
+
+    L = _lib.lib()
+    buf = (C.c_uint64 * 64)()
+    p = C.cast(buf, C.c_void_p)
+    s = _settings()
+    cam = _lib.Camera()
+    cam.fov, cam.width, cam.height, cam.model = 1.0, 8, 8, 0
+
+    def call(diff_entries=4, camera=cam, start=p):
+        return L.sdf_trace_benchmark(3, C.byref(s), 10, p, p, 4, p, p, p, diff_entries,
+                                     C.byref(camera) if camera is not None else None, None,
+                                     start, p, p, None)
+
+    assert call(diff_entries=3) == 1 and b"adjacent_diff must hold" in L.sdf_last_error()
+    assert call(camera=None) == 1 and b"camera must not be NULL" in L.sdf_last_error()
+    bad = _lib.Camera()
+    bad.fov, bad.width, bad.height, bad.model = 1.0, 8, 8, 7
+    assert call(camera=bad) == 1 and L.sdf_last_error() == b"Invalid camera model"
+    big = _lib.Camera()
+    big.fov, big.width, big.height, big.model = 1.0, 1 << 16, 1 << 16, 0
+    assert call(camera=big) == 1 and b"width * height" in L.sdf_last_error()
+    assert call(start=None) == 1 and b"start_point" in L.sdf_last_error()
+
+
 def test_nn_and_tree_argument_errors():
     from sdfoam_amd import _lib
 
