@@ -72,8 +72,10 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3])
-    ap.add_argument("--cpu-stride", type=int, default=8,
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5],
+                    help="workload C1-C5; C3 is the headline (C5: each step draws its own "
+                         "2^20 rays and looks up their start cells)")
+    ap.add_argument("--cpu-stride", type=int, default=3,
                     help="CPU baseline traces every n-th ray (0 skips it)")
     ap.add_argument("--walk-record", type=int, default=1, choices=[0, 1],
                     help="1: the forward records each ray's steps and the backward replays "
@@ -126,47 +128,69 @@ def main() -> int:
     def u32(a):
         return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(dev).view(torch.uint32)
 
-    pts = torch.from_numpy(w.points).to(dev)
-    attrs = torch.from_numpy(w.attributes).to(dev)
+    def to_dev(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+    pts = to_dev(w.points)
+    attrs = to_dev(w.attributes)
     adj, offs = u32(w.adjacency), u32(w.offsets)
-    rays = torch.from_numpy(w.rays).to(dev)
-    q = torch.from_numpy(w.quantiles).to(dev)
-    grad_rgba = torch.from_numpy(w.grad_rgba).to(dev)
-    depth_grad = torch.from_numpy(w.depth_grad).to(dev)
     inv = torch.tensor([w.inv_s], dtype=torch.float32, device=dev)
     tree = sdfoam_amd.build_aabb_tree(pts)
-    start = sdfoam_amd.get_starting_point(rays, pts, tree)
-    torch.cuda.synchronize()
-    host_start = scenes.start_points_for(w.points, w.rays)
-    if not np.array_equal(start.view(torch.int32).cpu().numpy().view(np.uint32), host_start):
-        raise RuntimeError("GPU start cells differ from the host nearest neighbour")
-
     pipe = sdfoam_amd.create_pipeline(w.sh_degree)
     D = pipe.attribute_dim()
     Q = int(w.quantiles.shape[-1])
 
+    # ray batches: one fixed batch (C1-C4), or C5's ten seeded batches
+    batches = []
+    if args.config == 5:
+        cams = w.extra["cameras"]
+        for s in range(10):
+            if s == 0:
+                r_np, q_np, g_np, dg_np = w.rays, w.quantiles, w.grad_rgba, w.depth_grad
+            else:
+                r_np, q_np = scenes.c5_step_rays(cams, s, w.num_rays)
+                grng = np.random.default_rng(7000 + s)
+                g_np = grng.normal(size=(w.num_rays, 4)).astype(np.float32)
+                dg_np = grng.normal(size=(w.num_rays, Q)).astype(np.float32)
+            batches.append(dict(rays=to_dev(r_np), q=to_dev(q_np), g=to_dev(g_np),
+                                dg=to_dev(dg_np), rays_np=r_np))
+    else:
+        batches.append(dict(rays=to_dev(w.rays), q=to_dev(w.quantiles), g=to_dev(w.grad_rgba),
+                            dg=to_dev(w.depth_grad), rays_np=w.rays))
+    lookup_in_step = args.config == 5
+    for b in batches:
+        b["start"] = sdfoam_amd.get_starting_point(b["rays"], pts, tree)
+    torch.cuda.synchronize()
+    host_start = scenes.start_points_for(w.points, batches[0]["rays_np"])
+    if not np.array_equal(batches[0]["start"].view(torch.int32).cpu().numpy().view(np.uint32).reshape(-1),
+                          host_start.reshape(-1)):
+        raise RuntimeError("GPU start cells differ from the host nearest neighbour")
+
     use_record = bool(args.walk_record)
 
-    def step():
-        out = pipe.trace_forward(pts, attrs, adj, offs, rays, start, depth_quantiles=q,
+    def step(k):
+        b = batches[k % len(batches)]
+        start = (sdfoam_amd.get_starting_point(b["rays"], pts, tree) if lookup_in_step
+                 else b["start"])
+        out = pipe.trace_forward(pts, attrs, adj, offs, b["rays"], start, depth_quantiles=b["q"],
                                  return_contribution=True, alpha_mode="sdfoam", inv_s=inv,
                                  record_walk=use_record)
-        bwd = pipe.trace_backward(pts, attrs, adj, offs, rays, start, out["rgba"], grad_rgba, q,
-                                  out["depth_indices"], depth_grad, alpha_mode="sdfoam", inv_s=inv,
-                                  walk_record=out.get("walk_record"))
+        bwd = pipe.trace_backward(pts, attrs, adj, offs, b["rays"], start, out["rgba"], b["g"],
+                                  b["q"], out["depth_indices"], b["dg"], alpha_mode="sdfoam",
+                                  inv_s=inv, walk_record=out.get("walk_record"))
         return out, bwd
 
     log(f"warmup {args.warmup}")
-    for _ in range(args.warmup):
-        step()
+    for k in range(args.warmup):
+        step(k)
     torch.cuda.synchronize()
 
     log(f"timing {args.steps} steps")
     _lib.set_timing(True)
     torch.cuda.synchronize()
     t_start = time.perf_counter()
-    for _ in range(args.steps):
-        step()
+    for k in range(args.steps):
+        step(args.warmup + k)
     torch.cuda.synchronize()
     t_end = time.perf_counter()
     launches = _lib.collect_timings()
@@ -179,12 +203,22 @@ def main() -> int:
         per_kernel.setdefault(name, []).append(ms)
     avg = {k: float(np.mean(v)) for k, v in per_kernel.items()}
 
-    # walk statistics for the byte model (untimed)
-    st = pipe.walk_stats(pts, attrs, adj, offs, rays, start, alpha_mode="sdfoam", inv_s=inv)
-    torch.cuda.synchronize()
-    S = int(st["steps"].sum().item())
-    F_st = int(st["faces_stepped"].sum().item())
-    F_all = int(st["faces"].sum().item())
+    # walk statistics for the byte model (untimed), averaged over the timed steps
+    S = F_st = F_all = 0
+    for k in range(args.steps):
+        b = batches[(args.warmup + k) % len(batches)]
+        if "stats" not in b:
+            st = pipe.walk_stats(pts, attrs, adj, offs, b["rays"], b["start"], alpha_mode="sdfoam",
+                                 inv_s=inv)
+            torch.cuda.synchronize()
+            b["stats"] = (int(st["steps"].sum().item()), int(st["faces_stepped"].sum().item()),
+                          int(st["faces"].sum().item()))
+        S += b["stats"][0]
+        F_st += b["stats"][1]
+        F_all += b["stats"][2]
+    S //= args.steps
+    F_st //= args.steps
+    F_all //= args.steps
     R = w.num_rays
     N = w.num_points
     E = int(w.adjacency.size)
@@ -210,6 +244,12 @@ def main() -> int:
         with open(prof) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
+    if args.config == 5:
+        rays_desc = f"{R} rays per step sampled from 64 cameras 960x640 (10 seeded batches)"
+    elif args.config == 4:
+        rays_desc = f"8 cameras x {w.rays.shape[2]}x{w.rays.shape[1]} rays"
+    else:
+        rays_desc = f"{w.rays.shape[1]}x{w.rays.shape[0]} rays"
     result = {
         "metric": METRIC,
         "value": R / (ms_per_step * 1e-3) / 1e6,
@@ -225,8 +265,9 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": f"C{args.config}: {N} points, SH degree {w.sh_degree}, sdfoam alpha, "
-                        f"inv_s={w.inv_s:.4f}, {w.rays.shape[1]}x{w.rays.shape[0]} rays, Q={Q}, "
-                        "trace_forward(contribution, depth) + trace_backward"
+                        f"inv_s={w.inv_s:.4f}, {rays_desc}, Q={Q}, "
+                        + ("start-cell lookup + " if lookup_in_step else "")
+                        + "trace_forward(contribution, depth) + trace_backward"
                         + (" replaying the forward's walk record" if use_record else ""),
             "points": N,
             "adjacency": E,
@@ -254,14 +295,17 @@ def main() -> int:
     }
 
     if args.cpu_stride > 0:
-        result["cpu_baseline"] = cpu_baseline(w, host_start, args.cpu_stride)
+        b0 = batches[0]
+        result["cpu_baseline"] = cpu_baseline(
+            w, b0["rays_np"], host_start, b0["q"].cpu().numpy(), b0["g"].cpu().numpy(),
+            b0["dg"].cpu().numpy(), args.cpu_stride)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
     return 0
 
 
-def cpu_baseline(w, start, stride: int) -> dict:
+def cpu_baseline(w, rays, start, quantiles, grad_rgba, depth_grad, stride: int) -> dict:
     """Scalar host oracle, forward + backward, every `stride`-th ray."""
     import numpy as np
 
@@ -269,11 +313,11 @@ def cpu_baseline(w, start, stride: int) -> dict:
 
     oracle.build()
     threads = cpu_threads()
-    rays = w.rays.reshape(-1, 6)[::stride]
+    rays = rays.reshape(-1, 6)[::stride]
     sp = start.reshape(-1)[::stride]
-    qv = w.quantiles.reshape(-1, w.quantiles.shape[-1])[::stride]
-    g = w.grad_rgba.reshape(-1, 4)[::stride]
-    dg = w.depth_grad.reshape(-1, w.depth_grad.shape[-1])[::stride]
+    qv = quantiles.reshape(-1, quantiles.shape[-1])[::stride]
+    g = grad_rgba.reshape(-1, 4)[::stride]
+    dg = depth_grad.reshape(-1, depth_grad.shape[-1])[::stride]
     log(f"CPU baseline: {rays.shape[0]} rays on {threads} threads")
     t0 = time.perf_counter()
     f = oracle.trace_forward(w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, rays, sp,

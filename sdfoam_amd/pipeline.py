@@ -92,7 +92,7 @@ def _inv_s_to_tensor(inv_s, like: torch.Tensor) -> torch.Tensor:
     return s
 
 
-DEFAULT_WALK_BUDGET = 512
+DEFAULT_WALK_BUDGET = 256
 
 
 class WalkRecord:

@@ -78,6 +78,40 @@ def sort_points_order(points: np.ndarray) -> np.ndarray:
     return perm
 
 
+def _scene_blobs_shell(rng, n_blob: int, n_shell: int):
+    """32 Gaussian blobs (centres uniform in the unit ball, sigma U(0.05, 0.2),
+    samples outside r = 1 redrawn) plus a shell r in [1, 16] with density
+    proportional to 1 / r^2 (r uniform) and uniform directions."""
+    centres = np.empty((0, 3))
+    while centres.shape[0] < 32:
+        c = rng.uniform(-1.0, 1.0, size=(64, 3))
+        centres = np.concatenate([centres, c[np.linalg.norm(c, axis=1) <= 1.0]])
+    centres = centres[:32]
+    sigma = rng.uniform(0.05, 0.2, size=32)
+    counts = np.full(32, n_blob // 32)
+    counts[: n_blob - counts.sum()] += 1
+    blobs = []
+    for c, sg, k in zip(centres, sigma, counts):
+        got = np.empty((0, 3))
+        while got.shape[0] < k:
+            x = c + rng.normal(0.0, sg, size=(2 * (k - got.shape[0]) + 16, 3))
+            got = np.concatenate([got, x[np.linalg.norm(x, axis=1) <= 1.0]])
+        blobs.append(got[:k])
+    d = rng.normal(size=(n_shell, 3))
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    r = rng.uniform(1.0, 16.0, size=(n_shell, 1))
+    pts = np.concatenate(blobs + [d * r]).astype(np.float32)
+    return pts, centres
+
+
+def fibonacci_sphere(n: int, radius: float) -> np.ndarray:
+    k = np.arange(n, dtype=np.float64)
+    z = 1.0 - 2.0 * (k + 0.5) / n
+    rxy = np.sqrt(1.0 - z * z)
+    phi = k * math.pi * (3.0 - math.sqrt(5.0))
+    return radius * np.stack([rxy * np.cos(phi), rxy * np.sin(phi), z], axis=1)
+
+
 def delaunay_adjacency(points: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """CSR Delaunay adjacency with ascending rows.
 
@@ -261,10 +295,11 @@ def _scene_c3(rng):
 
 
 def make_config(index: int, *, mode: str = "sdfoam", inv_s: float | None = None,
-                image_scale: float = 1.0) -> Workload:
-    """Workload configuration C1-C3 (seed = config index).
+                image_scale: float = 1.0, point_scale: float = 1.0) -> Workload:
+    """Workload configuration C1-C5 (seed = config index).
 
-    ``image_scale`` < 1 shrinks the image (same camera) for quick tests.
+    ``image_scale`` < 1 shrinks the image (same camera) for quick tests;
+    ``point_scale`` < 1 shrinks the point counts of C4 / C5 (same proportions).
     """
     rng = np.random.default_rng(index if index != 1 else 0)
     inv_s = math.exp(0.3) if inv_s is None else float(inv_s)
@@ -279,6 +314,8 @@ def make_config(index: int, *, mode: str = "sdfoam", inv_s: float | None = None,
         th, ph = math.radians(60.0), math.radians(30.0)
         cam_pos = 3.0 * np.array([math.sin(th) * math.cos(ph), math.sin(th) * math.sin(ph), math.cos(th)])
         fov, w, h = math.radians(50.0), 400, 400
+    elif index in (4, 5):
+        return _make_blob_config(index, rng, mode, inv_s, image_scale, point_scale)
     elif index == 3:
         pts, sq = _scene_c3(rng)
         degree = 3
@@ -340,25 +377,132 @@ def make_config(index: int, *, mode: str = "sdfoam", inv_s: float | None = None,
     )
 
 
+def _make_blob_config(index: int, rng, mode: str, inv_s: float, image_scale: float,
+                      point_scale: float = 1.0) -> Workload:
+    """C4 (3M points, 8 ring cameras 1297x840, Q = 1) and C5 (2M points with
+    positions perturbed N(0, 0.001) after the adjacency is built, rays of
+    step 0: 2^20 (camera, pixel) samples over 64 cameras 960x640, Q = 2
+    descending quantiles).  SH degree 3, coefficients N(0, 0.3); SDF =
+    distance to the nearest blob centre - 0.1 (density: softplus of a
+    N(0, 1) logit)."""
+    degree = 3
+    n_blob, n_shell = (1_800_000, 1_200_000) if index == 4 else (1_200_000, 800_000)
+    pts, centres = _scene_blobs_shell(rng, int(n_blob * point_scale), int(n_shell * point_scale))
+    perm = sort_points_order(pts)
+    pts = np.ascontiguousarray(pts[perm])
+    n = pts.shape[0]
+    D = attribute_dim(degree)
+    attrs = np.empty((n, D), dtype=np.float32)
+    attrs[:, : D - 1] = rng.normal(0.0, 0.3, size=(n, D - 1))
+    if mode == "sdfoam":
+        from scipy.spatial import cKDTree
+
+        dist, _ = cKDTree(centres).query(pts.astype(np.float64))
+        last = dist - 0.1
+    else:
+        last = np.logaddexp(0.0, 10.0 * rng.normal(0.0, 1.0, size=n)) / 10.0
+    attrs[:, D - 1] = last.astype(np.float32)
+    adj, offs = delaunay_adjacency(pts)
+    extra = {"permutation": perm, "centres": centres}
+    if index == 4:
+        w, h = 1297, 840
+        if image_scale != 1.0:
+            w = max(8, int(round(w * image_scale)))
+            h = max(8, int(round(h * image_scale)))
+        cams = []
+        for k in range(8):
+            a = 2.0 * math.pi * k / 8
+            pos = 4.0 * np.array([math.cos(a), math.sin(a), 0.0])
+            cams.append(look_at(pos, np.zeros(3), default_up(pos), math.radians(50.0), w, h))
+        rays = np.stack([pinhole_rays(c) for c in cams])  # [8, H, W, 6]
+        q = np.full(rays.shape[:-1] + (1,), 0.5, dtype=np.float32)
+        extra["cameras"] = cams
+        extra["camera"] = cams[0]
+    else:
+        # stale adjacency: the training loop moves points between rebuilds
+        pts = (pts.astype(np.float64) + rng.normal(0.0, 1e-3, size=pts.shape)).astype(np.float32)
+        w, h = 960, 640
+        if image_scale != 1.0:
+            w = max(8, int(round(w * image_scale)))
+            h = max(8, int(round(h * image_scale)))
+        cams = [look_at(p, np.zeros(3), default_up(p), math.radians(50.0), w, h)
+                for p in fibonacci_sphere(64, 4.0)]
+        extra["cameras"] = cams
+        extra["camera"] = cams[0]
+        rays, q = c5_step_rays(cams, 0, max(1024, int((1 << 20) * point_scale)))
+    grad_rgba = rng.normal(size=rays.shape[:-1] + (4,)).astype(np.float32)
+    depth_grad = rng.normal(size=rays.shape[:-1] + (q.shape[-1],)).astype(np.float32)
+    return Workload(
+        name=f"C{index}", sh_degree=degree, points=pts, attributes=attrs, adjacency=adj,
+        offsets=offs, rays=rays, quantiles=q, grad_rgba=grad_rgba, depth_grad=depth_grad,
+        inv_s=inv_s, alpha_mode=mode, extra=extra)
+
+
+def c5_step_rays(cams, step: int, num_rays: int) -> tuple[np.ndarray, np.ndarray]:
+    """Rays of training step `step`: rng(5000 + step) draws (camera, pixel)
+    pairs uniformly with replacement (as src/utils/batch_fetcher.cpp:66-69
+    draws random rays), and two quantiles U(0, 1) sorted descending
+    (train.py:259-261).  Returns rays [R, 6] and quantiles [R, 2]."""
+    rng = np.random.default_rng(5000 + step)
+    ncam = len(cams)
+    w, h = cams[0].width, cams[0].height
+    ci = rng.integers(0, ncam, size=num_rays)
+    px = rng.integers(0, w * h, size=num_rays)
+    i = (px % w).astype(np.float64)
+    j = (px // w).astype(np.float64)
+    pos = np.stack([c.position for c in cams])
+    fw = np.stack([c.forward for c in cams])
+    rt = np.stack([c.right for c in cams])
+    up = np.stack([c.up for c in cams])
+    f = np.array([1.0 / math.tan(c.fov * 0.5) for c in cams])
+    u = (2.0 * i / w - 1.0) * (w / h)
+    v = 1.0 - 2.0 * j / h
+    d = f[ci, None] * fw[ci] + u[:, None] * rt[ci] + v[:, None] * up[ci]
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    rays = np.empty((num_rays, 6), dtype=np.float32)
+    rays[:, :3] = pos[ci]
+    rays[:, 3:] = d
+    q = -np.sort(-rng.uniform(0.0, 1.0, size=(num_rays, 2)), axis=1)
+    return rays, q.astype(np.float32)
+
+
 def save_workload(w: Workload, path: str) -> None:
     """Write a workload to an .npz file (arrays only; no pickled objects)."""
-    cam = w.extra.get("camera")
+    cams = w.extra.get("cameras") or ([w.extra["camera"]] if "camera" in w.extra else [])
+    cam_arrays = {}
+    if cams:
+        cam_arrays = dict(
+            cam_position=np.stack([c.position for c in cams]),
+            cam_forward=np.stack([c.forward for c in cams]),
+            cam_right=np.stack([c.right for c in cams]),
+            cam_up=np.stack([c.up for c in cams]),
+            cam_fov=np.array([c.fov for c in cams]),
+            cam_size=np.array([[c.width, c.height] for c in cams]),
+        )
     np.savez(
         path, name=np.array(w.name), sh_degree=np.array(w.sh_degree), points=w.points,
         attributes=w.attributes, adjacency=w.adjacency, offsets=w.offsets, rays=w.rays,
         quantiles=w.quantiles, grad_rgba=w.grad_rgba, depth_grad=w.depth_grad,
-        inv_s=np.array(w.inv_s), alpha_mode=np.array(w.alpha_mode),
+        inv_s=np.array(w.inv_s), alpha_mode=np.array(w.alpha_mode), **cam_arrays,
     )
 
 
 def load_workload(path: str) -> Workload:
     """Read a workload written by save_workload (allow_pickle stays off)."""
     z = np.load(path)
+    extra = {}
+    if "cam_position" in z.files:
+        cams = [Camera(z["cam_position"][k], z["cam_forward"][k], z["cam_right"][k],
+                       z["cam_up"][k], float(z["cam_fov"][k]), int(z["cam_size"][k][0]),
+                       int(z["cam_size"][k][1]))
+                for k in range(z["cam_position"].shape[0])]
+        extra = {"cameras": cams, "camera": cams[0]}
     return Workload(
         name=str(z["name"]), sh_degree=int(z["sh_degree"]), points=z["points"],
         attributes=z["attributes"], adjacency=z["adjacency"], offsets=z["offsets"],
         rays=z["rays"], quantiles=z["quantiles"], grad_rgba=z["grad_rgba"],
         depth_grad=z["depth_grad"], inv_s=float(z["inv_s"]), alpha_mode=str(z["alpha_mode"]),
+        extra=extra,
     )
 
 

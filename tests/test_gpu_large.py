@@ -1,0 +1,159 @@
+"""GPU checks at the full sizes of configs C4 (3M points, 8 ring cameras of
+1297x840) and C5 (2M points with a stale adjacency, 2^20 rays drawn from 64
+cameras, two quantiles), where the oracle would take minutes on every ray:
+
+* size-independent properties of the full batch: the start cells of
+  get_starting_point equal the host nearest neighbour; the contributions of
+  all cells sum to the sum of the rays' opacities (sum_k T_k alpha_k =
+  1 - T per ray); loop counts and depth indices are in range; gradients are
+  finite;
+* oracle parity (the bars of test_gpu_parity) on a seeded subset of the
+  same rays, forward and backward with the walk record, and the inference
+  render of a full C4 camera bit-exact.
+
+Scene generation (Qhull at 2-3M points) takes one to two minutes; progress
+lines are printed as each stage ends."""
+
+import dataclasses
+import time
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def say(pytestconfig):
+    capman = pytestconfig.pluginmanager.getplugin("capturemanager")
+    t0 = time.time()
+
+    def _say(msg):
+        with capman.global_and_fixture_disabled():
+            print(f"\n[large {time.time() - t0:6.1f}s] {msg}", flush=True)
+
+    return _say
+
+
+_CACHE = {}
+
+
+def big_scene(index, say):
+    if index not in _CACHE:
+        from sdfoam_amd import scenes
+
+        say(f"generating C{index}")
+        w = scenes.make_config(index)
+        say(f"C{index} ready: N={w.num_points} E={w.adjacency.size} R={w.num_rays}")
+        _CACHE[index] = w
+    return _CACHE[index]
+
+
+def _u32(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(dev).view(torch.uint32)
+
+
+def _full_batch_properties(w, dev, say, rays_np, q_np, g_np, dg_np):
+    """GPU start cells, forward + backward with the walk record over the
+    whole batch, and the properties that hold at any size."""
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import scenes
+
+    pts = torch.from_numpy(w.points).to(dev)
+    attrs = torch.from_numpy(w.attributes).to(dev)
+    adj, offs = _u32(w.adjacency, dev), _u32(w.offsets, dev)
+    rays = torch.from_numpy(rays_np).to(dev)
+    tree = sdfoam_amd.build_aabb_tree(pts)
+    start = sdfoam_amd.get_starting_point(rays, pts, tree)
+    torch.cuda.synchronize()
+    host_start = scenes.start_points_for(w.points, rays_np)
+    got_start = start.view(torch.int32).cpu().numpy().view(np.uint32)
+    assert np.array_equal(got_start.reshape(-1), host_start.reshape(-1)), "start cells"
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    inv = torch.tensor([w.inv_s], device=dev)
+    q = torch.from_numpy(q_np).to(dev)
+    fwd = pipe.trace_forward(pts, attrs, adj, offs, rays, start, depth_quantiles=q,
+                             return_contribution=True, alpha_mode="sdfoam", inv_s=inv,
+                             record_walk=True)
+    bwd = pipe.trace_backward(pts, attrs, adj, offs, rays, start, fwd["rgba"],
+                              torch.from_numpy(g_np).to(dev), q, fwd["depth_indices"],
+                              torch.from_numpy(dg_np).to(dev), alpha_mode="sdfoam", inv_s=inv,
+                              walk_record=fwd["walk_record"])
+    torch.cuda.synchronize()
+    say(f"full batch traced: {rays_np.size // 6} rays")
+    rgba = fwd["rgba"].cpu().numpy().reshape(-1, 4)
+    contrib = fwd["contribution"].cpu().numpy().astype(np.float64)
+    a_sum = float(np.sum(rgba[:, 3].astype(np.float64)))
+    c_sum = float(np.sum(contrib))
+    assert abs(c_sum - a_sum) <= 1e-4 * a_sum + 1e-3, (c_sum, a_sum)
+    ni = fwd["num_intersections"].view(torch.int32).cpu().numpy().reshape(-1)
+    assert ni.min() >= 1 and ni.max() <= 1025
+    didx = fwd["depth_indices"].view(torch.int32).cpu().numpy().view(np.uint32).reshape(-1)
+    assert np.all((didx < w.num_points) | (didx == 0xFFFFFFFF))
+    for k in ("points_grad", "attr_grad", "sharpness_grad"):
+        assert torch.isfinite(bwd[k]).all(), k
+    assert float(rgba[:, 3].mean()) > 0.05  # the batch sees geometry
+    return host_start
+
+
+def _subset(w, rays, q, g, dg, start):
+    return dataclasses.replace(w, rays=np.ascontiguousarray(rays), quantiles=np.ascontiguousarray(q),
+                               grad_rgba=np.ascontiguousarray(g),
+                               depth_grad=np.ascontiguousarray(dg),
+                               extra={"start": np.ascontiguousarray(start)})
+
+
+def test_c5_training_step(dev, oracle_lib, say):
+    from test_gpu_parity import _backward_both, _check_backward, _check_forward, _forward_both
+
+    w = big_scene(5, say)
+    start = _full_batch_properties(w, dev, say, w.rays, w.quantiles, w.grad_rgba, w.depth_grad)
+    sub = _subset(w, w.rays[::16], w.quantiles[::16], w.grad_rgba[::16], w.depth_grad[::16],
+                  start.reshape(-1)[::16])
+    out, st, ref = _forward_both(sub, dev, oracle_lib, "sdfoam", record=0)
+    _check_forward(out, st, ref, sub, 0)
+    say("C5 subset forward parity")
+    bwd, st, ref = _backward_both(sub, dev, oracle_lib, "sdfoam", walk=True)
+    _check_backward(bwd, st, ref, sub)
+    say("C5 subset backward parity")
+
+
+def test_c4_cameras(dev, oracle_lib, say):
+    from test_gpu_parity import _backward_both, _check_backward, _check_forward, _forward_both
+
+    w = big_scene(4, say)
+    start = _full_batch_properties(w, dev, say, w.rays, w.quantiles, w.grad_rgba, w.depth_grad)
+    # camera 3, every 8th row and column: an image-shaped subset (tile path)
+    sl = (3, slice(None, None, 8), slice(None, None, 8))
+    sub = _subset(w, w.rays[sl], w.quantiles[sl], w.grad_rgba[sl], w.depth_grad[sl], start[sl])
+    out, st, ref = _forward_both(sub, dev, oracle_lib, "sdfoam", record=0)
+    _check_forward(out, st, ref, sub, 0)
+    say("C4 subset forward parity")
+    bwd, st, ref = _backward_both(sub, dev, oracle_lib, "sdfoam", walk=True)
+    _check_backward(bwd, st, ref, sub)
+    say("C4 subset backward parity")
+
+
+def test_c4_render_full_camera(dev, oracle_lib, say):
+    from test_gpu_render import _render_both
+
+    from sdfoam_amd import scenes
+
+    w = big_scene(4, say)
+    cam = scenes.camera_dict(w.extra["cameras"][5])
+    got, ref = _render_both(w, dev, oracle_lib, cam)
+    assert np.array_equal(got, ref.rgba8)
+    say("C4 full-camera render bit-exact")

@@ -258,7 +258,9 @@ def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False, walk=F
     fwd = pipe.trace_forward(**g, depth_quantiles=q, alpha_mode=mode, inv_s=inv_t,
                              record_walk=walk, walk_budget=walk_budget)
     if walk and mode == "sdfoam":
-        assert fwd["walk_record"].budget == (walk_budget or min(1024 + 2, 512))
+        from sdfoam_amd.pipeline import DEFAULT_WALK_BUDGET
+
+        assert fwd["walk_record"].budget == (walk_budget or min(1024 + 2, DEFAULT_WALK_BUDGET))
     rerr = None
     if ray_error:
         rerr_np = np.random.default_rng(11).uniform(0, 1, w.rays.shape[:-1]).astype(np.float32)
