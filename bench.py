@@ -177,7 +177,7 @@ def main() -> int:
                                  record_walk=use_record)
         bwd = pipe.trace_backward(pts, attrs, adj, offs, b["rays"], start, out["rgba"], b["g"],
                                   b["q"], out["depth_indices"], b["dg"], alpha_mode="sdfoam",
-                                  inv_s=inv, walk_record=out.get("walk_record"))
+                                  inv_s=inv, trace_plan=out.get("trace_plan"))
         return out, bwd
 
     log(f"warmup {args.warmup}")

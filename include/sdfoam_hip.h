@@ -167,26 +167,45 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
                         uint32_t *output_rgba, const float *sharpness,
                         void *stream);
 
-/* ---- walk record (no counterpart in the reference) --------------------- *
- * The forward of an sdfoam-mode trace can record each ray's steps (next
- * cell and exit distance, 8 bytes a step, `budget` steps per wavefront of
- * 64 rays); the backward over the same rays, start points, scene and
- * settings then reads the steps instead of scanning the cell faces again.
- * Results are identical with and without the record.  A standard-mode
- * trace ignores it.  entries == NULL means no record.  Rays past `budget`
- * trips, or that walk further in the backward, scan as usual. */
-typedef struct sdf_walk_record {
-    void *entries;  /* device memory, 8-byte aligned */
-    size_t bytes;   /* >= sdf_walk_record_bytes(num_rays, ray_image_width, budget) */
-    uint32_t budget;
-} sdf_walk_record;
+/* ---- trace plan (no counterpart in the reference) ---------------------- *
+ * Two optional aids for a forward and the backward over the same rays, start
+ * points, scene and settings.  Results are identical with and without them.
+ *
+ * Walk record: the forward of an sdfoam-mode trace records each ray's steps
+ * (next cell and exit distance, 8 bytes a step, `walk_budget` trips per
+ * wavefront of 64 rays); the backward then reads the steps instead of
+ * scanning the cell faces again.  A standard-mode trace ignores it.  Rays
+ * past `walk_budget` trips, or that walk further in the backward, scan as
+ * usual.  walk_record == NULL: no record.
+ *
+ * Ray order: a permutation of [0, num_rays) from sdf_ray_order; the kernels
+ * trace rays in that order (outputs stay in the caller's order).  For rays
+ * in no particular order (random training batches) it makes the rays of a
+ * wavefront start in the same cell and point the same way.  Requires
+ * settings->ray_image_width == 0.  ray_order == NULL: the caller's order. */
+typedef struct sdf_trace_plan {
+    void *walk_record;        /* device memory, 8-byte aligned, or NULL */
+    size_t walk_record_bytes; /* >= sdf_walk_record_bytes(num_rays, ray_image_width, walk_budget) */
+    uint32_t walk_budget;
+    const uint32_t *ray_order; /* device memory [num_rays], or NULL */
+} sdf_trace_plan;
 
 size_t sdf_walk_record_bytes(uint32_t num_rays, uint32_t ray_image_width,
                              uint32_t budget);
 
-/* sdf_trace_forward that also writes the walk record. */
-int sdf_trace_forward_recorded(
-    const sdf_walk_record *record, int sh_degree,
+/* Scratch bytes of sdf_ray_order. */
+size_t sdf_ray_order_scratch_bytes(uint32_t num_points, uint32_t num_rays);
+
+/* order[num_rays]: rays sorted by (start cell, Z-order of the octahedral
+ * direction); stable, so the same inputs give the same order.  scratch must
+ * be 256-byte aligned. */
+int sdf_ray_order(uint32_t num_points, uint32_t num_rays, const float *rays,
+                  const uint32_t *start_point_index, uint32_t *order,
+                  void *scratch, size_t scratch_bytes, void *stream);
+
+/* sdf_trace_forward with a plan (writes the walk record if given). */
+int sdf_trace_forward_planned(
+    const sdf_trace_plan *plan, int sh_degree,
     const sdf_trace_settings *settings, uint32_t num_points,
     const float *points, const float *attributes, uint32_t adjacency_size,
     const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
@@ -197,9 +216,9 @@ int sdf_trace_forward_recorded(
     const float *sharpness, float *alpha_output, void *scratch,
     size_t scratch_bytes, void *stream);
 
-/* sdf_trace_backward that replays the forward's walk record. */
-int sdf_trace_backward_recorded(
-    const sdf_walk_record *record, int sh_degree,
+/* sdf_trace_backward with a plan (replays the forward's walk record). */
+int sdf_trace_backward_planned(
+    const sdf_trace_plan *plan, int sh_degree,
     const sdf_trace_settings *settings, uint32_t num_points,
     const float *points, const float *attributes, uint32_t adjacency_size,
     const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
@@ -264,6 +283,7 @@ int sdf_debug_fpmath(int op, const float *in, void *out, uint64_t n,
 #define SDF_KERNEL_AABB_TREE 3
 #define SDF_KERNEL_NN 4
 #define SDF_KERNEL_RENDER 5
+#define SDF_KERNEL_RAY_ORDER 6
 int sdf_set_timing(int enable);
 int sdf_timing_collect(int *kinds, float *ms, int max_n, int *n_out);
 

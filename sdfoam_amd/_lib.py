@@ -26,8 +26,10 @@ EXPORTS = (
     "sdf_trace_backward",
     "sdf_trace_benchmark",
     "sdf_walk_record_bytes",
-    "sdf_trace_forward_recorded",
-    "sdf_trace_backward_recorded",
+    "sdf_ray_order_scratch_bytes",
+    "sdf_ray_order",
+    "sdf_trace_forward_planned",
+    "sdf_trace_backward_planned",
     "sdf_build_aabb_tree",
     "sdf_nn",
     "sdf_trace_walk_stats",
@@ -37,7 +39,7 @@ EXPORTS = (
 )
 
 KERNEL_NAMES = {0: "prefetch_adjacent_diff", 1: "forward", 2: "backward", 3: "build_aabb_tree", 4: "nn",
-                5: "render"}
+                5: "render", 6: "ray_order"}
 
 SDF_CAMERA_PINHOLE = 0
 SDF_CAMERA_FISHEYE = 1
@@ -77,13 +79,14 @@ class Visualization(C.Structure):
     _fields_ = [("bg_color", C.c_float * 3), ("checker_bg", C.c_int32)]
 
 
-class WalkRecordDesc(C.Structure):
-    """sdf_walk_record: device buffer of the forward's walk steps."""
+class TracePlanDesc(C.Structure):
+    """sdf_trace_plan: the forward's walk record and the rays' launch order."""
 
     _fields_ = [
-        ("entries", C.c_void_p),
-        ("bytes", C.c_size_t),
-        ("budget", C.c_uint32),
+        ("walk_record", C.c_void_p),
+        ("walk_record_bytes", C.c_size_t),
+        ("walk_budget", C.c_uint32),
+        ("ray_order", C.c_void_p),
     ]
 
 
@@ -133,10 +136,14 @@ def lib() -> C.CDLL:
         C.POINTER(Visualization), P, P, P, P]
     L.sdf_walk_record_bytes.restype = SZ
     L.sdf_walk_record_bytes.argtypes = [U32, U32, U32]
-    L.sdf_trace_forward_recorded.restype = C.c_int
-    L.sdf_trace_forward_recorded.argtypes = [C.POINTER(WalkRecordDesc)] + L.sdf_trace_forward.argtypes
-    L.sdf_trace_backward_recorded.restype = C.c_int
-    L.sdf_trace_backward_recorded.argtypes = [C.POINTER(WalkRecordDesc)] + L.sdf_trace_backward.argtypes
+    L.sdf_ray_order_scratch_bytes.restype = SZ
+    L.sdf_ray_order_scratch_bytes.argtypes = [U32, U32]
+    L.sdf_ray_order.restype = C.c_int
+    L.sdf_ray_order.argtypes = [U32, U32, P, P, P, P, SZ, P]
+    L.sdf_trace_forward_planned.restype = C.c_int
+    L.sdf_trace_forward_planned.argtypes = [C.POINTER(TracePlanDesc)] + L.sdf_trace_forward.argtypes
+    L.sdf_trace_backward_planned.restype = C.c_int
+    L.sdf_trace_backward_planned.argtypes = [C.POINTER(TracePlanDesc)] + L.sdf_trace_backward.argtypes
     L.sdf_build_aabb_tree.restype = C.c_int
     L.sdf_build_aabb_tree.argtypes = [P, U32, P, P]
     L.sdf_nn.restype = C.c_int

@@ -100,27 +100,35 @@ SceneView make_scene(uint32_t num_points, const float *points, const float *attr
     return sc;
 }
 
-// record == NULL or record->entries == NULL: no record.  Otherwise it
-// must hold sdf_walk_record_bytes(num_rays, ray_image_width, budget) bytes.
-int check_record(const sdf_walk_record *record, uint32_t num_rays, uint32_t ray_image_width,
-                 WalkRecordArgs &out) {
-    out.entries = nullptr;
-    out.budget = 0;
-    if (!record || !record->entries) return SDF_OK;
-    if (record->budget == 0) return fail(SDF_E_INVALID, "walk record budget must be positive");
+// plan == NULL: neither aid.  A walk record must hold
+// sdf_walk_record_bytes(num_rays, ray_image_width, walk_budget) bytes; a ray
+// order needs ray_image_width == 0.
+int check_plan(const sdf_trace_plan *plan, uint32_t num_rays, uint32_t ray_image_width,
+               WalkRecordArgs &rec, const uint32_t *&order) {
+    rec.entries = nullptr;
+    rec.budget = 0;
+    order = nullptr;
+    if (!plan) return SDF_OK;
+    if (plan->ray_order) {
+        if (ray_image_width != 0)
+            return fail(SDF_E_INVALID, "a ray order needs ray_image_width == 0");
+        order = plan->ray_order;
+    }
+    if (!plan->walk_record) return SDF_OK;
+    if (plan->walk_budget == 0) return fail(SDF_E_INVALID, "walk record budget must be positive");
     const uint64_t need =
-        walk_record_entries(num_ray_tiles(num_rays, ray_image_width), record->budget) * 8u;
-    if (record->bytes < need)
+        walk_record_entries(num_ray_tiles(num_rays, ray_image_width), plan->walk_budget) * 8u;
+    if (plan->walk_record_bytes < need)
         return fail(SDF_E_INVALID, "walk record must hold %llu bytes (got %zu)",
-                    (unsigned long long)need, record->bytes);
-    if ((reinterpret_cast<uintptr_t>(record->entries) & 7u) != 0)
+                    (unsigned long long)need, plan->walk_record_bytes);
+    if ((reinterpret_cast<uintptr_t>(plan->walk_record) & 7u) != 0)
         return fail(SDF_E_INVALID, "walk record must be 8-byte aligned");
-    out.entries = static_cast<uint2 *>(record->entries);
-    out.budget = record->budget;
+    rec.entries = static_cast<uint2 *>(plan->walk_record);
+    rec.budget = plan->walk_budget;
     return SDF_OK;
 }
 
-int trace_forward_impl(const sdf_walk_record *record, int sh_degree,
+int trace_forward_impl(const sdf_trace_plan *plan, int sh_degree,
                        const sdf_trace_settings *settings, uint32_t num_points,
                        const float *points, const float *attributes, uint32_t adjacency_size,
                        const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
@@ -140,7 +148,8 @@ int trace_forward_impl(const sdf_walk_record *record, int sh_degree,
     if ((reinterpret_cast<uintptr_t>(ray_rgba) & 15u) != 0)
         return fail(SDF_E_INVALID, "ray_rgba must be 16-byte aligned");
     WalkRecordArgs rec = {};
-    rc = check_record(record, num_rays, settings->ray_image_width, rec);
+    const uint32_t *order = nullptr;
+    rc = check_plan(plan, num_rays, settings->ray_image_width, rec, order);
     if (rc != SDF_OK) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     tbegin(SDF_KERNEL_PREFETCH, s);
@@ -151,6 +160,7 @@ int trace_forward_impl(const sdf_walk_record *record, int sh_degree,
     if (num_rays == 0) return SDF_OK;
     FwdArgs a = {};
     a.record = rec;
+    a.order = order;
     a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
                          point_adjacency_offsets, scratch);
     a.settings = *settings;
@@ -174,7 +184,7 @@ int trace_forward_impl(const sdf_walk_record *record, int sh_degree,
     return SDF_OK;
 }
 
-int trace_backward_impl(const sdf_walk_record *record, int sh_degree,
+int trace_backward_impl(const sdf_trace_plan *plan, int sh_degree,
                         const sdf_trace_settings *settings, uint32_t num_points,
                         const float *points, const float *attributes, uint32_t adjacency_size,
                         const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
@@ -202,7 +212,8 @@ int trace_backward_impl(const sdf_walk_record *record, int sh_degree,
          15u) != 0)
         return fail(SDF_E_INVALID, "ray_rgba and ray_rgba_grad must be 16-byte aligned");
     WalkRecordArgs rec = {};
-    rc = check_record(record, num_rays, settings->ray_image_width, rec);
+    const uint32_t *order = nullptr;
+    rc = check_plan(plan, num_rays, settings->ray_image_width, rec, order);
     if (rc != SDF_OK) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     tbegin(SDF_KERNEL_PREFETCH, s);
@@ -213,6 +224,7 @@ int trace_backward_impl(const sdf_walk_record *record, int sh_degree,
     if (num_rays == 0) return SDF_OK;
     BwdArgs a = {};
     a.record = rec;
+    a.order = order;
     a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
                          point_adjacency_offsets, scratch);
     a.settings = *settings;
@@ -377,12 +389,37 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings, uint3
     return SDF_OK;
 }
 
+size_t sdf_ray_order_scratch_bytes(uint32_t num_points, uint32_t num_rays) {
+    return ray_order_scratch_bytes(num_points, num_rays);
+}
+
+int sdf_ray_order(uint32_t num_points, uint32_t num_rays, const float *rays,
+                  const uint32_t *start_point_index, uint32_t *order, void *scratch,
+                  size_t scratch_bytes, void *stream) {
+    if (num_rays == 0) return SDF_OK;
+    if (!rays || !start_point_index || !order || !scratch)
+        return fail(SDF_E_INVALID, "NULL pointer argument");
+    const size_t need = ray_order_scratch_bytes(num_points, num_rays);
+    if (need == 0) return fail(SDF_E_HIP, "ray order: scratch size query failed");
+    if (scratch_bytes < need)
+        return fail(SDF_E_INVALID, "scratch must hold %zu bytes (got %zu)", need, scratch_bytes);
+    if ((reinterpret_cast<uintptr_t>(scratch) & 255u) != 0)
+        return fail(SDF_E_INVALID, "scratch must be 256-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    tbegin(SDF_KERNEL_RAY_ORDER, s);
+    hipError_t e = launch_ray_order(num_points, num_rays, rays, start_point_index, order, scratch,
+                                    scratch_bytes, s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "ray_order");
+    return SDF_OK;
+}
+
 size_t sdf_walk_record_bytes(uint32_t num_rays, uint32_t ray_image_width, uint32_t budget) {
     return (size_t)walk_record_entries(num_ray_tiles(num_rays, ray_image_width), budget) * 8u;
 }
 
-int sdf_trace_forward_recorded(
-    const sdf_walk_record *record, int sh_degree, const sdf_trace_settings *settings,
+int sdf_trace_forward_planned(
+    const sdf_trace_plan *plan, int sh_degree, const sdf_trace_settings *settings,
     uint32_t num_points, const float *points, const float *attributes, uint32_t adjacency_size,
     const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets, uint32_t num_rays,
     const float *rays, const uint32_t *start_point_index, uint32_t num_depth_quantiles,
@@ -390,7 +427,7 @@ int sdf_trace_forward_recorded(
     uint32_t *quantile_point_indices, uint32_t *num_intersections, float *point_contribution,
     const float *sharpness, float *alpha_output, void *scratch, size_t scratch_bytes,
     void *stream) {
-    return trace_forward_impl(record, sh_degree, settings, num_points, points, attributes,
+    return trace_forward_impl(plan, sh_degree, settings, num_points, points, attributes,
                               adjacency_size, point_adjacency, point_adjacency_offsets, num_rays,
                               rays, start_point_index, num_depth_quantiles, depth_quantiles,
                               ray_rgba, quantile_depths, quantile_point_indices,
@@ -398,8 +435,8 @@ int sdf_trace_forward_recorded(
                               scratch, scratch_bytes, stream);
 }
 
-int sdf_trace_backward_recorded(
-    const sdf_walk_record *record, int sh_degree, const sdf_trace_settings *settings,
+int sdf_trace_backward_planned(
+    const sdf_trace_plan *plan, int sh_degree, const sdf_trace_settings *settings,
     uint32_t num_points, const float *points, const float *attributes, uint32_t adjacency_size,
     const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets, uint32_t num_rays,
     const float *rays, const uint32_t *start_point_index, uint32_t num_depth_quantiles,
@@ -407,7 +444,7 @@ int sdf_trace_backward_recorded(
     const float *ray_rgba_grad, const float *depth_grad, const float *ray_error,
     float *points_grad, float *attribute_grad, float *point_error, const float *sharpness,
     float *sharpness_grad, void *scratch, size_t scratch_bytes, void *stream) {
-    return trace_backward_impl(record, sh_degree, settings, num_points, points, attributes,
+    return trace_backward_impl(plan, sh_degree, settings, num_points, points, attributes,
                                adjacency_size, point_adjacency, point_adjacency_offsets,
                                num_rays, rays, start_point_index, num_depth_quantiles,
                                depth_quantiles, quantile_point_indices, ray_rgba, ray_rgba_grad,

@@ -58,12 +58,23 @@ __device__ __forceinline__ uint32_t block_tile() {
     return (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
 }
 
+// The ray this lane traces: with `order` (a permutation of the rays, see
+// order_kernels.hip) lane i of the launch takes ray order[i]; entries out of
+// range leave the lane idle.  Otherwise rays in their own order, or 16x16
+// pixel tiles of an image `width` pixels wide.
 __device__ __forceinline__ uint32_t ray_for_lane(uint32_t num_rays, uint32_t width,
-                                                 uint32_t num_tiles, bool &valid) {
+                                                 uint32_t num_tiles, bool &valid,
+                                                 const uint32_t *__restrict__ order = nullptr) {
     const uint32_t t = block_tile();
     if (t >= num_tiles) {
         valid = false;
         return 0;
+    }
+    if (order) {
+        const uint32_t i = t * kBlock + threadIdx.x;
+        const uint32_t r = i < num_rays ? order[i] : num_rays;
+        valid = r < num_rays;
+        return valid ? r : 0u;
     }
     if (width == 0) {
         const uint32_t i = t * kBlock + threadIdx.x;

@@ -34,6 +34,7 @@ __device__ inline uint2 *walk_record_lane(const WalkRecordArgs &r, uint32_t lane
 
 struct FwdArgs {
     WalkRecordArgs record;
+    const uint32_t *order; // NULL, or the launch order of the rays (num_tiles from num_rays)
     SceneView scene;
     sdf_trace_settings settings;
     const float *rays;
@@ -60,6 +61,7 @@ struct FwdArgs {
 
 struct BwdArgs {
     WalkRecordArgs record;
+    const uint32_t *order;
     SceneView scene;
     sdf_trace_settings settings;
     const float *rays;
@@ -103,6 +105,14 @@ struct RenderArgs {
 };
 
 hipError_t launch_render(int L, const RenderArgs &a, bool neus, hipStream_t stream);
+
+// Ray launch order for rays in no particular order: sort by (start cell,
+// Morton code of the octahedral direction) so a wavefront's rays start
+// together and point the same way.
+size_t ray_order_scratch_bytes(uint32_t num_points, uint32_t num_rays);
+hipError_t launch_ray_order(uint32_t num_points, uint32_t num_rays, const float *rays,
+                            const uint32_t *start, uint32_t *order, void *scratch,
+                            size_t scratch_bytes, hipStream_t stream);
 
 hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32_t num_adj,
                                 const uint32_t *adj, const uint32_t *offs, uint2 *diff,

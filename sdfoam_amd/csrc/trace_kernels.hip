@@ -82,7 +82,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     __shared__ float sh_all[kBlock * nsh];
     bool valid;
     const uint32_t ray_idx =
-        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid);
+        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid, a.order);
     const uint32_t lane = lane_id();
 
     RayF ray = {};
@@ -406,7 +406,7 @@ backward_sdf_kernel(BwdArgs a) {
     __shared__ WaveTables<L> tables[kBlock / 64];
     bool valid;
     const uint32_t ray_idx =
-        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid);
+        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid, a.order);
     const uint32_t lane = lane_id();
     WaveTables<L> &tb = tables[threadIdx.x >> 6];
 
@@ -590,7 +590,7 @@ backward_density_kernel(BwdArgs a) {
     __shared__ WaveTables<L> tables[kBlock / 64];
     bool valid;
     const uint32_t ray_idx =
-        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid);
+        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid, a.order);
     const uint32_t lane = lane_id();
     WaveTables<L> &tb = tables[threadIdx.x >> 6];
 

@@ -93,45 +93,80 @@ def _inv_s_to_tensor(inv_s, like: torch.Tensor) -> torch.Tensor:
 
 
 DEFAULT_WALK_BUDGET = 256
+# rays in no particular order are traced in sorted order from this many on
+AUTO_SORT_MIN_RAYS = 32768
 
 
-class WalkRecord:
-    """Device buffer of a forward trace's walk steps (8 bytes per step and
-    ray, ``budget`` trips per wavefront of 64 rays; sdf_walk_record in the C
-    ABI).  Valid for a backward over the same rays, start points, scene and
+class TracePlan:
+    """What a forward hands its backward (no counterpart in the reference;
+    sdf_trace_plan in the C ABI):
+
+    * ``order``: the launch order of the rays (sdf_ray_order), for rays in no
+      particular order;
+    * ``entries``: the walk record, each ray's steps (8 bytes per step, up to
+      ``budget`` trips per wavefront of 64 rays), sdfoam mode only.
+
+    Valid for a backward over the same rays, start points, scene and
     settings; the tracer checks the ray count, image width and walk limit."""
 
-    def __init__(self, entries: torch.Tensor, nbytes: int, budget: int, num_rays: int,
-                 ray_image_width: int, max_intersections: int):
-        self.entries = entries
-        self.nbytes = nbytes
-        self.budget = budget
+    def __init__(self, num_rays: int, settings, device):
         self.num_rays = num_rays
-        self.ray_image_width = ray_image_width
-        self.max_intersections = max_intersections
+        self.ray_image_width = int(settings.ray_image_width)
+        self.max_intersections = int(settings.max_intersections)
+        self.device = torch.device(device)
+        self.order = None
+        self.entries = None
+        self.nbytes = 0
+        self.budget = 0
 
-    @classmethod
-    def allocate(cls, num_rays: int, settings, budget, device) -> "WalkRecord":
+    def sort_rays(self, num_points: int, rays: torch.Tensor, start: torch.Tensor) -> None:
+        L = _lib.lib()
+        nbytes = int(L.sdf_ray_order_scratch_bytes(num_points, self.num_rays))
+        if nbytes == 0:
+            raise RuntimeError("sdf_ray_order_scratch_bytes failed")
+        # 256-byte alignment for the sort's scratch
+        scratch = torch.empty(nbytes + 256, dtype=torch.uint8, device=self.device)
+        base = scratch.data_ptr()
+        aligned = (base + 255) & ~255
+        self.order = torch.empty(self.num_rays, dtype=torch.int32, device=self.device)
+        with torch.cuda.device(self.device):
+            check(L.sdf_ray_order(num_points, self.num_rays, ptr(rays), ptr(start),
+                                  ptr(self.order), aligned, nbytes,
+                                  _lib.stream_handle(self.device)))
+        # `scratch` may be freed now: torch reuses it only for later work on
+        # this stream, which runs after the sort
+
+    def allocate_record(self, budget) -> None:
         if budget is None:
             # a wavefront walks at most max_intersections + 1 trips, plus the
             # terminating row
-            budget = min(int(settings.max_intersections) + 2, DEFAULT_WALK_BUDGET)
+            budget = min(self.max_intersections + 2, DEFAULT_WALK_BUDGET)
         budget = int(budget)
         if budget <= 0:
             raise RuntimeError("walk_budget must be positive")
-        nbytes = int(_lib.lib().sdf_walk_record_bytes(num_rays, settings.ray_image_width, budget))
-        entries = torch.empty(max(1, nbytes // 8), dtype=torch.int64, device=device)
-        return cls(entries, nbytes, budget, num_rays, int(settings.ray_image_width),
-                   int(settings.max_intersections))
+        self.nbytes = int(_lib.lib().sdf_walk_record_bytes(self.num_rays, self.ray_image_width,
+                                                           budget))
+        self.entries = torch.empty(max(1, self.nbytes // 8), dtype=torch.int64, device=self.device)
+        self.budget = budget
 
     def desc(self):
-        return _lib.WalkRecordDesc(self.entries.data_ptr(), self.nbytes, self.budget)
+        return _lib.TracePlanDesc(
+            None if self.entries is None else self.entries.data_ptr(), self.nbytes, self.budget,
+            None if self.order is None else self.order.data_ptr())
 
     def check_matches(self, num_rays: int, settings, device) -> None:
         if (num_rays != self.num_rays or int(settings.ray_image_width) != self.ray_image_width
                 or int(settings.max_intersections) != self.max_intersections
-                or self.entries.device != torch.device(device)):
-            raise RuntimeError("walk_record does not belong to these rays and settings")
+                or self.device != torch.device(device)):
+            raise RuntimeError("trace_plan does not belong to these rays and settings")
+
+
+def _auto_sort(sort_rays, settings, num_rays: int) -> bool:
+    if sort_rays is None:
+        return int(settings.ray_image_width) == 0 and num_rays >= AUTO_SORT_MIN_RAYS
+    if sort_rays and int(settings.ray_image_width) != 0:
+        raise RuntimeError("sort_rays needs rays in no image layout (shape [R, 6])")
+    return bool(sort_rays)
 
 
 class Pipeline:
@@ -237,12 +272,20 @@ class Pipeline:
                       start_point, depth_quantiles=None, weight_threshold=None,
                       max_intersections=None, return_contribution=False, alpha_mode=None,
                       inv_s=None, eps=None, sdf_channel=None, record_walk=False,
-                      walk_budget=None):
+                      walk_budget=None, sort_rays=None):
         """Reference arguments and outputs, plus (no counterpart in the
-        reference): ``record_walk=True`` in sdfoam mode also returns
-        ``"walk_record"``, the rays' steps, which ``trace_backward`` over the
-        same rays and settings takes as ``walk_record=`` to skip its face
-        scans.  ``walk_budget`` bounds the recorded trips per wavefront."""
+        reference):
+
+        * ``record_walk=True`` (sdfoam mode) records the rays' steps so that
+          the backward skips its face scans; ``walk_budget`` bounds the
+          recorded trips per wavefront;
+        * ``sort_rays``: trace rays of shape [R, 6] in sorted order
+          (sdf_ray_order); None sorts from 32768 rays on.  Outputs stay in
+          the caller's order.
+
+        When either applies, the result holds ``"trace_plan"``, which
+        ``trace_backward(trace_plan=...)`` over the same rays and settings
+        takes."""
         points_c = points.contiguous()
         attributes_c = attributes.contiguous()
         adj_c = point_adjacency.contiguous()
@@ -283,19 +326,25 @@ class Pipeline:
             didx = torch.zeros(lead + (num_q,), dtype=torch.uint32, device=dev)
         alpha = torch.zeros((num_points, 1), dtype=torch.float32, device=dev)
         scratch, nbytes = self._scratch(num_points, num_adj, dev)
-        record = None
-        if record_walk and settings.alpha_mode == _lib.SDF_ALPHA_NEUS:
-            record = WalkRecord.allocate(num_rays, settings, walk_budget, dev)
+        plan = None
+        want_record = record_walk and settings.alpha_mode == _lib.SDF_ALPHA_NEUS
+        want_sort = num_rays > 0 and _auto_sort(sort_rays, settings, num_rays)
+        if want_record or want_sort:
+            plan = TracePlan(num_rays, settings, dev)
+            if want_sort:
+                plan.sort_rays(num_points, rays_c, start_c)
+            if want_record:
+                plan.allocate_record(walk_budget)
         args = (
             self._sh_degree, C.byref(settings), num_points, ptr(points_c), ptr(attributes_c),
             num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c), ptr(start_c), num_q,
             ptr(dq), ptr(rgba), ptr(depth), ptr(didx), ptr(nisect), ptr(contribution),
             ptr(sharpness), ptr(alpha), ptr(scratch), nbytes, _lib.stream_handle(dev))
         with torch.cuda.device(dev):
-            if record is None:
+            if plan is None:
                 check(_lib.lib().sdf_trace_forward(*args))
             else:
-                check(_lib.lib().sdf_trace_forward_recorded(C.byref(record.desc()), *args))
+                check(_lib.lib().sdf_trace_forward_planned(C.byref(plan.desc()), *args))
         out = {"rgba": rgba}
         if return_depth:
             out["depth"] = depth
@@ -304,8 +353,8 @@ class Pipeline:
             out["contribution"] = contribution
         out["num_intersections"] = nisect
         out["alpha"] = alpha
-        if record is not None:
-            out["walk_record"] = record
+        if plan is not None:
+            out["trace_plan"] = plan
         return out
 
     # -- trace_backward (torch_bindings/pipeline_bindings.cpp:336-607) ------
@@ -313,7 +362,10 @@ class Pipeline:
                        start_point, rgb_out, grad_in, depth_quantiles=None, depth_indices=None,
                        depth_grad_in=None, ray_error=None, weight_threshold=None,
                        max_intersections=None, alpha_mode=None, inv_s=None, eps=None,
-                       sdf_channel=None, walk_record=None):
+                       sdf_channel=None, trace_plan=None, sort_rays=None):
+        """Reference arguments and outputs, plus ``trace_plan`` (the
+        forward's "trace_plan": its ray order and walk record) and
+        ``sort_rays`` (as in trace_forward, when no plan is given)."""
         points_c = points.contiguous()
         attributes_c = attributes.contiguous()
         adj_c = point_adjacency.contiguous()
@@ -403,8 +455,11 @@ class Pipeline:
         ray_grad = torch.zeros_like(rays_c)
         sharpness_grad = torch.zeros_like(sharpness, dtype=torch.float32)
         scratch, nbytes = self._scratch(num_points, num_adj, dev)
-        if walk_record is not None:
-            walk_record.check_matches(num_rays, settings, dev)
+        if trace_plan is not None:
+            trace_plan.check_matches(num_rays, settings, dev)
+        elif num_rays > 0 and _auto_sort(sort_rays, settings, num_rays):
+            trace_plan = TracePlan(num_rays, settings, dev)
+            trace_plan.sort_rays(num_points, rays_c, start_c)
         args = (
             self._sh_degree, C.byref(settings), num_points, ptr(points_c), ptr(attributes_c),
             num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c), ptr(start_c), num_q,
@@ -412,10 +467,10 @@ class Pipeline:
             ptr(attr_grad), ptr(point_error), ptr(sharpness), ptr(sharpness_grad),
             ptr(scratch), nbytes, _lib.stream_handle(dev))
         with torch.cuda.device(dev):
-            if walk_record is None:
+            if trace_plan is None:
                 check(_lib.lib().sdf_trace_backward(*args))
             else:
-                check(_lib.lib().sdf_trace_backward_recorded(C.byref(walk_record.desc()), *args))
+                check(_lib.lib().sdf_trace_backward_planned(C.byref(trace_plan.desc()), *args))
         out = {
             "points_grad": points_grad,
             "attr_grad": attr_grad,

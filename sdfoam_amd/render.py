@@ -3,8 +3,8 @@
 Same forward/backward contract as the reference's ``TraceRays``
 (sdfoam_model/render.py:10-189): forward returns
 ``(rgba, depth, contribution, num_intersections, ErrorBox, alpha)``; backward
-calls ``trace_backward`` with the saved forward outputs (and, in sdfoam
-mode, the forward's walk record), zeroes non-finite
+calls ``trace_backward`` with the saved forward outputs (and the forward's
+trace plan: ray order, and in sdfoam mode its walk record), zeroes non-finite
 gradients and returns gradients for ``points``, ``attributes`` and, in
 sdfoam mode, ``inv_s``.
 """
@@ -54,9 +54,9 @@ class TraceRays(torch.autograd.Function):
             record_walk=ctx.use_sdfoam,
         )
         ctx.rgba = results["rgba"]
-        # the forward's walk steps, replayed by the backward instead of
-        # scanning the cell faces again (no counterpart in the reference)
-        ctx.walk_record = results.get("walk_record", None)
+        # the forward's ray order and walk steps, replayed by the backward
+        # (no counterpart in the reference)
+        ctx.trace_plan = results.get("trace_plan", None)
         ctx.depth_indices = results.get("depth_indices", None)
         errbox = ErrorBox()
         ctx.errbox = errbox
@@ -81,7 +81,7 @@ class TraceRays(torch.autograd.Function):
             inv_s=ctx.inv_s,
             eps=ctx.eps,
             sdf_channel=ctx.sdf_channel,
-            walk_record=ctx.walk_record,
+            trace_plan=ctx.trace_plan,
         )
         points_grad = results["points_grad"].contiguous()
         attr_grad = results["attr_grad"].contiguous()
@@ -95,7 +95,7 @@ class TraceRays(torch.autograd.Function):
             sharpness_grad[~sharpness_grad.isfinite()] = 0
         del (ctx.rays, ctx.start_point, ctx.pipeline, ctx.rgba, ctx.points, ctx.attributes,
              ctx.point_adjacency, ctx.point_adjacency_offsets, ctx.depth_quantiles,
-             ctx.walk_record)
+             ctx.trace_plan)
         return (
             None,
             points_grad,

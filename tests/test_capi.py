@@ -92,14 +92,34 @@ def test_walk_record_sizes_and_errors():
     nb = L.sdf_trace_scratch_bytes(10, 4)
     for budget, nbytes, msg in ((0, 1 << 20, b"budget must be positive"),
                                 (2, 100, b"walk record must hold")):
-        rec = _lib.WalkRecordDesc(C.cast(buf, C.c_void_p).value, nbytes, budget)
-        rc = L.sdf_trace_forward_recorded(C.byref(rec), 3, C.byref(s), 10, p, p, 4, p, p, 1, p,
+        rec = _lib.TracePlanDesc(C.cast(buf, C.c_void_p).value, nbytes, budget, None)
+        rc = L.sdf_trace_forward_planned(C.byref(rec), 3, C.byref(s), 10, p, p, 4, p, p, 1, p,
                                           p, 0, None, p, None, None, p, None, p, p, p, nb, None)
         assert rc == 1 and msg in L.sdf_last_error()
-        rc = L.sdf_trace_backward_recorded(C.byref(rec), 3, C.byref(s), 10, p, p, 4, p, p, 1, p,
+        rc = L.sdf_trace_backward_planned(C.byref(rec), 3, C.byref(s), 10, p, p, 4, p, p, 1, p,
                                            p, 0, None, None, p, p, None, None, p, p, None, p,
                                            None, p, nb, None)
         assert rc == 1 and msg in L.sdf_last_error()
+
+
+def test_ray_order_and_plan_errors():
+    from sdfoam_amd import _lib
+
+    L = _lib.lib()
+    buf = (C.c_uint64 * 64)()
+    p = C.cast(buf, C.c_void_p)
+    # (the scratch size comes from rocPRIM's query for the current device, so
+    # it is only known on a GPU host)
+    assert L.sdf_ray_order(1000, 5000, p, p, None, p, 100, None) == 1
+    assert b"NULL pointer" in L.sdf_last_error()
+    assert L.sdf_ray_order(1000, 0, None, None, None, None, 0, None) == 0
+    # a ray order with an image layout is rejected before any launch
+    s = _settings(width=1)
+    plan = _lib.TracePlanDesc(None, 0, 0, p)
+    nb = L.sdf_trace_scratch_bytes(10, 4)
+    rc = L.sdf_trace_forward_planned(C.byref(plan), 3, C.byref(s), 10, p, p, 4, p, p, 1, p, p, 0,
+                                     None, p, None, None, p, None, p, p, p, nb, None)
+    assert rc == 1 and b"ray order needs ray_image_width == 0" in L.sdf_last_error()
 
 
 def test_trace_benchmark_argument_errors():

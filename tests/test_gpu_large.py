@@ -91,7 +91,7 @@ def _full_batch_properties(w, dev, say, rays_np, q_np, g_np, dg_np):
     bwd = pipe.trace_backward(pts, attrs, adj, offs, rays, start, fwd["rgba"],
                               torch.from_numpy(g_np).to(dev), q, fwd["depth_indices"],
                               torch.from_numpy(dg_np).to(dev), alpha_mode="sdfoam", inv_s=inv,
-                              walk_record=fwd["walk_record"])
+                              trace_plan=fwd["trace_plan"])
     torch.cuda.synchronize()
     say(f"full batch traced: {rays_np.size // 6} rays")
     rgba = fwd["rgba"].cpu().numpy().reshape(-1, 4)

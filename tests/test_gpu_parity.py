@@ -161,7 +161,7 @@ def test_prefetch_diff_bitexact(torch_dev, oracle_lib, cfg):
     assert np.array_equal(got, ref)
 
 
-def _forward_both(w, dev, oracle_lib, mode, record=0, inv_s=None):
+def _forward_both(w, dev, oracle_lib, mode, record=0, inv_s=None, sort_rays=None):
     import torch
 
     import sdfoam_amd
@@ -171,7 +171,7 @@ def _forward_both(w, dev, oracle_lib, mode, record=0, inv_s=None):
     pipe = sdfoam_amd.create_pipeline(w.sh_degree)
     q = to_dev(w.quantiles, dev)
     out = pipe.trace_forward(**g, depth_quantiles=q, return_contribution=True, alpha_mode=mode,
-                             inv_s=torch.tensor([inv], device=dev))
+                             inv_s=torch.tensor([inv], device=dev), sort_rays=sort_rays)
     st = pipe.walk_stats(**g, alpha_mode=mode, inv_s=torch.tensor([inv], device=dev),
                          record_cells=record)
     torch.cuda.synchronize()
@@ -242,7 +242,7 @@ def test_forward_parity_c2_sharp(torch_dev, oracle_lib):
 
 
 def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False, walk=False,
-                   walk_budget=None):
+                   walk_budget=None, sort_rays=None):
     """GPU forward + backward (with walk=True: the backward replays the
     forward's walk record, `walk_budget` trips per wavefront) and the
     oracle's backward on the same inputs."""
@@ -256,11 +256,11 @@ def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False, walk=F
     q = to_dev(w.quantiles, dev)
     inv_t = torch.tensor([inv], device=dev)
     fwd = pipe.trace_forward(**g, depth_quantiles=q, alpha_mode=mode, inv_s=inv_t,
-                             record_walk=walk, walk_budget=walk_budget)
+                             record_walk=walk, walk_budget=walk_budget, sort_rays=sort_rays)
     if walk and mode == "sdfoam":
         from sdfoam_amd.pipeline import DEFAULT_WALK_BUDGET
 
-        assert fwd["walk_record"].budget == (walk_budget or min(1024 + 2, DEFAULT_WALK_BUDGET))
+        assert fwd["trace_plan"].budget == (walk_budget or min(1024 + 2, DEFAULT_WALK_BUDGET))
     rerr = None
     if ray_error:
         rerr_np = np.random.default_rng(11).uniform(0, 1, w.rays.shape[:-1]).astype(np.float32)
@@ -269,7 +269,7 @@ def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False, walk=F
                               depth_quantiles=q, depth_indices=fwd["depth_indices"],
                               depth_grad_in=to_dev(w.depth_grad, dev), ray_error=rerr,
                               alpha_mode=mode, inv_s=inv_t,
-                              walk_record=fwd.get("walk_record"))
+                              trace_plan=fwd.get("trace_plan"))
     st = pipe.walk_stats(**g, backward=True, alpha_mode=mode, inv_s=inv_t)
     torch.cuda.synchronize()
     rgba = fwd["rgba"].cpu().numpy()
@@ -355,10 +355,64 @@ def test_walk_record_mismatch_raises(torch_dev):
     pipe = sdfoam_amd.create_pipeline(w.sh_degree)
     inv_t = torch.tensor([w.inv_s], device=torch_dev)
     fwd = pipe.trace_forward(**g, alpha_mode="sdfoam", inv_s=inv_t, record_walk=True)
-    with pytest.raises(RuntimeError, match="walk_record does not belong"):
+    with pytest.raises(RuntimeError, match="trace_plan does not belong"):
         pipe.trace_backward(**g, rgb_out=fwd["rgba"], grad_in=to_dev(w.grad_rgba, torch_dev),
                             alpha_mode="sdfoam", inv_s=inv_t, max_intersections=100,
-                            walk_record=fwd["walk_record"])
+                            trace_plan=fwd["trace_plan"])
+
+
+def flat(w):
+    """The workload with its rays as a flat [R, 6] batch (no image layout)."""
+    import dataclasses
+
+    R = w.num_rays
+    return dataclasses.replace(
+        w, rays=w.rays.reshape(R, 6), quantiles=w.quantiles.reshape(R, -1),
+        grad_rgba=w.grad_rgba.reshape(R, 4), depth_grad=w.depth_grad.reshape(R, -1),
+        extra=dict(w.extra, start=w.extra["start"].reshape(R)))
+
+
+@pytest.mark.parametrize("mode", ["sdfoam", "standard"])
+def test_sorted_rays_c1(torch_dev, oracle_lib, mode):
+    """Rays traced in the order of sdf_ray_order: same results, forward and
+    backward (the backward sorts again when it gets no plan)."""
+    w = flat(scene(1, mode=mode))
+    out, st, ref = _forward_both(w, torch_dev, oracle_lib, mode, record=1100, sort_rays=True)
+    _check_forward(out, st, ref, w, 1100)
+    assert out["trace_plan"].order is not None
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, mode, ray_error=True, sort_rays=True)
+    _check_backward(bwd, st, ref, w)
+
+
+def test_sorted_rays_with_walk_record_c2(torch_dev, oracle_lib):
+    """C2's 160000 rays as a flat batch: sorted automatically (>= 32768 rays)
+    and replayed from the walk record."""
+    w = flat(scene(2))
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "sdfoam", walk=True)
+    _check_backward(bwd, st, ref, w)
+    out, st, ref = _forward_both(w, torch_dev, oracle_lib, "sdfoam", record=0)
+    _check_forward(out, st, ref, w, 0)
+    assert out["trace_plan"].order is not None
+
+
+def test_ray_order_is_a_stable_permutation(torch_dev):
+    """sdf_ray_order: a permutation of the rays, grouped by start cell, the
+    same on every call."""
+    import torch
+
+    import sdfoam_amd
+
+    w = flat(scene(2))
+    g = gpu_scene(w, torch_dev)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    o1 = pipe.trace_forward(**g, sort_rays=True)["trace_plan"].order
+    o2 = pipe.trace_forward(**g, sort_rays=True)["trace_plan"].order
+    torch.cuda.synchronize()
+    a = o1.cpu().numpy().view(np.uint32)
+    assert np.array_equal(a, o2.cpu().numpy().view(np.uint32))
+    assert np.array_equal(np.sort(a), np.arange(w.num_rays, dtype=np.uint32))
+    st = w.extra["start"][a]
+    assert np.all(np.diff(st.astype(np.int64)) >= 0)
 
 
 def test_aabb_tree_and_nn_exact(torch_dev, oracle_lib):
