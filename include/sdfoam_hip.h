@@ -230,6 +230,35 @@ int sdf_trace_backward_planned(
     float *point_error, const float *sharpness, float *sharpness_grad,
     void *scratch, size_t scratch_bytes, void *stream);
 
+/* ---- batch prefetcher ---------------------------------------------------
+ * Replaces BatchFetcher (src/utils/batch_fetcher.h:7-21,
+ * src/utils/batch_fetcher.cpp:29-157; torch_bindings/torch_bindings.cpp:
+ * 32-63).  A worker thread gathers batches of `batch_size` rows (`stride`
+ * bytes each) of the host array `data` -- random rows seeded per element as
+ * the reference seeds them (shuffle), or consecutive rows wrapping around --
+ * into pinned staging buffers, and uploads them into a ring of 4 slots of
+ * caller-allocated device memory on its own stream.  Each
+ * sdf_batch_fetcher_next copies the next batch, in order, into `dst` on the
+ * caller's stream (the stream first waits for the batch's upload; the call
+ * blocks only until the worker has queued it).  `data` and `device_ring` must
+ * stay valid until sdf_batch_fetcher_destroy returns. */
+typedef struct sdf_batch_fetcher sdf_batch_fetcher;
+
+/* Device bytes of the ring: 4 * stride * batch_size. */
+size_t sdf_batch_fetcher_ring_bytes(size_t stride, size_t batch_size);
+
+/* num_threads: gather threads (0 = 8). */
+int sdf_batch_fetcher_create(const void *data, size_t num_bytes, size_t stride,
+                             size_t batch_size, int shuffle, void *device_ring,
+                             size_t device_ring_bytes, uint32_t num_threads,
+                             sdf_batch_fetcher **out);
+int sdf_batch_fetcher_next(sdf_batch_fetcher *fetcher, void *dst, void *stream);
+int sdf_batch_fetcher_destroy(sdf_batch_fetcher *fetcher);
+
+/* The rows batch `batch_index` takes (host computation, for tests). */
+void sdf_batch_rows(uint32_t batch_index, size_t batch_size, size_t num_rows,
+                    int shuffle, uint32_t *rows);
+
 /* Implicit AABB tree over consecutive point pairs, tree [pow2(N), 2, 3]
  * (node (d, i) at 2^td - 2^(d+1) + i; the last entry is zeroed).
  * Replaces build_aabb_tree (src/aabb_tree/aabb_tree.h:10-13,

@@ -409,3 +409,34 @@ def trace_benchmark(sh_degree, points, attributes, adjacency, offsets, adjacent_
     if rc != 0:
         raise RuntimeError("oracle_trace_benchmark failed")
     return RenderResult(out, rgbt, nis)
+
+
+# ---------------------------------------------------------------------------
+# BatchFetcher row selection (src/utils/batch_fetcher.cpp:63-72 with the RNG
+# of src/utils/random.h:11-56), restated with numpy uint32 arithmetic.
+
+def _mix32(x: np.ndarray) -> np.ndarray:
+    x = x.astype(np.uint32)
+    with np.errstate(over="ignore"):
+        x ^= x >> np.uint32(17)
+        x *= np.uint32(0xED5AD4BB)
+        x ^= x >> np.uint32(11)
+        x *= np.uint32(0xAC4C1B51)
+        x ^= x >> np.uint32(15)
+        x *= np.uint32(0x31848BAB)
+        x ^= x >> np.uint32(14)
+    return x
+
+
+def batch_rows(batch_index: int, batch_size: int, num_rows: int, shuffle: bool) -> np.ndarray:
+    """Rows of batch `batch_index`: element j uses the first draw of
+    make_rng(batch_index * batch_size + j) scaled by randint(rng, 0, n), or
+    row (batch_index * batch_size + j) mod n without shuffling."""
+    k = np.uint64(batch_index) * np.uint64(batch_size) + np.arange(batch_size, dtype=np.uint64)
+    if not shuffle:
+        return (k % np.uint64(num_rows)).astype(np.uint32)
+    seed = (k & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+    draw = _mix32(seed ^ np.uint32(0x2815DB5B))
+    diff = np.uint32(num_rows)
+    x = draw // (np.uint32(0xFFFFFFFF) // diff)
+    return np.minimum(x, diff - np.uint32(1)).astype(np.uint32)

@@ -3,11 +3,13 @@
 Drop-in for the tracing surface of the reference's ``sdfoam`` module:
 ``create_pipeline`` -> ``Pipeline.trace_forward`` / ``trace_backward``,
 ``build_aabb_tree``, ``nn``, plus the ``TraceRays`` autograd Function and
-``get_starting_point``.  Compute runs in libsdfoam_hip.so (hand-written HIP
+``get_starting_point``, and ``BatchFetcher`` (the training loop's batch
+prefetcher).  Compute runs in libsdfoam_hip.so (hand-written HIP
 for gfx950) through its C ABI; importing this package does not need a GPU,
 calling the tracer does.
 """
 
+from .fetch import BatchFetcher
 from .pipeline import Pipeline, create_pipeline, prefetch_adjacent_diff
 from .render import ErrorBox, TraceRays
 from .spatial import build_aabb_tree, get_starting_point, nn
@@ -21,4 +23,5 @@ __all__ = [
     "build_aabb_tree",
     "nn",
     "get_starting_point",
+    "BatchFetcher",
 ]

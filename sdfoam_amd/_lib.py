@@ -30,6 +30,11 @@ EXPORTS = (
     "sdf_ray_order",
     "sdf_trace_forward_planned",
     "sdf_trace_backward_planned",
+    "sdf_batch_fetcher_ring_bytes",
+    "sdf_batch_fetcher_create",
+    "sdf_batch_fetcher_next",
+    "sdf_batch_fetcher_destroy",
+    "sdf_batch_rows",
     "sdf_build_aabb_tree",
     "sdf_nn",
     "sdf_trace_walk_stats",
@@ -144,6 +149,16 @@ def lib() -> C.CDLL:
     L.sdf_trace_forward_planned.argtypes = [C.POINTER(TracePlanDesc)] + L.sdf_trace_forward.argtypes
     L.sdf_trace_backward_planned.restype = C.c_int
     L.sdf_trace_backward_planned.argtypes = [C.POINTER(TracePlanDesc)] + L.sdf_trace_backward.argtypes
+    L.sdf_batch_fetcher_ring_bytes.restype = SZ
+    L.sdf_batch_fetcher_ring_bytes.argtypes = [SZ, SZ]
+    L.sdf_batch_fetcher_create.restype = C.c_int
+    L.sdf_batch_fetcher_create.argtypes = [P, SZ, SZ, SZ, C.c_int, P, SZ, U32, C.POINTER(P)]
+    L.sdf_batch_fetcher_next.restype = C.c_int
+    L.sdf_batch_fetcher_next.argtypes = [P, P, P]
+    L.sdf_batch_fetcher_destroy.restype = C.c_int
+    L.sdf_batch_fetcher_destroy.argtypes = [P]
+    L.sdf_batch_rows.restype = None
+    L.sdf_batch_rows.argtypes = [U32, SZ, SZ, C.c_int, P]
     L.sdf_build_aabb_tree.restype = C.c_int
     L.sdf_build_aabb_tree.argtypes = [P, U32, P, P]
     L.sdf_nn.restype = C.c_int

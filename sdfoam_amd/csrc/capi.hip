@@ -10,8 +10,10 @@
 using namespace sdfoam_hip;
 
 namespace {
-
 thread_local char g_err[512] = "";
+} // namespace
+
+namespace sdfoam_hip {
 
 int fail(int code, const char *fmt, ...) {
     va_list ap;
@@ -24,6 +26,10 @@ int fail(int code, const char *fmt, ...) {
 int hip_fail(hipError_t e, const char *where) {
     return fail(SDF_E_HIP, "%s: %s", where, hipGetErrorString(e));
 }
+
+} // namespace sdfoam_hip
+
+namespace {
 
 // ---- optional kernel timing ----------------------------------------------
 // When enabled, every kernel launch is bracketed by two HIP events recorded

@@ -6,6 +6,11 @@
 
 namespace sdfoam_hip {
 
+// Set the calling thread's sdf_last_error() message and return `code`
+// (capi.hip).
+int fail(int code, const char *fmt, ...);
+int hip_fail(hipError_t e, const char *where);
+
 // Walk record: for every wavefront, `budget` trips of 64 entries (one per
 // lane) of {next cell, bits of t1}, with next = kNoIndex where the lane's
 // walk ended on that trip and kWalkUnrecorded where the lane was not
