@@ -41,13 +41,24 @@ extern "C" {
  * ray_image_width is a layout hint with no counterpart in the reference: 0
  * for rays in any order, or W when the rays are image rows of W pixels
  * ([..., H, W, 6]); the kernels then give each wavefront an 8x8 pixel tile.
- * Results do not depend on it. */
+ * Results do not depend on it.
+ * attr_type is the pipeline's attribute type (the reference's
+ * CUDATracingPipeline<float | __half, L>, src/tracing/pipeline.cu:1482-1502):
+ * with SDF_ATTR_F16, attributes, ray_rgba, ray_rgba_grad, ray_error,
+ * point_contribution, attribute_grad and point_error are fp16; positions,
+ * rays, depths, quantiles, alpha, points_grad and sharpness stay fp32.  The
+ * fp16 buffers that are accumulated atomically (point_contribution,
+ * attribute_grad, point_error) must be 4-byte aligned and hold one padding
+ * half past an odd element count. */
+#define SDF_ATTR_F32 0u
+#define SDF_ATTR_F16 1u
 typedef struct sdf_trace_settings {
     float weight_threshold;
     uint32_t max_intersections;
     uint32_t alpha_mode;
     int32_t sdf_channel;
     uint32_t ray_image_width;
+    uint32_t attr_type;
 } sdf_trace_settings;
 
 /* Library version string. */

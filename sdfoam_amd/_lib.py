@@ -14,6 +14,8 @@ from .build import LIB_PATH
 SDF_OK = 0
 SDF_ALPHA_STANDARD = 0
 SDF_ALPHA_NEUS = 1
+SDF_ATTR_F32 = 0
+SDF_ATTR_F16 = 1
 
 # every symbol include/sdfoam_hip.h declares
 EXPORTS = (
@@ -60,6 +62,7 @@ class TraceSettings(C.Structure):
         ("alpha_mode", C.c_uint32),
         ("sdf_channel", C.c_int32),
         ("ray_image_width", C.c_uint32),
+        ("attr_type", C.c_uint32),
     ]
 
 

@@ -71,6 +71,8 @@ int check_scene(int sh_degree, const sdf_trace_settings *settings, uint32_t num_
     if (!settings) return fail(SDF_E_INVALID, "settings must not be NULL");
     if (settings->alpha_mode != SDF_ALPHA_STANDARD && settings->alpha_mode != SDF_ALPHA_NEUS)
         return fail(SDF_E_INVALID, "alpha_mode must be 0 (standard) or 1 (sdfoam)");
+    if (settings->attr_type != SDF_ATTR_F32 && settings->attr_type != SDF_ATTR_F16)
+        return fail(SDF_E_INVALID, "attr_type must be 0 (float32) or 1 (float16)");
     const int D = 1 + 3 * (sh_degree + 1) * (sh_degree + 1);
     if (settings->sdf_channel >= D)
         return fail(SDF_E_INVALID, "sdf_channel %d out of range for attribute dim %d",
@@ -151,8 +153,11 @@ int trace_forward_impl(const sdf_trace_plan *plan, int sh_degree,
     if (num_rays > 0 && !ray_rgba) return fail(SDF_E_INVALID, "ray_rgba must not be NULL");
     if (num_depth_quantiles > 0 && (!depth_quantiles || !quantile_depths || !quantile_point_indices))
         return fail(SDF_E_INVALID, "depth buffers must not be NULL when num_depth_quantiles > 0");
-    if ((reinterpret_cast<uintptr_t>(ray_rgba) & 15u) != 0)
-        return fail(SDF_E_INVALID, "ray_rgba must be 16-byte aligned");
+    const bool half = settings->attr_type == SDF_ATTR_F16;
+    if ((reinterpret_cast<uintptr_t>(ray_rgba) & (half ? 7u : 15u)) != 0)
+        return fail(SDF_E_INVALID, "ray_rgba must be %d-byte aligned", half ? 8 : 16);
+    if (half && (reinterpret_cast<uintptr_t>(point_contribution) & 3u) != 0)
+        return fail(SDF_E_INVALID, "fp16 point_contribution must be 4-byte aligned");
     WalkRecordArgs rec = {};
     const uint32_t *order = nullptr;
     rc = check_plan(plan, num_rays, settings->ray_image_width, rec, order);
@@ -184,7 +189,7 @@ int trace_forward_impl(const sdf_trace_plan *plan, int sh_degree,
     a.contribution = point_contribution;
     a.alpha_out = alpha_output;
     tbegin(SDF_KERNEL_FORWARD, s);
-    e = launch_forward(sh_degree, a, settings->alpha_mode == SDF_ALPHA_NEUS, false, s);
+    e = launch_forward(sh_degree, a, settings->alpha_mode == SDF_ALPHA_NEUS, false, half, s);
     tend(s);
     if (e != hipSuccess) return hip_fail(e, "forward");
     return SDF_OK;
@@ -214,9 +219,14 @@ int trace_backward_impl(const sdf_trace_plan *plan, int sh_degree,
         return fail(SDF_E_INVALID, "depth_grad must be provided if depth_quantiles is provided");
     if (!neus && num_depth_quantiles > 0 && !quantile_point_indices)
         return fail(SDF_E_INVALID, "depth_indices must be provided in standard mode");
+    const bool half = settings->attr_type == SDF_ATTR_F16;
     if (((reinterpret_cast<uintptr_t>(ray_rgba) | reinterpret_cast<uintptr_t>(ray_rgba_grad)) &
-         15u) != 0)
-        return fail(SDF_E_INVALID, "ray_rgba and ray_rgba_grad must be 16-byte aligned");
+         (half ? 7u : 15u)) != 0)
+        return fail(SDF_E_INVALID, "ray_rgba and ray_rgba_grad must be %d-byte aligned",
+                    half ? 8 : 16);
+    if (half && ((reinterpret_cast<uintptr_t>(attribute_grad) |
+                  reinterpret_cast<uintptr_t>(point_error)) & 3u) != 0)
+        return fail(SDF_E_INVALID, "fp16 attribute_grad and point_error must be 4-byte aligned");
     WalkRecordArgs rec = {};
     const uint32_t *order = nullptr;
     rc = check_plan(plan, num_rays, settings->ray_image_width, rec, order);
@@ -251,7 +261,7 @@ int trace_backward_impl(const sdf_trace_plan *plan, int sh_degree,
     a.point_error = ray_error ? point_error : nullptr;
     a.sharpness_grad = sharpness_grad;
     tbegin(SDF_KERNEL_BACKWARD, s);
-    e = launch_backward(sh_degree, a, neus, false, s);
+    e = launch_backward(sh_degree, a, neus, false, half, s);
     tend(s);
     if (e != hipSuccess) return hip_fail(e, "backward");
     return SDF_OK;
@@ -339,6 +349,8 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings, uint3
     if (!settings) return fail(SDF_E_INVALID, "settings must not be NULL");
     if (settings->alpha_mode != SDF_ALPHA_STANDARD && settings->alpha_mode != SDF_ALPHA_NEUS)
         return fail(SDF_E_INVALID, "alpha_mode must be 0 (standard) or 1 (sdfoam)");
+    if (settings->attr_type != SDF_ATTR_F32 && settings->attr_type != SDF_ATTR_F16)
+        return fail(SDF_E_INVALID, "attr_type must be 0 (float32) or 1 (float16)");
     const int D = 1 + 3 * (sh_degree + 1) * (sh_degree + 1);
     if (settings->sdf_channel >= D)
         return fail(SDF_E_INVALID, "sdf_channel %d out of range for attribute dim %d",
@@ -389,7 +401,8 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings, uint3
     a.out = output_rgba;
     hipStream_t s = static_cast<hipStream_t>(stream);
     tbegin(SDF_KERNEL_RENDER, s);
-    hipError_t e = launch_render(sh_degree, a, settings->alpha_mode == SDF_ALPHA_NEUS, s);
+    hipError_t e = launch_render(sh_degree, a, settings->alpha_mode == SDF_ALPHA_NEUS,
+                                 settings->attr_type == SDF_ATTR_F16, s);
     tend(s);
     if (e != hipSuccess) return hip_fail(e, "trace_benchmark");
     return SDF_OK;
@@ -519,7 +532,7 @@ int sdf_trace_walk_stats(int sh_degree, const sdf_trace_settings *settings, int 
         a.faces_stepped = faces_stepped;
         a.cells = cells;
         a.cells_stride = cells ? cells_stride : 0;
-        e = launch_forward(sh_degree, a, neus, true, s);
+        e = launch_forward(sh_degree, a, neus, true, settings->attr_type == SDF_ATTR_F16, s);
     } else {
         BwdArgs a = {};
         a.scene = sc;
@@ -535,7 +548,7 @@ int sdf_trace_walk_stats(int sh_degree, const sdf_trace_settings *settings, int 
         a.faces_stepped = faces_stepped;
         a.cells = cells;
         a.cells_stride = cells ? cells_stride : 0;
-        e = launch_backward(sh_degree, a, neus, true, s);
+        e = launch_backward(sh_degree, a, neus, true, settings->attr_type == SDF_ATTR_F16, s);
     }
     if (e != hipSuccess) return hip_fail(e, "walk_stats");
     return SDF_OK;

@@ -29,6 +29,78 @@ __device__ __forceinline__ uint32_t f32_to_f16(float x) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
+// ---- attribute types -------------------------------------------------------
+// Pipelines trace fp32 or fp16 attributes (CUDATracingPipeline<float | __half,
+// L>, src/tracing/pipeline.cu:1482-1502).  Attributes, rgba, its gradient,
+// ray error, contribution, attribute gradients and point error have the
+// attribute type; arithmetic is fp32 throughout.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+template <typename AT>
+__device__ __forceinline__ float4 load_attr4(const void *base, uint64_t i) {
+    if constexpr (sizeof(AT) == 4) {
+        return reinterpret_cast<const float4 *>(base)[i];
+    } else {
+        const uint2 raw = reinterpret_cast<const uint2 *>(base)[i];
+        return make_float4(f16_to_f32(raw.x), f16_to_f32(raw.x >> 16), f16_to_f32(raw.y),
+                           f16_to_f32(raw.y >> 16));
+    }
+}
+
+template <typename AT>
+__device__ __forceinline__ void store_attr4(void *base, uint64_t i, float4 v) {
+    if constexpr (sizeof(AT) == 4) {
+        reinterpret_cast<float4 *>(base)[i] = v;
+    } else {
+        reinterpret_cast<uint2 *>(base)[i] =
+            make_uint2(f32_to_f16(v.x) | (f32_to_f16(v.y) << 16), f32_to_f16(v.z) | (f32_to_f16(v.w) << 16));
+    }
+}
+
+// fp16 atomics are packed pairs (global_atomic_pk_add_f16 on the 4-byte word
+// holding the element); the other half of the word gets + 0.  Buffers must
+// be 4-byte aligned and hold one padding half past an odd element count.
+__device__ __forceinline__ void pk_add_f16(_Float16 *word_lo, _Float16 lo, _Float16 hi) {
+    half2_t v = {lo, hi};
+    __builtin_amdgcn_global_atomic_fadd_v2f16(
+        (__attribute__((address_space(1))) half2_t *)word_lo, v);
+}
+
+template <typename AT>
+__device__ __forceinline__ void atomic_add_elem(void *base, uint64_t i, float v) {
+    if constexpr (sizeof(AT) == 4) {
+        atomicAdd(reinterpret_cast<float *>(base) + i, v);
+    } else {
+        _Float16 *p = reinterpret_cast<_Float16 *>(base) + i;
+        if ((reinterpret_cast<uintptr_t>(p) & 3u) == 0) {
+            pk_add_f16(p, (_Float16)v, (_Float16)0.0f);
+        } else {
+            pk_add_f16(p - 1, (_Float16)0.0f, (_Float16)v);
+        }
+    }
+}
+
+// Lanes 0..n-1 of the wave add v to elements row[0..n-1] of row `row` of an
+// [*, n] buffer.  Called by all 64 lanes (fp16 pairs neighbouring lanes'
+// values into one packed atomic).
+template <typename AT>
+__device__ __forceinline__ void atomic_add_row(void *base, uint64_t row, uint32_t lane,
+                                               uint32_t n, float v) {
+    if constexpr (sizeof(AT) == 4) {
+        if (lane < n) atomicAdd(reinterpret_cast<float *>(base) + row * n + lane, v);
+    } else {
+        const float vn = __shfl_down(v, 1, 64);
+        _Float16 *p = reinterpret_cast<_Float16 *>(base) + row * n + lane;
+        if (lane < n) {
+            if ((reinterpret_cast<uintptr_t>(p) & 3u) == 0) {
+                pk_add_f16(p, (_Float16)v, lane + 1 < n ? (_Float16)vn : (_Float16)0.0f);
+            } else if (lane == 0) {
+                pk_add_f16(p - 1, (_Float16)0.0f, (_Float16)v);
+            }
+        }
+    }
+}
+
 struct RayF {
     float ox, oy, oz;
     float dx, dy, dz;
@@ -137,9 +209,10 @@ __device__ __forceinline__ void sh_basis(float x, float y, float z, float *sh) {
     }
 }
 
-// rgb = max(0, 0.5 + sum_j Y_j * row[3j + c])  (src/tracing/sh_utils.cuh:64-75)
-template <int L>
-__device__ __forceinline__ void sh_rgb(const float *sh, const float *__restrict__ row,
+// rgb = max(0, 0.5 + sum_j Y_j * row[3j + c])  (src/tracing/sh_utils.cuh:64-75);
+// fp16 rows are widened exactly (sh_utils.cuh:79, `(float)sh_rgb_vals[i]`).
+template <int L, typename AT>
+__device__ __forceinline__ void sh_rgb(const float *sh, const AT *__restrict__ row,
                                        float &r, float &g, float &b) {
     constexpr int nsh = (L + 1) * (L + 1);
     float a0 = 0.5f, a1 = 0.5f, a2 = 0.5f;
@@ -147,9 +220,9 @@ __device__ __forceinline__ void sh_rgb(const float *sh, const float *__restrict_
     // the kernels' register count low (same FMA order per channel)
 #pragma unroll 4
     for (int j = 0; j < nsh; ++j) {
-        a0 = fmaf(sh[j], row[3 * j + 0], a0);
-        a1 = fmaf(sh[j], row[3 * j + 1], a1);
-        a2 = fmaf(sh[j], row[3 * j + 2], a2);
+        a0 = fmaf(sh[j], (float)row[3 * j + 0], a0);
+        a1 = fmaf(sh[j], (float)row[3 * j + 1], a1);
+        a2 = fmaf(sh[j], (float)row[3 * j + 2], a2);
     }
     r = fmaxf(a0, 0.0f);
     g = fmaxf(a1, 0.0f);
@@ -158,7 +231,7 @@ __device__ __forceinline__ void sh_rgb(const float *sh, const float *__restrict_
 
 struct SceneView {
     const float *__restrict__ points;
-    const float *__restrict__ attrs;
+    const void *__restrict__ attrs; // [N, D] of the pipeline's attribute type
     const uint32_t *__restrict__ adj;
     const uint32_t *__restrict__ offs;
     const uint2 *__restrict__ diff; // fp16 x, y | z, 0 per CSR entry

@@ -49,11 +49,11 @@ struct FwdArgs {
     uint32_t num_quantiles;
     const float *quantiles;
     const float *sharpness;
-    float *rgba;
+    void *rgba; // [R, 4] of the attribute type
     float *depth;
     uint32_t *depth_indices;
     uint32_t *num_intersections;
-    float *contribution;
+    void *contribution; // [N] of the attribute type
     float *alpha_out;
     // walk statistics (STATS instantiation only)
     uint64_t *visit_hash;
@@ -76,14 +76,14 @@ struct BwdArgs {
     uint32_t num_quantiles;
     const float *quantiles;
     const uint32_t *depth_indices;
-    const float *rgba;
-    const float *rgba_grad;
+    const void *rgba;      // attribute type
+    const void *rgba_grad; // attribute type
     const float *depth_grad;
-    const float *ray_error;
+    const void *ray_error; // attribute type
     const float *sharpness;
     float *points_grad;
-    float *attr_grad;
-    float *point_error;
+    void *attr_grad;   // attribute type
+    void *point_error; // attribute type
     float *sharpness_grad;
     // walk statistics (STATS instantiation only)
     uint64_t *visit_hash;
@@ -109,7 +109,7 @@ struct RenderArgs {
     uint32_t *out;
 };
 
-hipError_t launch_render(int L, const RenderArgs &a, bool neus, hipStream_t stream);
+hipError_t launch_render(int L, const RenderArgs &a, bool neus, bool half, hipStream_t stream);
 
 // Ray launch order for rays in no particular order: sort by (start cell,
 // Morton code of the octahedral direction) so a wavefront's rays start
@@ -122,8 +122,11 @@ hipError_t launch_ray_order(uint32_t num_points, uint32_t num_rays, const float 
 hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32_t num_adj,
                                 const uint32_t *adj, const uint32_t *offs, uint2 *diff,
                                 hipStream_t stream);
-hipError_t launch_forward(int L, const FwdArgs &a, bool neus, bool stats, hipStream_t stream);
-hipError_t launch_backward(int L, const BwdArgs &a, bool neus, bool stats, hipStream_t stream);
+// half: fp16 attributes (settings.attr_type == SDF_ATTR_F16)
+hipError_t launch_forward(int L, const FwdArgs &a, bool neus, bool stats, bool half,
+                          hipStream_t stream);
+hipError_t launch_backward(int L, const BwdArgs &a, bool neus, bool stats, bool half,
+                           hipStream_t stream);
 hipError_t launch_fpmath(int op, const float *in, void *out, uint64_t n, hipStream_t stream);
 
 hipError_t launch_build_aabb_tree(const float *points, uint32_t num_points, float *tree,

@@ -74,7 +74,7 @@ __device__ __forceinline__ int first_lane(uint64_t mask) { return __builtin_ctzl
 // ---------------------------------------------------------------------------
 // forward (src/tracing/pipeline.cu:36-264)
 
-template <int L, bool NEUS, bool STATS>
+template <int L, bool NEUS, bool STATS, typename AT>
 __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
@@ -135,11 +135,11 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         if (si.stepped) {
             const uint32_t cell = ws.cell;
             const float t0 = ws.t0, t1 = si.t1;
-            const float *__restrict__ row = a.scene.attrs + (uint64_t)cell * D;
-            float s = row[D - 1];
+            const AT *__restrict__ row = static_cast<const AT *>(a.scene.attrs) + (uint64_t)cell * D;
+            float s = (float)row[D - 1];
             const float dt = fmaxf(t1 - t0, 0.0f);
             if (neus_alpha) {
-                const float d = row[sdf_ch];
+                const float d = (float)row[sdf_ch];
                 const float phi = sdf_sigmoidf(-sha * d);
                 s = sha * phi * (1.0f - phi);
             }
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
             const float Tn = T * (1.0f - alpha);
             if constexpr (!STATS) {
                 float r, g, b;
-                if (NEUS || row[D - 1] > 1e-6f) {
+                if (NEUS || (float)row[D - 1] > 1e-6f) {
                     sh_rgb<L>(sh, row, r, g, b);
                 } else {
                     r = g = b = 0.0f;
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
                     float sum = 0.0f;
                     for (uint64_t mm = grp; mm; mm &= mm - 1) sum += readlane_f(w, first_lane(mm));
                     const float al = readlane_f(alpha, leader);
-                    if (lane == 0 && a.contribution) atomicAdd(a.contribution + c, sum);
+                    if (lane == 0 && a.contribution) atomic_add_elem<AT>(a.contribution, c, sum);
                     if (lane == 1 && a.alpha_out) a.alpha_out[c] = al;
                 }
             }
@@ -223,8 +223,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         a.depth[(uint64_t)ray_idx * Q + k] = -1.0f;
         a.depth_indices[(uint64_t)ray_idx * Q + k] = kNoIndex;
     }
-    float4 out = make_float4(C0, C1, C2, 1.0f - T);
-    *reinterpret_cast<float4 *>(a.rgba + 4ull * ray_idx) = out;
+    store_attr4<AT>(a.rgba, ray_idx, make_float4(C0, C1, C2, 1.0f - T));
     if (a.num_intersections) a.num_intersections[ray_idx] = ws.n;
 }
 
@@ -306,11 +305,11 @@ __device__ __forceinline__ int pop_member(uint64_t &mm) {
 // every flushed cell lanes 0..2 add the flushed position gradients.  The
 // stepping lanes publish their values in the wave's LDS tables; the owner
 // lane of each component reads the members four at a time.
-template <int L>
+template <int L, typename AT>
 __device__ __forceinline__ void grouped_backward_updates(
     bool stepped, uint32_t cell, float gr, float gg, float gb, float g_last, int last_ch,
     float pe, bool flush, uint32_t flush_idx, const float *flush_g, WaveTables<L> &tb,
-    float *__restrict__ attr_grad, float *__restrict__ point_error,
+    void *__restrict__ attr_grad, void *__restrict__ point_error,
     float *__restrict__ points_grad) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
@@ -354,8 +353,8 @@ __device__ __forceinline__ void grouped_backward_updates(
                 pacc = pacc + e[u];
             }
         }
-        if (lane < (uint32_t)D) atomicAdd(attr_grad + (uint64_t)c * D + lane, acc);
-        if (point_error && lane == 63u) atomicAdd(point_error + c, pacc);
+        atomic_add_row<AT>(attr_grad, c, lane, (uint32_t)D, acc);
+        if (point_error && lane == 63u) atomic_add_elem<AT>(point_error, c, pacc);
     }
     todo = __ballot(flush);
     const int pl = lane < 3u ? (int)lane : 0;
@@ -398,7 +397,7 @@ __device__ __forceinline__ void tables_init(WaveTables<L> &tb, const float *sh) 
 // ---------------------------------------------------------------------------
 // backward_sdf (src/tracing/pipeline.cu:267-550)
 
-template <int L, bool STATS>
+template <int L, bool STATS, typename AT>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(5, 8))) void
 backward_sdf_kernel(BwdArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
@@ -430,10 +429,11 @@ backward_sdf_kernel(BwdArgs a) {
     float4 g4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float4 c4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (!STATS && valid) {
-        g4 = *reinterpret_cast<const float4 *>(a.rgba_grad + 4ull * ray_idx);
-        c4 = *reinterpret_cast<const float4 *>(a.rgba + 4ull * ray_idx);
+        g4 = load_attr4<AT>(a.rgba_grad, ray_idx);
+        c4 = load_attr4<AT>(a.rgba, ray_idx);
     }
-    const float err = (valid && a.ray_error) ? a.ray_error[ray_idx] : 0.0f;
+    const float err =
+        (valid && a.ray_error) ? (float)static_cast<const AT *>(a.ray_error)[ray_idx] : 0.0f;
 
     float T = 1.0f;
     float C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
@@ -495,9 +495,9 @@ backward_sdf_kernel(BwdArgs a) {
                 if (a.cells && rec < a.cells_stride) a.cells[(uint64_t)ray_idx * a.cells_stride + rec] = cell;
                 ++rec;
             }
-            const float *__restrict__ row = a.scene.attrs + (uint64_t)cell * D;
+            const AT *__restrict__ row = static_cast<const AT *>(a.scene.attrs) + (uint64_t)cell * D;
             const float dt = fmaxf(t1 - t0, 0.0f);
-            const float d = row[sdf_ch];
+            const float d = (float)row[sdf_ch];
             const float phi = sdf_sigmoidf(-sha * d);
             const float s = sha * phi * (1.0f - phi);
             const float alpha = 1.0f - sdf_expf(-s * dt);
@@ -557,7 +557,7 @@ backward_sdf_kernel(BwdArgs a) {
             keep = T > thr;
         }
         if constexpr (!STATS) {
-            grouped_backward_updates<L>(si.stepped, ws.cell, dr, dg, db, dsdf,
+            grouped_backward_updates<L, AT>(si.stepped, ws.cell, dr, dg, db, dsdf,
                                         write_sdf ? sdf_ch : -1, pe, flush, flush_idx, flush_g,
                                         tb, a.attr_grad, a.point_error, a.points_grad);
         }
@@ -582,7 +582,7 @@ backward_sdf_kernel(BwdArgs a) {
 
 // backward, density mode (src/tracing/pipeline.cu:553-791); the walk runs in
 // the reference's unsafe mode (no t > t0 test, :782-790).
-template <int L, bool STATS>
+template <int L, bool STATS, typename AT>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(5, 8))) void
 backward_density_kernel(BwdArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
@@ -611,16 +611,18 @@ backward_density_kernel(BwdArgs a) {
     float4 c4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float cur_dg = 0.0f; // src/tracing/pipeline.cu:620-629
     if (!STATS && valid) {
-        g4 = *reinterpret_cast<const float4 *>(a.rgba_grad + 4ull * ray_idx);
-        c4 = *reinterpret_cast<const float4 *>(a.rgba + 4ull * ray_idx);
+        g4 = load_attr4<AT>(a.rgba_grad, ray_idx);
+        c4 = load_attr4<AT>(a.rgba, ray_idx);
         for (uint32_t k = 0; k < Q; ++k) {
             const uint32_t pi = a.depth_indices[(uint64_t)ray_idx * Q + k];
             if (pi != kNoIndex && pi < a.scene.num_points) {
-                cur_dg = cur_dg + rdg[k] / a.scene.attrs[(uint64_t)pi * D + D - 1];
+                cur_dg = cur_dg +
+                         rdg[k] / (float)static_cast<const AT *>(a.scene.attrs)[(uint64_t)pi * D + D - 1];
             }
         }
     }
-    const float err = (valid && a.ray_error) ? a.ray_error[ray_idx] : 0.0f;
+    const float err =
+        (valid && a.ray_error) ? (float)static_cast<const AT *>(a.ray_error)[ray_idx] : 0.0f;
 
     float T = 1.0f;
     float C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
@@ -654,8 +656,8 @@ backward_density_kernel(BwdArgs a) {
                 if (a.cells && rec < a.cells_stride) a.cells[(uint64_t)ray_idx * a.cells_stride + rec] = cell;
                 ++rec;
             }
-            const float *__restrict__ row = a.scene.attrs + (uint64_t)cell * D;
-            const float s = row[D - 1];
+            const AT *__restrict__ row = static_cast<const AT *>(a.scene.attrs) + (uint64_t)cell * D;
+            const float s = (float)row[D - 1];
             const float dt = fmaxf(t1 - t0, 0.0f);
             const float alpha = 1.0f - sdf_expf(-s * dt);
             const float Tn = T * (1.0f - alpha);
@@ -709,7 +711,7 @@ backward_density_kernel(BwdArgs a) {
             keep = T > thr;
         }
         if constexpr (!STATS) {
-            grouped_backward_updates<L>(si.stepped, ws.cell, dr, dg, db, dds, D - 1, pe, flush,
+            grouped_backward_updates<L, AT>(si.stepped, ws.cell, dr, dg, db, dds, D - 1, pe, flush,
                                         flush_idx, flush_g, tb, a.attr_grad, a.point_error,
                                         a.points_grad);
         }
@@ -740,62 +742,80 @@ hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32
     return hipGetLastError();
 }
 
-template <int L>
+template <int L, typename AT>
 static hipError_t launch_forward_L(const FwdArgs &a, bool neus, bool stats, hipStream_t stream) {
     const dim3 grid(grid_blocks_for_tiles(a.num_tiles));
     if (neus) {
         if (stats) {
-            hipLaunchKernelGGL((forward_kernel<L, true, true>), grid, dim3(kBlock), 0, stream, a);
+            hipLaunchKernelGGL((forward_kernel<L, true, true, AT>), grid, dim3(kBlock), 0, stream, a);
         } else {
-            hipLaunchKernelGGL((forward_kernel<L, true, false>), grid, dim3(kBlock), 0, stream, a);
+            hipLaunchKernelGGL((forward_kernel<L, true, false, AT>), grid, dim3(kBlock), 0, stream, a);
         }
     } else {
         if (stats) {
-            hipLaunchKernelGGL((forward_kernel<L, false, true>), grid, dim3(kBlock), 0, stream, a);
+            hipLaunchKernelGGL((forward_kernel<L, false, true, AT>), grid, dim3(kBlock), 0, stream, a);
         } else {
-            hipLaunchKernelGGL((forward_kernel<L, false, false>), grid, dim3(kBlock), 0, stream, a);
+            hipLaunchKernelGGL((forward_kernel<L, false, false, AT>), grid, dim3(kBlock), 0, stream, a);
         }
     }
     return hipGetLastError();
 }
 
-hipError_t launch_forward(int L, const FwdArgs &a, bool neus, bool stats, hipStream_t stream) {
+template <typename AT>
+static hipError_t launch_forward_T(int L, const FwdArgs &a, bool neus, bool stats,
+                                   hipStream_t stream) {
     switch (L) {
-    case 0: return launch_forward_L<0>(a, neus, stats, stream);
-    case 1: return launch_forward_L<1>(a, neus, stats, stream);
-    case 2: return launch_forward_L<2>(a, neus, stats, stream);
-    case 3: return launch_forward_L<3>(a, neus, stats, stream);
+    case 0: return launch_forward_L<0, AT>(a, neus, stats, stream);
+    case 1: return launch_forward_L<1, AT>(a, neus, stats, stream);
+    case 2: return launch_forward_L<2, AT>(a, neus, stats, stream);
+    case 3: return launch_forward_L<3, AT>(a, neus, stats, stream);
     default: return hipErrorInvalidValue;
     }
 }
 
-template <int L>
+hipError_t launch_forward(int L, const FwdArgs &a, bool neus, bool stats, bool half,
+                          hipStream_t stream) {
+    return half ? launch_forward_T<_Float16>(L, a, neus, stats, stream)
+                : launch_forward_T<float>(L, a, neus, stats, stream);
+}
+
+template <int L, typename AT>
 static hipError_t launch_backward_L(const BwdArgs &a, bool neus, bool stats, hipStream_t stream) {
     const dim3 grid(grid_blocks_for_tiles(a.num_tiles));
     if (neus) {
         if (stats) {
-            hipLaunchKernelGGL((backward_sdf_kernel<L, true>), grid, dim3(kBlock), 0, stream, a);
+            hipLaunchKernelGGL((backward_sdf_kernel<L, true, AT>), grid, dim3(kBlock), 0, stream, a);
         } else {
-            hipLaunchKernelGGL((backward_sdf_kernel<L, false>), grid, dim3(kBlock), 0, stream, a);
+            hipLaunchKernelGGL((backward_sdf_kernel<L, false, AT>), grid, dim3(kBlock), 0, stream, a);
         }
     } else {
         if (stats) {
-            hipLaunchKernelGGL((backward_density_kernel<L, true>), grid, dim3(kBlock), 0, stream, a);
+            hipLaunchKernelGGL((backward_density_kernel<L, true, AT>), grid, dim3(kBlock), 0, stream,
+                               a);
         } else {
-            hipLaunchKernelGGL((backward_density_kernel<L, false>), grid, dim3(kBlock), 0, stream, a);
+            hipLaunchKernelGGL((backward_density_kernel<L, false, AT>), grid, dim3(kBlock), 0,
+                               stream, a);
         }
     }
     return hipGetLastError();
 }
 
-hipError_t launch_backward(int L, const BwdArgs &a, bool neus, bool stats, hipStream_t stream) {
+template <typename AT>
+static hipError_t launch_backward_T(int L, const BwdArgs &a, bool neus, bool stats,
+                                    hipStream_t stream) {
     switch (L) {
-    case 0: return launch_backward_L<0>(a, neus, stats, stream);
-    case 1: return launch_backward_L<1>(a, neus, stats, stream);
-    case 2: return launch_backward_L<2>(a, neus, stats, stream);
-    case 3: return launch_backward_L<3>(a, neus, stats, stream);
+    case 0: return launch_backward_L<0, AT>(a, neus, stats, stream);
+    case 1: return launch_backward_L<1, AT>(a, neus, stats, stream);
+    case 2: return launch_backward_L<2, AT>(a, neus, stats, stream);
+    case 3: return launch_backward_L<3, AT>(a, neus, stats, stream);
     default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_backward(int L, const BwdArgs &a, bool neus, bool stats, bool half,
+                           hipStream_t stream) {
+    return half ? launch_backward_T<_Float16>(L, a, neus, stats, stream)
+                : launch_backward_T<float>(L, a, neus, stats, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -805,7 +825,7 @@ hipError_t launch_backward(int L, const BwdArgs &a, bool neus, bool stats, hipSt
 // One lane per pixel, 16x16 pixel tiles per block as the traced kernels.  The
 // step is the forward's compositing without its per-point outputs; the walk
 // reads the caller's unpadded offset table with guarded loads.
-template <int L, bool NEUS>
+template <int L, bool NEUS, typename AT>
 __global__ __launch_bounds__(kBlock) void render_kernel(RenderArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
@@ -859,18 +879,18 @@ __global__ __launch_bounds__(kBlock) void render_kernel(RenderArgs a) {
                                             wc);
         bool keep = true;
         if (si.stepped) {
-            const float *__restrict__ row = a.scene.attrs + (uint64_t)ws.cell * D;
-            float s = row[D - 1];
+            const AT *__restrict__ row = static_cast<const AT *>(a.scene.attrs) + (uint64_t)ws.cell * D;
+            float s = (float)row[D - 1];
             const float dt = fmaxf(si.t1 - ws.t0, 0.0f);
             if (neus_alpha) {
-                const float d = row[sdf_ch];
+                const float d = (float)row[sdf_ch];
                 const float phi = sdf_sigmoidf(-sha * d);
                 s = sha * phi * (1.0f - phi);
             }
             const float alpha = 1.0f - sdf_expf(-s * dt);
             const float w = T * alpha;
             float r, g, b;
-            if (NEUS || row[D - 1] > 1e-6f) {
+            if (NEUS || (float)row[D - 1] > 1e-6f) {
                 sh_rgb<L>(sh, row, r, g, b);
             } else {
                 r = g = b = 0.0f;
@@ -900,25 +920,31 @@ __global__ __launch_bounds__(kBlock) void render_kernel(RenderArgs a) {
     a.out[out_idx] = sdf_make_rgba8(fmaf(T, bg0, C0), fmaf(T, bg1, C1), fmaf(T, bg2, C2), 1.0f);
 }
 
-template <int L>
+template <int L, typename AT>
 static hipError_t launch_render_L(const RenderArgs &a, bool neus, hipStream_t stream) {
     const dim3 grid(grid_blocks_for_tiles(a.num_tiles));
     if (neus) {
-        hipLaunchKernelGGL((render_kernel<L, true>), grid, dim3(kBlock), 0, stream, a);
+        hipLaunchKernelGGL((render_kernel<L, true, AT>), grid, dim3(kBlock), 0, stream, a);
     } else {
-        hipLaunchKernelGGL((render_kernel<L, false>), grid, dim3(kBlock), 0, stream, a);
+        hipLaunchKernelGGL((render_kernel<L, false, AT>), grid, dim3(kBlock), 0, stream, a);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_render(int L, const RenderArgs &a, bool neus, hipStream_t stream) {
+template <typename AT>
+static hipError_t launch_render_T(int L, const RenderArgs &a, bool neus, hipStream_t stream) {
     switch (L) {
-    case 0: return launch_render_L<0>(a, neus, stream);
-    case 1: return launch_render_L<1>(a, neus, stream);
-    case 2: return launch_render_L<2>(a, neus, stream);
-    case 3: return launch_render_L<3>(a, neus, stream);
+    case 0: return launch_render_L<0, AT>(a, neus, stream);
+    case 1: return launch_render_L<1, AT>(a, neus, stream);
+    case 2: return launch_render_L<2, AT>(a, neus, stream);
+    case 3: return launch_render_L<3, AT>(a, neus, stream);
     default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_render(int L, const RenderArgs &a, bool neus, bool half, hipStream_t stream) {
+    return half ? launch_render_T<_Float16>(L, a, neus, stream)
+                : launch_render_T<float>(L, a, neus, stream);
 }
 
 // ---------------------------------------------------------------------------

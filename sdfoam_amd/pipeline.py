@@ -253,13 +253,19 @@ class Pipeline:
             mode,
             ch,
             width,
+            _lib.SDF_ATTR_F16 if self._attr_dtype == torch.float16 else _lib.SDF_ATTR_F32,
         )
 
-    def _require_native(self):
-        if self._attr_dtype != torch.float32:
-            raise RuntimeError(
-                "float16 attribute pipelines are not available in this build "
-                "(only float32 attributes are traced)")
+    def _zeros_attr(self, shape, device) -> torch.Tensor:
+        """Zeroed buffer of the attribute type for atomic accumulation: fp16
+        atomics are packed 4-byte words, so an odd element count gets one
+        padding half (the result is a view of the first elements)."""
+        n = 1
+        for d in shape:
+            n *= int(d)
+        if self._attr_dtype == torch.float16 and n % 2 == 1:
+            return torch.zeros(n + 1, dtype=self._attr_dtype, device=device)[:n].view(shape)
+        return torch.zeros(shape, dtype=self._attr_dtype, device=device)
 
     @staticmethod
     def _scratch(num_points: int, num_adj: int, device) -> tuple[torch.Tensor, int]:
@@ -312,14 +318,12 @@ class Pipeline:
             if num_q == 0 or dq.numel() // num_q != num_rays:
                 raise RuntimeError("depth_quantiles must have the same batch size as rays")
         settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel, rays_c)
-        self._require_native()
 
         dev = rays_c.device
         lead = tuple(rays_c.shape[:-1])
         rgba = torch.empty(lead + (4,), dtype=self._attr_dtype, device=dev)
         nisect = torch.empty(lead + (1,), dtype=torch.uint32, device=dev)
-        contribution = (torch.zeros((num_points, 1), dtype=self._attr_dtype, device=dev)
-                        if return_contribution else None)
+        contribution = self._zeros_attr((num_points, 1), dev) if return_contribution else None
         depth = didx = None
         if return_depth:
             depth = torch.zeros(lead + (num_q,), dtype=torch.float32, device=dev)
@@ -441,16 +445,15 @@ class Pipeline:
                 raise RuntimeError("ray_error must be on CUDA device")
             if rerr.numel() != num_rays:
                 raise RuntimeError("ray_error must have the same batch size as rays")
-            point_error = torch.zeros((num_points, 1), dtype=self._attr_dtype, device=dev)
+            point_error = self._zeros_attr((num_points, 1), dev)
 
         settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel, rays_c)
-        self._require_native()
         rgba = rgb_out.contiguous()
         if rgba.dtype != self._attr_dtype or rgba.numel() != 4 * num_rays or not _is_cuda(rgba):
             raise RuntimeError("rgb_out must be the forward's rgba output")
 
         num_attr = attributes_c.size(0)
-        attr_grad = torch.zeros((num_attr, self.attribute_dim()), dtype=self._attr_dtype, device=dev)
+        attr_grad = self._zeros_attr((num_attr, self.attribute_dim()), dev)
         points_grad = torch.zeros((num_points, 3), dtype=rays_c.dtype, device=dev)
         ray_grad = torch.zeros_like(rays_c)
         sharpness_grad = torch.zeros_like(sharpness, dtype=torch.float32)
@@ -542,7 +545,6 @@ class Pipeline:
             raise RuntimeError("adjacent_diff must be a CUDA tensor of 4 halves per adjacency entry")
 
         settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel)
-        self._require_native()
         vis = _lib.Visualization()
         bg = [1.0, 1.0, 1.0] if bg_color is None else [float(x) for x in bg_color]
         vis.bg_color[:] = bg
@@ -572,7 +574,6 @@ class Pipeline:
         self._validate_scene_data(points, attributes, point_adjacency, point_adjacency_offsets)
         num_rays = rays_c.numel() // 6
         self._validate_rays(rays_c, start_c, num_rays)
-        self._require_native()
         sharpness = _inv_s_to_tensor(inv_s, rays_c)
         settings = self._settings(weight_threshold, max_intersections, alpha_mode, sdf_channel, rays_c)
         dev = rays_c.device
