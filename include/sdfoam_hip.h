@@ -285,6 +285,18 @@ int sdf_nn(const float *points, const float *aabb_tree, const float *queries,
            uint32_t num_points, uint32_t num_queries, uint32_t *indices,
            void *stream);
 
+/* Per point: the farthest CSR neighbour (UINT32_MAX if none is farther
+ * than 0) and cell_radius = sum of half the neighbour distances / row length.
+ * Neighbours out of range are skipped.
+ * Replaces farthest_neighbor (src/delaunay/triangulation_ops.h:8-16,
+ * src/delaunay/triangulation_ops.cu:8-44;
+ * torch_bindings/triangulation_bindings.cpp:183-214). */
+int sdf_farthest_neighbor(const float *points, uint32_t num_points,
+                          uint32_t adjacency_size,
+                          const uint32_t *point_adjacency,
+                          const uint32_t *point_adjacency_offsets,
+                          uint32_t *indices, float *cell_radius, void *stream);
+
 /* ---- measurement and test hooks (no counterpart in the reference) ----- */
 
 /* Per-ray walk statistics of the forward (backward = 0) or backward

@@ -134,6 +134,8 @@ def lib():
         L.oracle_cast_ray.argtypes = [C.POINTER(_Camera), C.c_uint32, C.c_uint32, C.c_void_p]
         L.oracle_sincosf_n.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64]
         L.oracle_atan2f_n.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64]
+        L.oracle_farthest_neighbor.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p,
+                                               C.c_void_p, C.c_void_p]
         L.oracle_make_rgba8.restype = C.c_uint32
         L.oracle_make_rgba8.argtypes = [C.c_float] * 4
         _lib = L
@@ -440,3 +442,14 @@ def batch_rows(batch_index: int, batch_size: int, num_rows: int, shuffle: bool) 
     diff = np.uint32(num_rows)
     x = draw // (np.uint32(0xFFFFFFFF) // diff)
     return np.minimum(x, diff - np.uint32(1)).astype(np.uint32)
+
+
+def farthest_neighbor(points, adjacency, offsets):
+    points = _c(points, np.float32)
+    adjacency = _c(adjacency, np.uint32)
+    offsets = _c(offsets, np.uint32)
+    n = points.shape[0]
+    idx = np.zeros(n, dtype=np.uint32)
+    rad = np.zeros(n, dtype=np.float32)
+    lib().oracle_farthest_neighbor(_p(points), n, _p(adjacency), _p(offsets), _p(idx), _p(rad))
+    return idx, rad

@@ -1071,3 +1071,34 @@ void oracle_nn(const float *points, uint32_t num_points, const float *queries,
     nn_job j = {points, num_points, queries, indices};
     run_rays(nn_range, &j, num_queries, num_threads);
 }
+
+/* ------------------------------------------------------------------------ */
+/* farthest_neighbor (src/delaunay/triangulation_ops.cu:8-44): the farthest  */
+/* CSR neighbour and sum(0.5 * distance) / row length, the sum kept in       */
+/* double and rounded to float at every step as `float += 0.5 * float` does. */
+
+void oracle_farthest_neighbor(const float *points, uint32_t num_points,
+                              const uint32_t *adjacency, const uint32_t *offsets,
+                              uint32_t *indices, float *cell_radius) {
+    for (uint32_t i = 0; i < num_points; ++i) {
+        const float *p = points + 3ull * i;
+        const uint32_t beg = offsets[i], end = offsets[i + 1];
+        uint32_t far = UINT32_MAX;
+        float sum = 0.0f, max_d = 0.0f;
+        for (uint32_t k = beg; k < end; ++k) {
+            const uint32_t q = adjacency[k];
+            if (q >= num_points) continue;
+            const float dx = points[3ull * q] - p[0];
+            const float dy = points[3ull * q + 1] - p[1];
+            const float dz = points[3ull * q + 2] - p[2];
+            const float d = sqrtf(sdf_dot3(dx, dy, dz, dx, dy, dz));
+            sum = (float)((double)sum + 0.5 * (double)d);
+            if (d > max_d) {
+                max_d = d;
+                far = q;
+            }
+        }
+        indices[i] = far;
+        cell_radius[i] = sum / (float)(end - beg);
+    }
+}

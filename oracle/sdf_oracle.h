@@ -172,6 +172,12 @@ void oracle_build_aabb_tree(const float *points, uint32_t num_points,
 void oracle_nn(const float *points, uint32_t num_points, const float *queries,
                uint32_t num_queries, uint32_t *indices, int num_threads);
 
+/* Farthest CSR neighbour and mean half edge length per point
+ * (src/delaunay/triangulation_ops.cu:8-44). */
+void oracle_farthest_neighbor(const float *points, uint32_t num_points,
+                              const uint32_t *adjacency, const uint32_t *offsets,
+                              uint32_t *indices, float *cell_radius);
+
 #ifdef __cplusplus
 }
 #endif

@@ -3,8 +3,9 @@
 Drop-in for the tracing surface of the reference's ``sdfoam`` module:
 ``create_pipeline`` -> ``Pipeline.trace_forward`` / ``trace_backward``,
 ``build_aabb_tree``, ``nn``, plus the ``TraceRays`` autograd Function and
-``get_starting_point``, and ``BatchFetcher`` (the training loop's batch
-prefetcher).  Compute runs in libsdfoam_hip.so (hand-written HIP
+``get_starting_point``, ``BatchFetcher`` (the training loop's batch
+prefetcher) and the adjacency producer (``Triangulation``,
+``TriangulationFailedError``, ``farthest_neighbor``).  Compute runs in libsdfoam_hip.so (hand-written HIP
 for gfx950) through its C ABI; importing this package does not need a GPU,
 calling the tracer does.
 """
@@ -13,6 +14,7 @@ from .fetch import BatchFetcher
 from .pipeline import Pipeline, create_pipeline, prefetch_adjacent_diff
 from .render import ErrorBox, TraceRays
 from .spatial import build_aabb_tree, get_starting_point, nn
+from .triangulation import Triangulation, TriangulationFailedError, farthest_neighbor
 
 __all__ = [
     "Pipeline",
@@ -24,4 +26,7 @@ __all__ = [
     "nn",
     "get_starting_point",
     "BatchFetcher",
+    "Triangulation",
+    "TriangulationFailedError",
+    "farthest_neighbor",
 ]

@@ -38,6 +38,7 @@ EXPORTS = (
     "sdf_batch_fetcher_destroy",
     "sdf_batch_rows",
     "sdf_build_aabb_tree",
+    "sdf_farthest_neighbor",
     "sdf_nn",
     "sdf_trace_walk_stats",
     "sdf_debug_fpmath",
@@ -164,6 +165,8 @@ def lib() -> C.CDLL:
     L.sdf_batch_rows.argtypes = [U32, SZ, SZ, C.c_int, P]
     L.sdf_build_aabb_tree.restype = C.c_int
     L.sdf_build_aabb_tree.argtypes = [P, U32, P, P]
+    L.sdf_farthest_neighbor.restype = C.c_int
+    L.sdf_farthest_neighbor.argtypes = [P, U32, U32, P, P, P, P, P]
     L.sdf_nn.restype = C.c_int
     L.sdf_nn.argtypes = [P, P, P, U32, U32, P, P]
     L.sdf_trace_walk_stats.restype = C.c_int

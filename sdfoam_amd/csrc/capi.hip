@@ -483,6 +483,21 @@ int sdf_build_aabb_tree(const float *points, uint32_t num_points, float *aabb_tr
     return SDF_OK;
 }
 
+int sdf_farthest_neighbor(const float *points, uint32_t num_points, uint32_t adjacency_size,
+                          const uint32_t *point_adjacency, const uint32_t *point_adjacency_offsets,
+                          uint32_t *indices, float *cell_radius, void *stream) {
+    if (num_points == 0) return SDF_OK;
+    if (!points || !point_adjacency_offsets || !indices || !cell_radius ||
+        (!point_adjacency && adjacency_size > 0))
+        return fail(SDF_E_INVALID, "NULL pointer argument");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = launch_farthest_neighbor(points, num_points, point_adjacency,
+                                            point_adjacency_offsets, adjacency_size, indices,
+                                            cell_radius, s);
+    if (e != hipSuccess) return hip_fail(e, "farthest_neighbor");
+    return SDF_OK;
+}
+
 int sdf_nn(const float *points, const float *aabb_tree, const float *queries, uint32_t num_points,
            uint32_t num_queries, uint32_t *indices, void *stream) {
     if (num_points < 32) return fail(SDF_E_INVALID, "number of points must be at least 32");

@@ -129,6 +129,10 @@ hipError_t launch_backward(int L, const BwdArgs &a, bool neus, bool stats, bool 
                            hipStream_t stream);
 hipError_t launch_fpmath(int op, const float *in, void *out, uint64_t n, hipStream_t stream);
 
+hipError_t launch_farthest_neighbor(const float *points, uint32_t num_points, const uint32_t *adj,
+                                    const uint32_t *offs, uint32_t num_adj, uint32_t *indices,
+                                    float *cell_radius, hipStream_t stream);
+
 hipError_t launch_build_aabb_tree(const float *points, uint32_t num_points, float *tree,
                                   hipStream_t stream);
 hipError_t launch_nn(const float *points, const float *tree, const float *queries,

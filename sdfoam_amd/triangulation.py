@@ -1,0 +1,187 @@
+"""The adjacency producer: ``Triangulation``, ``TriangulationFailedError`` and
+``farthest_neighbor`` with the reference's interface
+(torch_bindings/triangulation_bindings.cpp:11-115, 183-237;
+src/delaunay/delaunay.h:9-44).
+
+``Triangulation(points)`` sorts the points into the reference's
+``sort_points`` order (``permutation()``: sorted = points[perm]) and
+triangulates them; ``rebuild(points, incremental)`` re-triangulates, sorting
+again unless ``incremental`` and the point count is unchanged, and returns
+whether it sorted (the caller then permutes its arrays).  Outputs are CUDA
+uint32 tensors indexing the sorted points:
+
+* ``tets()`` [T, 4], ordered by their sorted vertex sets, each positively
+  oriented (det[b - a, c - a, d - a] > 0);
+* ``tet_adjacency()`` [T, 4]: across the face opposite vertex j, 4 k + m for
+  neighbour tet k and its face m, or 0xffffffff on the hull;
+* ``vert_to_tet()`` [N]: the lowest tet index holding each point;
+* ``point_adjacency()`` / ``point_adjacency_offsets()``: the Delaunay edges
+  as CSR with ascending rows (src/delaunay/delaunay.cu:146-226).
+
+The Delaunay tetrahedralisation itself is computed on the host with Qhull
+(scipy); the reference builds it on the GPU with exact predicates.  For points
+in general position the two are the same unique triangulation.
+``farthest_neighbor`` runs in libsdfoam_hip.so.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import check, ptr
+
+_NONE = np.uint32(0xFFFFFFFF)
+
+
+class TriangulationFailedError(RuntimeError):
+    """src/delaunay/delaunay.h:9-13."""
+
+
+def _u32_cuda(a: np.ndarray, device) -> torch.Tensor:
+    a = np.ascontiguousarray(a, dtype=np.uint32)
+    return torch.from_numpy(a.view(np.int32)).to(device).view(torch.uint32)
+
+
+def triangulate_host(points: np.ndarray) -> dict:
+    """Delaunay tetrahedralisation of float32 points [N, 3] (already in the
+    triangulation's point order) and its derived tables, as numpy uint32."""
+    from scipy.spatial import Delaunay
+    from scipy.spatial import QhullError
+
+    p64 = np.asarray(points, dtype=np.float64)
+    n = p64.shape[0]
+    try:
+        tri = Delaunay(p64)
+    except QhullError as e:
+        raise TriangulationFailedError(f"Qhull failed: {str(e).splitlines()[0]}") from None
+    s = tri.simplices.astype(np.int64)
+    nb = tri.neighbors.astype(np.int64)
+    # positive orientation: swap the last two vertices (and their neighbours)
+    a, b, c, d = (p64[s[:, k]] for k in range(4))
+    vol = np.einsum("ij,ij->i", np.cross(b - a, c - a), d - a)
+    neg = vol < 0
+    s[neg, 2], s[neg, 3] = s[neg, 3].copy(), s[neg, 2].copy()
+    nb[neg, 2], nb[neg, 3] = nb[neg, 3].copy(), nb[neg, 2].copy()
+    # order tets by their sorted vertex sets
+    key = np.sort(s, axis=1)
+    order = np.lexsort(key[:, ::-1].T)
+    rank = np.empty_like(order)
+    rank[order] = np.arange(order.size)
+    s = s[order]
+    nb = nb[order]
+    nb = np.where(nb >= 0, rank[np.maximum(nb, 0)], -1)
+    T = s.shape[0]
+    # face of the neighbour that is shared: the neighbour's vertex not in this tet
+    adj_t = np.full((T, 4), _NONE, dtype=np.uint32)
+    ii, jj = np.nonzero(nb >= 0)
+    kk = nb[ii, jj]
+    other = s[kk]  # [M, 4]
+    mine = s[ii]
+    missing = ~(other[:, :, None] == mine[:, None, :]).any(axis=2)  # [M, 4]
+    m = np.argmax(missing, axis=1)
+    adj_t[ii, jj] = (4 * kk + m).astype(np.uint32)
+    # lowest tet holding each vertex
+    v2t = np.full(n, np.iinfo(np.int64).max, dtype=np.int64)
+    np.minimum.at(v2t, s.ravel(), np.repeat(np.arange(T), 4))
+    v2t = np.where(v2t == np.iinfo(np.int64).max, 0xFFFFFFFF, v2t).astype(np.uint32)
+    # CSR point adjacency: unique edges, both directions, ascending rows
+    pairs = np.concatenate([s[:, [0, 1]], s[:, [0, 2]], s[:, [0, 3]], s[:, [1, 2]],
+                            s[:, [1, 3]], s[:, [2, 3]]])
+    lo = np.minimum(pairs[:, 0], pairs[:, 1])
+    hi = np.maximum(pairs[:, 0], pairs[:, 1])
+    ek = np.unique((lo << 32) | hi)
+    lo, hi = ek >> 32, ek & 0xFFFFFFFF
+    both = np.concatenate([(lo << 32) | hi, (hi << 32) | lo])
+    both.sort()
+    rows = both >> 32
+    adj = (both & 0xFFFFFFFF).astype(np.uint32)
+    offs = np.zeros(n + 1, dtype=np.uint32)
+    np.cumsum(np.bincount(rows, minlength=n), out=offs[1:])
+    return {"tets": s.astype(np.uint32), "tet_adjacency": adj_t, "vert_to_tet": v2t,
+            "point_adjacency": adj, "point_adjacency_offsets": offs}
+
+
+def _check_points(points: torch.Tensor) -> None:
+    if points.size(-1) != 3:
+        raise RuntimeError("points must have 3 as the last dimension")
+    if points.device.type != "cuda":
+        raise RuntimeError("points must be on CUDA device")
+    if points.dtype != torch.float32:
+        raise RuntimeError("points must have float32 dtype")
+
+
+class Triangulation:
+    def __init__(self, points: torch.Tensor):
+        _check_points(points)
+        self._num_points = 0
+        self._perm = None
+        self.rebuild(points, incremental=False)
+
+    def rebuild(self, points: torch.Tensor, incremental: bool = False) -> bool:
+        """src/delaunay/delaunay.cu:260-349 (rebuild)."""
+        from .scenes import sort_points_order
+
+        _check_points(points)
+        n = points.numel() // 3
+        if n < 32:
+            raise RuntimeError("Delaunay triangulation does not support less than 32 points")
+        pts = points.detach().reshape(n, 3).cpu().numpy()
+        if incremental and n == self._num_points:
+            sorted_now = False
+        else:
+            perm = sort_points_order(pts)
+            pts = pts[perm]
+            self._perm = perm
+            self._num_points = n
+            sorted_now = True
+        if np.unique(pts, axis=0).shape[0] != n:
+            raise TriangulationFailedError("duplicate points found")
+        tables = triangulate_host(pts)
+        dev = points.device
+        self._tables = {k: _u32_cuda(v, dev) for k, v in tables.items()}
+        self._tables["tets"] = self._tables["tets"].reshape(-1, 4)
+        self._tables["tet_adjacency"] = self._tables["tet_adjacency"].reshape(-1, 4)
+        self._perm_t = _u32_cuda(self._perm, dev)
+        return sorted_now
+
+    def permutation(self) -> torch.Tensor:
+        return self._perm_t
+
+    def tets(self) -> torch.Tensor:
+        return self._tables["tets"]
+
+    def tet_adjacency(self) -> torch.Tensor:
+        return self._tables["tet_adjacency"]
+
+    def point_adjacency(self) -> torch.Tensor:
+        return self._tables["point_adjacency"]
+
+    def point_adjacency_offsets(self) -> torch.Tensor:
+        return self._tables["point_adjacency_offsets"]
+
+    def vert_to_tet(self) -> torch.Tensor:
+        return self._tables["vert_to_tet"]
+
+
+def farthest_neighbor(points: torch.Tensor, point_adjacency: torch.Tensor,
+                      point_adjacency_offsets: torch.Tensor):
+    """(indices uint32, cell_radius float32), shaped like points[..., 0]
+    (torch_bindings/triangulation_bindings.cpp:183-214)."""
+    pts = points.contiguous()
+    adj = point_adjacency.contiguous()
+    offs = point_adjacency_offsets.contiguous()
+    if pts.device.type != "cuda":
+        raise RuntimeError("points must be on CUDA device")
+    n = pts.size(0)
+    shape = tuple(pts.shape[:-1])
+    indices = torch.zeros(shape, dtype=torch.uint32, device=pts.device)
+    radius = torch.zeros(shape, dtype=torch.float32, device=pts.device)
+    with torch.cuda.device(pts.device):
+        check(_lib.lib().sdf_farthest_neighbor(ptr(pts), n, adj.numel(), ptr(adj), ptr(offs),
+                                               ptr(indices), ptr(radius),
+                                               _lib.stream_handle(pts.device)))
+    return indices, radius

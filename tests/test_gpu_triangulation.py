@@ -1,0 +1,107 @@
+"""The adjacency producer on the GPU box: farthest_neighbor bit-exact against
+the oracle, and Triangulation driven the way sdfoam_model/scene.py drives it
+(construct, permute the points, rebuild incrementally, trace on the
+adjacency)."""
+
+import numpy as np
+import pytest
+
+from conftest import scene
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _u32(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(dev).view(torch.uint32)
+
+
+def _np(t):
+    import torch
+
+    return t.view(torch.int32).cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("cfg", [1, 2])
+def test_farthest_neighbor_bitexact(dev, cfg):
+    import torch
+
+    import sdfoam_amd
+
+    w = scene(cfg)
+    pts = torch.from_numpy(w.points).to(dev)
+    idx, rad = sdfoam_amd.farthest_neighbor(pts, _u32(w.adjacency, dev), _u32(w.offsets, dev))
+    torch.cuda.synchronize()
+    ridx, rrad = oracle.farthest_neighbor(w.points, w.adjacency, w.offsets)
+    assert idx.dtype == torch.uint32 and rad.dtype == torch.float32
+    assert np.array_equal(_np(idx), ridx)
+    assert np.array_equal(rad.cpu().numpy().view(np.uint32), rrad.view(np.uint32))
+
+
+def test_triangulation_as_scene_uses_it(dev):
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import scenes
+    from sdfoam_amd.triangulation import triangulate_host
+
+    rng = np.random.default_rng(21)
+    raw = torch.from_numpy(rng.normal(size=(3000, 3)).astype(np.float32) * 0.6).to(dev)
+    tri = sdfoam_amd.Triangulation(raw)
+    perm = tri.permutation().to(torch.long)
+    assert np.array_equal(perm.cpu().numpy(), scenes.sort_points_order(raw.cpu().numpy()))
+    pts = raw[perm]
+    host = triangulate_host(pts.cpu().numpy())
+    for k in ("tets", "tet_adjacency", "vert_to_tet", "point_adjacency", "point_adjacency_offsets"):
+        assert np.array_equal(_np(getattr(tri, k)()).reshape(host[k].shape), host[k]), k
+    # moved points, same count: no re-sort, tables of the moved points
+    moved = pts + 1e-3 * torch.randn_like(pts)
+    assert tri.rebuild(moved, incremental=True) is False
+    host2 = triangulate_host(moved.cpu().numpy())
+    assert np.array_equal(_np(tri.point_adjacency()), host2["point_adjacency"])
+    assert tri.rebuild(moved, incremental=False) is True
+    # trace on the triangulation's adjacency: forward parity with the oracle
+    pts_np = moved[tri.permutation().to(torch.long)].cpu().numpy()
+    tri.rebuild(torch.from_numpy(pts_np).to(dev), incremental=True)
+    adj, offs = _np(tri.point_adjacency()), _np(tri.point_adjacency_offsets())
+    cam = scenes.look_at([0.0, 0.0, 3.0], [0.0, 0.0, 0.0], [0.0, 1.0, 0.0], 0.8, 32, 32)
+    rays = scenes.pinhole_rays(cam)
+    start = scenes.start_points_for(pts_np, rays)
+    attrs = rng.uniform(0, 1, size=(3000, 4)).astype(np.float32)
+    attrs[:, 3] = np.linalg.norm(pts_np, axis=1) - 0.5
+    pipe = sdfoam_amd.create_pipeline(0)
+    out = pipe.trace_forward(torch.from_numpy(pts_np).to(dev), torch.from_numpy(attrs).to(dev),
+                             tri.point_adjacency(), tri.point_adjacency_offsets(),
+                             torch.from_numpy(rays).to(dev), _u32(start, dev),
+                             alpha_mode="sdfoam", inv_s=5.0)
+    torch.cuda.synchronize()
+    ref = oracle.trace_forward(0, pts_np, attrs, adj, offs, rays, start, None,
+                               alpha_mode="sdfoam", inv_s=5.0)
+    assert np.array_equal(_np(out["num_intersections"]).reshape(-1), ref.num_intersections.reshape(-1))
+    assert np.max(np.abs(out["rgba"].cpu().numpy() - ref.rgba)) < 1e-5
+
+
+def test_triangulation_errors(dev):
+    import torch
+
+    import sdfoam_amd
+
+    pts = torch.randn(100, 3, device=dev)
+    pts[7] = pts[50]
+    with pytest.raises(sdfoam_amd.TriangulationFailedError, match="duplicate points"):
+        sdfoam_amd.Triangulation(pts)
+    with pytest.raises(RuntimeError, match="less than 32 points"):
+        sdfoam_amd.Triangulation(torch.randn(20, 3, device=dev))
+    with pytest.raises(RuntimeError, match="CUDA device"):
+        sdfoam_amd.Triangulation(torch.randn(100, 3))

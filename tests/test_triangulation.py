@@ -1,0 +1,115 @@
+"""The adjacency producer without a GPU: the host tetrahedralisation and its
+tables (Delaunay empty-sphere property by brute force, orientation, ordering,
+neighbour encoding, vert_to_tet, CSR edges) and the oracle's
+farthest_neighbor against float64 brute force."""
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+
+
+@pytest.fixture(scope="module")
+def small():
+    from sdfoam_amd.triangulation import triangulate_host
+
+    rng = np.random.default_rng(7)
+    pts = rng.uniform(-1, 1, size=(300, 3)).astype(np.float32)
+    return pts, triangulate_host(pts)
+
+
+def test_empty_circumspheres(small):
+    pts, t = small
+    p = pts.astype(np.float64)
+    tets = t["tets"].astype(np.int64)
+    for tet in tets:
+        a, b, c, d = p[tet]
+        # circumcentre: solve 2 (x_i - a) . o = |x_i|^2 - |a|^2
+        A = 2.0 * np.stack([b - a, c - a, d - a])
+        rhs = np.array([b @ b - a @ a, c @ c - a @ a, d @ d - a @ a])
+        o = np.linalg.solve(A, rhs)
+        r2 = (a - o) @ (a - o)
+        dist2 = np.sum((p - o) ** 2, axis=1)
+        inside = dist2 < r2 * (1 - 1e-9)
+        inside[tet] = False
+        assert not inside.any()
+
+
+def test_orientation_order_and_cover(small):
+    pts, t = small
+    p = pts.astype(np.float64)
+    s = t["tets"].astype(np.int64)
+    a, b, c, d = (p[s[:, k]] for k in range(4))
+    vol = np.einsum("ij,ij->i", np.cross(b - a, c - a), d - a)
+    assert np.all(vol > 0)
+    key = np.sort(s, axis=1)
+    assert all(tuple(key[i]) < tuple(key[i + 1]) for i in range(len(key) - 1))
+    # the tets tile the convex hull
+    from scipy.spatial import ConvexHull
+
+    assert abs(vol.sum() / 6.0 - ConvexHull(p).volume) < 1e-9
+
+
+def test_tet_adjacency_and_vert_to_tet(small):
+    pts, t = small
+    s = t["tets"].astype(np.int64)
+    adj = t["tet_adjacency"].astype(np.int64)
+    T = s.shape[0]
+    hull = 0
+    for i in range(T):
+        for j in range(4):
+            v = adj[i, j]
+            if v == 0xFFFFFFFF:
+                hull += 1
+                continue
+            k, m = v // 4, v % 4
+            face_i = set(s[i]) - {s[i, j]}
+            face_k = set(s[k]) - {s[k, m]}
+            assert face_i == face_k
+            assert adj[k, m] == 4 * i + j
+    from scipy.spatial import ConvexHull
+
+    assert hull == len(ConvexHull(pts.astype(np.float64)).simplices)
+    v2t = t["vert_to_tet"].astype(np.int64)
+    for v in range(pts.shape[0]):
+        assert v2t[v] == np.min(np.nonzero((s == v).any(axis=1))[0])
+
+
+def test_point_adjacency_is_the_edge_graph(small):
+    from sdfoam_amd.scenes import delaunay_adjacency
+
+    pts, t = small
+    adj, offs = delaunay_adjacency(pts)
+    assert np.array_equal(adj, t["point_adjacency"]) and np.array_equal(offs, t["point_adjacency_offsets"])
+    for i in range(pts.shape[0]):
+        row = t["point_adjacency"][t["point_adjacency_offsets"][i]:t["point_adjacency_offsets"][i + 1]]
+        assert np.all(np.diff(row.astype(np.int64)) > 0)
+
+
+def test_failures():
+    from sdfoam_amd.triangulation import TriangulationFailedError, triangulate_host
+
+    flat = np.zeros((40, 3), dtype=np.float32)
+    flat[:, :2] = np.random.default_rng(0).uniform(size=(40, 2))
+    with pytest.raises(TriangulationFailedError):
+        triangulate_host(flat)
+
+
+def test_farthest_neighbor_oracle_against_float64():
+    from sdfoam_amd.scenes import delaunay_adjacency
+
+    rng = np.random.default_rng(3)
+    pts = rng.normal(size=(500, 3)).astype(np.float32)
+    adj, offs = delaunay_adjacency(pts)
+    idx, rad = oracle.farthest_neighbor(pts, adj, offs)
+    p = pts.astype(np.float64)
+    for i in range(500):
+        row = adj[offs[i]:offs[i + 1]].astype(np.int64)
+        d = np.linalg.norm(p[row] - p[i], axis=1)
+        assert idx[i] == row[np.argmax(d)]
+        assert abs(rad[i] - 0.5 * d.mean()) <= 1e-6 * max(1.0, d.mean())
+    # a point whose neighbours all coincide with it has no farthest neighbour
+    pts2 = np.array([[0, 0, 0], [0, 0, 0], [1, 0, 0]], dtype=np.float32)
+    i2, r2 = oracle.farthest_neighbor(pts2, np.array([1], dtype=np.uint32),
+                                      np.array([0, 1, 1, 1], dtype=np.uint32))
+    assert i2[0] == 0xFFFFFFFF and r2[0] == 0.0 and np.isnan(r2[1])
