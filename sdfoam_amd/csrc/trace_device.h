@@ -317,9 +317,11 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
             const float dx = f16_to_f32(h[u].x);
             const float dy = f16_to_f32(h[u].x >> 16);
             const float dz = f16_to_f32(h[u].y);
-            const float fx = ws.xc[0] + dx * 0.5f;
-            const float fy = ws.xc[1] + dy * 0.5f;
-            const float fz = ws.xc[2] + dz * 0.5f;
+            // xc + d * 0.5 (src/tracing/tracing_utils.cuh:73): d * 0.5 is
+            // exact for a widened half, so one fused op gives the same bits
+            const float fx = fmaf(dx, 0.5f, ws.xc[0]);
+            const float fy = fmaf(dy, 0.5f, ws.xc[1]);
+            const float fz = fmaf(dz, 0.5f, ws.xc[2]);
             const float dp = sdf_dot3(dx, dy, dz, ray.dx, ray.dy, ray.dz);
             const float t = sdf_dot3(fx - ray.ox, fy - ray.oy, fz - ray.oz, dx, dy, dz) / dp;
             bool take;

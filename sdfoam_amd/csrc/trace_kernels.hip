@@ -71,6 +71,36 @@ __device__ __forceinline__ uint32_t readlane_u(uint32_t v, int lane) {
 
 __device__ __forceinline__ int first_lane(uint64_t mask) { return __builtin_ctzll(mask); }
 
+// Groups of lanes per forward slot round.
+constexpr int kSlots = 16;
+
+// Assigns the next up-to-kSlots groups of lanes with equal `key` among
+// `todo` to slots 0..n-1 (lanes of group k get slot k, tb_cell[k] = key);
+// returns n and clears those lanes from `todo`.
+__device__ __forceinline__ int assign_slots(uint64_t &todo, uint32_t key, int &slot,
+                                            uint32_t *tb_cell) {
+    const uint32_t lane = lane_id();
+    int n = 0;
+    slot = -1;
+    while (todo && n < kSlots) {
+        const int leader = first_lane(todo);
+        const uint32_t c = readlane_u(key, leader);
+        const uint64_t grp = __ballot(((todo >> lane) & 1ull) && key == c);
+        todo &= ~grp;
+        if ((grp >> lane) & 1ull) slot = n;
+        if (lane == 0) tb_cell[n] = c;
+        ++n;
+    }
+    return n;
+}
+
+// Per-wave LDS slots of the forward's grouped contribution updates.
+struct FwdSlots {
+    float w[kSlots];
+    float alpha[kSlots];
+    uint32_t cell[kSlots];
+};
+
 // ---------------------------------------------------------------------------
 // forward (src/tracing/pipeline.cu:36-264)
 
@@ -80,6 +110,10 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     constexpr int D = 1 + 3 * nsh;
     // SH basis of each lane's ray, in LDS (frees nsh VGPRs)
     __shared__ float sh_all[kBlock * nsh];
+    __shared__ FwdSlots fwd_slots[STATS ? 1 : kBlock / 64];
+    if constexpr (!STATS) {
+        if ((threadIdx.x & 63u) < (uint32_t)kSlots) fwd_slots[threadIdx.x >> 6].w[threadIdx.x & 63u] = 0.0f;
+    }
     bool valid;
     const uint32_t ray_idx =
         ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid, a.order);
@@ -191,17 +225,27 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
             // visiting step's alpha (the reference's last-writer store,
             // src/tracing/pipeline.cu:159-163)
             if (a.contribution || a.alpha_out) {
+                // groups of lanes in one cell: weights summed in an LDS slot
+                // per group (ds_add), then lane k writes group k's sum and a
+                // member's alpha
+                FwdSlots &fs = fwd_slots[threadIdx.x >> 6];
                 uint64_t todo = __ballot(si.stepped);
                 while (todo) {
-                    const int leader = first_lane(todo);
-                    const uint32_t c = readlane_u(ws.cell, leader);
-                    const uint64_t grp = __ballot(si.stepped && ws.cell == c);
-                    todo &= ~grp;
-                    float sum = 0.0f;
-                    for (uint64_t mm = grp; mm; mm &= mm - 1) sum += readlane_f(w, first_lane(mm));
-                    const float al = readlane_f(alpha, leader);
-                    if (lane == 0 && a.contribution) atomic_add_elem<AT>(a.contribution, c, sum);
-                    if (lane == 1 && a.alpha_out) a.alpha_out[c] = al;
+                    int slot;
+                    const int n = assign_slots(todo, ws.cell, slot, fs.cell);
+                    if (slot >= 0) {
+                        atomicAdd(fs.w + slot, w);
+                        fs.alpha[slot] = alpha;
+                    }
+                    __builtin_amdgcn_wave_barrier();
+                    if ((int)lane < n) {
+                        const uint32_t c = fs.cell[lane];
+                        const float sum = fs.w[lane];
+                        fs.w[lane] = 0.0f;
+                        if (a.contribution) atomic_add_elem<AT>(a.contribution, c, sum);
+                        if (a.alpha_out) a.alpha_out[c] = fs.alpha[lane];
+                    }
+                    __builtin_amdgcn_wave_barrier();
                 }
             }
         }
@@ -279,14 +323,20 @@ __device__ __forceinline__ bool geom_step(GeomState &gs, uint32_t cell, const fl
     return flush;
 }
 
-// Per-wave LDS tables of the grouped updates.  Row 64 of each is zero: it
-// pads a batch of members, so padded slots add exact zeros.
+// Per-wave LDS tables of the backward's grouped updates.  Row 64 of `rec`
+// is zero: it pads a batch of members, so padded slots add exact zeros.
 template <int L>
 struct WaveTables {
     static constexpr int nsh = (L + 1) * (L + 1);
-    float y[65 * nsh]; // SH basis of each lane's ray, written once
-    float4 g[65];      // per step: d L / d rgb (r, g, b), d L / d last channel
-    float4 p[65];      // per step: flushed position gradient (x, y, z), point error
+    static constexpr int kRec = 64 * nsh; // offset of rec
+    static constexpr int kOne = kRec + 65 * 8;
+    // [0, kRec): SH basis of each lane's ray, written once;
+    // rec [kRec, kOne): per step and lane 8 floats: dL/d(r, g, b, last
+    //   channel), flushed position gradient (x, y, z), point error;
+    // [kOne]: 1.0, the multiplier of the non-SH components
+    float buf[kOne + 1];
+    __device__ float *y() { return buf; }
+    __device__ float *rec() { return buf + kRec; }
 };
 
 // Next member of a lane mask (64 = padding once the mask is empty).
@@ -297,87 +347,123 @@ __device__ __forceinline__ int pop_member(uint64_t &mm) {
     return m;
 }
 
+// What owner lane i of the wave accumulates for a member m: the product
+// y[m * y_stride + y_base] * rec[m * g_stride + g_base]:
+//   i < 3 nsh (SH):      Y_{i/3}(m) * dL/drgb_{i%3}(m)   (sh_utils.cuh:85-92)
+//   i == last_ch:        1 * dL/dlast(m)
+//   i == 60, 61, 62:     1 * flushed position gradient x, y, z (m)
+//   i == 63:             1 * point error(m)
+//   others:              1 * 0 (the zero row)
+struct OwnerLane {
+    int y_base, y_stride, g_base, g_stride;
+    bool also_last; // last_ch is an SH component too: add dL/dlast as well
+};
+
+template <int L>
+__device__ __forceinline__ OwnerLane owner_lane(int last_ch) {
+    constexpr int nsh = (L + 1) * (L + 1);
+    constexpr int one_idx = WaveTables<L>::kOne;
+    const int lane = (int)lane_id();
+    OwnerLane o;
+    o.also_last = false;
+    if (lane < 3 * nsh) {
+        o.y_base = lane / 3;
+        o.y_stride = nsh;
+        o.g_base = lane % 3;
+        o.g_stride = 8;
+        o.also_last = lane == last_ch;
+    } else {
+        o.y_base = one_idx;
+        o.y_stride = 0;
+        if (lane == last_ch) {
+            o.g_base = 3;
+            o.g_stride = 8;
+        } else if (lane >= 60 && lane < 63) {
+            o.g_base = 4 + (lane - 60);
+            o.g_stride = 8;
+        } else if (lane == 63) {
+            o.g_base = 7;
+            o.g_stride = 8;
+        } else {
+            o.g_base = 64 * 8;
+            o.g_stride = 0;
+        }
+    }
+    return o;
+}
+
 // Grouped gradient updates of one wave-synchronous step (all 64 lanes
-// active).  For every cell some lanes stepped into, lane i < D adds
-//   sum over those lanes of  Y_{i/3} * g_{i%3}      (i < 3 nsh; SH, sh_utils.cuh:85-92)
-//   + sum of g_last                                 (i == last_ch)
-// to row `cell` of attr_grad, lane 63 adds the point-error sum; then for
-// every flushed cell lanes 0..2 add the flushed position gradients.  The
-// stepping lanes publish their values in the wave's LDS tables; the owner
-// lane of each component reads the members four at a time.
+// active).  A lane's attribute gradients are applied one step late, together
+// with the position gradient flushed for the same cell
+// (src/tracing/pipeline.cu:495-506 flushes a cell's position gradient one
+// step late), so each trip needs one grouping pass instead of two.  The
+// participating lanes (`part`) have their pending step in the wave's LDS
+// record; `key` is that step's cell.  For every key, owner lane i < D adds
+// the sum of its component over the group to row `key` of attr_grad (one
+// coalesced atomic instruction per cell), lanes 60..62 add the summed
+// flushed position gradient (if a member flushed one) and lane 63 the point
+// error.  The owner lanes read the members four at a time, two LDS reads and
+// one fma per member.
 template <int L, typename AT>
 __device__ __forceinline__ void grouped_backward_updates(
-    bool stepped, uint32_t cell, float gr, float gg, float gb, float g_last, int last_ch,
-    float pe, bool flush, uint32_t flush_idx, const float *flush_g, WaveTables<L> &tb,
-    void *__restrict__ attr_grad, void *__restrict__ point_error,
+    bool part, uint32_t key, bool flush, const float *flush_g, const OwnerLane &ow,
+    WaveTables<L> &tb, void *__restrict__ attr_grad, void *__restrict__ point_error,
     float *__restrict__ points_grad) {
-    constexpr int nsh = (L + 1) * (L + 1);
-    constexpr int D = 1 + 3 * nsh;
+    constexpr int D = 1 + 3 * (L + 1) * (L + 1);
     const uint32_t lane = lane_id();
-    if (stepped) {
-        tb.g[lane] = make_float4(gr, gg, gb, g_last);
-        tb.p[lane] = make_float4(flush_g[0], flush_g[1], flush_g[2], pe);
+    float *rec = tb.rec();
+    if (part) {
+        rec[lane * 8 + 4] = flush ? flush_g[0] : 0.0f;
+        rec[lane * 8 + 5] = flush ? flush_g[1] : 0.0f;
+        rec[lane * 8 + 6] = flush ? flush_g[2] : 0.0f;
     }
     __builtin_amdgcn_wave_barrier();
-    const bool sh_lane = lane < 3u * nsh;
-    const int j = sh_lane ? (int)lane / 3 : 0;
-    const int ch = sh_lane ? (int)lane % 3 : 0;
-    const bool last_lane = (int)lane == last_ch;
-    const float *gf = reinterpret_cast<const float *>(tb.g);
-    const float *pf = reinterpret_cast<const float *>(tb.p);
-    uint64_t todo = __ballot(stepped);
+    const float *ybase = tb.buf + ow.y_base;
+    const float *gbase = rec + ow.g_base;
+    const bool any_also_last = __ballot(ow.also_last) != 0ull;
+    const uint64_t flushing = __ballot(part && flush);
+    uint64_t todo = __ballot(part);
     while (todo) {
         const int leader = first_lane(todo);
-        const uint32_t c = readlane_u(cell, leader);
-        const uint64_t grp = __ballot(stepped && cell == c);
+        const uint32_t c = readlane_u(key, leader);
+        const uint64_t grp = __ballot(part && key == c);
         todo &= ~grp;
         float acc = 0.0f;
-        float pacc = 0.0f;
         uint64_t mm = grp;
         while (mm) {
             int m[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) m[u] = pop_member(mm);
-            float y[4], g[4], l[4], e[4];
+            float y[4], g[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                y[u] = tb.y[m[u] * nsh + j];
-                g[u] = gf[m[u] * 4 + ch];
-                l[u] = gf[m[u] * 4 + 3];
-                e[u] = pf[m[u] * 4 + 3];
+                y[u] = ybase[m[u] * ow.y_stride];
+                g[u] = gbase[m[u] * ow.g_stride];
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                if (sh_lane) acc = acc + y[u] * g[u];
-                if (last_lane) acc = acc + l[u];
-                pacc = pacc + e[u];
+            for (int u = 0; u < 4; ++u) acc = acc + y[u] * g[u];
+            if (any_also_last) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (ow.also_last) acc = acc + rec[m[u] * 8 + 3];
+                }
             }
         }
         atomic_add_row<AT>(attr_grad, c, lane, (uint32_t)D, acc);
-        if (point_error && lane == 63u) atomic_add_elem<AT>(point_error, c, pacc);
-    }
-    todo = __ballot(flush);
-    const int pl = lane < 3u ? (int)lane : 0;
-    while (todo) {
-        const int leader = first_lane(todo);
-        const uint32_t c = readlane_u(flush_idx, leader);
-        const uint64_t grp = __ballot(flush && flush_idx == c);
-        todo &= ~grp;
-        float acc = 0.0f;
-        uint64_t mm = grp;
-        while (mm) {
-            int m[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) m[u] = pop_member(mm);
-            float v[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = pf[m[u] * 4 + pl];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) acc = acc + v[u];
-        }
-        if (lane < 3u) atomicAdd(points_grad + 3ull * c + lane, acc);
+        if (point_error && lane == 63u) atomic_add_elem<AT>(point_error, c, acc);
+        if ((grp & flushing) && lane >= 60u && lane < 63u)
+            atomicAdd(points_grad + 3ull * c + (lane - 60u), acc);
     }
     __builtin_amdgcn_wave_barrier();
+}
+
+// Publishes a lane's step for the next grouping pass (record slots 0..3, 7).
+template <int L>
+__device__ __forceinline__ void publish_step(WaveTables<L> &tb, float gr, float gg, float gb,
+                                             float g_last, float pe) {
+    float *r = tb.rec() + lane_id() * 8;
+    *reinterpret_cast<float4 *>(r) = make_float4(gr, gg, gb, g_last);
+    r[7] = pe;
 }
 
 template <int L>
@@ -385,12 +471,9 @@ __device__ __forceinline__ void tables_init(WaveTables<L> &tb, const float *sh) 
     constexpr int nsh = (L + 1) * (L + 1);
     const uint32_t lane = lane_id();
 #pragma unroll
-    for (int k = 0; k < nsh; ++k) tb.y[lane * nsh + k] = sh[k];
-    if (lane < (uint32_t)nsh) tb.y[64 * nsh + lane] = 0.0f;
-    if (lane == 0) {
-        tb.g[64] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        tb.p[64] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
+    for (int k = 0; k < nsh; ++k) tb.y()[lane * nsh + k] = sh[k];
+    if (lane < 8u) tb.rec()[64 * 8 + lane] = 0.0f;
+    if (lane == 0) tb.buf[WaveTables<L>::kOne] = 1.0f;
     __builtin_amdgcn_wave_barrier();
 }
 
@@ -416,11 +499,12 @@ backward_sdf_kernel(BwdArgs a) {
         sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
         tables_init<L>(tb, sh0);
     }
-    const float *sh = tb.y + lane * nsh; // this ray's SH basis, in LDS
+    const float *sh = tb.y() + lane * nsh; // this ray's SH basis, in LDS
 
     const float sha = a.sharpness[0];
     const int32_t sdf_ch = a.settings.sdf_channel >= 0 ? a.settings.sdf_channel : D - 1;
     const bool write_sdf = a.settings.sdf_channel >= 0;
+    const OwnerLane owner = owner_lane<L>(write_sdf ? sdf_ch : -1);
     const float thr = a.settings.weight_threshold;
     const uint32_t Q = a.num_quantiles;
     const float *rq = (valid && a.quantiles) ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
@@ -455,6 +539,8 @@ backward_sdf_kernel(BwdArgs a) {
     const uint2 *wrec = nullptr;
     if (!STATS && a.record.entries) wrec = walk_record_lane(a.record, lane);
     uint32_t trip = 0;
+    bool pend = false;       // a step whose updates are not applied yet
+    uint32_t pend_cell = 0u; // its cell
 
     while (__ballot(ws.alive) != 0ull) {
         StepInfo si;
@@ -556,13 +642,26 @@ backward_sdf_kernel(BwdArgs a) {
             T = Tn;
             keep = T > thr;
         }
-        if constexpr (!STATS) {
-            grouped_backward_updates<L, AT>(si.stepped, ws.cell, dr, dg, db, dsdf,
-                                        write_sdf ? sdf_ch : -1, pe, flush, flush_idx, flush_g,
-                                        tb, a.attr_grad, a.point_error, a.points_grad);
-        }
         if (si.stepped && !keep) ws.alive = false;
+        if constexpr (!STATS) {
+            // the pending step goes out when the lane steps again (with the
+            // flush of the same cell) or when its walk ends
+            const bool part = pend && (si.stepped || !ws.alive);
+            grouped_backward_updates<L, AT>(part, pend_cell, si.stepped && flush, flush_g, owner,
+                                            tb, a.attr_grad, a.point_error, a.points_grad);
+            if (si.stepped) {
+                publish_step<L>(tb, dr, dg, db, dsdf, pe);
+                pend_cell = ws.cell;
+            }
+            pend = si.stepped || (pend && !part);
+        }
         if (ws.alive && si.found) walk_move(ws, si);
+    }
+    if constexpr (!STATS) {
+        // steps still pending when their walks ended
+        const float zero3[3] = {0.0f, 0.0f, 0.0f};
+        grouped_backward_updates<L, AT>(pend, pend_cell, false, zero3, owner, tb, a.attr_grad,
+                                        a.point_error, a.points_grad);
     }
 
     if constexpr (STATS) {
@@ -601,8 +700,9 @@ backward_density_kernel(BwdArgs a) {
         sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
         tables_init<L>(tb, sh0);
     }
-    const float *sh = tb.y + lane * nsh; // this ray's SH basis, in LDS
+    const float *sh = tb.y() + lane * nsh; // this ray's SH basis, in LDS
 
+    const OwnerLane owner = owner_lane<L>(D - 1);
     const float thr = a.settings.weight_threshold;
     const uint32_t Q = a.num_quantiles;
     const float *rq = (valid && a.quantiles) ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
@@ -636,6 +736,8 @@ backward_density_kernel(BwdArgs a) {
     WalkState ws;
     walk_init(a.scene, valid ? a.start[ray_idx] : kNoIndex, ws);
     WalkCounters wc = {0u, 0u, 0ull, 0ull};
+    bool pend = false;
+    uint32_t pend_cell = 0u;
 
     while (__ballot(ws.alive) != 0ull) {
         StepInfo si;
@@ -710,13 +812,23 @@ backward_density_kernel(BwdArgs a) {
             T = Tn;
             keep = T > thr;
         }
-        if constexpr (!STATS) {
-            grouped_backward_updates<L, AT>(si.stepped, ws.cell, dr, dg, db, dds, D - 1, pe, flush,
-                                        flush_idx, flush_g, tb, a.attr_grad, a.point_error,
-                                        a.points_grad);
-        }
         if (si.stepped && !keep) ws.alive = false;
+        if constexpr (!STATS) {
+            const bool part = pend && (si.stepped || !ws.alive);
+            grouped_backward_updates<L, AT>(part, pend_cell, si.stepped && flush, flush_g, owner,
+                                            tb, a.attr_grad, a.point_error, a.points_grad);
+            if (si.stepped) {
+                publish_step<L>(tb, dr, dg, db, dds, pe);
+                pend_cell = ws.cell;
+            }
+            pend = si.stepped || (pend && !part);
+        }
         if (ws.alive && si.found) walk_move(ws, si);
+    }
+    if constexpr (!STATS) {
+        const float zero3[3] = {0.0f, 0.0f, 0.0f};
+        grouped_backward_updates<L, AT>(pend, pend_cell, false, zero3, owner, tb, a.attr_grad,
+                                        a.point_error, a.points_grad);
     }
 
     if constexpr (STATS) {
