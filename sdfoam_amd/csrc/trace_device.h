@@ -211,8 +211,10 @@ __device__ __forceinline__ void sh_basis(float x, float y, float z, float *sh) {
 
 // rgb = max(0, 0.5 + sum_j Y_j * row[3j + c])  (src/tracing/sh_utils.cuh:64-75);
 // fp16 rows are widened exactly (sh_utils.cuh:79, `(float)sh_rgb_vals[i]`).
+// `sh` holds the ray's basis at a stride of `sh_stride` floats (the LDS
+// tables keep one basis function per row, so lanes hit distinct banks).
 template <int L, typename AT>
-__device__ __forceinline__ void sh_rgb(const float *sh, const AT *__restrict__ row,
+__device__ __forceinline__ void sh_rgb(const float *sh, int sh_stride, const AT *__restrict__ row,
                                        float &r, float &g, float &b) {
     constexpr int nsh = (L + 1) * (L + 1);
     float a0 = 0.5f, a1 = 0.5f, a2 = 0.5f;
@@ -220,9 +222,10 @@ __device__ __forceinline__ void sh_rgb(const float *sh, const AT *__restrict__ r
     // the kernels' register count low (same FMA order per channel)
 #pragma unroll 4
     for (int j = 0; j < nsh; ++j) {
-        a0 = fmaf(sh[j], (float)row[3 * j + 0], a0);
-        a1 = fmaf(sh[j], (float)row[3 * j + 1], a1);
-        a2 = fmaf(sh[j], (float)row[3 * j + 2], a2);
+        const float y = sh[j * sh_stride];
+        a0 = fmaf(y, (float)row[3 * j + 0], a0);
+        a1 = fmaf(y, (float)row[3 * j + 1], a1);
+        a2 = fmaf(y, (float)row[3 * j + 2], a2);
     }
     r = fmaxf(a0, 0.0f);
     g = fmaxf(a1, 0.0f);

@@ -121,12 +121,12 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
 
     RayF ray = {};
     if (valid) ray = load_ray(a.rays, ray_idx);
-    float *sh = sh_all + threadIdx.x * nsh;
+    float *sh = sh_all + threadIdx.x; // basis function k at sh[k * kBlock]
     {
         float sh0[nsh];
         sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
 #pragma unroll
-        for (int k = 0; k < nsh; ++k) sh[k] = sh0[k];
+        for (int k = 0; k < nsh; ++k) sh[k * kBlock] = sh0[k];
     }
     const float sha = a.sharpness[0];
     const int32_t sdf_ch = a.settings.sdf_channel;
@@ -183,7 +183,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
             if constexpr (!STATS) {
                 float r, g, b;
                 if (NEUS || (float)row[D - 1] > 1e-6f) {
-                    sh_rgb<L>(sh, row, r, g, b);
+                    sh_rgb<L>(sh, kBlock, row, r, g, b);
                 } else {
                     r = g = b = 0.0f;
                 }
@@ -325,14 +325,20 @@ __device__ __forceinline__ bool geom_step(GeomState &gs, uint32_t cell, const fl
 
 // Per-wave LDS tables of the backward's grouped updates.  Row 64 of `rec`
 // is zero: it pads a batch of members, so padded slots add exact zeros.
+// Tables are component-major with a pitch of 65 floats (lane 64 = the zero
+// padding member): a lane reading its own values and the owner lanes reading
+// one member's components both hit distinct LDS banks.
+constexpr int kPitch = 65;
+
 template <int L>
 struct WaveTables {
     static constexpr int nsh = (L + 1) * (L + 1);
-    static constexpr int kRec = 64 * nsh; // offset of rec
-    static constexpr int kOne = kRec + 65 * 8;
-    // [0, kRec): SH basis of each lane's ray, written once;
-    // rec [kRec, kOne): per step and lane 8 floats: dL/d(r, g, b, last
-    //   channel), flushed position gradient (x, y, z), point error;
+    static constexpr int kRec = kPitch * nsh; // offset of rec
+    static constexpr int kOne = kRec + kPitch * 8;
+    // y [0, kRec): SH basis function k of lane l at k * kPitch + l;
+    // rec [kRec, kOne): per step, component c of lane l at c * kPitch + l:
+    //   dL/d(r, g, b, last channel), flushed position gradient (x, y, z),
+    //   point error;
     // [kOne]: 1.0, the multiplier of the non-SH components
     float buf[kOne + 1];
     __device__ float *y() { return buf; }
@@ -367,25 +373,23 @@ __device__ __forceinline__ OwnerLane owner_lane(int last_ch) {
     OwnerLane o;
     o.also_last = false;
     if (lane < 3 * nsh) {
-        o.y_base = lane / 3;
-        o.y_stride = nsh;
-        o.g_base = lane % 3;
-        o.g_stride = 8;
+        o.y_base = (lane / 3) * kPitch;
+        o.y_stride = 1;
+        o.g_base = (lane % 3) * kPitch;
+        o.g_stride = 1;
         o.also_last = lane == last_ch;
     } else {
         o.y_base = one_idx;
         o.y_stride = 0;
+        o.g_stride = 1;
         if (lane == last_ch) {
-            o.g_base = 3;
-            o.g_stride = 8;
+            o.g_base = 3 * kPitch;
         } else if (lane >= 60 && lane < 63) {
-            o.g_base = 4 + (lane - 60);
-            o.g_stride = 8;
+            o.g_base = (4 + (lane - 60)) * kPitch;
         } else if (lane == 63) {
-            o.g_base = 7;
-            o.g_stride = 8;
+            o.g_base = 7 * kPitch;
         } else {
-            o.g_base = 64 * 8;
+            o.g_base = 64; // the zero padding member of component 0
             o.g_stride = 0;
         }
     }
@@ -413,9 +417,9 @@ __device__ __forceinline__ void grouped_backward_updates(
     const uint32_t lane = lane_id();
     float *rec = tb.rec();
     if (part) {
-        rec[lane * 8 + 4] = flush ? flush_g[0] : 0.0f;
-        rec[lane * 8 + 5] = flush ? flush_g[1] : 0.0f;
-        rec[lane * 8 + 6] = flush ? flush_g[2] : 0.0f;
+        rec[4 * kPitch + lane] = flush ? flush_g[0] : 0.0f;
+        rec[5 * kPitch + lane] = flush ? flush_g[1] : 0.0f;
+        rec[6 * kPitch + lane] = flush ? flush_g[2] : 0.0f;
     }
     __builtin_amdgcn_wave_barrier();
     const float *ybase = tb.buf + ow.y_base;
@@ -445,7 +449,7 @@ __device__ __forceinline__ void grouped_backward_updates(
             if (any_also_last) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    if (ow.also_last) acc = acc + rec[m[u] * 8 + 3];
+                    if (ow.also_last) acc = acc + rec[3 * kPitch + m[u]];
                 }
             }
         }
@@ -461,9 +465,12 @@ __device__ __forceinline__ void grouped_backward_updates(
 template <int L>
 __device__ __forceinline__ void publish_step(WaveTables<L> &tb, float gr, float gg, float gb,
                                              float g_last, float pe) {
-    float *r = tb.rec() + lane_id() * 8;
-    *reinterpret_cast<float4 *>(r) = make_float4(gr, gg, gb, g_last);
-    r[7] = pe;
+    float *r = tb.rec() + lane_id();
+    r[0] = gr;
+    r[kPitch] = gg;
+    r[2 * kPitch] = gb;
+    r[3 * kPitch] = g_last;
+    r[7 * kPitch] = pe;
 }
 
 template <int L>
@@ -471,8 +478,10 @@ __device__ __forceinline__ void tables_init(WaveTables<L> &tb, const float *sh) 
     constexpr int nsh = (L + 1) * (L + 1);
     const uint32_t lane = lane_id();
 #pragma unroll
-    for (int k = 0; k < nsh; ++k) tb.y()[lane * nsh + k] = sh[k];
-    if (lane < 8u) tb.rec()[64 * 8 + lane] = 0.0f;
+    for (int k = 0; k < nsh; ++k) tb.y()[k * kPitch + lane] = sh[k];
+    // the padding member (lane 64): zero basis and zero record
+    if (lane < (uint32_t)nsh) tb.y()[lane * kPitch + 64] = 0.0f;
+    if (lane < 8u) tb.rec()[lane * kPitch + 64] = 0.0f;
     if (lane == 0) tb.buf[WaveTables<L>::kOne] = 1.0f;
     __builtin_amdgcn_wave_barrier();
 }
@@ -499,7 +508,7 @@ backward_sdf_kernel(BwdArgs a) {
         sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
         tables_init<L>(tb, sh0);
     }
-    const float *sh = tb.y() + lane * nsh; // this ray's SH basis, in LDS
+    const float *sh = tb.y() + lane; // this ray's SH basis, in LDS (stride kPitch)
 
     const float sha = a.sharpness[0];
     const int32_t sdf_ch = a.settings.sdf_channel >= 0 ? a.settings.sdf_channel : D - 1;
@@ -590,7 +599,7 @@ backward_sdf_kernel(BwdArgs a) {
             const float Tn = T * (1.0f - alpha);
             if constexpr (!STATS) {
                 float r, g, b;
-                sh_rgb<L>(sh, row, r, g, b);
+                sh_rgb<L>(sh, kPitch, row, r, g, b);
                 const float w = T * alpha;
                 C0 = fmaf(w, r, C0);
                 C1 = fmaf(w, g, C1);
@@ -700,7 +709,7 @@ backward_density_kernel(BwdArgs a) {
         sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
         tables_init<L>(tb, sh0);
     }
-    const float *sh = tb.y() + lane * nsh; // this ray's SH basis, in LDS
+    const float *sh = tb.y() + lane; // this ray's SH basis, in LDS (stride kPitch)
 
     const OwnerLane owner = owner_lane<L>(D - 1);
     const float thr = a.settings.weight_threshold;
@@ -766,7 +775,7 @@ backward_density_kernel(BwdArgs a) {
             if constexpr (!STATS) {
                 float r, g, b;
                 if (s > 1e-6f) {
-                    sh_rgb<L>(sh, row, r, g, b);
+                    sh_rgb<L>(sh, kPitch, row, r, g, b);
                 } else {
                     r = g = b = 0.0f;
                 }
@@ -964,12 +973,12 @@ __global__ __launch_bounds__(kBlock) void render_kernel(RenderArgs a) {
             ray.dz = dir[2] / n;
         }
     }
-    float *sh = sh_all + threadIdx.x * nsh;
+    float *sh = sh_all + threadIdx.x; // basis function k at sh[k * kBlock]
     {
         float sh0[nsh];
         sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
 #pragma unroll
-        for (int k = 0; k < nsh; ++k) sh[k] = sh0[k];
+        for (int k = 0; k < nsh; ++k) sh[k * kBlock] = sh0[k];
     }
     const float sha = a.sharpness[0];
     const int32_t sdf_ch = a.settings.sdf_channel;
@@ -1003,7 +1012,7 @@ __global__ __launch_bounds__(kBlock) void render_kernel(RenderArgs a) {
             const float w = T * alpha;
             float r, g, b;
             if (NEUS || (float)row[D - 1] > 1e-6f) {
-                sh_rgb<L>(sh, row, r, g, b);
+                sh_rgb<L>(sh, kBlock, row, r, g, b);
             } else {
                 r = g = b = 0.0f;
             }
