@@ -333,14 +333,16 @@ constexpr int kPitch = 65;
 template <int L>
 struct WaveTables {
     static constexpr int nsh = (L + 1) * (L + 1);
-    static constexpr int kRec = kPitch * nsh; // offset of rec
-    static constexpr int kOne = kRec + kPitch * 8;
-    // y [0, kRec): SH basis function k of lane l at k * kPitch + l;
-    // rec [kRec, kOne): per step, component c of lane l at c * kPitch + l:
+    static constexpr int kOnes = kPitch * nsh;      // offset of the row of ones
+    static constexpr int kRec = kOnes + kPitch;     // offset of rec
+    static constexpr int kZeros = kRec + kPitch * 8; // offset of the row of zeros
+    // y [0, kOnes): SH basis function k of lane l at k * kPitch + l;
+    // ones: the multiplier of the non-SH components;
+    // rec [kRec, kZeros): per step, component c of lane l at c * kPitch + l:
     //   dL/d(r, g, b, last channel), flushed position gradient (x, y, z),
     //   point error;
-    // [kOne]: 1.0, the multiplier of the non-SH components
-    float buf[kOne + 1];
+    // zeros: what the idle owner lanes read
+    float buf[kZeros + kPitch];
     __device__ float *y() { return buf; }
     __device__ float *rec() { return buf + kRec; }
 };
@@ -361,39 +363,64 @@ __device__ __forceinline__ int pop_member(uint64_t &mm) {
 //   i == 63:             1 * point error(m)
 //   others:              1 * 0 (the zero row)
 struct OwnerLane {
-    int y_base, y_stride, g_base, g_stride;
-    bool also_last; // last_ch is an SH component too: add dL/dlast as well
+    int y_base, g_base; // member m: y = buf[y_base + m], g = buf[g_base + m]
+    bool also_last;     // last_ch is an SH component too: add dL/dlast as well
 };
 
 template <int L>
 __device__ __forceinline__ OwnerLane owner_lane(int last_ch) {
+    using T = WaveTables<L>;
     constexpr int nsh = (L + 1) * (L + 1);
-    constexpr int one_idx = WaveTables<L>::kOne;
     const int lane = (int)lane_id();
     OwnerLane o;
     o.also_last = false;
     if (lane < 3 * nsh) {
         o.y_base = (lane / 3) * kPitch;
-        o.y_stride = 1;
-        o.g_base = (lane % 3) * kPitch;
-        o.g_stride = 1;
+        o.g_base = T::kRec + (lane % 3) * kPitch;
         o.also_last = lane == last_ch;
     } else {
-        o.y_base = one_idx;
-        o.y_stride = 0;
-        o.g_stride = 1;
+        o.y_base = T::kOnes;
         if (lane == last_ch) {
-            o.g_base = 3 * kPitch;
+            o.g_base = T::kRec + 3 * kPitch;
         } else if (lane >= 60 && lane < 63) {
-            o.g_base = (4 + (lane - 60)) * kPitch;
+            o.g_base = T::kRec + (4 + (lane - 60)) * kPitch;
         } else if (lane == 63) {
-            o.g_base = 7 * kPitch;
+            o.g_base = T::kRec + 7 * kPitch;
         } else {
-            o.g_base = 64; // the zero padding member of component 0
-            o.g_stride = 0;
+            o.g_base = T::kZeros;
         }
     }
     return o;
+}
+
+// Sum over the members in `mm` of buf[y_base + m] * buf[g_base + m] (+ the
+// last channel on the also_last lane), four members at a time.
+template <bool ALSO_LAST>
+__device__ __forceinline__ float sum_members(uint64_t mm, const float *__restrict__ buf,
+                                             const OwnerLane &ow, const float *last) {
+    const float *yb = buf + ow.y_base;
+    const float *gb = buf + ow.g_base;
+    float acc = 0.0f;
+    while (mm) {
+        int m[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) m[u] = pop_member(mm);
+        float y[4], g[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            y[u] = yb[m[u]];
+            g[u] = gb[m[u]];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc = acc + y[u] * g[u];
+        if constexpr (ALSO_LAST) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (ow.also_last) acc = acc + last[m[u]];
+            }
+        }
+    }
+    return acc;
 }
 
 // Grouped gradient updates of one wave-synchronous step (all 64 lanes
@@ -422,8 +449,6 @@ __device__ __forceinline__ void grouped_backward_updates(
         rec[6 * kPitch + lane] = flush ? flush_g[2] : 0.0f;
     }
     __builtin_amdgcn_wave_barrier();
-    const float *ybase = tb.buf + ow.y_base;
-    const float *gbase = rec + ow.g_base;
     const bool any_also_last = __ballot(ow.also_last) != 0ull;
     const uint64_t flushing = __ballot(part && flush);
     uint64_t todo = __ballot(part);
@@ -432,31 +457,27 @@ __device__ __forceinline__ void grouped_backward_updates(
         const uint32_t c = readlane_u(key, leader);
         const uint64_t grp = __ballot(part && key == c);
         todo &= ~grp;
-        float acc = 0.0f;
-        uint64_t mm = grp;
-        while (mm) {
-            int m[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) m[u] = pop_member(mm);
-            float y[4], g[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                y[u] = ybase[m[u] * ow.y_stride];
-                g[u] = gbase[m[u] * ow.g_stride];
+        const float acc = any_also_last
+                              ? sum_members<true>(grp, tb.buf, ow, rec + 3 * kPitch)
+                              : sum_members<false>(grp, tb.buf, ow, rec + 3 * kPitch);
+        const bool pos = (grp & flushing) != 0ull;
+        if constexpr (sizeof(AT) == 4) {
+            // one atomic instruction: the row, the position and the point error
+            float *dst = nullptr;
+            if (lane < (uint32_t)D) {
+                dst = static_cast<float *>(attr_grad) + (uint64_t)c * D + lane;
+            } else if (lane >= 60u && lane < 63u) {
+                if (pos) dst = points_grad + 3ull * c + (lane - 60u);
+            } else if (lane == 63u && point_error) {
+                dst = static_cast<float *>(point_error) + c;
             }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) acc = acc + y[u] * g[u];
-            if (any_also_last) {
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    if (ow.also_last) acc = acc + rec[3 * kPitch + m[u]];
-                }
-            }
+            if (dst) atomicAdd(dst, acc);
+        } else {
+            atomic_add_row<AT>(attr_grad, c, lane, (uint32_t)D, acc);
+            if (point_error && lane == 63u) atomic_add_elem<AT>(point_error, c, acc);
+            if (pos && lane >= 60u && lane < 63u)
+                atomicAdd(points_grad + 3ull * c + (lane - 60u), acc);
         }
-        atomic_add_row<AT>(attr_grad, c, lane, (uint32_t)D, acc);
-        if (point_error && lane == 63u) atomic_add_elem<AT>(point_error, c, acc);
-        if ((grp & flushing) && lane >= 60u && lane < 63u)
-            atomicAdd(points_grad + 3ull * c + (lane - 60u), acc);
     }
     __builtin_amdgcn_wave_barrier();
 }
@@ -482,7 +503,12 @@ __device__ __forceinline__ void tables_init(WaveTables<L> &tb, const float *sh) 
     // the padding member (lane 64): zero basis and zero record
     if (lane < (uint32_t)nsh) tb.y()[lane * kPitch + 64] = 0.0f;
     if (lane < 8u) tb.rec()[lane * kPitch + 64] = 0.0f;
-    if (lane == 0) tb.buf[WaveTables<L>::kOne] = 1.0f;
+    tb.buf[WaveTables<L>::kOnes + lane] = 1.0f;
+    tb.buf[WaveTables<L>::kZeros + lane] = 0.0f;
+    if (lane == 0) {
+        tb.buf[WaveTables<L>::kOnes + 64] = 1.0f;
+        tb.buf[WaveTables<L>::kZeros + 64] = 0.0f;
+    }
     __builtin_amdgcn_wave_barrier();
 }
 
