@@ -193,16 +193,29 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
  * trace rays in that order (outputs stay in the caller's order).  For rays
  * in no particular order (random training batches) it makes the rays of a
  * wavefront start in the same cell and point the same way.  Requires
- * settings->ray_image_width == 0.  ray_order == NULL: the caller's order. */
+ * settings->ray_image_width == 0.  ray_order == NULL: the caller's order.
+ *
+ * Gradient accumulator (backward, fp32 attributes; an fp16 trace ignores
+ * it): one 256-byte-aligned row per cell holding that cell's attribute,
+ * position and point-error gradients side by side.  The backward clears it,
+ * adds every ray's contributions into it, then adds each row into
+ * attribute_grad, points_grad and point_error.  A wavefront's atomic update
+ * of a cell then touches fewer 64-byte memory segments than updates of the
+ * three output arrays do.  grad_accum == NULL: updates go to the outputs. */
 typedef struct sdf_trace_plan {
     void *walk_record;        /* device memory, 8-byte aligned, or NULL */
     size_t walk_record_bytes; /* >= sdf_walk_record_bytes(num_rays, ray_image_width, walk_budget) */
     uint32_t walk_budget;
     const uint32_t *ray_order; /* device memory [num_rays], or NULL */
+    void *grad_accum;          /* device memory, 256-byte aligned, or NULL */
+    size_t grad_accum_bytes;   /* >= sdf_grad_accum_bytes(sh_degree, num_points) */
 } sdf_trace_plan;
 
 size_t sdf_walk_record_bytes(uint32_t num_rays, uint32_t ray_image_width,
                              uint32_t budget);
+
+/* Bytes of the backward's gradient accumulator (0 for an invalid degree). */
+size_t sdf_grad_accum_bytes(int sh_degree, uint32_t num_points);
 
 /* Scratch bytes of sdf_ray_order. */
 size_t sdf_ray_order_scratch_bytes(uint32_t num_points, uint32_t num_rays);
@@ -336,6 +349,8 @@ int sdf_debug_fpmath(int op, const float *in, void *out, uint64_t n,
 #define SDF_KERNEL_NN 4
 #define SDF_KERNEL_RENDER 5
 #define SDF_KERNEL_RAY_ORDER 6
+#define SDF_KERNEL_GRAD_CLEAR 7
+#define SDF_KERNEL_GRAD_FINALIZE 8
 int sdf_set_timing(int enable);
 int sdf_timing_collect(int *kinds, float *ms, int max_n, int *n_out);
 

@@ -28,6 +28,7 @@ EXPORTS = (
     "sdf_trace_backward",
     "sdf_trace_benchmark",
     "sdf_walk_record_bytes",
+    "sdf_grad_accum_bytes",
     "sdf_ray_order_scratch_bytes",
     "sdf_ray_order",
     "sdf_trace_forward_planned",
@@ -47,7 +48,7 @@ EXPORTS = (
 )
 
 KERNEL_NAMES = {0: "prefetch_adjacent_diff", 1: "forward", 2: "backward", 3: "build_aabb_tree", 4: "nn",
-                5: "render", 6: "ray_order"}
+                5: "render", 6: "ray_order", 7: "grad_clear", 8: "grad_finalize"}
 
 SDF_CAMERA_PINHOLE = 0
 SDF_CAMERA_FISHEYE = 1
@@ -89,13 +90,16 @@ class Visualization(C.Structure):
 
 
 class TracePlanDesc(C.Structure):
-    """sdf_trace_plan: the forward's walk record and the rays' launch order."""
+    """sdf_trace_plan: the forward's walk record, the rays' launch order and
+    the backward's gradient accumulator."""
 
     _fields_ = [
         ("walk_record", C.c_void_p),
         ("walk_record_bytes", C.c_size_t),
         ("walk_budget", C.c_uint32),
         ("ray_order", C.c_void_p),
+        ("grad_accum", C.c_void_p),
+        ("grad_accum_bytes", C.c_size_t),
     ]
 
 
@@ -145,6 +149,8 @@ def lib() -> C.CDLL:
         C.POINTER(Visualization), P, P, P, P]
     L.sdf_walk_record_bytes.restype = SZ
     L.sdf_walk_record_bytes.argtypes = [U32, U32, U32]
+    L.sdf_grad_accum_bytes.restype = SZ
+    L.sdf_grad_accum_bytes.argtypes = [C.c_int, U32]
     L.sdf_ray_order_scratch_bytes.restype = SZ
     L.sdf_ray_order_scratch_bytes.argtypes = [U32, U32]
     L.sdf_ray_order.restype = C.c_int

@@ -231,6 +231,16 @@ int trace_backward_impl(const sdf_trace_plan *plan, int sh_degree,
     const uint32_t *order = nullptr;
     rc = check_plan(plan, num_rays, settings->ray_image_width, rec, order);
     if (rc != SDF_OK) return rc;
+    float *accum = nullptr;
+    if (plan && plan->grad_accum && !half) {
+        const size_t need = sdf_grad_accum_bytes(sh_degree, num_points);
+        if (plan->grad_accum_bytes < need)
+            return fail(SDF_E_INVALID, "gradient accumulator must hold %zu bytes (got %zu)", need,
+                        plan->grad_accum_bytes);
+        if ((reinterpret_cast<uintptr_t>(plan->grad_accum) & 255u) != 0)
+            return fail(SDF_E_INVALID, "gradient accumulator must be 256-byte aligned");
+        accum = static_cast<float *>(plan->grad_accum);
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     tbegin(SDF_KERNEL_PREFETCH, s);
     hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
@@ -238,6 +248,12 @@ int trace_backward_impl(const sdf_trace_plan *plan, int sh_degree,
     tend(s);
     if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
     if (num_rays == 0) return SDF_OK;
+    if (accum) {
+        tbegin(SDF_KERNEL_GRAD_CLEAR, s);
+        e = launch_grad_clear(sh_degree, accum, num_points, s);
+        tend(s);
+        if (e != hipSuccess) return hip_fail(e, "gradient accumulator clear");
+    }
     BwdArgs a = {};
     a.record = rec;
     a.order = order;
@@ -260,10 +276,18 @@ int trace_backward_impl(const sdf_trace_plan *plan, int sh_degree,
     a.attr_grad = attribute_grad;
     a.point_error = ray_error ? point_error : nullptr;
     a.sharpness_grad = sharpness_grad;
+    a.accum = accum;
     tbegin(SDF_KERNEL_BACKWARD, s);
     e = launch_backward(sh_degree, a, neus, false, half, s);
     tend(s);
     if (e != hipSuccess) return hip_fail(e, "backward");
+    if (accum) {
+        tbegin(SDF_KERNEL_GRAD_FINALIZE, s);
+        e = launch_grad_finalize(sh_degree, accum, num_points, attribute_grad, points_grad,
+                                 static_cast<float *>(a.point_error), s);
+        tend(s);
+        if (e != hipSuccess) return hip_fail(e, "gradient accumulator finalize");
+    }
     return SDF_OK;
 }
 
@@ -278,6 +302,11 @@ const char *sdf_last_error(void) { return g_err; }
 int sdf_attribute_dim(int sh_degree) {
     if (sh_degree < 0 || sh_degree > 3) return -1;
     return 1 + 3 * (sh_degree + 1) * (sh_degree + 1);
+}
+
+size_t sdf_grad_accum_bytes(int sh_degree, uint32_t num_points) {
+    if (sh_degree < 0 || sh_degree > 3) return 0;
+    return (size_t)num_points * accum_stride(sh_degree) * sizeof(float);
 }
 
 size_t sdf_trace_scratch_bytes(uint32_t num_points, uint32_t adjacency_size) {

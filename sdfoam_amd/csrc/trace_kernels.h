@@ -85,6 +85,10 @@ struct BwdArgs {
     void *attr_grad;   // attribute type
     void *point_error; // attribute type
     float *sharpness_grad;
+    // fp32 only: per-cell gradient rows (accum_stride(L) floats: attribute
+    // row, position x/y/z, point error), added into the outputs by
+    // launch_grad_finalize; nullptr: atomics go to the outputs directly
+    float *accum;
     // walk statistics (STATS instantiation only)
     uint64_t *visit_hash;
     uint32_t *steps;
@@ -125,6 +129,21 @@ hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32
 // half: fp16 attributes (settings.attr_type == SDF_ATTR_F16)
 hipError_t launch_forward(int L, const FwdArgs &a, bool neus, bool stats, bool half,
                           hipStream_t stream);
+// Floats per cell row of the backward's gradient accumulator: the next
+// power of two >= D + 4 (attribute row, position, point error), at least 8,
+// so that a row spans the fewest 64-byte segments.
+constexpr uint32_t accum_stride(int L) {
+    return L <= 0 ? 8u : L <= 2 ? 32u : 64u;
+}
+
+// Clears num_points rows of the accumulator.
+hipError_t launch_grad_clear(int L, float *accum, uint32_t num_points, hipStream_t stream);
+
+// attribute_grad [N, D] += rows[:, :D]; points_grad [N, 3] += rows[:, D:D+3];
+// point_error [N] += rows[:, D+3] (point_error may be nullptr).
+hipError_t launch_grad_finalize(int L, const float *accum, uint32_t num_points, float *attr_grad,
+                                float *points_grad, float *point_error, hipStream_t stream);
+
 hipError_t launch_backward(int L, const BwdArgs &a, bool neus, bool stats, bool half,
                            hipStream_t stream);
 hipError_t launch_fpmath(int op, const float *in, void *out, uint64_t n, hipStream_t stream);

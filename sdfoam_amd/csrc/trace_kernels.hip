@@ -434,12 +434,16 @@ __device__ __forceinline__ float sum_members(uint64_t mm, const float *__restric
 // coalesced atomic instruction per cell), lanes 60..62 add the summed
 // flushed position gradient (if a member flushed one) and lane 63 the point
 // error.  The owner lanes read the members four at a time, two LDS reads and
-// one fma per member.
+// one fma per member.  With an accumulator (fp32), the instruction's targets
+// are one row of accum_stride(L) floats per cell: an atomic add costs about
+// one memory transaction per 64-byte segment it touches, and the row spans
+// ceil((D + 4) / 16) of them where the three output arrays span up to
+// ceil(D / 16) + 3.
 template <int L, typename AT>
 __device__ __forceinline__ void grouped_backward_updates(
     bool part, uint32_t key, bool flush, const float *flush_g, const OwnerLane &ow,
     WaveTables<L> &tb, void *__restrict__ attr_grad, void *__restrict__ point_error,
-    float *__restrict__ points_grad) {
+    float *__restrict__ points_grad, float *__restrict__ accum) {
     constexpr int D = 1 + 3 * (L + 1) * (L + 1);
     const uint32_t lane = lane_id();
     float *rec = tb.rec();
@@ -464,7 +468,16 @@ __device__ __forceinline__ void grouped_backward_updates(
         if constexpr (sizeof(AT) == 4) {
             // one atomic instruction: the row, the position and the point error
             float *dst = nullptr;
-            if (lane < (uint32_t)D) {
+            if (accum) {
+                float *row = accum + (uint64_t)c * accum_stride(L);
+                if (lane < (uint32_t)D) {
+                    dst = row + lane;
+                } else if (lane >= 60u && lane < 63u) {
+                    if (pos) dst = row + D + (lane - 60u);
+                } else if (lane == 63u && point_error) {
+                    dst = row + D + 3;
+                }
+            } else if (lane < (uint32_t)D) {
                 dst = static_cast<float *>(attr_grad) + (uint64_t)c * D + lane;
             } else if (lane >= 60u && lane < 63u) {
                 if (pos) dst = points_grad + 3ull * c + (lane - 60u);
@@ -683,7 +696,7 @@ backward_sdf_kernel(BwdArgs a) {
             // flush of the same cell) or when its walk ends
             const bool part = pend && (si.stepped || !ws.alive);
             grouped_backward_updates<L, AT>(part, pend_cell, si.stepped && flush, flush_g, owner,
-                                            tb, a.attr_grad, a.point_error, a.points_grad);
+                                            tb, a.attr_grad, a.point_error, a.points_grad, a.accum);
             if (si.stepped) {
                 publish_step<L>(tb, dr, dg, db, dsdf, pe);
                 pend_cell = ws.cell;
@@ -696,7 +709,7 @@ backward_sdf_kernel(BwdArgs a) {
         // steps still pending when their walks ended
         const float zero3[3] = {0.0f, 0.0f, 0.0f};
         grouped_backward_updates<L, AT>(pend, pend_cell, false, zero3, owner, tb, a.attr_grad,
-                                        a.point_error, a.points_grad);
+                                        a.point_error, a.points_grad, a.accum);
     }
 
     if constexpr (STATS) {
@@ -851,7 +864,7 @@ backward_density_kernel(BwdArgs a) {
         if constexpr (!STATS) {
             const bool part = pend && (si.stepped || !ws.alive);
             grouped_backward_updates<L, AT>(part, pend_cell, si.stepped && flush, flush_g, owner,
-                                            tb, a.attr_grad, a.point_error, a.points_grad);
+                                            tb, a.attr_grad, a.point_error, a.points_grad, a.accum);
             if (si.stepped) {
                 publish_step<L>(tb, dr, dg, db, dds, pe);
                 pend_cell = ws.cell;
@@ -863,7 +876,7 @@ backward_density_kernel(BwdArgs a) {
     if constexpr (!STATS) {
         const float zero3[3] = {0.0f, 0.0f, 0.0f};
         grouped_backward_updates<L, AT>(pend, pend_cell, false, zero3, owner, tb, a.attr_grad,
-                                        a.point_error, a.points_grad);
+                                        a.point_error, a.points_grad, a.accum);
     }
 
     if constexpr (STATS) {
@@ -963,6 +976,83 @@ hipError_t launch_backward(int L, const BwdArgs &a, bool neus, bool stats, bool 
                            hipStream_t stream) {
     return half ? launch_backward_T<_Float16>(L, a, neus, stats, stream)
                 : launch_backward_T<float>(L, a, neus, stats, stream);
+}
+
+// ---------------------------------------------------------------------------
+// backward gradient accumulator: clear, then add the rows into the outputs
+
+constexpr uint32_t kAccumBlocks = 16384; // grid-stride cap of the two passes
+
+__global__ __launch_bounds__(kBlock) void grad_clear_kernel(float4 *__restrict__ rows,
+                                                            uint64_t n4) {
+    const uint64_t step = (uint64_t)gridDim.x * kBlock;
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += step)
+        rows[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+// One thread per row element; an element that is exactly zero (a cell no
+// ray reached) leaves its output untouched.
+template <int L>
+__global__ __launch_bounds__(kBlock) void grad_finalize_kernel(
+    const float *__restrict__ rows, uint32_t num_points, float *__restrict__ attr_grad,
+    float *__restrict__ points_grad, float *__restrict__ point_error) {
+    constexpr uint32_t S = accum_stride(L);
+    constexpr uint32_t D = 1 + 3 * (L + 1) * (L + 1);
+    const uint64_t total = (uint64_t)num_points * S;
+    const uint64_t step = (uint64_t)gridDim.x * kBlock;
+    for (uint64_t t = (uint64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += step) {
+        const uint32_t j = (uint32_t)(t % S);
+        if (j >= D + 4) continue;
+        const float v = rows[t];
+        if (v == 0.0f) continue;
+        const uint64_t c = t / S;
+        if (j < D) {
+            attr_grad[c * D + j] += v;
+        } else if (j < D + 3) {
+            points_grad[c * 3 + (j - D)] += v;
+        } else if (point_error) {
+            point_error[c] += v;
+        }
+    }
+}
+
+static inline dim3 accum_grid(uint64_t threads) {
+    const uint64_t b = (threads + kBlock - 1) / kBlock;
+    return dim3((unsigned)(b < kAccumBlocks ? (b ? b : 1) : kAccumBlocks));
+}
+
+hipError_t launch_grad_clear(int L, float *accum, uint32_t num_points, hipStream_t stream) {
+    if (L < 0 || L > 3) return hipErrorInvalidValue;
+    const uint64_t n4 = (uint64_t)num_points * accum_stride(L) / 4;
+    hipLaunchKernelGGL(grad_clear_kernel, accum_grid(n4), dim3(kBlock), 0, stream,
+                       reinterpret_cast<float4 *>(accum), n4);
+    return hipGetLastError();
+}
+
+hipError_t launch_grad_finalize(int L, const float *accum, uint32_t num_points, float *attr_grad,
+                                float *points_grad, float *point_error, hipStream_t stream) {
+    const dim3 grid = accum_grid((uint64_t)num_points * accum_stride(L));
+    switch (L) {
+    case 0:
+        hipLaunchKernelGGL(grad_finalize_kernel<0>, grid, dim3(kBlock), 0, stream, accum,
+                           num_points, attr_grad, points_grad, point_error);
+        break;
+    case 1:
+        hipLaunchKernelGGL(grad_finalize_kernel<1>, grid, dim3(kBlock), 0, stream, accum,
+                           num_points, attr_grad, points_grad, point_error);
+        break;
+    case 2:
+        hipLaunchKernelGGL(grad_finalize_kernel<2>, grid, dim3(kBlock), 0, stream, accum,
+                           num_points, attr_grad, points_grad, point_error);
+        break;
+    case 3:
+        hipLaunchKernelGGL(grad_finalize_kernel<3>, grid, dim3(kBlock), 0, stream, accum,
+                           num_points, attr_grad, points_grad, point_error);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

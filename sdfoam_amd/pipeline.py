@@ -366,10 +366,14 @@ class Pipeline:
                        start_point, rgb_out, grad_in, depth_quantiles=None, depth_indices=None,
                        depth_grad_in=None, ray_error=None, weight_threshold=None,
                        max_intersections=None, alpha_mode=None, inv_s=None, eps=None,
-                       sdf_channel=None, trace_plan=None, sort_rays=None):
+                       sdf_channel=None, trace_plan=None, sort_rays=None, grad_accum=True):
         """Reference arguments and outputs, plus ``trace_plan`` (the
-        forward's "trace_plan": its ray order and walk record) and
-        ``sort_rays`` (as in trace_forward, when no plan is given)."""
+        forward's "trace_plan": its ray order and walk record),
+        ``sort_rays`` (as in trace_forward, when no plan is given) and
+        ``grad_accum``: with fp32 attributes, accumulate each cell's
+        gradients in one aligned row of a temporary buffer (16 bytes more
+        than the outputs per cell at SH degree 3) before adding them to the
+        outputs; False updates the outputs directly."""
         points_c = points.contiguous()
         attributes_c = attributes.contiguous()
         adj_c = point_adjacency.contiguous()
@@ -469,11 +473,20 @@ class Pipeline:
             ptr(dq), ptr(didx), ptr(rgba), ptr(g), ptr(dgrad), ptr(rerr), ptr(points_grad),
             ptr(attr_grad), ptr(point_error), ptr(sharpness), ptr(sharpness_grad),
             ptr(scratch), nbytes, _lib.stream_handle(dev))
+        desc = trace_plan.desc() if trace_plan is not None else _lib.TracePlanDesc()
+        accum = None
+        if grad_accum and num_rays > 0 and self._attr_dtype == torch.float32:
+            accum_bytes = int(_lib.lib().sdf_grad_accum_bytes(self._sh_degree, num_points))
+            accum = torch.empty(accum_bytes + 256, dtype=torch.uint8, device=dev)
+            desc.grad_accum = (accum.data_ptr() + 255) & ~255
+            desc.grad_accum_bytes = accum_bytes
         with torch.cuda.device(dev):
-            if trace_plan is None:
+            if trace_plan is None and accum is None:
                 check(_lib.lib().sdf_trace_backward(*args))
             else:
-                check(_lib.lib().sdf_trace_backward_planned(C.byref(trace_plan.desc()), *args))
+                check(_lib.lib().sdf_trace_backward_planned(C.byref(desc), *args))
+        # `accum` may be freed now: torch reuses it only for later work on
+        # this stream
         out = {
             "points_grad": points_grad,
             "attr_grad": attr_grad,

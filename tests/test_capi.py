@@ -102,6 +102,30 @@ def test_walk_record_sizes_and_errors():
         assert rc == 1 and msg in L.sdf_last_error()
 
 
+def test_grad_accum_sizes_and_errors():
+    from sdfoam_amd import _lib
+
+    L = _lib.lib()
+    # one row per cell: D + 4 floats (attributes, position, point error)
+    # rounded up to 8, 32, 32, 64 floats
+    assert [L.sdf_grad_accum_bytes(d, 10) for d in range(4)] == [320, 1280, 1280, 2560]
+    assert L.sdf_grad_accum_bytes(4, 10) == 0
+    assert L.sdf_grad_accum_bytes(3, 1 << 20) == 256 << 20
+    s = _settings()
+    buf = (C.c_uint64 * 512)()
+    p = C.cast(buf, C.c_void_p)
+    nb = L.sdf_trace_scratch_bytes(10, 4)
+    base = C.cast(buf, C.c_void_p).value
+    misaligned = base + 8 if (base + 8) % 256 else base + 16
+    for addr, nbytes, msg in ((base, 2559, b"gradient accumulator must hold 2560 bytes"),
+                              (misaligned, 2560, b"must be 256-byte aligned")):
+        plan = _lib.TracePlanDesc(None, 0, 0, None, addr, nbytes)
+        rc = L.sdf_trace_backward_planned(C.byref(plan), 3, C.byref(s), 10, p, p, 4, p, p, 1, p,
+                                          p, 0, None, None, p, p, None, None, p, p, None, p,
+                                          None, p, nb, None)
+        assert rc == 1 and msg in L.sdf_last_error()
+
+
 def test_ray_order_and_plan_errors():
     from sdfoam_amd import _lib
 

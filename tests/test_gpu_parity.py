@@ -242,10 +242,11 @@ def test_forward_parity_c2_sharp(torch_dev, oracle_lib):
 
 
 def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False, walk=False,
-                   walk_budget=None, sort_rays=None):
+                   walk_budget=None, sort_rays=None, grad_accum=True):
     """GPU forward + backward (with walk=True: the backward replays the
-    forward's walk record, `walk_budget` trips per wavefront) and the
-    oracle's backward on the same inputs."""
+    forward's walk record, `walk_budget` trips per wavefront; with
+    grad_accum=False: atomics go to the output arrays, not to the per-cell
+    accumulator rows) and the oracle's backward on the same inputs."""
     import torch
 
     import sdfoam_amd
@@ -269,7 +270,7 @@ def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False, walk=F
                               depth_quantiles=q, depth_indices=fwd["depth_indices"],
                               depth_grad_in=to_dev(w.depth_grad, dev), ray_error=rerr,
                               alpha_mode=mode, inv_s=inv_t,
-                              trace_plan=fwd.get("trace_plan"))
+                              trace_plan=fwd.get("trace_plan"), grad_accum=grad_accum)
     st = pipe.walk_stats(**g, backward=True, alpha_mode=mode, inv_s=inv_t)
     torch.cuda.synchronize()
     rgba = fwd["rgba"].cpu().numpy()
@@ -311,6 +312,23 @@ def test_backward_parity_c1(torch_dev, oracle_lib, mode):
 def test_backward_parity_c2(torch_dev, oracle_lib):
     w = scene(2)
     bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "sdfoam")
+    _check_backward(bwd, st, ref, w)
+
+
+@pytest.mark.parametrize("mode", ["sdfoam", "standard"])
+def test_backward_direct_updates_c1(torch_dev, oracle_lib, mode):
+    """The backward without the gradient accumulator: atomics straight into
+    points_grad, attribute_grad and point_error."""
+    w = scene(1, mode=mode)
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, mode, ray_error=True, walk=True,
+                                  grad_accum=False)
+    _check_backward(bwd, st, ref, w)
+
+
+def test_backward_direct_updates_c2(torch_dev, oracle_lib):
+    w = scene(2)
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "sdfoam", walk=True,
+                                  grad_accum=False)
     _check_backward(bwd, st, ref, w)
 
 
