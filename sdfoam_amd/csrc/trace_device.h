@@ -125,19 +125,40 @@ __host__ inline uint32_t grid_blocks_for_tiles(uint32_t num_tiles) {
     return kXcds * ((num_tiles + kXcds - 1) / kXcds);
 }
 
+// The tile of this block.  Blocks go to the XCDs round robin (block b runs
+// on XCD b % 8).  CHUNK == 0: XCD x takes one contiguous run of the tiles;
+// otherwise the XCDs take turns on runs of CHUNK tiles, so each XCD's work
+// is spread over the whole image (the cost of a tile varies a lot across an
+// image) while neighbouring tiles still share an XCD's L2.  Both are
+// permutations of [0, gridDim.x).
+template <uint32_t CHUNK>
 __device__ __forceinline__ uint32_t block_tile() {
     const uint32_t per = gridDim.x / kXcds;
-    return (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+    const uint32_t k = blockIdx.x / kXcds, x = blockIdx.x % kXcds;
+    if constexpr (CHUNK == 0) {
+        return x * per + k;
+    } else {
+        const uint32_t full = (per / CHUNK) * CHUNK;
+        return k < full ? ((k / CHUNK) * kXcds + x) * CHUNK + k % CHUNK
+                        : kXcds * full + (k - full) * kXcds + x;
+    }
 }
+
+// Tile runs of the forward and the inference render (measured on a
+// 1600x1200 camera: the forward is about 13% faster than with one run per
+// XCD, the backward about 2% slower, so it keeps one run per XCD).
+constexpr uint32_t kForwardChunk = 128;
+constexpr uint32_t kBackwardChunk = 0;
 
 // The ray this lane traces: with `order` (a permutation of the rays, see
 // order_kernels.hip) lane i of the launch takes ray order[i]; entries out of
 // range leave the lane idle.  Otherwise rays in their own order, or 16x16
 // pixel tiles of an image `width` pixels wide.
+template <uint32_t CHUNK>
 __device__ __forceinline__ uint32_t ray_for_lane(uint32_t num_rays, uint32_t width,
                                                  uint32_t num_tiles, bool &valid,
                                                  const uint32_t *__restrict__ order = nullptr) {
-    const uint32_t t = block_tile();
+    const uint32_t t = block_tile<CHUNK>();
     if (t >= num_tiles) {
         valid = false;
         return 0;

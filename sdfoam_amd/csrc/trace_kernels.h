@@ -31,9 +31,11 @@ __host__ inline uint64_t walk_record_entries(uint32_t num_tiles, uint32_t budget
     return (uint64_t)grid_blocks_for_tiles(num_tiles) * (kBlock / 64) * budget * 64;
 }
 
-// this lane's entry of trip 0; trip k is 64 * k entries further
+// this lane's entry of trip 0; trip k is 64 * k entries further.  Rows
+// belong to tiles, not blocks, so kernels with different tile runs share them.
+template <uint32_t CHUNK>
 __device__ inline uint2 *walk_record_lane(const WalkRecordArgs &r, uint32_t lane) {
-    const uint64_t wave = (uint64_t)block_tile() * (kBlock / 64) + (threadIdx.x >> 6);
+    const uint64_t wave = (uint64_t)block_tile<CHUNK>() * (kBlock / 64) + (threadIdx.x >> 6);
     return r.entries + wave * r.budget * 64 + lane;
 }
 

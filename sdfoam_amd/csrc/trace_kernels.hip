@@ -116,7 +116,8 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     }
     bool valid;
     const uint32_t ray_idx =
-        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid, a.order);
+        ray_for_lane<kForwardChunk>(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid,
+                                    a.order);
     const uint32_t lane = lane_id();
 
     RayF ray = {};
@@ -149,7 +150,8 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     // walk record of this wavefront (sdfoam walks only; the density
     // backward walks differently): one row of 64 entries per trip
     uint2 *wrec = nullptr;
-    if (!STATS && NEUS && a.record.entries) wrec = walk_record_lane(a.record, lane);
+    if (!STATS && NEUS && a.record.entries)
+        wrec = walk_record_lane<kForwardChunk>(a.record, lane);
     uint32_t trip = 0;
 
     while (__ballot(ws.alive) != 0ull) {
@@ -536,7 +538,8 @@ backward_sdf_kernel(BwdArgs a) {
     __shared__ WaveTables<L> tables[kBlock / 64];
     bool valid;
     const uint32_t ray_idx =
-        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid, a.order);
+        ray_for_lane<kBackwardChunk>(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid,
+                                     a.order);
     const uint32_t lane = lane_id();
     WaveTables<L> &tb = tables[threadIdx.x >> 6];
 
@@ -585,7 +588,7 @@ backward_sdf_kernel(BwdArgs a) {
     // recorded, the step is read instead of scanned; from the first
     // unrecorded (or out-of-range) entry on, the lane scans.
     const uint2 *wrec = nullptr;
-    if (!STATS && a.record.entries) wrec = walk_record_lane(a.record, lane);
+    if (!STATS && a.record.entries) wrec = walk_record_lane<kBackwardChunk>(a.record, lane);
     uint32_t trip = 0;
     bool pend = false;       // a step whose updates are not applied yet
     uint32_t pend_cell = 0u; // its cell
@@ -737,7 +740,8 @@ backward_density_kernel(BwdArgs a) {
     __shared__ WaveTables<L> tables[kBlock / 64];
     bool valid;
     const uint32_t ray_idx =
-        ray_for_lane(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid, a.order);
+        ray_for_lane<kBackwardChunk>(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid,
+                                     a.order);
     const uint32_t lane = lane_id();
     WaveTables<L> &tb = tables[threadIdx.x >> 6];
 
@@ -1068,7 +1072,7 @@ __global__ __launch_bounds__(kBlock) void render_kernel(RenderArgs a) {
     constexpr int D = 1 + 3 * nsh;
     __shared__ float sh_all[kBlock * nsh];
     bool valid;
-    const uint32_t px = ray_for_lane(a.width * a.height, a.width, a.num_tiles, valid);
+    const uint32_t px = ray_for_lane<kForwardChunk>(a.width * a.height, a.width, a.num_tiles, valid);
     const uint32_t pi = valid ? px % a.width : 0u, pj = valid ? px / a.width : 0u;
 
     RayF ray = {};
