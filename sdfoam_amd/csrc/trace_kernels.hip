@@ -367,15 +367,24 @@ __device__ __forceinline__ int pop_member(uint64_t &mm) {
 struct OwnerLane {
     int y_base, g_base; // member m: y = buf[y_base + m], g = buf[g_base + m]
     bool also_last;     // last_ch is an SH component too: add dL/dlast as well
+    // gradient accumulator row: this lane's float in a cell's row, and whether
+    // it adds to it always (attribute components) or only when a member
+    // flushed a position gradient (position components)
+    uint32_t row_off;
+    bool row_always, row_pos;
 };
 
 template <int L>
-__device__ __forceinline__ OwnerLane owner_lane(int last_ch) {
+__device__ __forceinline__ OwnerLane owner_lane(int last_ch, bool point_error) {
     using T = WaveTables<L>;
     constexpr int nsh = (L + 1) * (L + 1);
     const int lane = (int)lane_id();
+    constexpr int D = 1 + 3 * nsh;
     OwnerLane o;
     o.also_last = false;
+    o.row_off = lane < D ? (uint32_t)lane : lane >= 60 ? (uint32_t)(D + lane - 60) : 0u;
+    o.row_always = lane < D || (lane == 63 && point_error);
+    o.row_pos = lane >= 60 && lane < 63;
     if (lane < 3 * nsh) {
         o.y_base = (lane / 3) * kPitch;
         o.g_base = T::kRec + (lane % 3) * kPitch;
@@ -471,14 +480,9 @@ __device__ __forceinline__ void grouped_backward_updates(
             // one atomic instruction: the row, the position and the point error
             float *dst = nullptr;
             if (accum) {
-                float *row = accum + (uint64_t)c * accum_stride(L);
-                if (lane < (uint32_t)D) {
-                    dst = row + lane;
-                } else if (lane >= 60u && lane < 63u) {
-                    if (pos) dst = row + D + (lane - 60u);
-                } else if (lane == 63u && point_error) {
-                    dst = row + D + 3;
-                }
+                // uniform row base + this lane's precomputed offset
+                if (ow.row_always || (pos && ow.row_pos))
+                    atomicAdd(accum + (uint64_t)c * accum_stride(L) + ow.row_off, acc);
             } else if (lane < (uint32_t)D) {
                 dst = static_cast<float *>(attr_grad) + (uint64_t)c * D + lane;
             } else if (lane >= 60u && lane < 63u) {
@@ -555,7 +559,7 @@ backward_sdf_kernel(BwdArgs a) {
     const float sha = a.sharpness[0];
     const int32_t sdf_ch = a.settings.sdf_channel >= 0 ? a.settings.sdf_channel : D - 1;
     const bool write_sdf = a.settings.sdf_channel >= 0;
-    const OwnerLane owner = owner_lane<L>(write_sdf ? sdf_ch : -1);
+    const OwnerLane owner = owner_lane<L>(write_sdf ? sdf_ch : -1, a.point_error != nullptr);
     const float thr = a.settings.weight_threshold;
     const uint32_t Q = a.num_quantiles;
     const float *rq = (valid && a.quantiles) ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
@@ -754,7 +758,7 @@ backward_density_kernel(BwdArgs a) {
     }
     const float *sh = tb.y() + lane; // this ray's SH basis, in LDS (stride kPitch)
 
-    const OwnerLane owner = owner_lane<L>(D - 1);
+    const OwnerLane owner = owner_lane<L>(D - 1, a.point_error != nullptr);
     const float thr = a.settings.weight_threshold;
     const uint32_t Q = a.num_quantiles;
     const float *rq = (valid && a.quantiles) ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
