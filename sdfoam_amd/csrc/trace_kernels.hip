@@ -332,17 +332,24 @@ __device__ __forceinline__ bool geom_step(GeomState &gs, uint32_t cell, const fl
 // one member's components both hit distinct LDS banks.
 constexpr int kPitch = 65;
 
+// Trips per grouping pass.  A lane's steps wait in kWindow LDS entry slots
+// and are applied together every kWindow trips: rays of a wavefront enter
+// the cells that others of it have just left, so a pass over two trips'
+// steps meets about a third fewer distinct cells than two passes do.
+constexpr int kWindow = 2;
+
 template <int L>
 struct WaveTables {
     static constexpr int nsh = (L + 1) * (L + 1);
     static constexpr int kOnes = kPitch * nsh;      // offset of the row of ones
     static constexpr int kRec = kOnes + kPitch;     // offset of rec
-    static constexpr int kZeros = kRec + kPitch * 8; // offset of the row of zeros
+    static constexpr int kSlot = kPitch * 8;        // floats per entry slot
+    static constexpr int kZeros = kRec + kSlot * kWindow; // offset of the row of zeros
     // y [0, kOnes): SH basis function k of lane l at k * kPitch + l;
     // ones: the multiplier of the non-SH components;
-    // rec [kRec, kZeros): per step, component c of lane l at c * kPitch + l:
-    //   dL/d(r, g, b, last channel), flushed position gradient (x, y, z),
-    //   point error;
+    // rec [kRec, kZeros): kWindow entry slots; in slot s, component c of
+    //   lane l's entry at s * kSlot + c * kPitch + l: dL/d(r, g, b, last
+    //   channel), flushed position gradient (x, y, z), point error;
     // zeros: what the idle owner lanes read
     float buf[kZeros + kPitch];
     __device__ float *y() { return buf; }
@@ -365,7 +372,8 @@ __device__ __forceinline__ int pop_member(uint64_t &mm) {
 //   i == 63:             1 * point error(m)
 //   others:              1 * 0 (the zero row)
 struct OwnerLane {
-    int y_base, g_base; // member m: y = buf[y_base + m], g = buf[g_base + m]
+    int y_base, g_base; // member m of slot 0: y = buf[y_base + m], g = buf[g_base + m]
+    int g_slot;         // g of slot s is s * g_slot further (0 on the zero row)
     bool also_last;     // last_ch is an SH component too: add dL/dlast as well
     // gradient accumulator row: this lane's float in a cell's row, and whether
     // it adds to it always (attribute components) or only when a member
@@ -401,16 +409,18 @@ __device__ __forceinline__ OwnerLane owner_lane(int last_ch, bool point_error) {
             o.g_base = T::kZeros;
         }
     }
+    o.g_slot = o.g_base == T::kZeros ? 0 : T::kSlot;
     return o;
 }
 
-// Sum over the members in `mm` of buf[y_base + m] * buf[g_base + m] (+ the
-// last channel on the also_last lane), four members at a time.
+// Sum over the members in `mm` (entries in slot `slot`) of
+// buf[y_base + m] * buf[g_base + slot * g_slot + m] (+ the last channel on
+// the also_last lane), four members at a time.
 template <bool ALSO_LAST>
 __device__ __forceinline__ float sum_members(uint64_t mm, const float *__restrict__ buf,
-                                             const OwnerLane &ow, const float *last) {
+                                             const OwnerLane &ow, int slot, const float *last) {
     const float *yb = buf + ow.y_base;
-    const float *gb = buf + ow.g_base;
+    const float *gb = buf + ow.g_base + slot * ow.g_slot;
     float acc = 0.0f;
     while (mm) {
         int m[4];
@@ -434,48 +444,123 @@ __device__ __forceinline__ float sum_members(uint64_t mm, const float *__restric
     return acc;
 }
 
-// Grouped gradient updates of one wave-synchronous step (all 64 lanes
-// active).  A lane's attribute gradients are applied one step late, together
-// with the position gradient flushed for the same cell
+// A lane's steps between grouping passes.  Entry n (the lane's n-th step)
+// sits in slot n % kWindow; it is complete once the position gradient that
+// the lane's next step flushes for the same cell is attached
 // (src/tracing/pipeline.cu:495-506 flushes a cell's position gradient one
-// step late), so each trip needs one grouping pass instead of two.  The
-// participating lanes (`part`) have their pending step in the wave's LDS
-// record; `key` is that step's cell.  For every key, owner lane i < D adds
-// the sum of its component over the group to row `key` of attr_grad (one
-// coalesced atomic instruction per cell), lanes 60..62 add the summed
-// flushed position gradient (if a member flushed one) and lane 63 the point
-// error.  The owner lanes read the members four at a time, two LDS reads and
-// one fma per member.  With an accumulator (fp32), the instruction's targets
+// step late), or once the walk has ended.  A lane holds at most kWindow
+// unapplied entries: up to kWindow - 1 complete ones and one pending.
+struct StepEntries {
+    uint32_t key[kWindow]; // cell of the complete entry in slot s
+    uint32_t ready;        // bit s: slot s holds a complete entry not yet applied
+    uint32_t flushed;      // bit s: that entry carries a flushed position gradient
+    uint32_t count;        // entries published so far
+    uint32_t pend_slot;    // slot of the pending entry
+    uint32_t pend_cell;    // its cell
+    bool pend;             // an entry waits for its position flush
+};
+
+__device__ __forceinline__ void entries_init(StepEntries &e) {
+#pragma unroll
+    for (int s = 0; s < kWindow; ++s) e.key[s] = 0u;
+    e.ready = 0u;
+    e.flushed = 0u;
+    e.count = 0u;
+    e.pend_slot = 0u;
+    e.pend_cell = 0u;
+    e.pend = false;
+}
+
+// Attaches the flushed position gradient (flush) or zeros to the pending
+// entry and marks it complete.
+template <int L>
+__device__ __forceinline__ void complete_entry(StepEntries &e, bool flush, const float *flush_g,
+                                               WaveTables<L> &tb) {
+    float *r = tb.rec() + e.pend_slot * WaveTables<L>::kSlot + lane_id();
+    r[4 * kPitch] = flush ? flush_g[0] : 0.0f;
+    r[5 * kPitch] = flush ? flush_g[1] : 0.0f;
+    r[6 * kPitch] = flush ? flush_g[2] : 0.0f;
+#pragma unroll
+    for (int s = 0; s < kWindow; ++s) {
+        if (e.pend_slot == (uint32_t)s) e.key[s] = e.pend_cell;
+    }
+    e.ready |= 1u << e.pend_slot;
+    if (flush) e.flushed |= 1u << e.pend_slot;
+    e.pend = false;
+}
+
+// Publishes a lane's step (components 0..3, 7 of its entry) as the pending
+// entry.
+template <int L>
+__device__ __forceinline__ void publish_step(WaveTables<L> &tb, StepEntries &e, uint32_t cell,
+                                             float gr, float gg, float gb, float g_last,
+                                             float perr) {
+    const uint32_t slot = e.count % (uint32_t)kWindow;
+    float *r = tb.rec() + slot * WaveTables<L>::kSlot + lane_id();
+    r[0] = gr;
+    r[kPitch] = gg;
+    r[2 * kPitch] = gb;
+    r[3 * kPitch] = g_last;
+    r[7 * kPitch] = perr;
+    e.pend_slot = slot;
+    e.pend_cell = cell;
+    e.pend = true;
+    ++e.count;
+}
+
+// Grouped gradient updates of the wave's complete entries (all 64 lanes
+// active).  For every distinct cell among them, owner lane i < D adds the
+// sum of its component over the cell's entries to the cell's attribute row
+// (one coalesced atomic instruction per cell), lanes 60..62 add the summed
+// flushed position gradient (if an entry carries one) and lane 63 the point
+// error.  The owner lanes read the entries four at a time, two LDS reads and
+// one fma per entry.  With an accumulator (fp32), the instruction's targets
 // are one row of accum_stride(L) floats per cell: an atomic add costs about
 // one memory transaction per 64-byte segment it touches, and the row spans
 // ceil((D + 4) / 16) of them where the three output arrays span up to
 // ceil(D / 16) + 3.
 template <int L, typename AT>
-__device__ __forceinline__ void grouped_backward_updates(
-    bool part, uint32_t key, bool flush, const float *flush_g, const OwnerLane &ow,
-    WaveTables<L> &tb, void *__restrict__ attr_grad, void *__restrict__ point_error,
-    float *__restrict__ points_grad, float *__restrict__ accum) {
+__device__ __forceinline__ void grouped_pass(StepEntries &e, const OwnerLane &ow,
+                                             WaveTables<L> &tb, void *__restrict__ attr_grad,
+                                             void *__restrict__ point_error,
+                                             float *__restrict__ points_grad,
+                                             float *__restrict__ accum) {
     constexpr int D = 1 + 3 * (L + 1) * (L + 1);
     const uint32_t lane = lane_id();
-    float *rec = tb.rec();
-    if (part) {
-        rec[4 * kPitch + lane] = flush ? flush_g[0] : 0.0f;
-        rec[5 * kPitch + lane] = flush ? flush_g[1] : 0.0f;
-        rec[6 * kPitch + lane] = flush ? flush_g[2] : 0.0f;
-    }
+    const float *last = tb.rec() + 3 * kPitch;
     __builtin_amdgcn_wave_barrier();
     const bool any_also_last = __ballot(ow.also_last) != 0ull;
-    const uint64_t flushing = __ballot(part && flush);
-    uint64_t todo = __ballot(part);
-    while (todo) {
-        const int leader = first_lane(todo);
-        const uint32_t c = readlane_u(key, leader);
-        const uint64_t grp = __ballot(part && key == c);
-        todo &= ~grp;
-        const float acc = any_also_last
-                              ? sum_members<true>(grp, tb.buf, ow, rec + 3 * kPitch)
-                              : sum_members<false>(grp, tb.buf, ow, rec + 3 * kPitch);
-        const bool pos = (grp & flushing) != 0ull;
+    uint64_t todo[kWindow], flushing[kWindow];
+#pragma unroll
+    for (int s = 0; s < kWindow; ++s) {
+        todo[s] = __ballot((e.ready >> s) & 1u);
+        flushing[s] = __ballot((e.flushed >> s) & 1u);
+    }
+    while (true) {
+        // leader: the first entry left, in slot order
+        uint32_t c = 0u;
+        bool found = false;
+#pragma unroll
+        for (int s = 0; s < kWindow; ++s) {
+            if (!found && todo[s]) {
+                c = readlane_u(e.key[s], first_lane(todo[s]));
+                found = true;
+            }
+        }
+        if (!found) break;
+        float acc = 0.0f;
+        bool pos = false;
+#pragma unroll
+        for (int s = 0; s < kWindow; ++s) {
+            const uint64_t grp = __ballot(((e.ready >> s) & 1u) && e.key[s] == c);
+            if (grp) {
+                todo[s] &= ~grp;
+                pos = pos || (grp & flushing[s]) != 0ull;
+                const float *ls = last + s * WaveTables<L>::kSlot;
+                acc = acc + (any_also_last ? sum_members<true>(grp, tb.buf, ow, s, ls)
+                                           : sum_members<false>(grp, tb.buf, ow, s, ls));
+            }
+        }
         if constexpr (sizeof(AT) == 4) {
             // one atomic instruction: the row, the position and the point error
             float *dst = nullptr;
@@ -498,19 +583,9 @@ __device__ __forceinline__ void grouped_backward_updates(
                 atomicAdd(points_grad + 3ull * c + (lane - 60u), acc);
         }
     }
+    e.ready = 0u;
+    e.flushed = 0u;
     __builtin_amdgcn_wave_barrier();
-}
-
-// Publishes a lane's step for the next grouping pass (record slots 0..3, 7).
-template <int L>
-__device__ __forceinline__ void publish_step(WaveTables<L> &tb, float gr, float gg, float gb,
-                                             float g_last, float pe) {
-    float *r = tb.rec() + lane_id();
-    r[0] = gr;
-    r[kPitch] = gg;
-    r[2 * kPitch] = gb;
-    r[3 * kPitch] = g_last;
-    r[7 * kPitch] = pe;
 }
 
 template <int L>
@@ -521,7 +596,7 @@ __device__ __forceinline__ void tables_init(WaveTables<L> &tb, const float *sh) 
     for (int k = 0; k < nsh; ++k) tb.y()[k * kPitch + lane] = sh[k];
     // the padding member (lane 64): zero basis and zero record
     if (lane < (uint32_t)nsh) tb.y()[lane * kPitch + 64] = 0.0f;
-    if (lane < 8u) tb.rec()[lane * kPitch + 64] = 0.0f;
+    if (lane < 8u * kWindow) tb.rec()[lane * kPitch + 64] = 0.0f;
     tb.buf[WaveTables<L>::kOnes + lane] = 1.0f;
     tb.buf[WaveTables<L>::kZeros + lane] = 0.0f;
     if (lane == 0) {
@@ -535,7 +610,7 @@ __device__ __forceinline__ void tables_init(WaveTables<L> &tb, const float *sh) 
 // backward_sdf (src/tracing/pipeline.cu:267-550)
 
 template <int L, bool STATS, typename AT>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(5, 8))) void
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 backward_sdf_kernel(BwdArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
@@ -594,8 +669,8 @@ backward_sdf_kernel(BwdArgs a) {
     const uint2 *wrec = nullptr;
     if (!STATS && a.record.entries) wrec = walk_record_lane<kBackwardChunk>(a.record, lane);
     uint32_t trip = 0;
-    bool pend = false;       // a step whose updates are not applied yet
-    uint32_t pend_cell = 0u; // its cell
+    StepEntries ents; // steps whose updates are not applied yet
+    entries_init(ents);
 
     while (__ballot(ws.alive) != 0ull) {
         StepInfo si;
@@ -699,24 +774,23 @@ backward_sdf_kernel(BwdArgs a) {
         }
         if (si.stepped && !keep) ws.alive = false;
         if constexpr (!STATS) {
-            // the pending step goes out when the lane steps again (with the
-            // flush of the same cell) or when its walk ends
-            const bool part = pend && (si.stepped || !ws.alive);
-            grouped_backward_updates<L, AT>(part, pend_cell, si.stepped && flush, flush_g, owner,
-                                            tb, a.attr_grad, a.point_error, a.points_grad, a.accum);
-            if (si.stepped) {
-                publish_step<L>(tb, dr, dg, db, dsdf, pe);
-                pend_cell = ws.cell;
-            }
-            pend = si.stepped || (pend && !part);
+            // the pending step is complete when the lane steps again (with
+            // the flush of the same cell) or when its walk ends; complete
+            // steps go out every kWindow trips
+            if (ents.pend && (si.stepped || !ws.alive))
+                complete_entry<L>(ents, si.stepped && flush, flush_g, tb);
+            if (trip % kWindow == 0)
+                grouped_pass<L, AT>(ents, owner, tb, a.attr_grad, a.point_error, a.points_grad,
+                                    a.accum);
+            if (si.stepped) publish_step<L>(tb, ents, ws.cell, dr, dg, db, dsdf, pe);
         }
         if (ws.alive && si.found) walk_move(ws, si);
     }
     if constexpr (!STATS) {
-        // steps still pending when their walks ended
+        // steps not applied when the walks ended
         const float zero3[3] = {0.0f, 0.0f, 0.0f};
-        grouped_backward_updates<L, AT>(pend, pend_cell, false, zero3, owner, tb, a.attr_grad,
-                                        a.point_error, a.points_grad, a.accum);
+        if (ents.pend) complete_entry<L>(ents, false, zero3, tb);
+        grouped_pass<L, AT>(ents, owner, tb, a.attr_grad, a.point_error, a.points_grad, a.accum);
     }
 
     if constexpr (STATS) {
@@ -737,7 +811,7 @@ backward_sdf_kernel(BwdArgs a) {
 // backward, density mode (src/tracing/pipeline.cu:553-791); the walk runs in
 // the reference's unsafe mode (no t > t0 test, :782-790).
 template <int L, bool STATS, typename AT>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(5, 8))) void
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 backward_density_kernel(BwdArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
@@ -792,14 +866,16 @@ backward_density_kernel(BwdArgs a) {
     WalkState ws;
     walk_init(a.scene, valid ? a.start[ray_idx] : kNoIndex, ws);
     WalkCounters wc = {0u, 0u, 0ull, 0ull};
-    bool pend = false;
-    uint32_t pend_cell = 0u;
+    StepEntries ents;
+    entries_init(ents);
+    uint32_t trip = 0;
 
     while (__ballot(ws.alive) != 0ull) {
         StepInfo si;
         si.stepped = false;
         si.found = false;
         if (ws.alive) walk_advance<false, STATS>(a.scene, ray, a.settings.max_intersections, ws, si, wc);
+        ++trip;
 
         bool keep = true;
         float dr = 0.0f, dg = 0.0f, db = 0.0f, dds = 0.0f, pe = 0.0f;
@@ -870,21 +946,19 @@ backward_density_kernel(BwdArgs a) {
         }
         if (si.stepped && !keep) ws.alive = false;
         if constexpr (!STATS) {
-            const bool part = pend && (si.stepped || !ws.alive);
-            grouped_backward_updates<L, AT>(part, pend_cell, si.stepped && flush, flush_g, owner,
-                                            tb, a.attr_grad, a.point_error, a.points_grad, a.accum);
-            if (si.stepped) {
-                publish_step<L>(tb, dr, dg, db, dds, pe);
-                pend_cell = ws.cell;
-            }
-            pend = si.stepped || (pend && !part);
+            if (ents.pend && (si.stepped || !ws.alive))
+                complete_entry<L>(ents, si.stepped && flush, flush_g, tb);
+            if (trip % kWindow == 0)
+                grouped_pass<L, AT>(ents, owner, tb, a.attr_grad, a.point_error, a.points_grad,
+                                    a.accum);
+            if (si.stepped) publish_step<L>(tb, ents, ws.cell, dr, dg, db, dds, pe);
         }
         if (ws.alive && si.found) walk_move(ws, si);
     }
     if constexpr (!STATS) {
         const float zero3[3] = {0.0f, 0.0f, 0.0f};
-        grouped_backward_updates<L, AT>(pend, pend_cell, false, zero3, owner, tb, a.attr_grad,
-                                        a.point_error, a.points_grad, a.accum);
+        if (ents.pend) complete_entry<L>(ents, false, zero3, tb);
+        grouped_pass<L, AT>(ents, owner, tb, a.attr_grad, a.point_error, a.points_grad, a.accum);
     }
 
     if constexpr (STATS) {
