@@ -71,24 +71,31 @@ __device__ __forceinline__ uint32_t readlane_u(uint32_t v, int lane) {
 
 __device__ __forceinline__ int first_lane(uint64_t mask) { return __builtin_ctzll(mask); }
 
+// Lane mask of a per-lane predicate, taking the bool as the compare mask it
+// already is (no widening to a 0/1 integer first).
+__device__ __forceinline__ uint64_t lane_mask(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
 // Groups of lanes per forward slot round.
 constexpr int kSlots = 16;
 
-// Assigns the next up-to-kSlots groups of lanes with equal `key` among
-// `todo` to slots 0..n-1 (lanes of group k get slot k, tb_cell[k] = key);
-// returns n and clears those lanes from `todo`.
-__device__ __forceinline__ int assign_slots(uint64_t &todo, uint32_t key, int &slot,
-                                            uint32_t *tb_cell) {
-    const uint32_t lane = lane_id();
+// Assigns the next up-to-kSlots groups of `pending` lanes with equal `key`
+// to slots 0..n-1 (lanes of group k get slot k and leave `pending`; lane k
+// of `cells` gets group k's key); returns n.  `pending` stays a per-lane
+// predicate (a scalar lane mask), so a group costs one compare and a few
+// scalar operations.
+__device__ __forceinline__ int assign_slots(bool &pending, uint32_t key, int &slot,
+                                            uint32_t &cells) {
     int n = 0;
     slot = -1;
+    uint64_t todo = lane_mask(pending);
     while (todo && n < kSlots) {
-        const int leader = first_lane(todo);
-        const uint32_t c = readlane_u(key, leader);
-        const uint64_t grp = __ballot(((todo >> lane) & 1ull) && key == c);
+        const uint32_t c = readlane_u(key, first_lane(todo));
+        const bool eq = key == c;
+        const uint64_t grp = todo & lane_mask(eq);
+        if (pending && eq) slot = n;
+        pending = pending && !eq;
+        if (lane_id() == (uint32_t)n) cells = c;
         todo &= ~grp;
-        if ((grp >> lane) & 1ull) slot = n;
-        if (lane == 0) tb_cell[n] = c;
         ++n;
     }
     return n;
@@ -98,7 +105,6 @@ __device__ __forceinline__ int assign_slots(uint64_t &todo, uint32_t key, int &s
 struct FwdSlots {
     float w[kSlots];
     float alpha[kSlots];
-    uint32_t cell[kSlots];
 };
 
 // ---------------------------------------------------------------------------
@@ -231,17 +237,18 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
                 // per group (ds_add), then lane k writes group k's sum and a
                 // member's alpha
                 FwdSlots &fs = fwd_slots[threadIdx.x >> 6];
-                uint64_t todo = __ballot(si.stepped);
-                while (todo) {
+                bool pending = si.stepped;
+                uint32_t cells = 0u;
+                while (__ballot(pending)) {
                     int slot;
-                    const int n = assign_slots(todo, ws.cell, slot, fs.cell);
+                    const int n = assign_slots(pending, ws.cell, slot, cells);
                     if (slot >= 0) {
                         atomicAdd(fs.w + slot, w);
                         fs.alpha[slot] = alpha;
                     }
                     __builtin_amdgcn_wave_barrier();
                     if ((int)lane < n) {
-                        const uint32_t c = fs.cell[lane];
+                        const uint32_t c = cells;
                         const float sum = fs.w[lane];
                         fs.w[lane] = 0.0f;
                         if (a.contribution) atomic_add_elem<AT>(a.contribution, c, sum);
@@ -552,7 +559,8 @@ __device__ __forceinline__ void grouped_pass(StepEntries &e, const OwnerLane &ow
         bool pos = false;
 #pragma unroll
         for (int s = 0; s < kWindow; ++s) {
-            const uint64_t grp = __ballot(((e.ready >> s) & 1u) && e.key[s] == c);
+            // every ready entry of cell c is still in todo[s]
+            const uint64_t grp = todo[s] & lane_mask(e.key[s] == c);
             if (grp) {
                 todo[s] &= ~grp;
                 pos = pos || (grp & flushing[s]) != 0ull;
