@@ -78,34 +78,68 @@ __device__ __forceinline__ uint64_t lane_mask(bool p) { return __builtin_amdgcn_
 // Groups of lanes per forward slot round.
 constexpr int kSlots = 16;
 
-// Assigns the next up-to-kSlots groups of `pending` lanes with equal `key`
-// to slots 0..n-1 (lanes of group k get slot k and leave `pending`; lane k
-// of `cells` gets group k's key); returns n.  `pending` stays a per-lane
-// predicate (a scalar lane mask), so a group costs one compare and a few
-// scalar operations.
-__device__ __forceinline__ int assign_slots(bool &pending, uint32_t key, int &slot,
-                                            uint32_t &cells) {
-    int n = 0;
-    slot = -1;
-    uint64_t todo = lane_mask(pending);
-    while (todo && n < kSlots) {
-        const uint32_t c = readlane_u(key, first_lane(todo));
-        const bool eq = key == c;
-        const uint64_t grp = todo & lane_mask(eq);
-        if (pending && eq) slot = n;
-        pending = pending && !eq;
-        if (lane_id() == (uint32_t)n) cells = c;
-        todo &= ~grp;
-        ++n;
-    }
-    return n;
-}
-
 // Per-wave LDS slots of the forward's grouped contribution updates.
 struct FwdSlots {
     float w[kSlots];
     float alpha[kSlots];
 };
+
+// A lane's step for the contribution updates: its cell, weight and alpha.
+struct FwdEntry {
+    uint32_t cell;
+    float w, alpha;
+    bool valid;
+};
+
+// Contribution updates of two entries per lane (all 64 lanes active):
+// `contribution[cell] += sum of the weights` and `alpha[cell] = one entry's
+// alpha` (the reference's last-writer store, src/tracing/pipeline.cu:159-163)
+// for every distinct cell among the entries.  Up to kSlots cells per round:
+// the entries of group k add their weights into LDS slot k (ds_add), then
+// lane k issues group k's contribution atomic and alpha store.  The pending
+// entries stay per-lane predicates (scalar lane masks) and each group costs
+// one compare per entry.
+template <typename AT>
+__device__ __forceinline__ void contribution_pass(FwdSlots &fs, const FwdEntry &ea,
+                                                  const FwdEntry &eb, void *contribution,
+                                                  float *alpha_out) {
+    const uint32_t lane = lane_id();
+    bool pa = ea.valid, pb = eb.valid;
+    uint64_t ta = lane_mask(pa), tb = lane_mask(pb);
+    while (ta | tb) {
+        int n = 0, sa = -1, sb = -1;
+        uint32_t cells = 0u;
+        while ((ta | tb) && n < kSlots) {
+            const uint32_t c =
+                ta ? readlane_u(ea.cell, first_lane(ta)) : readlane_u(eb.cell, first_lane(tb));
+            const bool qa = ea.cell == c, qb = eb.cell == c;
+            if (pa && qa) sa = n;
+            if (pb && qb) sb = n;
+            pa = pa && !qa;
+            pb = pb && !qb;
+            ta &= ~lane_mask(qa);
+            tb &= ~lane_mask(qb);
+            if (lane == (uint32_t)n) cells = c;
+            ++n;
+        }
+        if (sa >= 0) {
+            atomicAdd(fs.w + sa, ea.w);
+            fs.alpha[sa] = ea.alpha;
+        }
+        if (sb >= 0) {
+            atomicAdd(fs.w + sb, eb.w);
+            fs.alpha[sb] = eb.alpha;
+        }
+        __builtin_amdgcn_wave_barrier();
+        if ((int)lane < n) {
+            const float sum = fs.w[lane];
+            fs.w[lane] = 0.0f;
+            if (contribution) atomic_add_elem<AT>(contribution, cells, sum);
+            if (alpha_out) alpha_out[cells] = fs.alpha[lane];
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
 
 // ---------------------------------------------------------------------------
 // forward (src/tracing/pipeline.cu:36-264)
@@ -159,6 +193,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     if (!STATS && NEUS && a.record.entries)
         wrec = walk_record_lane<kForwardChunk>(a.record, lane);
     uint32_t trip = 0;
+    FwdEntry held = {0u, 0.0f, 0.0f, false}; // step waiting for the next contribution pass
 
     while (__ballot(ws.alive) != 0ull) {
         StepInfo si;
@@ -229,32 +264,17 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         }
 
         if constexpr (!STATS) {
-            // per cell: contribution += sum of the weights; alpha = one
-            // visiting step's alpha (the reference's last-writer store,
-            // src/tracing/pipeline.cu:159-163)
+            // per cell: contribution += sum of the weights, alpha = one
+            // visiting step's alpha; a step waits one trip in `held` so each
+            // pass covers two trips (fewer distinct cells than two passes)
             if (a.contribution || a.alpha_out) {
-                // groups of lanes in one cell: weights summed in an LDS slot
-                // per group (ds_add), then lane k writes group k's sum and a
-                // member's alpha
-                FwdSlots &fs = fwd_slots[threadIdx.x >> 6];
-                bool pending = si.stepped;
-                uint32_t cells = 0u;
-                while (__ballot(pending)) {
-                    int slot;
-                    const int n = assign_slots(pending, ws.cell, slot, cells);
-                    if (slot >= 0) {
-                        atomicAdd(fs.w + slot, w);
-                        fs.alpha[slot] = alpha;
-                    }
-                    __builtin_amdgcn_wave_barrier();
-                    if ((int)lane < n) {
-                        const uint32_t c = cells;
-                        const float sum = fs.w[lane];
-                        fs.w[lane] = 0.0f;
-                        if (a.contribution) atomic_add_elem<AT>(a.contribution, c, sum);
-                        if (a.alpha_out) a.alpha_out[c] = fs.alpha[lane];
-                    }
-                    __builtin_amdgcn_wave_barrier();
+                const FwdEntry cur = {ws.cell, w, alpha, si.stepped};
+                if (trip % 2u == 0u) {
+                    contribution_pass<AT>(fwd_slots[threadIdx.x >> 6], held, cur, a.contribution,
+                                          a.alpha_out);
+                    held.valid = false;
+                } else {
+                    held = cur;
                 }
             }
         }
@@ -263,6 +283,13 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     }
     // a backward lane that outlives this wave's walk reads "unrecorded"
     if (wrec && trip < a.record.budget) wrec[(uint64_t)trip * 64] = make_uint2(kWalkUnrecorded, 0u);
+    if constexpr (!STATS) {
+        if (a.contribution || a.alpha_out) {
+            const FwdEntry none = {0u, 0.0f, 0.0f, false};
+            contribution_pass<AT>(fwd_slots[threadIdx.x >> 6], held, none, a.contribution,
+                                  a.alpha_out);
+        }
+    }
 
     if (!valid) return;
     if constexpr (STATS) {
