@@ -209,6 +209,10 @@ typedef struct sdf_trace_plan {
     const uint32_t *ray_order; /* device memory [num_rays], or NULL */
     void *grad_accum;          /* device memory, 256-byte aligned, or NULL */
     size_t grad_accum_bytes;   /* >= sdf_grad_accum_bytes(sh_degree, num_points) */
+    uint32_t scratch_ready;    /* backward: nonzero if `scratch` already holds this
+                                  scene's offset table (the forward over the same
+                                  scene filled it); the backward then skips
+                                  rebuilding it */
 } sdf_trace_plan;
 
 size_t sdf_walk_record_bytes(uint32_t num_rays, uint32_t ray_image_width,

@@ -100,6 +100,7 @@ class TracePlanDesc(C.Structure):
         ("ray_order", C.c_void_p),
         ("grad_accum", C.c_void_p),
         ("grad_accum_bytes", C.c_size_t),
+        ("scratch_ready", C.c_uint32),
     ]
 
 

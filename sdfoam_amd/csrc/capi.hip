@@ -242,11 +242,14 @@ int trace_backward_impl(const sdf_trace_plan *plan, int sh_degree,
         accum = static_cast<float *>(plan->grad_accum);
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
-    tbegin(SDF_KERNEL_PREFETCH, s);
-    hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
-                                        point_adjacency_offsets, static_cast<uint2 *>(scratch), s);
-    tend(s);
-    if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
+    hipError_t e = hipSuccess;
+    if (!(plan && plan->scratch_ready)) {
+        tbegin(SDF_KERNEL_PREFETCH, s);
+        e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
+                                 point_adjacency_offsets, static_cast<uint2 *>(scratch), s);
+        tend(s);
+        if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
+    }
     if (num_rays == 0) return SDF_OK;
     if (accum) {
         tbegin(SDF_KERNEL_GRAD_CLEAR, s);

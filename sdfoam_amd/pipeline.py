@@ -104,7 +104,11 @@ class TracePlan:
     * ``order``: the launch order of the rays (sdf_ray_order), for rays in no
       particular order;
     * ``entries``: the walk record, each ray's steps (8 bytes per step, up to
-      ``budget`` trips per wavefront of 64 rays), sdfoam mode only.
+      ``budget`` trips per wavefront of 64 rays), sdfoam mode only;
+    * ``table``: the forward's fp16 offset table of the scene, which the
+      backward reuses instead of rebuilding it while the points, adjacency
+      and offsets tensors are the same and unmodified (same storage and
+      version counter).
 
     Valid for a backward over the same rays, start points, scene and
     settings; the tracer checks the ray count, image width and walk limit."""
@@ -118,6 +122,20 @@ class TracePlan:
         self.entries = None
         self.nbytes = 0
         self.budget = 0
+        self.table = None
+        self.table_bytes = 0
+        self.table_key = None
+
+    @staticmethod
+    def scene_key(points, adjacency, offsets) -> tuple:
+        return tuple((t.data_ptr(), t._version, t.numel()) for t in (points, adjacency, offsets))
+
+    def keep_table(self, table: torch.Tensor, nbytes: int, key: tuple) -> None:
+        self.table, self.table_bytes, self.table_key = table, nbytes, key
+
+    def table_for(self, key: tuple):
+        """The kept offset table if it belongs to this scene, else None."""
+        return self.table if self.table is not None and key == self.table_key else None
 
     def sort_rays(self, num_points: int, rays: torch.Tensor, start: torch.Tensor) -> None:
         L = _lib.lib()
@@ -339,6 +357,7 @@ class Pipeline:
                 plan.sort_rays(num_points, rays_c, start_c)
             if want_record:
                 plan.allocate_record(walk_budget)
+            plan.keep_table(scratch, nbytes, TracePlan.scene_key(points_c, adj_c, offs_c))
         args = (
             self._sh_degree, C.byref(settings), num_points, ptr(points_c), ptr(attributes_c),
             num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c), ptr(start_c), num_q,
@@ -461,10 +480,15 @@ class Pipeline:
         points_grad = torch.zeros((num_points, 3), dtype=rays_c.dtype, device=dev)
         ray_grad = torch.zeros_like(rays_c)
         sharpness_grad = torch.zeros_like(sharpness, dtype=torch.float32)
-        scratch, nbytes = self._scratch(num_points, num_adj, dev)
+        table_ready = False
         if trace_plan is not None:
             trace_plan.check_matches(num_rays, settings, dev)
-        elif num_rays > 0 and _auto_sort(sort_rays, settings, num_rays):
+            kept = trace_plan.table_for(TracePlan.scene_key(points_c, adj_c, offs_c))
+            if kept is not None:
+                scratch, nbytes, table_ready = kept, trace_plan.table_bytes, True
+        if not table_ready:
+            scratch, nbytes = self._scratch(num_points, num_adj, dev)
+        if trace_plan is None and num_rays > 0 and _auto_sort(sort_rays, settings, num_rays):
             trace_plan = TracePlan(num_rays, settings, dev)
             trace_plan.sort_rays(num_points, rays_c, start_c)
         args = (
@@ -474,6 +498,7 @@ class Pipeline:
             ptr(attr_grad), ptr(point_error), ptr(sharpness), ptr(sharpness_grad),
             ptr(scratch), nbytes, _lib.stream_handle(dev))
         desc = trace_plan.desc() if trace_plan is not None else _lib.TracePlanDesc()
+        desc.scratch_ready = 1 if table_ready else 0
         accum = None
         if grad_accum and num_rays > 0 and self._attr_dtype == torch.float32:
             accum_bytes = int(_lib.lib().sdf_grad_accum_bytes(self._sh_degree, num_points))

@@ -379,6 +379,47 @@ def test_walk_record_mismatch_raises(torch_dev):
                             trace_plan=fwd["trace_plan"])
 
 
+def test_backward_reuses_forward_table(torch_dev):
+    """With the forward's plan the backward skips rebuilding the offset table
+    while the scene tensors are unmodified, and rebuilds it after an in-place
+    change of the points (version counter)."""
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import _lib
+
+    w = scene(2)
+    g = gpu_scene(w, torch_dev)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    inv_t = torch.tensor([w.inv_s], device=torch_dev)
+    grad = to_dev(w.grad_rgba, torch_dev)
+
+    def backward(plan):
+        _lib.set_timing(True)
+        b = pipe.trace_backward(**g, rgb_out=fwd["rgba"], grad_in=grad, alpha_mode="sdfoam",
+                                inv_s=inv_t, trace_plan=plan)
+        torch.cuda.synchronize()
+        kinds = [k for k, _ in _lib.collect_timings()]
+        _lib.set_timing(False)
+        return b, kinds
+
+    fwd = pipe.trace_forward(**g, alpha_mode="sdfoam", inv_s=inv_t, record_walk=True)
+    b_reuse, kinds = backward(fwd["trace_plan"])
+    assert "prefetch_adjacent_diff" not in kinds and "backward" in kinds
+    b_plain, kinds = backward(None)
+    assert "prefetch_adjacent_diff" in kinds
+    g["points"].add_(0.0)  # same values, new version: the kept table is not trusted
+    b_again, kinds = backward(fwd["trace_plan"])
+    assert "prefetch_adjacent_diff" in kinds
+    # the runs differ only in the order of their fp32 atomics (parity with the
+    # oracle is tested above); a wrong table would change the walks entirely
+    for k in ("points_grad", "attr_grad", "sharpness_grad"):
+        ref = b_plain[k].cpu().numpy()
+        for b in (b_reuse, b_again):
+            np.testing.assert_allclose(b[k].cpu().numpy(), ref, rtol=1e-4,
+                                       atol=1e-5 * float(np.abs(ref).max()))
+
+
 def flat(w):
     """The workload with its rays as a flat [R, 6] batch (no image layout)."""
     import dataclasses
