@@ -79,6 +79,13 @@ def main() -> int:
                     help="CPU baseline traces every n-th ray (0 skips it; default: the "
                          "smallest n >= 3 that keeps the sample to about 640k rays, "
                          "10-20 s on 16 threads)")
+    ap.add_argument("--alpha-mode", default="sdfoam", choices=["sdfoam", "standard"],
+                    help="sdfoam (NeuS alpha, backward_sdf; the headline) or standard "
+                         "(density alpha, the density backward; the scene's last channel is a "
+                         "density)")
+    ap.add_argument("--attr-dtype", default="float32", choices=["float32", "float16"],
+                    help="attribute storage of the pipeline (fp16: create_pipeline(L, "
+                         "'float16'); arithmetic stays fp32)")
     ap.add_argument("--walk-record", type=int, default=1, choices=[0, 1],
                     help="1: the forward records each ray's steps and the backward replays "
                          "them (TraceRays does this); 0: the backward scans the faces again")
@@ -122,7 +129,7 @@ def main() -> int:
         w = scenes.load_workload(args.scene_cache)
     else:
         log(f"generating config C{args.config} (Delaunay via Qhull)")
-        w = scenes.make_config(args.config)
+        w = scenes.make_config(args.config, mode=args.alpha_mode)
         if args.scene_cache:
             scenes.save_workload(w, args.scene_cache)
     log(f"scene ready in {time.time() - t0:.1f}s: N={w.num_points} E={w.adjacency.size} R={w.num_rays}")
@@ -133,12 +140,16 @@ def main() -> int:
     def to_dev(a):
         return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
+    if w.alpha_mode != args.alpha_mode:
+        raise RuntimeError(f"scene cache holds a {w.alpha_mode} scene")
+    half = args.attr_dtype == "float16"
+    adt = torch.float16 if half else torch.float32
     pts = to_dev(w.points)
-    attrs = to_dev(w.attributes)
+    attrs = to_dev(w.attributes).to(adt)
     adj, offs = u32(w.adjacency), u32(w.offsets)
     inv = torch.tensor([w.inv_s], dtype=torch.float32, device=dev)
     tree = sdfoam_amd.build_aabb_tree(pts)
-    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree, args.attr_dtype)
     D = pipe.attribute_dim()
     Q = int(w.quantiles.shape[-1])
 
@@ -154,11 +165,12 @@ def main() -> int:
                 grng = np.random.default_rng(7000 + s)
                 g_np = grng.normal(size=(w.num_rays, 4)).astype(np.float32)
                 dg_np = grng.normal(size=(w.num_rays, Q)).astype(np.float32)
-            batches.append(dict(rays=to_dev(r_np), q=to_dev(q_np), g=to_dev(g_np),
+            batches.append(dict(rays=to_dev(r_np), q=to_dev(q_np), g=to_dev(g_np).to(adt),
                                 dg=to_dev(dg_np), rays_np=r_np))
     else:
-        batches.append(dict(rays=to_dev(w.rays), q=to_dev(w.quantiles), g=to_dev(w.grad_rgba),
-                            dg=to_dev(w.depth_grad), rays_np=w.rays))
+        batches.append(dict(rays=to_dev(w.rays), q=to_dev(w.quantiles),
+                            g=to_dev(w.grad_rgba).to(adt), dg=to_dev(w.depth_grad),
+                            rays_np=w.rays))
     lookup_in_step = args.config == 5
     for b in batches:
         b["start"] = sdfoam_amd.get_starting_point(b["rays"], pts, tree)
@@ -175,11 +187,12 @@ def main() -> int:
         start = (sdfoam_amd.get_starting_point(b["rays"], pts, tree) if lookup_in_step
                  else b["start"])
         out = pipe.trace_forward(pts, attrs, adj, offs, b["rays"], start, depth_quantiles=b["q"],
-                                 return_contribution=True, alpha_mode="sdfoam", inv_s=inv,
-                                 record_walk=use_record)
+                                 return_contribution=True, alpha_mode=args.alpha_mode,
+                                 inv_s=inv, record_walk=use_record)
         bwd = pipe.trace_backward(pts, attrs, adj, offs, b["rays"], start, out["rgba"], b["g"],
-                                  b["q"], out["depth_indices"], b["dg"], alpha_mode="sdfoam",
-                                  inv_s=inv, trace_plan=out.get("trace_plan"))
+                                  b["q"], out["depth_indices"], b["dg"],
+                                  alpha_mode=args.alpha_mode, inv_s=inv,
+                                  trace_plan=out.get("trace_plan"))
         return out, bwd
 
     log(f"warmup {args.warmup}")
@@ -210,8 +223,8 @@ def main() -> int:
     for k in range(args.steps):
         b = batches[(args.warmup + k) % len(batches)]
         if "stats" not in b:
-            st = pipe.walk_stats(pts, attrs, adj, offs, b["rays"], b["start"], alpha_mode="sdfoam",
-                                 inv_s=inv)
+            st = pipe.walk_stats(pts, attrs, adj, offs, b["rays"], b["start"],
+                                 alpha_mode=args.alpha_mode, inv_s=inv)
             torch.cuda.synchronize()
             b["stats"] = (int(st["steps"].sum().item()), int(st["faces_stepped"].sum().item()),
                           int(st["faces"].sum().item()))
@@ -224,23 +237,31 @@ def main() -> int:
     R = w.num_rays
     N = w.num_points
     E = int(w.adjacency.size)
-    if use_record:
+    # attribute elements (rows, contribution, gradient rows) at their storage
+    # width; the walk record only in sdfoam mode (standard mode ignores it)
+    ab = 2 if half else 4
+    recorded = use_record and args.alpha_mode == "sdfoam"
+    if recorded:
         # the forward also writes 8 B per step; the backward reads them
         # instead of the stepped cells' face rows
-        bytes_fwd = R * (48 + 12 * Q) + S * (28 + 4 * D + 4 + 8) + 8 * F_st
-        bytes_bwd = R * (60 + 12 * Q) + S * (36 + 8 * D + 8)
+        bytes_fwd = R * (48 + 12 * Q) + S * (28 + ab * D + ab + 8) + 8 * F_st
+        bytes_bwd = R * (60 + 12 * Q) + S * (36 + 2 * ab * D + 8)
     else:
-        bytes_fwd = R * (48 + 12 * Q) + S * (28 + 4 * D + 4) + 8 * F_st
-        bytes_bwd = R * (60 + 12 * Q) + S * (36 + 8 * D) + 8 * F_st
+        bytes_fwd = R * (48 + 12 * Q) + S * (28 + ab * D + ab) + 8 * F_st
+        bytes_bwd = R * (60 + 12 * Q) + S * (36 + 2 * ab * D) + 8 * F_st
     bytes_pre = 12 * E + 16 * N
-    bytes_step = bytes_fwd + bytes_bwd + 2 * bytes_pre
+    # offset-table builds per step (the backward reuses the forward's table
+    # when it gets the forward's trace plan)
+    pre_per_step = len(per_kernel.get("prefetch_adjacent_diff", [])) / args.steps
+    bytes_step = bytes_fwd + bytes_bwd + pre_per_step * bytes_pre
 
     kernel_bytes = {"forward": bytes_fwd, "backward": bytes_bwd, "prefetch_adjacent_diff": bytes_pre}
     dominant = max((k for k in avg if k in kernel_bytes), key=lambda k: avg[k] * len(per_kernel[k]))
     achieved = kernel_bytes[dominant] / (avg[dominant] * 1e-3) / 1e9
 
     traffic = None
-    variant = "" if use_record else "_scan"
+    variant = ("" if use_record else "_scan") + ("" if args.alpha_mode == "sdfoam" else "_standard") \
+        + ("_f16" if half else "")
     prof = os.path.join(ROOT, "profiles", f"traffic_{dominant}{variant}_C{args.config}.json")
     if os.path.exists(prof):
         with open(prof) as f:
@@ -266,15 +287,18 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": f"C{args.config}: {N} points, SH degree {w.sh_degree}, sdfoam alpha, "
+            "workload": f"C{args.config}: {N} points, SH degree {w.sh_degree}, "
+                        f"{args.alpha_mode} alpha, {args.attr_dtype} attributes, "
                         f"inv_s={w.inv_s:.4f}, {rays_desc}, Q={Q}, "
                         + ("start-cell lookup + " if lookup_in_step else "")
                         + "trace_forward(contribution, depth) + trace_backward"
-                        + (" replaying the forward's walk record" if use_record else ""),
+                        + (" replaying the forward's walk record" if recorded else ""),
             "points": N,
             "adjacency": E,
             "rays": R,
             "sh_degree": w.sh_degree,
+            "alpha_mode": args.alpha_mode,
+            "attr_dtype": args.attr_dtype,
         },
         "rays_per_s": R / (ms_per_step * 1e-3),
         "cell_steps_per_s": S / (ms_per_step * 1e-3),
@@ -301,8 +325,8 @@ def main() -> int:
         n_rays = b0["rays_np"].size // 6
         stride = args.cpu_stride if args.cpu_stride > 0 else max(3, -(-n_rays // CPU_SAMPLE_RAYS))
         result["cpu_baseline"] = cpu_baseline(
-            w, b0["rays_np"], host_start, b0["q"].cpu().numpy(), b0["g"].cpu().numpy(),
-            b0["dg"].cpu().numpy(), stride)
+            w, b0["rays_np"], host_start, b0["q"].cpu().numpy(),
+            b0["g"].float().cpu().numpy(), b0["dg"].cpu().numpy(), stride, args.alpha_mode)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
@@ -312,8 +336,10 @@ def main() -> int:
 CPU_SAMPLE_RAYS = 640_000
 
 
-def cpu_baseline(w, rays, start, quantiles, grad_rgba, depth_grad, stride: int) -> dict:
-    """Scalar host oracle, forward + backward, every `stride`-th ray."""
+def cpu_baseline(w, rays, start, quantiles, grad_rgba, depth_grad, stride: int,
+                 alpha_mode: str = "sdfoam") -> dict:
+    """Scalar host oracle (fp32 attributes), forward + backward, every
+    `stride`-th ray."""
     import numpy as np
 
     from oracle import oracle
@@ -328,9 +354,10 @@ def cpu_baseline(w, rays, start, quantiles, grad_rgba, depth_grad, stride: int) 
     log(f"CPU baseline: {rays.shape[0]} rays on {threads} threads")
     t0 = time.perf_counter()
     f = oracle.trace_forward(w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, rays, sp,
-                             qv, alpha_mode="sdfoam", inv_s=w.inv_s, threads=threads)
+                             qv, alpha_mode=alpha_mode, inv_s=w.inv_s, threads=threads)
     oracle.trace_backward(w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, rays, sp,
-                          f.rgba, g, qv, f.depth_indices, dg, alpha_mode="sdfoam", inv_s=w.inv_s,
+                          f.rgba, g, qv, f.depth_indices, dg, alpha_mode=alpha_mode,
+                          inv_s=w.inv_s,
                           threads=threads, side_buffers=False)
     dt = time.perf_counter() - t0
     log(f"CPU baseline: {dt:.1f}s")

@@ -195,11 +195,11 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
  * wavefront start in the same cell and point the same way.  Requires
  * settings->ray_image_width == 0.  ray_order == NULL: the caller's order.
  *
- * Gradient accumulator (backward, fp32 attributes; an fp16 trace ignores
- * it): one 256-byte-aligned row per cell holding that cell's attribute,
- * position and point-error gradients side by side.  The backward clears it,
- * adds every ray's contributions into it, then adds each row into
- * attribute_grad, points_grad and point_error.  A wavefront's atomic update
+ * Gradient accumulator (backward): one 256-byte-aligned fp32 row per cell
+ * holding that cell's attribute, position and point-error gradients side by
+ * side.  The backward clears it, adds every ray's contributions into it,
+ * then adds each row into attribute_grad, points_grad and point_error (fp16
+ * outputs of an fp16 pipeline get the fp32 sums rounded once).  A wavefront's atomic update
  * of a cell then touches fewer 64-byte memory segments than updates of the
  * three output arrays do.  grad_accum == NULL: updates go to the outputs. */
 typedef struct sdf_trace_plan {

@@ -232,7 +232,7 @@ int trace_backward_impl(const sdf_trace_plan *plan, int sh_degree,
     rc = check_plan(plan, num_rays, settings->ray_image_width, rec, order);
     if (rc != SDF_OK) return rc;
     float *accum = nullptr;
-    if (plan && plan->grad_accum && !half) {
+    if (plan && plan->grad_accum) {
         const size_t need = sdf_grad_accum_bytes(sh_degree, num_points);
         if (plan->grad_accum_bytes < need)
             return fail(SDF_E_INVALID, "gradient accumulator must hold %zu bytes (got %zu)", need,
@@ -287,7 +287,7 @@ int trace_backward_impl(const sdf_trace_plan *plan, int sh_degree,
     if (accum) {
         tbegin(SDF_KERNEL_GRAD_FINALIZE, s);
         e = launch_grad_finalize(sh_degree, accum, num_points, attribute_grad, points_grad,
-                                 static_cast<float *>(a.point_error), s);
+                                 a.point_error, half, s);
         tend(s);
         if (e != hipSuccess) return hip_fail(e, "gradient accumulator finalize");
     }

@@ -87,8 +87,8 @@ struct BwdArgs {
     void *attr_grad;   // attribute type
     void *point_error; // attribute type
     float *sharpness_grad;
-    // fp32 only: per-cell gradient rows (accum_stride(L) floats: attribute
-    // row, position x/y/z, point error), added into the outputs by
+    // per-cell fp32 gradient rows (accum_stride(L) floats: attribute row,
+    // position x/y/z, point error), added into the outputs by
     // launch_grad_finalize; nullptr: atomics go to the outputs directly
     float *accum;
     // walk statistics (STATS instantiation only)
@@ -142,9 +142,11 @@ constexpr uint32_t accum_stride(int L) {
 hipError_t launch_grad_clear(int L, float *accum, uint32_t num_points, hipStream_t stream);
 
 // attribute_grad [N, D] += rows[:, :D]; points_grad [N, 3] += rows[:, D:D+3];
-// point_error [N] += rows[:, D+3] (point_error may be nullptr).
-hipError_t launch_grad_finalize(int L, const float *accum, uint32_t num_points, float *attr_grad,
-                                float *points_grad, float *point_error, hipStream_t stream);
+// point_error [N] += rows[:, D+3] (point_error may be nullptr).  attr_grad and
+// point_error are fp16 when `half` (the sum is rounded once), else fp32.
+hipError_t launch_grad_finalize(int L, const float *accum, uint32_t num_points, void *attr_grad,
+                                float *points_grad, void *point_error, bool half,
+                                hipStream_t stream);
 
 hipError_t launch_backward(int L, const BwdArgs &a, bool neus, bool stats, bool half,
                            hipStream_t stream);

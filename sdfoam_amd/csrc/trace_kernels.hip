@@ -596,14 +596,15 @@ __device__ __forceinline__ void grouped_pass(StepEntries &e, const OwnerLane &ow
                                            : sum_members<false>(grp, tb.buf, ow, s, ls));
             }
         }
-        if constexpr (sizeof(AT) == 4) {
+        if (accum) {
+            // one atomic instruction into the cell's fp32 row (for either
+            // attribute type): uniform row base + this lane's precomputed offset
+            if (ow.row_always || (pos && ow.row_pos))
+                atomicAdd(accum + (uint64_t)c * accum_stride(L) + ow.row_off, acc);
+        } else if constexpr (sizeof(AT) == 4) {
             // one atomic instruction: the row, the position and the point error
             float *dst = nullptr;
-            if (accum) {
-                // uniform row base + this lane's precomputed offset
-                if (ow.row_always || (pos && ow.row_pos))
-                    atomicAdd(accum + (uint64_t)c * accum_stride(L) + ow.row_off, acc);
-            } else if (lane < (uint32_t)D) {
+            if (lane < (uint32_t)D) {
                 dst = static_cast<float *>(attr_grad) + (uint64_t)c * D + lane;
             } else if (lane >= 60u && lane < 63u) {
                 if (pos) dst = points_grad + 3ull * c + (lane - 60u);
@@ -1108,11 +1109,12 @@ __global__ __launch_bounds__(kBlock) void grad_clear_kernel(float4 *__restrict__
 }
 
 // One thread per row element; an element that is exactly zero (a cell no
-// ray reached) leaves its output untouched.
-template <int L>
+// ray reached) leaves its output untouched.  fp16 outputs (attribute
+// gradients, point error) get the fp32 sum added and rounded once.
+template <int L, typename AT>
 __global__ __launch_bounds__(kBlock) void grad_finalize_kernel(
-    const float *__restrict__ rows, uint32_t num_points, float *__restrict__ attr_grad,
-    float *__restrict__ points_grad, float *__restrict__ point_error) {
+    const float *__restrict__ rows, uint32_t num_points, AT *__restrict__ attr_grad,
+    float *__restrict__ points_grad, AT *__restrict__ point_error) {
     constexpr uint32_t S = accum_stride(L);
     constexpr uint32_t D = 1 + 3 * (L + 1) * (L + 1);
     const uint64_t total = (uint64_t)num_points * S;
@@ -1124,11 +1126,13 @@ __global__ __launch_bounds__(kBlock) void grad_finalize_kernel(
         if (v == 0.0f) continue;
         const uint64_t c = t / S;
         if (j < D) {
-            attr_grad[c * D + j] += v;
+            AT &o = attr_grad[c * D + j];
+            o = (AT)((float)o + v);
         } else if (j < D + 3) {
             points_grad[c * 3 + (j - D)] += v;
         } else if (point_error) {
-            point_error[c] += v;
+            AT &o = point_error[c];
+            o = (AT)((float)o + v);
         }
     }
 }
@@ -1146,30 +1150,43 @@ hipError_t launch_grad_clear(int L, float *accum, uint32_t num_points, hipStream
     return hipGetLastError();
 }
 
-hipError_t launch_grad_finalize(int L, const float *accum, uint32_t num_points, float *attr_grad,
-                                float *points_grad, float *point_error, hipStream_t stream) {
+template <typename AT>
+static hipError_t launch_grad_finalize_T(int L, const float *accum, uint32_t num_points,
+                                        void *attr_grad, float *points_grad, void *point_error,
+                                        hipStream_t stream) {
     const dim3 grid = accum_grid((uint64_t)num_points * accum_stride(L));
+    AT *ag = static_cast<AT *>(attr_grad);
+    AT *pe = static_cast<AT *>(point_error);
     switch (L) {
     case 0:
-        hipLaunchKernelGGL(grad_finalize_kernel<0>, grid, dim3(kBlock), 0, stream, accum,
-                           num_points, attr_grad, points_grad, point_error);
+        hipLaunchKernelGGL((grad_finalize_kernel<0, AT>), grid, dim3(kBlock), 0, stream, accum,
+                           num_points, ag, points_grad, pe);
         break;
     case 1:
-        hipLaunchKernelGGL(grad_finalize_kernel<1>, grid, dim3(kBlock), 0, stream, accum,
-                           num_points, attr_grad, points_grad, point_error);
+        hipLaunchKernelGGL((grad_finalize_kernel<1, AT>), grid, dim3(kBlock), 0, stream, accum,
+                           num_points, ag, points_grad, pe);
         break;
     case 2:
-        hipLaunchKernelGGL(grad_finalize_kernel<2>, grid, dim3(kBlock), 0, stream, accum,
-                           num_points, attr_grad, points_grad, point_error);
+        hipLaunchKernelGGL((grad_finalize_kernel<2, AT>), grid, dim3(kBlock), 0, stream, accum,
+                           num_points, ag, points_grad, pe);
         break;
     case 3:
-        hipLaunchKernelGGL(grad_finalize_kernel<3>, grid, dim3(kBlock), 0, stream, accum,
-                           num_points, attr_grad, points_grad, point_error);
+        hipLaunchKernelGGL((grad_finalize_kernel<3, AT>), grid, dim3(kBlock), 0, stream, accum,
+                           num_points, ag, points_grad, pe);
         break;
     default:
         return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_grad_finalize(int L, const float *accum, uint32_t num_points, void *attr_grad,
+                                float *points_grad, void *point_error, bool half,
+                                hipStream_t stream) {
+    return half ? launch_grad_finalize_T<_Float16>(L, accum, num_points, attr_grad, points_grad,
+                                                   point_error, stream)
+                : launch_grad_finalize_T<float>(L, accum, num_points, attr_grad, points_grad,
+                                                point_error, stream);
 }
 
 // ---------------------------------------------------------------------------

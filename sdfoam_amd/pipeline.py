@@ -302,7 +302,9 @@ class Pipeline:
 
         * ``record_walk=True`` (sdfoam mode) records the rays' steps so that
           the backward skips its face scans; ``walk_budget`` bounds the
-          recorded trips per wavefront;
+          recorded trips per wavefront (in standard mode the plan carries
+          no record, only what the backward reuses: the offset table and
+          the ray order);
         * ``sort_rays``: trace rays of shape [R, 6] in sorted order
           (sdf_ray_order); None sorts from 32768 rays on.  Outputs stay in
           the caller's order.
@@ -351,7 +353,7 @@ class Pipeline:
         plan = None
         want_record = record_walk and settings.alpha_mode == _lib.SDF_ALPHA_NEUS
         want_sort = num_rays > 0 and _auto_sort(sort_rays, settings, num_rays)
-        if want_record or want_sort:
+        if record_walk or want_sort:
             plan = TracePlan(num_rays, settings, dev)
             if want_sort:
                 plan.sort_rays(num_points, rays_c, start_c)
@@ -389,10 +391,10 @@ class Pipeline:
         """Reference arguments and outputs, plus ``trace_plan`` (the
         forward's "trace_plan": its ray order and walk record),
         ``sort_rays`` (as in trace_forward, when no plan is given) and
-        ``grad_accum``: with fp32 attributes, accumulate each cell's
-        gradients in one aligned row of a temporary buffer (16 bytes more
-        than the outputs per cell at SH degree 3) before adding them to the
-        outputs; False updates the outputs directly."""
+        ``grad_accum``: accumulate each cell's gradients in one aligned fp32
+        row of a temporary buffer (256 bytes per cell at SH degree 3) before
+        adding them to the outputs (fp16 outputs: rounded once); False
+        updates the outputs directly."""
         points_c = points.contiguous()
         attributes_c = attributes.contiguous()
         adj_c = point_adjacency.contiguous()
@@ -500,7 +502,7 @@ class Pipeline:
         desc = trace_plan.desc() if trace_plan is not None else _lib.TracePlanDesc()
         desc.scratch_ready = 1 if table_ready else 0
         accum = None
-        if grad_accum and num_rays > 0 and self._attr_dtype == torch.float32:
+        if grad_accum and num_rays > 0:
             accum_bytes = int(_lib.lib().sdf_grad_accum_bytes(self._sh_degree, num_points))
             accum = torch.empty(accum_bytes + 256, dtype=torch.uint8, device=dev)
             desc.grad_accum = (accum.data_ptr() + 255) & ~255

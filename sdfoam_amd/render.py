@@ -51,11 +51,11 @@ class TraceRays(torch.autograd.Function):
             inv_s=ctx.inv_s,
             eps=ctx.eps,
             sdf_channel=ctx.sdf_channel,
-            record_walk=ctx.use_sdfoam,
+            record_walk=True,
         )
         ctx.rgba = results["rgba"]
-        # the forward's ray order and walk steps, replayed by the backward
-        # (no counterpart in the reference)
+        # the forward's ray order, walk steps (sdfoam mode) and offset table,
+        # reused by the backward (no counterpart in the reference)
         ctx.trace_plan = results.get("trace_plan", None)
         ctx.depth_indices = results.get("depth_indices", None)
         errbox = ErrorBox()

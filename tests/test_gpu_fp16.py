@@ -62,8 +62,12 @@ def _inputs(w, dev):
     return g
 
 
-@pytest.mark.parametrize("cfg,mode", [(1, "sdfoam"), (1, "standard"), (2, "sdfoam")])
-def test_fp16_forward_backward(dev, oracle_lib, cfg, mode):
+@pytest.mark.parametrize("cfg,mode,accum", [(1, "sdfoam", True), (1, "standard", True),
+                                            (2, "sdfoam", True), (1, "sdfoam", False),
+                                            (2, "sdfoam", False)])
+def test_fp16_forward_backward(dev, oracle_lib, cfg, mode, accum):
+    """accum: the backward's fp32 cell rows rounded once into the fp16
+    outputs; without: packed fp16 atomics per group into the outputs."""
     import torch
 
     import sdfoam_amd
@@ -84,7 +88,7 @@ def test_fp16_forward_backward(dev, oracle_lib, cfg, mode):
                               depth_quantiles=q, depth_indices=fwd["depth_indices"],
                               depth_grad_in=to_dev(w.depth_grad, dev),
                               ray_error=to_dev(rerr, dev), alpha_mode=mode, inv_s=inv_t,
-                              trace_plan=fwd.get("trace_plan"))
+                              trace_plan=fwd.get("trace_plan"), grad_accum=accum)
     torch.cuda.synchronize()
     assert bwd["attr_grad"].dtype == torch.float16 and bwd["points_grad"].dtype == torch.float32
     R = w.num_rays
