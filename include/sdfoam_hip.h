@@ -182,12 +182,13 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
  * Two optional aids for a forward and the backward over the same rays, start
  * points, scene and settings.  Results are identical with and without them.
  *
- * Walk record: the forward of an sdfoam-mode trace records each ray's steps
- * (next cell and exit distance, 8 bytes a step, `walk_budget` trips per
- * wavefront of 64 rays); the backward then reads the steps instead of
- * scanning the cell faces again.  A standard-mode trace ignores it.  Rays
- * past `walk_budget` trips, or that walk further in the backward, scan as
- * usual.  walk_record == NULL: no record.
+ * Walk record: the forward records each ray's steps (next cell and exit
+ * distance, 8 bytes a step, `walk_budget` trips per wavefront of 64 rays);
+ * the backward then reads the steps instead of scanning the cell faces
+ * again.  In standard mode a step is recorded only while the density
+ * backward's unsafe walk takes the same exit.  Rays past `walk_budget`
+ * trips, or that walk further in the backward, scan as usual.
+ * walk_record == NULL: no record.
  *
  * Ray order: a permutation of [0, num_rays) from sdf_ray_order; the kernels
  * trace rays in that order (outputs stay in the caller's order).  For rays

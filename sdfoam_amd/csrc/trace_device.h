@@ -283,6 +283,7 @@ struct WalkState {
 struct StepInfo {
     bool found;    // an exit face was found: the walk moves to `next`
     bool stepped;  // ... and t1 > t0: the step functor runs for `cell`
+    bool agrees;   // (DUAL scans) an unsafe-mode walk takes the same exit
     uint32_t next;
     float t1;
     float xn[3];
@@ -308,11 +309,17 @@ __device__ __forceinline__ void walk_init(const SceneView &sc, uint32_t start, W
 // of bounds otherwise.  Clears ws.alive when the walk ends.
 // GUARD: the offset table has no padding past E (a caller's table), so the
 // last batch of a row re-reads the row's last entry instead of over-reading.
-template <bool SAFE, bool COUNT, bool GUARD = false>
+// DUAL (safe scans): also tell whether the unsafe mode's exit (the first
+// minimum t over dp > 0 alone) is the same face: it is unless the smallest
+// such t is <= t0 (then it lies outside the safe set, or the safe set is
+// empty while the unsafe one is not); sets si.agrees.
+template <bool SAFE, bool COUNT, bool GUARD = false, bool DUAL = false>
 __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ray,
                                              uint32_t max_steps, WalkState &ws, StepInfo &si,
                                              WalkCounters &wc) {
+    static_assert(SAFE || !DUAL, "DUAL compares a safe scan with the unsafe one");
     si.found = false;
+    si.agrees = true;
     si.stepped = false;
     ++ws.n;
     if (ws.n > max_steps) {
@@ -328,6 +335,7 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
     const uint32_t nf = end - beg;
     const float t0 = ws.t0;
     float t1 = __builtin_bit_cast(float, 0x7f800000u);
+    float tmin_u = t1; // DUAL: smallest t over dp > 0 (NaN never taken)
     uint32_t best = kNoIndex;
     const uint2 *__restrict__ row = sc.diff + beg;
     // batches of 4: the table is padded, so the last batch may over-read
@@ -358,9 +366,13 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
                 t1 = t;
                 best = k;
             }
+            if constexpr (DUAL) {
+                if (dp > 0.0f && k < nf) tmin_u = fminf(tmin_u, t);
+            }
         }
     }
     if constexpr (COUNT) wc.faces += nf;
+    if constexpr (DUAL) si.agrees = !(tmin_u <= t0);
     if (best == kNoIndex) {
         ws.alive = false;
         return;

@@ -187,11 +187,9 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     WalkState ws;
     walk_init(a.scene, valid ? a.start[ray_idx] : kNoIndex, ws);
     WalkCounters wc = {0u, 0u, 0ull, 0ull};
-    // walk record of this wavefront (sdfoam walks only; the density
-    // backward walks differently): one row of 64 entries per trip
+    // walk record of this wavefront: one row of 64 entries per trip
     uint2 *wrec = nullptr;
-    if (!STATS && NEUS && a.record.entries)
-        wrec = walk_record_lane<kForwardChunk>(a.record, lane);
+    if (!STATS && a.record.entries) wrec = walk_record_lane<kForwardChunk>(a.record, lane);
     uint32_t trip = 0;
     FwdEntry held = {0u, 0.0f, 0.0f, false}; // step waiting for the next contribution pass
 
@@ -201,8 +199,19 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         si.found = false;
         uint2 entry = make_uint2(kWalkUnrecorded, 0u);
         if (ws.alive) {
-            walk_advance<true, STATS>(a.scene, ray, max_steps, ws, si, wc);
-            entry = make_uint2(si.found ? si.next : kNoIndex, __builtin_bit_cast(uint32_t, si.t1));
+            if constexpr (NEUS || STATS) {
+                walk_advance<true, STATS>(a.scene, ray, max_steps, ws, si, wc);
+                entry = make_uint2(si.found ? si.next : kNoIndex,
+                                   __builtin_bit_cast(uint32_t, si.t1));
+            } else {
+                // the density backward walks in the unsafe mode: a step is
+                // recorded while that walk takes the same exit; from the first
+                // step where it would not, the backward scans for itself
+                walk_advance<true, false, false, true>(a.scene, ray, max_steps, ws, si, wc);
+                if (si.agrees)
+                    entry = make_uint2(si.found ? si.next : kNoIndex,
+                                       __builtin_bit_cast(uint32_t, si.t1));
+            }
         }
         if (wrec && trip < a.record.budget) wrec[(uint64_t)trip * 64] = entry;
         ++trip;
@@ -904,13 +913,37 @@ backward_density_kernel(BwdArgs a) {
     WalkCounters wc = {0u, 0u, 0ull, 0ull};
     StepEntries ents;
     entries_init(ents);
+    // replay of the forward's walk record as in backward_sdf; the forward
+    // records a step only where the unsafe walk takes the same exit
+    const uint2 *wrec = nullptr;
+    if (!STATS && a.record.entries) wrec = walk_record_lane<kBackwardChunk>(a.record, lane);
     uint32_t trip = 0;
 
     while (__ballot(ws.alive) != 0ull) {
         StepInfo si;
         si.stepped = false;
         si.found = false;
-        if (ws.alive) walk_advance<false, STATS>(a.scene, ray, a.settings.max_intersections, ws, si, wc);
+        if (ws.alive) {
+            uint2 e = make_uint2(kWalkUnrecorded, 0u);
+            if (wrec && trip < a.record.budget) e = wrec[(uint64_t)trip * 64];
+            if (e.x == kNoIndex) {
+                ++ws.n;
+                ws.alive = false;
+            } else if (e.x < a.scene.num_points) {
+                ++ws.n;
+                si.found = true;
+                si.next = e.x;
+                si.t1 = __builtin_bit_cast(float, e.y);
+                si.xn[0] = a.scene.points[3ull * e.x];
+                si.xn[1] = a.scene.points[3ull * e.x + 1];
+                si.xn[2] = a.scene.points[3ull * e.x + 2];
+                si.stepped = si.t1 > ws.t0;
+            } else {
+                wrec = nullptr;
+                walk_advance<false, STATS>(a.scene, ray, a.settings.max_intersections, ws, si,
+                                           wc);
+            }
+        }
         ++trip;
 
         bool keep = true;

@@ -104,7 +104,7 @@ class TracePlan:
     * ``order``: the launch order of the rays (sdf_ray_order), for rays in no
       particular order;
     * ``entries``: the walk record, each ray's steps (8 bytes per step, up to
-      ``budget`` trips per wavefront of 64 rays), sdfoam mode only;
+      ``budget`` trips per wavefront of 64 rays);
     * ``table``: the forward's fp16 offset table of the scene, which the
       backward reuses instead of rebuilding it while the points, adjacency
       and offsets tensors are the same and unmodified (same storage and
@@ -300,11 +300,11 @@ class Pipeline:
         """Reference arguments and outputs, plus (no counterpart in the
         reference):
 
-        * ``record_walk=True`` (sdfoam mode) records the rays' steps so that
-          the backward skips its face scans; ``walk_budget`` bounds the
-          recorded trips per wavefront (in standard mode the plan carries
-          no record, only what the backward reuses: the offset table and
-          the ray order);
+        * ``record_walk=True`` records the rays' steps so that the backward
+          skips its face scans (standard mode: the steps where the density
+          backward's unsafe walk takes the same exit, which is all of them
+          but for degenerate ties); ``walk_budget`` bounds the recorded trips
+          per wavefront;
         * ``sort_rays``: trace rays of shape [R, 6] in sorted order
           (sdf_ray_order); None sorts from 32768 rays on.  Outputs stay in
           the caller's order.
@@ -351,7 +351,7 @@ class Pipeline:
         alpha = torch.zeros((num_points, 1), dtype=torch.float32, device=dev)
         scratch, nbytes = self._scratch(num_points, num_adj, dev)
         plan = None
-        want_record = record_walk and settings.alpha_mode == _lib.SDF_ALPHA_NEUS
+        want_record = bool(record_walk)
         want_sort = num_rays > 0 and _auto_sort(sort_rays, settings, num_rays)
         if record_walk or want_sort:
             plan = TracePlan(num_rays, settings, dev)

@@ -4,7 +4,7 @@ Same forward/backward contract as the reference's ``TraceRays``
 (sdfoam_model/render.py:10-189): forward returns
 ``(rgba, depth, contribution, num_intersections, ErrorBox, alpha)``; backward
 calls ``trace_backward`` with the saved forward outputs (and the forward's
-trace plan: ray order, and in sdfoam mode its walk record), zeroes non-finite
+trace plan: ray order, walk record and offset table), zeroes non-finite
 gradients and returns gradients for ``points``, ``attributes`` and, in
 sdfoam mode, ``inv_s``.
 """

@@ -356,9 +356,19 @@ def test_backward_walk_record_c2_sharp(torch_dev, oracle_lib):
     _check_backward(bwd, st, ref, w)
 
 
-def test_walk_record_standard_mode_ignored(torch_dev, oracle_lib):
-    """Standard mode records nothing; its backward runs as without a record."""
+@pytest.mark.parametrize("budget", [None, 2])
+def test_walk_record_standard_mode(torch_dev, oracle_lib, budget):
+    """Standard mode: the forward records the steps where the density
+    backward's unsafe walk takes the same exit and the backward replays them
+    (budget 2: every wavefront goes back to its own unsafe scan mid-walk)."""
     w = scene(1, mode="standard")
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "standard", ray_error=True,
+                                  walk=True, walk_budget=budget)
+    _check_backward(bwd, st, ref, w)
+
+
+def test_walk_record_standard_mode_c2(torch_dev, oracle_lib):
+    w = scene(2, mode="standard")
     bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "standard", walk=True)
     _check_backward(bwd, st, ref, w)
 
