@@ -315,6 +315,45 @@ int sdf_farthest_neighbor(const float *points, uint32_t num_points,
                           const uint32_t *point_adjacency_offsets,
                           uint32_t *indices, float *cell_radius, void *stream);
 
+/* Scratch bytes of sdf_sort_points (0 where no GPU is present). */
+size_t sdf_sort_points_scratch_bytes(uint32_t num_points);
+
+/* perm[num_points]: the point order the reference's tree builder leaves
+ * (sorted points = points[perm]); scratch 256-byte aligned.
+ * Replaces sort_points (src/aabb_tree/aabb_tree.h:10-14,
+ * src/aabb_tree/aabb_tree.cu:62-190). */
+int sdf_sort_points(const float *points, uint32_t num_points, uint32_t *perm,
+                    void *scratch, size_t scratch_bytes, void *stream);
+
+/* point_adjacency entries sdf_delaunay_tables needs room for: 4 N + 2 T + 64
+ * (2 E <= 4 N + 2 T for a tetrahedralised ball). */
+uint64_t sdf_delaunay_adjacency_capacity(uint32_t num_points, uint32_t num_tets);
+
+/* Scratch bytes of sdf_delaunay_tables (0 where no GPU is present). */
+size_t sdf_delaunay_tables_scratch_bytes(uint32_t num_points, uint32_t num_tets);
+
+/* Tables of a Delaunay tetrahedralisation given as tets [T,4] (vertex ids,
+ * either orientation, any order) and neighbors [T,4] (the tet across the
+ * face opposite vertex j, or -1 on the hull), as Qhull returns them:
+ * tets_out [T,4] positively oriented (det[b-a, c-a, d-a] > 0 in double),
+ * ordered by their sorted vertex sets; tet_adjacency [T,4] = 4 k + m for
+ * neighbour k and its face m, UINT32_MAX on the hull; vert_to_tet [N] the
+ * lowest tet holding each point (UINT32_MAX if none);
+ * point_adjacency_offsets [N+1] and point_adjacency (the Delaunay edges, CSR
+ * with ascending rows; offsets[N] entries are written).  Synchronizes the
+ * stream once.  scratch 256-byte aligned.
+ * Replaces the tables of Triangulation (src/delaunay/delaunay.h:14-44,
+ * src/delaunay/delaunay.cu:146-226;
+ * torch_bindings/triangulation_bindings.cpp:11-115). */
+int sdf_delaunay_tables(const float *points, uint32_t num_points,
+                        const uint32_t *tets, const int32_t *neighbors,
+                        uint32_t num_tets, uint32_t *tets_out,
+                        uint32_t *tet_adjacency, uint32_t *vert_to_tet,
+                        uint32_t *point_adjacency_offsets,
+                        uint32_t *point_adjacency,
+                        uint64_t point_adjacency_capacity, void *scratch,
+                        size_t scratch_bytes, void *stream);
+
 /* ---- measurement and test hooks (no counterpart in the reference) ----- */
 
 /* Per-ray walk statistics of the forward (backward = 0) or backward

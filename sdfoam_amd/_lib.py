@@ -40,6 +40,11 @@ EXPORTS = (
     "sdf_batch_rows",
     "sdf_build_aabb_tree",
     "sdf_farthest_neighbor",
+    "sdf_sort_points_scratch_bytes",
+    "sdf_sort_points",
+    "sdf_delaunay_adjacency_capacity",
+    "sdf_delaunay_tables_scratch_bytes",
+    "sdf_delaunay_tables",
     "sdf_nn",
     "sdf_trace_walk_stats",
     "sdf_debug_fpmath",
@@ -174,6 +179,16 @@ def lib() -> C.CDLL:
     L.sdf_build_aabb_tree.argtypes = [P, U32, P, P]
     L.sdf_farthest_neighbor.restype = C.c_int
     L.sdf_farthest_neighbor.argtypes = [P, U32, U32, P, P, P, P, P]
+    L.sdf_sort_points_scratch_bytes.restype = SZ
+    L.sdf_sort_points_scratch_bytes.argtypes = [U32]
+    L.sdf_sort_points.restype = C.c_int
+    L.sdf_sort_points.argtypes = [P, U32, P, P, SZ, P]
+    L.sdf_delaunay_adjacency_capacity.restype = C.c_uint64
+    L.sdf_delaunay_adjacency_capacity.argtypes = [U32, U32]
+    L.sdf_delaunay_tables_scratch_bytes.restype = SZ
+    L.sdf_delaunay_tables_scratch_bytes.argtypes = [U32, U32]
+    L.sdf_delaunay_tables.restype = C.c_int
+    L.sdf_delaunay_tables.argtypes = [P, U32, P, P, U32, P, P, P, P, P, C.c_uint64, P, SZ, P]
     L.sdf_nn.restype = C.c_int
     L.sdf_nn.argtypes = [P, P, P, U32, U32, P, P]
     L.sdf_trace_walk_stats.restype = C.c_int

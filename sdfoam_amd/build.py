@@ -23,7 +23,8 @@ LIB_NAME = "libsdfoam_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 ARCH = os.environ.get("SDFOAM_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["trace_kernels.hip", "aabb_kernels.hip", "order_kernels.hip", "batch_fetcher.hip",
+SOURCES = ["trace_kernels.hip", "aabb_kernels.hip", "order_kernels.hip", "delaunay_tables.hip",
+           "batch_fetcher.hip",
            "triangulation_kernels.hip", "capi.hip"]
 
 HIPCC_FLAGS = [

@@ -530,6 +530,69 @@ int sdf_farthest_neighbor(const float *points, uint32_t num_points, uint32_t adj
     return SDF_OK;
 }
 
+size_t sdf_sort_points_scratch_bytes(uint32_t num_points) {
+    return sort_points_scratch_bytes(num_points);
+}
+
+int sdf_sort_points(const float *points, uint32_t num_points, uint32_t *perm, void *scratch,
+                    size_t scratch_bytes, void *stream) {
+    if (num_points == 0) return SDF_OK;
+    if (!points || !perm || !scratch) return fail(SDF_E_INVALID, "NULL pointer argument");
+    if ((reinterpret_cast<uintptr_t>(scratch) & 255u) != 0)
+        return fail(SDF_E_INVALID, "scratch must be 256-byte aligned");
+    const size_t need = sort_points_scratch_bytes(num_points);
+    if (need == 0) return fail(SDF_E_HIP, "sort_points: no device to size the sort for");
+    if (scratch_bytes < need)
+        return fail(SDF_E_INVALID, "scratch must hold %zu bytes (got %zu)", need, scratch_bytes);
+    hipError_t e = launch_sort_points(points, num_points, perm, scratch, scratch_bytes,
+                                      static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "sort_points");
+    return SDF_OK;
+}
+
+uint64_t sdf_delaunay_adjacency_capacity(uint32_t num_points, uint32_t num_tets) {
+    return delaunay_edge_capacity(num_points, num_tets);
+}
+
+size_t sdf_delaunay_tables_scratch_bytes(uint32_t num_points, uint32_t num_tets) {
+    return delaunay_tables_scratch_bytes(num_points, num_tets);
+}
+
+int sdf_delaunay_tables(const float *points, uint32_t num_points, const uint32_t *tets,
+                        const int32_t *neighbors, uint32_t num_tets, uint32_t *tets_out,
+                        uint32_t *tet_adjacency, uint32_t *vert_to_tet,
+                        uint32_t *point_adjacency_offsets, uint32_t *point_adjacency,
+                        uint64_t point_adjacency_capacity, void *scratch, size_t scratch_bytes,
+                        void *stream) {
+    if (!points || !vert_to_tet || !point_adjacency_offsets || !scratch ||
+        (num_tets > 0 && (!tets || !neighbors || !tets_out || !tet_adjacency || !point_adjacency)))
+        return fail(SDF_E_INVALID, "NULL pointer argument");
+    if ((reinterpret_cast<uintptr_t>(scratch) & 255u) != 0)
+        return fail(SDF_E_INVALID, "scratch must be 256-byte aligned");
+    if (num_points == 0 && num_tets > 0)
+        return fail(SDF_E_INVALID, "tets need points");
+    const uint64_t cap = delaunay_edge_capacity(num_points, num_tets);
+    if (point_adjacency_capacity < cap)
+        return fail(SDF_E_INVALID, "point_adjacency must hold %llu entries (got %llu)",
+                    (unsigned long long)cap, (unsigned long long)point_adjacency_capacity);
+    const size_t need = delaunay_tables_scratch_bytes(num_points, num_tets);
+    if (need == 0) return fail(SDF_E_HIP, "delaunay_tables: no device to size the sorts for");
+    if (scratch_bytes < need)
+        return fail(SDF_E_INVALID, "scratch must hold %zu bytes (got %zu)", need, scratch_bytes);
+    uint32_t input_error = 0;
+    hipError_t e = launch_delaunay_tables(points, num_points, tets, neighbors, num_tets, tets_out,
+                                          tet_adjacency, vert_to_tet, point_adjacency_offsets,
+                                          point_adjacency, point_adjacency_capacity, input_error,
+                                          scratch, scratch_bytes,
+                                          static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "delaunay_tables");
+    if (input_error & 1u)
+        return fail(SDF_E_INVALID, "tets or neighbors hold an index out of range");
+    if (input_error & 2u)
+        return fail(SDF_E_INVALID, "more edges than a tetrahedralised ball can have");
+    return SDF_OK;
+}
+
 int sdf_nn(const float *points, const float *aabb_tree, const float *queries, uint32_t num_points,
            uint32_t num_queries, uint32_t *indices, void *stream) {
     if (num_points < 32) return fail(SDF_E_INVALID, "number of points must be at least 32");

@@ -156,6 +156,22 @@ hipError_t launch_farthest_neighbor(const float *points, uint32_t num_points, co
                                     const uint32_t *offs, uint32_t num_adj, uint32_t *indices,
                                     float *cell_radius, hipStream_t stream);
 
+// delaunay_tables.hip
+size_t sort_points_scratch_bytes(uint32_t num_points);
+hipError_t launch_sort_points(const float *points, uint32_t num_points, uint32_t *perm,
+                              void *scratch, size_t scratch_bytes, hipStream_t stream);
+uint64_t delaunay_edge_capacity(uint32_t num_points, uint32_t num_tets);
+size_t delaunay_tables_scratch_bytes(uint32_t num_points, uint32_t num_tets);
+// Synchronizes `stream` once (the edge count sizes the last sort).
+// input_error: 1 = a vertex or neighbour index out of range, 2 = more edges
+// than a tetrahedralised ball can have.
+hipError_t launch_delaunay_tables(const float *points, uint32_t num_points,
+                                  const uint32_t *tets_in, const int32_t *nbr_in,
+                                  uint32_t num_tets, uint32_t *tets_out, uint32_t *tet_adj,
+                                  uint32_t *vert_to_tet, uint32_t *offsets, uint32_t *adjacency,
+                                  uint64_t adjacency_capacity, uint32_t &input_error,
+                                  void *scratch, size_t scratch_bytes, hipStream_t stream);
+
 hipError_t launch_build_aabb_tree(const float *points, uint32_t num_points, float *tree,
                                   hipStream_t stream);
 hipError_t launch_nn(const float *points, const float *tree, const float *queries,

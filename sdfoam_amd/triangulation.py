@@ -20,8 +20,10 @@ uint32 tensors indexing the sorted points:
 
 The Delaunay tetrahedralisation itself is computed on the host with Qhull
 (scipy); the reference builds it on the GPU with exact predicates.  For points
-in general position the two are the same unique triangulation.
-``farthest_neighbor`` runs in libsdfoam_hip.so.
+in general position the two are the same unique triangulation.  The point
+order (``sort_points``), the tables derived from Qhull's tetrahedra and
+``farthest_neighbor`` run in libsdfoam_hip.so; ``host_tables`` is the numpy
+statement of the same tables (the check of the device path).
 """
 
 from __future__ import annotations
@@ -46,23 +48,39 @@ def _u32_cuda(a: np.ndarray, device) -> torch.Tensor:
     return torch.from_numpy(a.view(np.int32)).to(device).view(torch.uint32)
 
 
-def triangulate_host(points: np.ndarray) -> dict:
-    """Delaunay tetrahedralisation of float32 points [N, 3] (already in the
-    triangulation's point order) and its derived tables, as numpy uint32."""
+def qhull_tetrahedra(points: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Delaunay tetrahedra of float32 points [N, 3] (Qhull, in double):
+    (simplices [T, 4] int32, neighbors [T, 4] int32, -1 on the hull)."""
     from scipy.spatial import Delaunay
     from scipy.spatial import QhullError
 
-    p64 = np.asarray(points, dtype=np.float64)
-    n = p64.shape[0]
     try:
-        tri = Delaunay(p64)
+        tri = Delaunay(np.asarray(points, dtype=np.float64))
     except QhullError as e:
         raise TriangulationFailedError(f"Qhull failed: {str(e).splitlines()[0]}") from None
-    s = tri.simplices.astype(np.int64)
-    nb = tri.neighbors.astype(np.int64)
+    return (np.ascontiguousarray(tri.simplices, dtype=np.int32),
+            np.ascontiguousarray(tri.neighbors, dtype=np.int32))
+
+
+def triangulate_host(points: np.ndarray) -> dict:
+    """Delaunay tetrahedralisation of float32 points [N, 3] (already in the
+    triangulation's point order) and its derived tables, as numpy uint32."""
+    simplices, neighbors = qhull_tetrahedra(points)
+    return host_tables(points, simplices, neighbors)
+
+
+def host_tables(points: np.ndarray, simplices: np.ndarray, neighbors: np.ndarray) -> dict:
+    """The tables of sdf_delaunay_tables in numpy (the statement the device
+    path is checked against)."""
+    p64 = np.asarray(points, dtype=np.float64)
+    n = p64.shape[0]
+    s = np.asarray(simplices, dtype=np.int64).copy()
+    nb = np.asarray(neighbors, dtype=np.int64).copy()
     # positive orientation: swap the last two vertices (and their neighbours)
     a, b, c, d = (p64[s[:, k]] for k in range(4))
-    vol = np.einsum("ij,ij->i", np.cross(b - a, c - a), d - a)
+    x = np.cross(b - a, c - a)
+    w = d - a
+    vol = (x[:, 0] * w[:, 0] + x[:, 1] * w[:, 1]) + x[:, 2] * w[:, 2]
     neg = vol < 0
     s[neg, 2], s[neg, 3] = s[neg, 3].copy(), s[neg, 2].copy()
     nb[neg, 2], nb[neg, 3] = nb[neg, 3].copy(), nb[neg, 2].copy()
@@ -105,6 +123,57 @@ def triangulate_host(points: np.ndarray) -> dict:
             "point_adjacency": adj, "point_adjacency_offsets": offs}
 
 
+def sort_points(points: torch.Tensor) -> torch.Tensor:
+    """The reference's sort_points order of CUDA float32 points [N, 3], as a
+    uint32 permutation (sorted = points[perm]) on the points' device."""
+    pts = points.contiguous()
+    n = pts.numel() // 3
+    perm = torch.empty(n, dtype=torch.int32, device=pts.device)
+    if n == 0:
+        return perm.view(torch.uint32)
+    L = _lib.lib()
+    nbytes = int(L.sdf_sort_points_scratch_bytes(n))
+    if nbytes == 0:
+        raise RuntimeError("sdf_sort_points_scratch_bytes failed")
+    scratch = torch.empty(nbytes + 256, dtype=torch.uint8, device=pts.device)
+    with torch.cuda.device(pts.device):
+        check(L.sdf_sort_points(ptr(pts), n, ptr(perm), (scratch.data_ptr() + 255) & ~255,
+                                nbytes, _lib.stream_handle(pts.device)))
+    return perm.view(torch.uint32)
+
+
+def device_tables(points: torch.Tensor, simplices: np.ndarray, neighbors: np.ndarray) -> dict:
+    """sdf_delaunay_tables over Qhull's tetrahedra of `points` (CUDA
+    float32 [N, 3]): the tables as uint32 tensors on the points' device."""
+    pts = points.contiguous()
+    dev = pts.device
+    n = pts.numel() // 3
+    T = int(simplices.shape[0])
+    L = _lib.lib()
+    tets_in = torch.from_numpy(np.ascontiguousarray(simplices, dtype=np.int32)).to(dev)
+    nbr_in = torch.from_numpy(np.ascontiguousarray(neighbors, dtype=np.int32)).to(dev)
+    tets = torch.empty((T, 4), dtype=torch.int32, device=dev)
+    tet_adj = torch.empty((T, 4), dtype=torch.int32, device=dev)
+    v2t = torch.empty(n, dtype=torch.int32, device=dev)
+    offs = torch.empty(n + 1, dtype=torch.int32, device=dev)
+    cap = int(L.sdf_delaunay_adjacency_capacity(n, T))
+    adj = torch.empty(cap, dtype=torch.int32, device=dev)
+    nbytes = int(L.sdf_delaunay_tables_scratch_bytes(n, T))
+    if nbytes == 0:
+        raise RuntimeError("sdf_delaunay_tables_scratch_bytes failed")
+    scratch = torch.empty(nbytes + 256, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check(L.sdf_delaunay_tables(ptr(pts), n, ptr(tets_in), ptr(nbr_in), T, ptr(tets),
+                                    ptr(tet_adj), ptr(v2t), ptr(offs), ptr(adj), cap,
+                                    (scratch.data_ptr() + 255) & ~255, nbytes,
+                                    _lib.stream_handle(dev)))
+    num_adj = int(offs[n].item())  # the call synchronised the stream
+    return {"tets": tets.view(torch.uint32), "tet_adjacency": tet_adj.view(torch.uint32),
+            "vert_to_tet": v2t.view(torch.uint32),
+            "point_adjacency": adj[:num_adj].clone().view(torch.uint32),
+            "point_adjacency_offsets": offs.view(torch.uint32)}
+
+
 def _check_points(points: torch.Tensor) -> None:
     if points.size(-1) != 3:
         raise RuntimeError("points must have 3 as the last dimension")
@@ -118,34 +187,28 @@ class Triangulation:
     def __init__(self, points: torch.Tensor):
         _check_points(points)
         self._num_points = 0
-        self._perm = None
+        self._perm_t = None
         self.rebuild(points, incremental=False)
 
     def rebuild(self, points: torch.Tensor, incremental: bool = False) -> bool:
         """src/delaunay/delaunay.cu:260-349 (rebuild)."""
-        from .scenes import sort_points_order
-
         _check_points(points)
         n = points.numel() // 3
         if n < 32:
             raise RuntimeError("Delaunay triangulation does not support less than 32 points")
-        pts = points.detach().reshape(n, 3).cpu().numpy()
+        pts_dev = points.detach().reshape(n, 3).contiguous()
         if incremental and n == self._num_points:
             sorted_now = False
         else:
-            perm = sort_points_order(pts)
-            pts = pts[perm]
-            self._perm = perm
+            self._perm_t = sort_points(pts_dev)
+            pts_dev = pts_dev[self._perm_t.view(torch.int32).long()]
             self._num_points = n
             sorted_now = True
+        pts = pts_dev.cpu().numpy()
         if np.unique(pts, axis=0).shape[0] != n:
             raise TriangulationFailedError("duplicate points found")
-        tables = triangulate_host(pts)
-        dev = points.device
-        self._tables = {k: _u32_cuda(v, dev) for k, v in tables.items()}
-        self._tables["tets"] = self._tables["tets"].reshape(-1, 4)
-        self._tables["tet_adjacency"] = self._tables["tet_adjacency"].reshape(-1, 4)
-        self._perm_t = _u32_cuda(self._perm, dev)
+        simplices, neighbors = qhull_tetrahedra(pts)
+        self._tables = device_tables(pts_dev, simplices, neighbors)
         return sorted_now
 
     def permutation(self) -> torch.Tensor:

@@ -126,6 +126,26 @@ def test_grad_accum_sizes_and_errors():
         assert rc == 1 and msg in L.sdf_last_error()
 
 
+def test_triangulation_table_argument_errors():
+    from sdfoam_amd import _lib
+
+    L = _lib.lib()
+    assert L.sdf_delaunay_adjacency_capacity(100, 500) == 4 * 100 + 2 * 500 + 64
+    buf = (C.c_uint64 * 128)()
+    p = C.cast(buf, C.c_void_p)
+    base = C.cast(buf, C.c_void_p).value
+    aligned = (base + 255) & ~255
+    rc = L.sdf_delaunay_tables(p, 100, p, p, 500, p, p, p, p, p, 10, aligned, 1 << 20, None)
+    assert rc == 1 and b"point_adjacency must hold 1464 entries" in L.sdf_last_error()
+    rc = L.sdf_delaunay_tables(p, 100, p, p, 500, p, p, p, p, p, 1464, aligned + 8, 1 << 20, None)
+    assert rc == 1 and b"256-byte aligned" in L.sdf_last_error()
+    rc = L.sdf_delaunay_tables(None, 100, p, p, 500, p, p, p, p, p, 1464, aligned, 1 << 20, None)
+    assert rc == 1 and b"NULL pointer" in L.sdf_last_error()
+    assert L.sdf_sort_points(p, 0, None, None, 0, None) == 0
+    assert L.sdf_sort_points(p, 10, None, p, 1 << 20, None) == 1
+    assert b"NULL pointer" in L.sdf_last_error()
+
+
 def test_ray_order_and_plan_errors():
     from sdfoam_amd import _lib
 

@@ -105,3 +105,39 @@ def test_triangulation_errors(dev):
         sdfoam_amd.Triangulation(torch.randn(20, 3, device=dev))
     with pytest.raises(RuntimeError, match="CUDA device"):
         sdfoam_amd.Triangulation(torch.randn(100, 3))
+
+
+@pytest.mark.parametrize("n", [33, 1025, 4097, 300_001, 2_500_000])
+def test_sort_points_matches_host(dev, n):
+    """Every branch of the pass rule: 1024-point blocks, whole-array passes
+    and (from more than 1024 segments of more than 1024 points, n > 2^21)
+    per-segment passes."""
+    import torch
+
+    from sdfoam_amd import scenes
+    from sdfoam_amd.triangulation import sort_points
+
+    rng = np.random.default_rng(n)
+    pts = rng.normal(size=(n, 3)).astype(np.float32)
+    pts[: n // 10, 1] = 0.25  # equal keys: the passes must be stable
+    got = _np(sort_points(torch.from_numpy(pts).to(dev)))
+    assert np.array_equal(got, scenes.sort_points_order(pts))
+
+
+@pytest.mark.parametrize("cfg", [1, 2])
+def test_device_tables_match_host(dev, cfg):
+    """sdf_delaunay_tables against the numpy statement on the same Qhull
+    tetrahedra: every table bit-exact."""
+    import torch
+
+    from sdfoam_amd.triangulation import device_tables, host_tables, qhull_tetrahedra
+
+    w = scene(cfg)
+    simplices, neighbors = qhull_tetrahedra(w.points)
+    got = device_tables(torch.from_numpy(w.points).to(dev), simplices, neighbors)
+    ref = host_tables(w.points, simplices, neighbors)
+    for k, v in ref.items():
+        assert np.array_equal(_np(got[k]).reshape(v.shape), v), k
+    # the scene's own CSR adjacency is the same edge graph
+    assert np.array_equal(_np(got["point_adjacency"]), w.adjacency)
+    assert np.array_equal(_np(got["point_adjacency_offsets"]), w.offsets)
