@@ -238,9 +238,11 @@ def main() -> int:
     N = w.num_points
     E = int(w.adjacency.size)
     # attribute elements (rows, contribution, gradient rows) at their storage
-    # width; the walk record only in sdfoam mode (standard mode ignores it)
+    # width; with the walk record the backward reads 8 B per step instead of
+    # the stepped cell's face rows (standard mode: all but the rare steps
+    # where the unsafe walk leaves the recorded one)
     ab = 2 if half else 4
-    recorded = use_record and args.alpha_mode == "sdfoam"
+    recorded = use_record
     if recorded:
         # the forward also writes 8 B per step; the backward reads them
         # instead of the stepped cells' face rows
