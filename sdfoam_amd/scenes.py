@@ -295,11 +295,13 @@ def _scene_c3(rng):
 
 
 def make_config(index: int, *, mode: str = "sdfoam", inv_s: float | None = None,
-                image_scale: float = 1.0, point_scale: float = 1.0) -> Workload:
+                image_scale: float = 1.0, point_scale: float = 1.0,
+                sh_degree: int | None = None) -> Workload:
     """Workload configuration C1-C5 (seed = config index).
 
     ``image_scale`` < 1 shrinks the image (same camera) for quick tests;
-    ``point_scale`` < 1 shrinks the point counts of C4 / C5 (same proportions).
+    ``point_scale`` < 1 shrinks the point counts of C4 / C5 (same proportions);
+    ``sh_degree`` replaces the configuration's SH degree (C1-C3).
     """
     rng = np.random.default_rng(index if index != 1 else 0)
     inv_s = math.exp(0.3) if inv_s is None else float(inv_s)
@@ -324,6 +326,8 @@ def make_config(index: int, *, mode: str = "sdfoam", inv_s: float | None = None,
         fov, w, h = math.radians(40.0), 1600, 1200
     else:
         raise ValueError(f"unknown config {index}")
+    if sh_degree is not None:
+        degree = int(sh_degree)
 
     perm = sort_points_order(pts)
     pts = np.ascontiguousarray(pts[perm])

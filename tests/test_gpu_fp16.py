@@ -47,10 +47,10 @@ def dev():
     return torch.device("cuda:0")
 
 
-def half_scene(index, mode="sdfoam"):
+def half_scene(index, mode="sdfoam", **kw):
     import dataclasses
 
-    w = scene(index, mode=mode)
+    w = scene(index, mode=mode, **kw)
     return dataclasses.replace(w, attributes=w.attributes.astype(np.float16).astype(np.float32))
 
 
@@ -62,17 +62,19 @@ def _inputs(w, dev):
     return g
 
 
-@pytest.mark.parametrize("cfg,mode,accum", [(1, "sdfoam", True), (1, "standard", True),
-                                            (2, "sdfoam", True), (1, "sdfoam", False),
-                                            (2, "sdfoam", False)])
-def test_fp16_forward_backward(dev, oracle_lib, cfg, mode, accum):
+@pytest.mark.parametrize("cfg,mode,accum,degree", [
+    (1, "sdfoam", True, None), (1, "standard", True, None), (2, "sdfoam", True, None),
+    (1, "sdfoam", False, None), (2, "sdfoam", False, None), (1, "sdfoam", True, 2),
+    (1, "sdfoam", False, 1)])
+def test_fp16_forward_backward(dev, oracle_lib, cfg, mode, accum, degree):
     """accum: the backward's fp32 cell rows rounded once into the fp16
-    outputs; without: packed fp16 atomics per group into the outputs."""
+    outputs; without: packed fp16 atomics per group into the outputs (odd
+    and even attribute counts: degrees 0-3 have 4, 13, 28, 49)."""
     import torch
 
     import sdfoam_amd
 
-    w = half_scene(cfg, mode)
+    w = half_scene(cfg, mode) if degree is None else half_scene(cfg, mode, sh_degree=degree)
     g = _inputs(w, dev)
     pipe = sdfoam_amd.create_pipeline(w.sh_degree, "float16")
     q = to_dev(w.quantiles, dev)

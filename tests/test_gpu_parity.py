@@ -315,6 +315,20 @@ def test_backward_parity_c2(torch_dev, oracle_lib):
     _check_backward(bwd, st, ref, w)
 
 
+@pytest.mark.parametrize("degree", [1, 2])
+@pytest.mark.parametrize("mode", ["sdfoam", "standard"])
+def test_sh_degrees_1_2(torch_dev, oracle_lib, mode, degree):
+    """SH degrees 1 and 2 (the accumulator's 32-float rows; owner lanes of
+    13 and 28 attribute components): forward and backward with the walk
+    record against the oracle."""
+    w = scene(1, mode=mode, sh_degree=degree)
+    assert w.sh_degree == degree
+    out, st, ref = _forward_both(w, torch_dev, oracle_lib, mode)
+    _check_forward(out, st, ref, w, 0)
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, mode, ray_error=True, walk=True)
+    _check_backward(bwd, st, ref, w)
+
+
 @pytest.mark.parametrize("mode", ["sdfoam", "standard"])
 def test_backward_direct_updates_c1(torch_dev, oracle_lib, mode):
     """The backward without the gradient accumulator: atomics straight into
