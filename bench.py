@@ -42,6 +42,7 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "Mrays/s fwd+bwd at 1M pts/1600x1200 rays; % HBM roofline"
+RENDER_METRIC = "Mpixels/s inference render (trace_benchmark, RGBA8)"
 
 
 def log(msg: str) -> None:
@@ -86,6 +87,9 @@ def main() -> int:
     ap.add_argument("--attr-dtype", default="float32", choices=["float32", "float16"],
                     help="attribute storage of the pipeline (fp16: create_pipeline(L, "
                          "'float16'); arithmetic stays fp32)")
+    ap.add_argument("--render", action="store_true",
+                    help="time the inference render (Pipeline.trace_benchmark, the reference's "
+                         "benchmark.py) on the config's camera instead of the training step")
     ap.add_argument("--walk-record", type=int, default=1, choices=[0, 1],
                     help="1: the forward records each ray's steps and the backward replays "
                          "them (TraceRays does this); 0: the backward scans the faces again")
@@ -152,6 +156,8 @@ def main() -> int:
     pipe = sdfoam_amd.create_pipeline(w.sh_degree, args.attr_dtype)
     D = pipe.attribute_dim()
     Q = int(w.quantiles.shape[-1])
+    if args.render:
+        return render_bench(args, w, pts, attrs, adj, offs, inv, pipe, D)
 
     # ray batches: one fixed batch (C1-C4), or C5's ten seeded batches
     batches = []
@@ -336,6 +342,118 @@ def main() -> int:
 
 
 CPU_SAMPLE_RAYS = 640_000
+RENDER_WEIGHT_THRESHOLD = 0.05  # the reference's benchmark.py
+
+
+def render_bench(args, w, pts, attrs, adj, offs, inv, pipe, D) -> int:
+    """Frames of Pipeline.trace_benchmark on the configuration's camera: the
+    reference's inference benchmark (benchmark.py:41-147) on a synthetic
+    scene.  Timed: the render kernel alone (the offset table and the start
+    cell are built once, as benchmark.py builds them once)."""
+    import numpy as np
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import _lib, scenes
+
+    if args.config not in (1, 2, 3):
+        print("--render needs a single-camera config (1-3)", file=sys.stderr)
+        return 2
+    dev = pts.device
+    cam = scenes.camera_dict(w.extra["camera"], "pinhole")
+    H, W = int(cam["height"]), int(cam["width"])
+    cam_t = dict(cam)
+    for k in ("position", "forward", "right", "up"):
+        cam_t[k] = torch.tensor(np.asarray(cam[k], dtype=np.float32))
+    diff = sdfoam_amd.prefetch_adjacent_diff(pts, adj, offs)
+    ray0 = np.concatenate([cam["position"], cam["forward"]]).reshape(1, 6).astype(np.float32)
+    start_np = scenes.start_points_for(w.points, ray0).astype(np.uint32)
+    start = torch.from_numpy(start_np.view(np.int32)).to(dev).view(torch.uint32)
+    out = torch.zeros((H, W), dtype=torch.uint32, device=dev)
+
+    def frame():
+        pipe.trace_benchmark(pts, attrs, adj, offs, diff, cam_t, start, out,
+                             weight_threshold=RENDER_WEIGHT_THRESHOLD,
+                             alpha_mode=args.alpha_mode, inv_s=inv)
+
+    for _ in range(args.warmup):
+        frame()
+    torch.cuda.synchronize()
+    _lib.set_timing(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        frame()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    launches = _lib.collect_timings()
+    _lib.set_timing(False)
+    ms_frame = (t1 - t0) * 1e3 / args.steps
+    render_ms = float(np.mean([ms for name, ms in launches if name == "render"]))
+    # byte model of the render: per pixel the RGBA8 store; per step the CSR
+    # bounds, the face rows, the next index and position, the attribute row
+    rays = torch.from_numpy(w.rays).to(dev)
+    st = pipe.walk_stats(pts, attrs, adj, offs, rays,
+                         torch.from_numpy(scenes.start_points_for(w.points, w.rays)
+                                          .astype(np.uint32).view(np.int32)).to(dev)
+                         .view(torch.uint32),
+                         alpha_mode=args.alpha_mode, inv_s=inv,
+                         weight_threshold=RENDER_WEIGHT_THRESHOLD)
+    torch.cuda.synchronize()
+    S = int(st["steps"].sum().item())
+    F_st = int(st["faces_stepped"].sum().item())
+    ab = 2 if args.attr_dtype == "float16" else 4
+    R = H * W
+    bytes_frame = R * 4 + S * (8 + 4 + 12 + ab * D) + 8 * F_st
+    achieved = bytes_frame / (render_ms * 1e-3) / 1e9
+    result = {
+        "metric": RENDER_METRIC,
+        "value": R / (ms_frame * 1e-3) / 1e6,
+        "unit": "Mpixels/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_frame,
+        "fps": 1e3 / ms_frame,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"C{args.config} camera {W}x{H}, {w.num_points} points, SH degree "
+                        f"{w.sh_degree}, {args.alpha_mode} alpha, {args.attr_dtype} attributes, "
+                        f"weight threshold {RENDER_WEIGHT_THRESHOLD}, inv_s={w.inv_s:.4f}",
+            "points": w.num_points,
+            "pixels": R,
+        },
+        "kernel_ms": {"render": render_ms},
+        "cell_steps_per_pixel": S / R,
+        "roofline": {"kernel": "render", "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None},
+    }
+    if args.cpu_stride != 0:
+        from oracle import oracle
+
+        # the same frame on the host (C3: about 7 s on 16 threads)
+        oracle.build()
+        small = cam
+        diff_np = diff.view(torch.int16).cpu().numpy().view(np.uint16)[: w.adjacency.size]
+        threads = cpu_threads()
+        t = time.perf_counter()
+        oracle.trace_benchmark(w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets,
+                               diff_np, small, int(start_np[0]), alpha_mode=args.alpha_mode,
+                               inv_s=w.inv_s, weight_threshold=RENDER_WEIGHT_THRESHOLD,
+                               threads=threads)
+        dt = time.perf_counter() - t
+        result["cpu_baseline"] = {
+            "value": W * H / dt / 1e6, "unit": "Mpixels/s", "cores": threads, "kind": "port",
+            "sample": f"one {W}x{H} frame of the same camera, {dt:.1f}s on {threads} threads "
+                      f"of {cpu_model()}"}
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
 
 
 def cpu_baseline(w, rays, start, quantiles, grad_rgba, depth_grad, stride: int,
