@@ -43,6 +43,8 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 METRIC = "Mrays/s fwd+bwd at 1M pts/1600x1200 rays; % HBM roofline"
 RENDER_METRIC = "Mpixels/s inference render (trace_benchmark, RGBA8)"
+FETCH_METRIC = "GB/s of training batches delivered by BatchFetcher (rays + rgb)"
+HOST_LINK_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
 
 
 def log(msg: str) -> None:
@@ -87,6 +89,9 @@ def main() -> int:
     ap.add_argument("--attr-dtype", default="float32", choices=["float32", "float16"],
                     help="attribute storage of the pipeline (fp16: create_pipeline(L, "
                          "'float16'); arithmetic stays fp32)")
+    ap.add_argument("--fetch", action="store_true",
+                    help="time BatchFetcher feeding training batches (2^20 shuffled rows of "
+                         "rays [M, 6] and colours [M, 3], M = 64 cameras x 960 x 640)")
     ap.add_argument("--render", action="store_true",
                     help="time the inference render (Pipeline.trace_benchmark, the reference's "
                          "benchmark.py) on the config's camera instead of the training step")
@@ -126,6 +131,9 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"calibration_copy_bytes": 4 * n, "launches": 3}), flush=True)
         return 0
+
+    if args.fetch:
+        return fetch_bench(args, dev)
 
     t0 = time.time()
     if args.scene_cache and os.path.exists(args.scene_cache):
@@ -342,6 +350,77 @@ def main() -> int:
 
 
 CPU_SAMPLE_RAYS = 640_000
+
+
+def fetch_bench(args, dev) -> int:
+    """Two BatchFetchers over parallel host arrays, as the reference's data
+    loader drives them (data_loader/__init__.py:126-141, train.py:130-131):
+    rays [M, 6] and colours [M, 3] float32, M = 64 x 960 x 640, batches of
+    2^20 shuffled rows.  Timed: `steps` pairs of next() with the copies done
+    on the GPU.  The naive path (numpy gather of the same rows, then a
+    pageable copy to the device) is timed beside it."""
+    import numpy as np
+    import torch
+
+    import sdfoam_amd
+
+    M = 64 * 960 * 640
+    B = 1 << 20
+    rng = np.random.default_rng(0)
+    rays = torch.from_numpy(rng.standard_normal((M, 6), dtype=np.float32))
+    rgb = torch.from_numpy(rng.random((M, 3), dtype=np.float32))
+    log(f"host arrays ready: {M} rows ({(rays.nbytes + rgb.nbytes) / 1e9:.2f} GB)")
+    fr = sdfoam_amd.BatchFetcher(rays, B, True)
+    fc = sdfoam_amd.BatchFetcher(rgb, B, True)
+    for _ in range(args.warmup):
+        fr.next()
+        fc.next()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        a = fr.next()
+        b = fc.next()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    del a, b
+    fr.close()
+    fc.close()
+    batch_bytes = B * (24 + 12)
+    # naive host path for the same batch shape
+    t0 = time.perf_counter()
+    n_naive = 3
+    for _ in range(n_naive):
+        idx = rng.integers(0, M, size=B)
+        ra = torch.from_numpy(rays.numpy()[idx]).to(dev)
+        ca = torch.from_numpy(rgb.numpy()[idx]).to(dev)
+    torch.cuda.synchronize()
+    dt_naive = (time.perf_counter() - t0) / n_naive
+    del ra, ca
+    achieved = batch_bytes / dt / 1e9
+    result = {
+        "metric": FETCH_METRIC,
+        "value": achieved,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dt * 1e3,
+        "batches_per_s": 1.0 / dt,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"BatchFetcher x2 (rays [M,6], rgb [M,3] float32), M={M}, "
+                               f"batch {B} shuffled rows", "rows": M, "batch": B},
+        "roofline": {"kernel": "host-to-device batches", "bound": "host link",
+                     "achieved": achieved, "peak": HOST_LINK_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HOST_LINK_PEAK_GBS, "traffic": None},
+        "naive_host_ms_per_step": dt_naive * 1e3,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
 RENDER_WEIGHT_THRESHOLD = 0.05  # the reference's benchmark.py
 
 
