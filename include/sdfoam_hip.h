@@ -335,8 +335,9 @@ size_t sdf_delaunay_tables_scratch_bytes(uint32_t num_points, uint32_t num_tets)
 /* Tables of a Delaunay tetrahedralisation given as tets [T,4] (vertex ids,
  * either orientation, any order) and neighbors [T,4] (the tet across the
  * face opposite vertex j, or -1 on the hull), as Qhull returns them:
- * tets_out [T,4] positively oriented (det[b-a, c-a, d-a] > 0 in double),
- * ordered by their sorted vertex sets; tet_adjacency [T,4] = 4 k + m for
+ * tets_out [T,4] with vertices ascending except the last two, swapped
+ * where that makes the tet positively oriented (det[b-a, c-a, d-a] > 0 in
+ * double), ordered by their sorted vertex sets; tet_adjacency [T,4] = 4 k + m for
  * neighbour k and its face m, UINT32_MAX on the hull; vert_to_tet [N] the
  * lowest tet holding each point (UINT32_MAX if none);
  * point_adjacency_offsets [N+1] and point_adjacency (the Delaunay edges, CSR
@@ -353,6 +354,46 @@ int sdf_delaunay_tables(const float *points, uint32_t num_points,
                         uint32_t *point_adjacency,
                         uint64_t point_adjacency_capacity, void *scratch,
                         size_t scratch_bytes, void *stream);
+
+/* The Delaunay tetrahedralisation on the GPU, in two calls around a host
+ * triangulation of the few points the GPU leaves open.  Together they
+ * replace the tetrahedra of Triangulation::rebuild
+ * (src/delaunay/delaunay.cu:271-345: sample_initial_tets, growth_iteration,
+ * delete_delaunay_violations).
+ *
+ * sdf_delaunay_certify: a Voronoi cell per point, clipped by its
+ * neighbours on a uniform grid; a cell closed by bisectors with every sign
+ * decided certifies its tetrahedra, written to reports [capacity, 4] as
+ * (point, a, b, c).  The other points go to open_points [N].  counts[5]
+ * (host): report rows asked for (more than report_capacity: nothing is
+ * lost but the rows past it; call again with room for counts[0]), open
+ * points, undecided cells, cells over the fixed capacity, coincident
+ * points seen (nonzero: duplicate points).  scratch 256-byte aligned, kept
+ * for sdf_delaunay_merge.  Synchronizes the stream. */
+size_t sdf_delaunay_certify_scratch_bytes(uint32_t num_points);
+int sdf_delaunay_certify(const float *points, uint32_t num_points,
+                         uint32_t *reports, uint64_t report_capacity,
+                         uint32_t *open_points, uint64_t *counts, void *scratch,
+                         size_t scratch_bytes, void *stream);
+
+/* sdf_delaunay_merge: candidates [M, 4] (the Delaunay tetrahedra of the open
+ * points, as global point ids) are kept where their circumsphere holds no
+ * point; each certified tetrahedron is kept once.  Writes tets [T, 4] (any
+ * orientation, any order) and neighbors [T, 4] (across the face opposite
+ * vertex j, -1 on the hull), the form sdf_delaunay_tables takes.  result[4]
+ * (host): T, hull faces, invalid or undecided rows, faces of three tets.
+ * certify_scratch: the scratch of the sdf_delaunay_certify call that made
+ * the reports.  Fails when a candidate's sign cannot be decided or
+ * T > tet_capacity (result[0] then holds T).  Synchronizes the stream. */
+size_t sdf_delaunay_merge_scratch_bytes(uint32_t num_points, uint64_t num_reports,
+                                        uint64_t num_candidates, uint64_t tet_capacity);
+int sdf_delaunay_merge(const float *points, uint32_t num_points,
+                       void *certify_scratch, size_t certify_scratch_bytes,
+                       const uint32_t *reports, uint64_t num_reports,
+                       const uint32_t *candidates, uint64_t num_candidates,
+                       uint32_t *tets, int32_t *neighbors, uint64_t tet_capacity,
+                       uint64_t *result, void *scratch, size_t scratch_bytes,
+                       void *stream);
 
 /* ---- measurement and test hooks (no counterpart in the reference) ----- */
 

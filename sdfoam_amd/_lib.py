@@ -45,6 +45,10 @@ EXPORTS = (
     "sdf_delaunay_adjacency_capacity",
     "sdf_delaunay_tables_scratch_bytes",
     "sdf_delaunay_tables",
+    "sdf_delaunay_certify_scratch_bytes",
+    "sdf_delaunay_certify",
+    "sdf_delaunay_merge_scratch_bytes",
+    "sdf_delaunay_merge",
     "sdf_nn",
     "sdf_trace_walk_stats",
     "sdf_debug_fpmath",
@@ -189,6 +193,15 @@ def lib() -> C.CDLL:
     L.sdf_delaunay_tables_scratch_bytes.argtypes = [U32, U32]
     L.sdf_delaunay_tables.restype = C.c_int
     L.sdf_delaunay_tables.argtypes = [P, U32, P, P, U32, P, P, P, P, P, C.c_uint64, P, SZ, P]
+    L.sdf_delaunay_certify_scratch_bytes.restype = SZ
+    L.sdf_delaunay_certify_scratch_bytes.argtypes = [U32]
+    L.sdf_delaunay_certify.restype = C.c_int
+    L.sdf_delaunay_certify.argtypes = [P, U32, P, C.c_uint64, P, P, P, SZ, P]
+    L.sdf_delaunay_merge_scratch_bytes.restype = SZ
+    L.sdf_delaunay_merge_scratch_bytes.argtypes = [U32, C.c_uint64, C.c_uint64, C.c_uint64]
+    L.sdf_delaunay_merge.restype = C.c_int
+    L.sdf_delaunay_merge.argtypes = [P, U32, P, SZ, P, C.c_uint64, P, C.c_uint64, P, P,
+                                     C.c_uint64, P, P, SZ, P]
     L.sdf_nn.restype = C.c_int
     L.sdf_nn.argtypes = [P, P, P, U32, U32, P, P]
     L.sdf_trace_walk_stats.restype = C.c_int

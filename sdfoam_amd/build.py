@@ -24,8 +24,7 @@ LIB_PATH = os.path.join(HERE, LIB_NAME)
 ARCH = os.environ.get("SDFOAM_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["trace_kernels.hip", "aabb_kernels.hip", "order_kernels.hip", "delaunay_tables.hip",
-           "batch_fetcher.hip",
-           "triangulation_kernels.hip", "capi.hip"]
+           "delaunay_gpu.hip", "batch_fetcher.hip", "triangulation_kernels.hip", "capi.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -593,6 +593,80 @@ int sdf_delaunay_tables(const float *points, uint32_t num_points, const uint32_t
     return SDF_OK;
 }
 
+size_t sdf_delaunay_certify_scratch_bytes(uint32_t num_points) {
+    return delaunay_certify_scratch_bytes(num_points);
+}
+
+int sdf_delaunay_certify(const float *points, uint32_t num_points, uint32_t *reports,
+                         uint64_t report_capacity, uint32_t *open_points, uint64_t *counts,
+                         void *scratch, size_t scratch_bytes, void *stream) {
+    if (!points || !open_points || !counts || !scratch || (report_capacity > 0 && !reports))
+        return fail(SDF_E_INVALID, "NULL pointer argument");
+    if ((reinterpret_cast<uintptr_t>(scratch) & 255u) != 0)
+        return fail(SDF_E_INVALID, "scratch must be 256-byte aligned");
+    if (num_points < 32)
+        return fail(SDF_E_INVALID, "Delaunay triangulation does not support less than 32 points");
+    const size_t need = delaunay_certify_scratch_bytes(num_points);
+    if (need == 0) return fail(SDF_E_HIP, "delaunay_certify: no device to size the sorts for");
+    if (scratch_bytes < need)
+        return fail(SDF_E_INVALID, "scratch must hold %zu bytes (got %zu)", need, scratch_bytes);
+    hipError_t e = launch_delaunay_certify(points, num_points, reports, report_capacity,
+                                           open_points, counts, scratch, scratch_bytes,
+                                           static_cast<hipStream_t>(stream));
+    if (e == hipErrorInvalidValue)
+        return fail(SDF_E_INVALID, "points must be finite and span a volume");
+    if (e != hipSuccess) return hip_fail(e, "delaunay_certify");
+    return SDF_OK;
+}
+
+size_t sdf_delaunay_merge_scratch_bytes(uint32_t num_points, uint64_t num_reports,
+                                        uint64_t num_candidates, uint64_t tet_capacity) {
+    return delaunay_merge_scratch_bytes(num_points, num_reports, num_candidates, tet_capacity);
+}
+
+int sdf_delaunay_merge(const float *points, uint32_t num_points, void *certify_scratch,
+                       size_t certify_scratch_bytes, const uint32_t *reports,
+                       uint64_t num_reports, const uint32_t *candidates, uint64_t num_candidates,
+                       uint32_t *tets, int32_t *neighbors, uint64_t tet_capacity,
+                       uint64_t *result, void *scratch, size_t scratch_bytes, void *stream) {
+    if (!points || !certify_scratch || !result || !scratch || (num_reports > 0 && !reports) ||
+        (num_candidates > 0 && !candidates) || (tet_capacity > 0 && (!tets || !neighbors)))
+        return fail(SDF_E_INVALID, "NULL pointer argument");
+    if ((reinterpret_cast<uintptr_t>(scratch) & 255u) != 0 ||
+        (reinterpret_cast<uintptr_t>(certify_scratch) & 255u) != 0)
+        return fail(SDF_E_INVALID, "scratch must be 256-byte aligned");
+    if (num_points < 32)
+        return fail(SDF_E_INVALID, "Delaunay triangulation does not support less than 32 points");
+    if (num_reports + num_candidates >= 0xffffffffull)
+        return fail(SDF_E_INVALID, "too many reports and candidates");
+    const size_t gneed = delaunay_certify_scratch_bytes(num_points);
+    const size_t need =
+        delaunay_merge_scratch_bytes(num_points, num_reports, num_candidates, tet_capacity);
+    if (gneed == 0 || need == 0)
+        return fail(SDF_E_HIP, "delaunay_merge: no device to size the scans for");
+    if (certify_scratch_bytes < gneed)
+        return fail(SDF_E_INVALID, "certify_scratch must hold %zu bytes (got %zu)", gneed,
+                    certify_scratch_bytes);
+    if (scratch_bytes < need)
+        return fail(SDF_E_INVALID, "scratch must hold %zu bytes (got %zu)", need, scratch_bytes);
+    hipError_t e = launch_delaunay_merge(points, num_points, certify_scratch,
+                                         certify_scratch_bytes, reports, num_reports, candidates,
+                                         num_candidates, tets, neighbors, tet_capacity, result,
+                                         scratch, scratch_bytes,
+                                         static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "delaunay_merge");
+    if (result[2] != 0)
+        return fail(SDF_E_INVALID, "%llu reports or candidates were invalid or undecided",
+                    (unsigned long long)result[2]);
+    if (result[0] > tet_capacity)
+        return fail(SDF_E_INVALID, "tets must hold %llu rows (got %llu)",
+                    (unsigned long long)result[0], (unsigned long long)tet_capacity);
+    if (result[3] != 0)
+        return fail(SDF_E_INVALID, "%llu faces are shared by more than two tets",
+                    (unsigned long long)result[3]);
+    return SDF_OK;
+}
+
 int sdf_nn(const float *points, const float *aabb_tree, const float *queries, uint32_t num_points,
            uint32_t num_queries, uint32_t *indices, void *stream) {
     if (num_points < 32) return fail(SDF_E_INVALID, "number of points must be at least 32");

@@ -1,0 +1,310 @@
+// The point grids of the GPU Delaunay and the two per-item steps that use
+// them (host and device): one point's certified Voronoi cell, and one
+// candidate tetrahedron's empty-circumsphere test.
+#pragma once
+
+#include <cmath>
+#include <cstdint>
+
+#include "voronoi_cell.h"
+
+namespace sdfoam_hip {
+namespace dgrid {
+
+// A hierarchy of uniform grids over the points: level 0 has about
+// kFineCellsPerPoint cells per point over the bounding box, each level above
+// is kLevelRatio times coarser per axis.  A cell is clipped ring by ring on
+// the finest level first and moves up a level when the rings it would still
+// need exceed kMaxRing (a point in a sparse region), so that dense and
+// sparse regions both see few candidates per cell.
+constexpr int kLevels = 3;
+constexpr double kLevelRatio = 4.0;
+constexpr double kFineCellsPerPoint = 8.0;
+constexpr int kMaxRing = 6;  // rings per level
+constexpr int kMinRing = 2;  // rings on a level before moving up
+constexpr int kBoxRing = 2;  // from here, a cell still reaching the box on a
+                             // level above 0 is left open (hull points)
+// Candidate points a cell may examine in all before it is left open (bounds
+// the slowest lane).
+constexpr uint32_t kMaxCandidates = 16384;
+
+struct GridLevel {
+    double h, inv_h; // cell edge
+    uint32_t dims[3];
+    uint32_t num_cells;
+};
+
+struct GridGeom {
+    double lo[3];     // grid origin (the points' bounding box)
+    double slack;     // rounding allowance of a cell's bounds
+    double box_lo[3]; // clipping box: the bounding box grown by its extent
+    double box_hi[3];
+    GridLevel level[kLevels];
+};
+
+struct GridView {
+    GridGeom g;
+    // level l: the points of cell c are sorted[l][start[l][c] : start[l][c + 1]]
+    const uint32_t *start[kLevels];
+    const uint32_t *sorted[kLevels];
+};
+
+// Cells of level 0 at most (every level has at most as many).
+inline uint64_t level_cell_capacity(uint32_t n) {
+    return (uint64_t)(kFineCellsPerPoint * 1.1 * (double)n) + 64;
+}
+
+// The grids over the bounding box [lo, hi] of n points.  False if the box
+// is not finite or has no extent.
+inline bool grid_geometry(const double *lo, const double *hi, uint32_t n, GridGeom &g) {
+    double ext = 0.0, mag = 0.0;
+    for (int k = 0; k < 3; ++k) {
+        if (!std::isfinite(lo[k]) || !std::isfinite(hi[k]) || !(hi[k] >= lo[k])) return false;
+        ext = std::fmax(ext, hi[k] - lo[k]);
+        mag = std::fmax(mag, std::fmax(std::fabs(lo[k]), std::fabs(hi[k])));
+    }
+    if (!(ext > 0.0)) return false;
+    double vol = 1.0;
+    int axes = 0;
+    for (int k = 0; k < 3; ++k)
+        if (hi[k] - lo[k] > 1e-6 * ext) {
+            vol *= hi[k] - lo[k];
+            ++axes;
+        }
+    double h = std::pow(vol / std::fmax(1.0, kFineCellsPerPoint * (double)n),
+                        1.0 / (double)(axes > 0 ? axes : 1));
+    h = std::fmax(h, ext * 1e-6);
+    const uint64_t cap = level_cell_capacity(n);
+    for (int l = 0; l < kLevels; ++l) {
+        GridLevel &lv = g.level[l];
+        for (;;) {
+            uint64_t cells = 1;
+            for (int k = 0; k < 3; ++k) {
+                const double d = std::ceil((hi[k] - lo[k]) / h);
+                lv.dims[k] = (uint32_t)std::fmax(1.0, std::fmin(d, 2097152.0));
+                cells *= lv.dims[k];
+            }
+            if (cells <= cap) {
+                lv.num_cells = (uint32_t)cells;
+                break;
+            }
+            h *= 1.05;
+        }
+        lv.h = h;
+        lv.inv_h = 1.0 / h;
+        h *= kLevelRatio;
+    }
+    g.slack = 1e-12 * (mag + ext);
+    for (int k = 0; k < 3; ++k) {
+        g.lo[k] = lo[k];
+        g.box_lo[k] = lo[k] - ext;
+        g.box_hi[k] = hi[k] + ext;
+    }
+    return true;
+}
+
+SDF_HD int axis_cell(double x, double lo, double inv_h, uint32_t dim) {
+    const double c = (x - lo) * inv_h;
+    if (!(c > 0.0)) return 0;
+    const uint32_t u = c < 4294967295.0 ? (uint32_t)c : 0xffffffffu;
+    return (int)(u < dim ? u : dim - 1);
+}
+
+SDF_HD uint32_t cell_index(const GridGeom &g, int l, double x, double y, double z) {
+    const GridLevel &lv = g.level[l];
+    const uint32_t cx = (uint32_t)axis_cell(x, g.lo[0], lv.inv_h, lv.dims[0]);
+    const uint32_t cy = (uint32_t)axis_cell(y, g.lo[1], lv.inv_h, lv.dims[1]);
+    const uint32_t cz = (uint32_t)axis_cell(z, g.lo[2], lv.inv_h, lv.dims[2]);
+    return (cz * lv.dims[1] + cy) * lv.dims[0] + cx;
+}
+
+SDF_HD bool touches_box(const vcell::Cell &cell) {
+    for (int i = 0; i < cell.num_verts; ++i)
+        for (int k = 0; k < 3; ++k)
+            if (cell.planes[cell.verts[i].p[k]].point < 0) return true;
+    return false;
+}
+
+// Was point x (absolute) in the part of a finer level already searched?
+SDF_HD bool searched(const GridGeom &g, int l, const double *x, const int (*hc)[3],
+                     const int *rings) {
+    for (int m = 0; m < l; ++m) {
+        if (rings[m] < 0) continue;
+        const GridLevel &lv = g.level[m];
+        bool in = true;
+        for (int k = 0; k < 3 && in; ++k) {
+            const int c = axis_cell(x[k], g.lo[k], lv.inv_h, lv.dims[k]);
+            in = c - hc[m][k] <= rings[m] && hc[m][k] - c <= rings[m];
+        }
+        if (in) return true;
+    }
+    return false;
+}
+
+// The Voronoi cell of point i, clipped by the grid rings around it, nearest
+// ring first, finest level first, until every point that could still cut
+// it has been seen (certified), it is left open, or a sign is undecided.
+// `coincident` is set when another point has the same coordinates (the cell
+// is then undecided).
+SDF_HD uint32_t certify_cell(const float *p, uint32_t i, const GridView &gv, vcell::Cell &cell,
+                             bool &coincident) {
+    const GridGeom &g = gv.g;
+    coincident = false;
+    const double o[3] = {(double)p[3ull * i], (double)p[3ull * i + 1], (double)p[3ull * i + 2]};
+    {
+        double rlo[3], rhi[3];
+        for (int k = 0; k < 3; ++k) {
+            rlo[k] = g.box_lo[k] - o[k];
+            rhi[k] = g.box_hi[k] - o[k];
+        }
+        vcell::cell_init(cell, rlo, rhi);
+    }
+    double mr2 = vcell::max_r2(cell);
+    int hc[kLevels][3];
+    int rings[kLevels];
+    for (int l = 0; l < kLevels; ++l) {
+        rings[l] = -1;
+        for (int k = 0; k < 3; ++k)
+            hc[l][k] = axis_cell(o[k], g.lo[k], g.level[l].inv_h, g.level[l].dims[k]);
+    }
+    uint32_t examined = 0;
+    for (int l = 0; l < kLevels; ++l) {
+        const GridLevel &lv = g.level[l];
+        const uint32_t *start = gv.start[l];
+        const uint32_t *sorted = gv.sorted[l];
+        const int *h = hc[l];
+        for (int r = 0; r <= kMaxRing; ++r) {
+            for (int dz = -r; dz <= r; ++dz) {
+                const int cz = h[2] + dz;
+                if (cz < 0 || cz >= (int)lv.dims[2]) continue;
+                for (int dy = -r; dy <= r; ++dy) {
+                    const int cy = h[1] + dy;
+                    if (cy < 0 || cy >= (int)lv.dims[1]) continue;
+                    // inside the shell only the two end cells of a row are new
+                    const bool full_row = r == 0 || dz == -r || dz == r || dy == -r || dy == r;
+                    const int step = full_row ? 1 : 2 * r;
+                    for (int dx = -r; dx <= r; dx += step) {
+                        const int cx = h[0] + dx;
+                        if (cx < 0 || cx >= (int)lv.dims[0]) continue;
+                        const uint32_t c = ((uint32_t)cz * lv.dims[1] + (uint32_t)cy) * lv.dims[0] +
+                                           (uint32_t)cx;
+                        const uint32_t begin = start[c], end = start[c + 1];
+                        examined += end - begin;
+                        if (examined > kMaxCandidates) return vcell::kOpen;
+                        for (uint32_t k = begin; k < end; ++k) {
+                            const uint32_t j = sorted[k];
+                            if (j == i) continue;
+                            const double x[3] = {(double)p[3ull * j], (double)p[3ull * j + 1],
+                                                 (double)p[3ull * j + 2]};
+                            const double q[3] = {x[0] - o[0], x[1] - o[1], x[2] - o[2]};
+                            const double d2 = q[0] * q[0] + q[1] * q[1] + q[2] * q[2];
+                            if (d2 == 0.0) {
+                                coincident = true;
+                                cell.status = vcell::kUncertain;
+                                return cell.status;
+                            }
+                            if (d2 > 4.0 * mr2 * (1.0 + 1e-9)) continue; // cannot cut
+                            if (l > 0 && searched(g, l, x, hc, rings)) continue;
+                            if (!vcell::clip(cell, q, (int32_t)j)) return cell.status;
+                            mr2 = vcell::max_r2(cell);
+                        }
+                    }
+                }
+            }
+            rings[l] = r;
+            // every point not yet seen lies r cells of this level away or
+            // more (or nowhere)
+            const bool all = h[0] - r <= 0 && h[0] + r >= (int)lv.dims[0] - 1 && h[1] - r <= 0 &&
+                             h[1] + r >= (int)lv.dims[1] - 1 && h[2] - r <= 0 &&
+                             h[2] + r >= (int)lv.dims[2] - 1;
+            const double reach = (double)r * lv.h - g.slack;
+            const double reach2 = all ? INFINITY : (reach > 0.0 ? reach * reach : 0.0);
+            if (4.0 * mr2 * (1.0 + 1e-9) < reach2) return vcell::settle(cell, reach2);
+            if (r >= kBoxRing && touches_box(cell)) {
+                if (l == 0) break;
+                return vcell::kOpen;
+            }
+            // rings this level would still need if the cell shrank no more
+            if (r >= kMinRing && 4.0 * mr2 * (1.0 + 1e-9) > (kMaxRing * lv.h) * (kMaxRing * lv.h))
+                break;
+        }
+    }
+    return vcell::kOpen;
+}
+
+// Candidate tetrahedron v[4] (ids below n): 1 if no point lies strictly
+// inside its circumsphere, 0 if one does, 2 if it is flat or a sign could
+// not be decided.  A point exactly on the sphere (cospherical with the
+// candidate) is passed over when it is open (status not certified): the
+// candidates' own triangulation of the open points already chose among
+// such points; a certified one is undecided.
+SDF_HD uint32_t sphere_empty(const float *p, const uint32_t *v, const GridView &gv,
+                             const uint32_t *status) {
+    const GridGeom &g = gv.g;
+    const double o[3] = {(double)p[3ull * v[0]], (double)p[3ull * v[0] + 1],
+                         (double)p[3ull * v[0] + 2]};
+    vcell::Plane pl[3];
+    for (int s = 0; s < 3; ++s) {
+        for (int k = 0; k < 3; ++k) pl[s].n[k] = (double)p[3ull * v[s + 1] + k] - o[k];
+        pl[s].c = 0.5 * (pl[s].n[0] * pl[s].n[0] + pl[s].n[1] * pl[s].n[1] +
+                         pl[s].n[2] * pl[s].n[2]);
+        pl[s].point = (int32_t)v[s + 1];
+    }
+    // the circumcentre (relative to o) is where the three bisectors meet;
+    // its error grows with the conditioning of that system
+    double ctr[3];
+    if (!vcell::meet(pl[0], pl[1], pl[2], ctr)) return 2u;
+    double perm;
+    const double d = vcell::det3(pl[0].n, pl[1].n, pl[2].n, perm);
+    const double cond = perm / vcell::dabs(d);
+    const double r2 = ctr[0] * ctr[0] + ctr[1] * ctr[1] + ctr[2] * ctr[2];
+    const double r = sqrt(r2) * (1.0 + 1e-6 + 1e-13 * cond) + g.slack;
+    // the finest level that covers the sphere's box with few cells
+    int l = 0, lo_c[3], hi_c[3];
+    for (;; ++l) {
+        const GridLevel &lv = g.level[l];
+        double cells = 1.0;
+        for (int k = 0; k < 3; ++k) {
+            lo_c[k] = axis_cell(o[k] + ctr[k] - r, g.lo[k], lv.inv_h, lv.dims[k]);
+            hi_c[k] = axis_cell(o[k] + ctr[k] + r, g.lo[k], lv.inv_h, lv.dims[k]);
+            cells *= (double)(hi_c[k] - lo_c[k] + 1);
+        }
+        if (cells <= 4096.0 || l == kLevels - 1) break;
+    }
+    const GridLevel &lv = g.level[l];
+    const uint32_t *start = gv.start[l];
+    const uint32_t *sorted = gv.sorted[l];
+    for (int cz = lo_c[2]; cz <= hi_c[2]; ++cz)
+        for (int cy = lo_c[1]; cy <= hi_c[1]; ++cy)
+            for (int cx = lo_c[0]; cx <= hi_c[0]; ++cx) {
+                // skip grid cells the sphere does not reach
+                const int cc[3] = {cx, cy, cz};
+                double dd = 0.0;
+                for (int k = 0; k < 3; ++k) {
+                    const double blo = g.lo[k] + (double)cc[k] * lv.h - o[k] - g.slack;
+                    const double bhi = blo + lv.h + 2.0 * g.slack;
+                    const double e =
+                        ctr[k] < blo ? blo - ctr[k] : (ctr[k] > bhi ? ctr[k] - bhi : 0.0);
+                    dd += e * e;
+                }
+                if (dd > r * r) continue;
+                const uint32_t c =
+                    ((uint32_t)cz * lv.dims[1] + (uint32_t)cy) * lv.dims[0] + (uint32_t)cx;
+                const uint32_t end = start[c + 1];
+                for (uint32_t k = start[c]; k < end; ++k) {
+                    const uint32_t j = sorted[k];
+                    if (j == v[0] || j == v[1] || j == v[2] || j == v[3]) continue;
+                    double q[3];
+                    for (int m = 0; m < 3; ++m) q[m] = (double)p[3ull * j + m] - o[m];
+                    const double e0 = q[0] - ctr[0], e1 = q[1] - ctr[1], e2 = q[2] - ctr[2];
+                    if (e0 * e0 + e1 * e1 + e2 * e2 > r * r) continue; // clearly outside
+                    const int s = vcell::in_sphere(pl[0].n, pl[1].n, pl[2].n, q);
+                    if (s > 0) return 0u;
+                    if (s == 0 && status[j] == vcell::kCertified) return 2u;
+                }
+            }
+    return 1u;
+}
+
+} // namespace dgrid
+} // namespace sdfoam_hip

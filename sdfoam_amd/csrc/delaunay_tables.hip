@@ -94,8 +94,9 @@ __device__ __forceinline__ double orient_vol(const float *__restrict__ p, const 
     return (x0 * w0 + x1 * w1) + x2 * w2;
 }
 
-// Orients tet t (swapping its last two vertices and neighbours when the
-// volume is negative) and forms its sort keys from the sorted vertex set.
+// Puts tet t in its canonical vertex order (ascending, the last two
+// swapped when the volume is negative; neighbours follow their vertices)
+// and forms its sort keys from the sorted vertex set.
 __global__ __launch_bounds__(256) void orient_kernel(
     const float *__restrict__ points, uint32_t num_points, const uint32_t *__restrict__ tets_in,
     const int32_t *__restrict__ nbr_in, uint32_t num_tets, uint32_t *__restrict__ tets_o,
@@ -116,7 +117,21 @@ __global__ __launch_bounds__(256) void orient_kernel(
         atomicOr(error, 1u);
         s[0] = s[1] = s[2] = s[3] = 0u;
         nb[0] = nb[1] = nb[2] = nb[3] = -1;
-    } else if (orient_vol(points, s) < 0.0) {
+    }
+    // canonical vertex order: ascending (each neighbour stays opposite its
+    // vertex), then the last two swapped when the volume is negative
+#define SDF_CSWAP2(i, j)                                                                           \
+    if (s[j] < s[i]) {                                                                            \
+        const uint32_t ts = s[i];                                                                 \
+        s[i] = s[j];                                                                              \
+        s[j] = ts;                                                                                \
+        const int32_t tn = nb[i];                                                                 \
+        nb[i] = nb[j];                                                                            \
+        nb[j] = tn;                                                                               \
+    }
+    SDF_CSWAP2(0, 1) SDF_CSWAP2(2, 3) SDF_CSWAP2(0, 2) SDF_CSWAP2(1, 3) SDF_CSWAP2(1, 2)
+#undef SDF_CSWAP2
+    if (ok && orient_vol(points, s) < 0.0) {
         uint32_t ts = s[2];
         s[2] = s[3];
         s[3] = ts;

@@ -172,6 +172,23 @@ hipError_t launch_delaunay_tables(const float *points, uint32_t num_points,
                                   uint64_t adjacency_capacity, uint32_t &input_error,
                                   void *scratch, size_t scratch_bytes, hipStream_t stream);
 
+// delaunay_gpu.hip
+size_t delaunay_certify_scratch_bytes(uint32_t num_points);
+// counts: report rows asked for, open points, undecided cells, cells over
+// capacity, coincident point pairs.  Synchronizes `stream` twice.
+hipError_t launch_delaunay_certify(const float *points, uint32_t num_points, uint32_t *reports,
+                                   uint64_t report_capacity, uint32_t *open, uint64_t counts[5],
+                                   void *scratch, size_t scratch_bytes, hipStream_t stream);
+size_t delaunay_merge_scratch_bytes(uint32_t num_points, uint64_t num_reports,
+                                    uint64_t num_candidates, uint64_t tet_capacity);
+// result: tets, hull faces, invalid or undecided rows, faces of three tets.
+hipError_t launch_delaunay_merge(const float *points, uint32_t num_points, void *grid_scratch,
+                                 size_t grid_bytes, const uint32_t *reports, uint64_t num_reports,
+                                 const uint32_t *candidates, uint64_t num_candidates,
+                                 uint32_t *tets, int32_t *neighbors, uint64_t tet_capacity,
+                                 uint64_t result[4], void *scratch, size_t scratch_bytes,
+                                 hipStream_t stream);
+
 hipError_t launch_build_aabb_tree(const float *points, uint32_t num_points, float *tree,
                                   hipStream_t stream);
 hipError_t launch_nn(const float *points, const float *tree, const float *queries,

@@ -30,8 +30,8 @@
 namespace sdfoam_hip {
 namespace vcell {
 
-constexpr int kMaxPlanes = 96;  // 6 box faces + bisectors
-constexpr int kMaxVerts = 160;  // triangles (cell vertices)
+constexpr int kMaxPlanes = 64;  // 6 box faces + bisectors
+constexpr int kMaxVerts = 128; // triangles (cell vertices)
 constexpr int kMaxEdges = 96;   // directed edges of the removed region
 
 enum Status : uint32_t {
@@ -50,6 +50,7 @@ struct Plane {
 struct Vert {
     uint8_t p[3]; // plane indices, counter-clockwise seen from outside
     double x[3];  // position
+    double e;     // bound on the error of each coordinate of x
     double r2;    // |x|^2
 };
 
@@ -106,8 +107,12 @@ SDF_HD int in_sphere(const double *a, const double *b, const double *c, const do
     return (det4 < 0.0) == (o3 > 0.0) ? 1 : -1;
 }
 
-// Meeting point of three planes; false if they are (nearly) dependent.
-SDF_HD bool meet(const Plane &A, const Plane &B, const Plane &C, double *x) {
+// Meeting point of three planes (Cramer's rule); false if they are (nearly)
+// dependent.  err: a bound on the rounding error of each coordinate (a few
+// times the first-order bound 9 eps sum|c| |minor| / |det| + 7 eps |x|
+// perm(det) / |det| of the rounded expressions below).
+SDF_HD bool meet(const Plane &A, const Plane &B, const Plane &C, double *x,
+                 double *err = nullptr) {
     const double bc[3] = {B.n[1] * C.n[2] - B.n[2] * C.n[1], B.n[2] * C.n[0] - B.n[0] * C.n[2],
                           B.n[0] * C.n[1] - B.n[1] * C.n[0]};
     const double ca[3] = {C.n[1] * A.n[2] - C.n[2] * A.n[1], C.n[2] * A.n[0] - C.n[0] * A.n[2],
@@ -120,6 +125,27 @@ SDF_HD bool meet(const Plane &A, const Plane &B, const Plane &C, double *x) {
     const double nc = dabs(C.n[0]) + dabs(C.n[1]) + dabs(C.n[2]);
     if (!(dabs(d) > 1e-12 * na * nb * nc)) return false;
     for (int k = 0; k < 3; ++k) x[k] = (A.c * bc[k] + B.c * ca[k] + C.c * ab[k]) / d;
+    if (err) {
+        // permanents of the 2x2 minors
+        const double pbc[3] = {dabs(B.n[1] * C.n[2]) + dabs(B.n[2] * C.n[1]),
+                               dabs(B.n[2] * C.n[0]) + dabs(B.n[0] * C.n[2]),
+                               dabs(B.n[0] * C.n[1]) + dabs(B.n[1] * C.n[0])};
+        const double pca[3] = {dabs(C.n[1] * A.n[2]) + dabs(C.n[2] * A.n[1]),
+                               dabs(C.n[2] * A.n[0]) + dabs(C.n[0] * A.n[2]),
+                               dabs(C.n[0] * A.n[1]) + dabs(C.n[1] * A.n[0])};
+        const double pab[3] = {dabs(A.n[1] * B.n[2]) + dabs(A.n[2] * B.n[1]),
+                               dabs(A.n[2] * B.n[0]) + dabs(A.n[0] * B.n[2]),
+                               dabs(A.n[0] * B.n[1]) + dabs(A.n[1] * B.n[0])};
+        const double pd = dabs(A.n[0]) * pbc[0] + dabs(A.n[1]) * pbc[1] + dabs(A.n[2]) * pbc[2];
+        const double ad = dabs(d);
+        double e = 0.0;
+        for (int k = 0; k < 3; ++k) {
+            const double m = dabs(A.c) * pbc[k] + dabs(B.c) * pca[k] + dabs(C.c) * pab[k];
+            const double ek = 32.0 * kEps * (m + dabs(x[k]) * pd) / ad + 4.0 * kEps * dabs(x[k]);
+            e = ek > e ? ek : e;
+        }
+        *err = e;
+    }
     return true;
 }
 
@@ -172,6 +198,7 @@ SDF_HD void cell_init(Cell &cell, const double *lo, const double *hi) {
                 v.x[0] = sx ? lo[0] : hi[0];
                 v.x[1] = sy ? lo[1] : hi[1];
                 v.x[2] = sz ? lo[2] : hi[2];
+                v.e = 0.0;
                 v.r2 = v.x[0] * v.x[0] + v.x[1] * v.x[1] + v.x[2] * v.x[2];
             }
 }
@@ -182,11 +209,32 @@ SDF_HD double max_r2(const Cell &cell) {
     return m;
 }
 
+// Drops the planes no vertex uses any more (cut away by later planes) and
+// renumbers the vertices' plane indices; true if room was made.
+SDF_HD bool compact_planes(Cell &cell) {
+    bool used[kMaxPlanes];
+    uint8_t map[kMaxPlanes];
+    for (int i = 0; i < cell.num_planes; ++i) used[i] = false;
+    for (int i = 0; i < cell.num_verts; ++i)
+        for (int k = 0; k < 3; ++k) used[cell.verts[i].p[k]] = true;
+    int w = 0;
+    for (int i = 0; i < cell.num_planes; ++i) {
+        if (!used[i]) continue;
+        map[i] = (uint8_t)w;
+        if (w != i) cell.planes[w] = cell.planes[i];
+        ++w;
+    }
+    for (int i = 0; i < cell.num_verts; ++i)
+        for (int k = 0; k < 3; ++k) cell.verts[i].p[k] = map[cell.verts[i].p[k]];
+    cell.num_planes = w;
+    return w < kMaxPlanes;
+}
+
 // Clips the cell by the bisector of o and candidate `point` at relative
 // position q.  Returns false when the cell became uncertain or overflowed
 // (cell.status says which).
 SDF_HD bool clip(Cell &cell, const double *q, int32_t point) {
-    if (cell.num_planes >= kMaxPlanes) {
+    if (cell.num_planes >= kMaxPlanes && !compact_planes(cell)) {
         cell.status = kOverflow;
         return false;
     }
@@ -196,11 +244,24 @@ SDF_HD bool clip(Cell &cell, const double *q, int32_t point) {
     P.n[2] = q[2];
     P.c = 0.5 * (q[0] * q[0] + q[1] * q[1] + q[2] * q[2]);
     P.point = point;
-    // conflicts
+    // conflicts: the vertex position decides where it is clear of the
+    // plane by more than its error bound (and the dot product's rounding),
+    // the exact test elsewhere
     bool out[kMaxVerts];
     int n_out = 0;
+    const double qn = dabs(q[0]) + dabs(q[1]) + dabs(q[2]);
     for (int i = 0; i < cell.num_verts; ++i) {
-        const int s = outside(cell, cell.verts[i], P, q);
+        const Vert &v = cell.verts[i];
+        const double sd = v.x[0] * q[0] + v.x[1] * q[1] + v.x[2] * q[2] - P.c;
+        const double bound =
+            v.e * qn +
+            4.0 * kEps * (dabs(v.x[0] * q[0]) + dabs(v.x[1] * q[1]) + dabs(v.x[2] * q[2]) + P.c);
+        if (sd < -bound || sd > bound) {
+            out[i] = sd > 0.0;
+            n_out += out[i] ? 1 : 0;
+            continue;
+        }
+        const int s = outside(cell, v, P, q);
         if (s == 0) {
             cell.status = kUncertain;
             return false;
@@ -252,7 +313,7 @@ SDF_HD bool clip(Cell &cell, const double *q, int32_t point) {
         v.p[0] = ea[e];
         v.p[1] = eb[e];
         v.p[2] = np;
-        if (!meet(cell.planes[v.p[0]], cell.planes[v.p[1]], P, v.x)) {
+        if (!meet(cell.planes[v.p[0]], cell.planes[v.p[1]], P, v.x, &v.e)) {
             cell.status = kUncertain;
             return false;
         }

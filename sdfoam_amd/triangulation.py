@@ -10,18 +10,21 @@ again unless ``incremental`` and the point count is unchanged, and returns
 whether it sorted (the caller then permutes its arrays).  Outputs are CUDA
 uint32 tensors indexing the sorted points:
 
-* ``tets()`` [T, 4], ordered by their sorted vertex sets, each positively
-  oriented (det[b - a, c - a, d - a] > 0);
+* ``tets()`` [T, 4], ordered by their sorted vertex sets, each listing its
+  vertices ascending except that the last two are swapped where that makes
+  it positively oriented (det[b - a, c - a, d - a] > 0);
 * ``tet_adjacency()`` [T, 4]: across the face opposite vertex j, 4 k + m for
   neighbour tet k and its face m, or 0xffffffff on the hull;
 * ``vert_to_tet()`` [N]: the lowest tet index holding each point;
 * ``point_adjacency()`` / ``point_adjacency_offsets()``: the Delaunay edges
   as CSR with ascending rows (src/delaunay/delaunay.cu:146-226).
 
-The Delaunay tetrahedralisation itself is computed on the host with Qhull
-(scipy); the reference builds it on the GPU with exact predicates.  For points
-in general position the two are the same unique triangulation.  The point
-order (``sort_points``), the tables derived from Qhull's tetrahedra and
+The Delaunay tetrahedralisation is computed on the GPU by certified Voronoi
+cells (``gpu_tetrahedra``), with Qhull (scipy) on the host for the few points
+whose cells the GPU leaves open; the reference grows it on the GPU by
+insertion with exact predicates.  For points in general position both give
+the same unique triangulation.  ``method="qhull"`` runs Qhull on every point.
+The point order (``sort_points``), the tables derived from the tetrahedra and
 ``farthest_neighbor`` run in libsdfoam_hip.so; ``host_tables`` is the numpy
 statement of the same tables (the check of the device path).
 """
@@ -76,7 +79,11 @@ def host_tables(points: np.ndarray, simplices: np.ndarray, neighbors: np.ndarray
     n = p64.shape[0]
     s = np.asarray(simplices, dtype=np.int64).copy()
     nb = np.asarray(neighbors, dtype=np.int64).copy()
-    # positive orientation: swap the last two vertices (and their neighbours)
+    # canonical vertex order: ascending (neighbour j stays opposite vertex j),
+    # then positive orientation by swapping the last two
+    o = np.argsort(s, axis=1, kind="stable")
+    s = np.take_along_axis(s, o, axis=1)
+    nb = np.take_along_axis(nb, o, axis=1)
     a, b, c, d = (p64[s[:, k]] for k in range(4))
     x = np.cross(b - a, c - a)
     w = d - a
@@ -142,16 +149,93 @@ def sort_points(points: torch.Tensor) -> torch.Tensor:
     return perm.view(torch.uint32)
 
 
-def device_tables(points: torch.Tensor, simplices: np.ndarray, neighbors: np.ndarray) -> dict:
-    """sdf_delaunay_tables over Qhull's tetrahedra of `points` (CUDA
-    float32 [N, 3]): the tables as uint32 tensors on the points' device."""
+def _aligned(nbytes: int, device) -> tuple[torch.Tensor, int]:
+    buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+    return buf, (buf.data_ptr() + 255) & ~255
+
+
+class _Undecided(RuntimeError):
+    """The GPU tetrahedralisation met a sign it could not decide."""
+
+
+def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, dict]:
+    """Delaunay tetrahedra of CUDA float32 points [N, 3] by certified
+    Voronoi cells (sdf_delaunay_certify / sdf_delaunay_merge): the points
+    whose cells the GPU cannot certify (the hull and the layer under it) are
+    triangulated by Qhull on the host, and their tetrahedra kept where no
+    point lies in the circumsphere.  Returns (tets [T, 4] int32, neighbors
+    [T, 4] int32, -1 on the hull, stats) on the points' device."""
+    pts = points.contiguous()
+    dev = pts.device
+    n = pts.numel() // 3
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    gbytes = int(L.sdf_delaunay_certify_scratch_bytes(n))
+    if gbytes == 0:
+        raise RuntimeError("sdf_delaunay_certify_scratch_bytes failed")
+    gbuf, gptr = _aligned(gbytes, dev)
+    open_pts = torch.empty(n, dtype=torch.int32, device=dev)
+    counts = (C.c_uint64 * 5)()
+    cap = 28 * n + 4096
+    with torch.cuda.device(dev):
+        for _ in range(2):
+            reports = torch.empty((cap, 4), dtype=torch.int32, device=dev)
+            check(L.sdf_delaunay_certify(ptr(pts), n, ptr(reports), cap, ptr(open_pts), counts,
+                                         gptr, gbytes, stream))
+            if counts[0] <= cap:
+                break
+            cap = int(counts[0])
+        nr, nu = int(counts[0]), int(counts[1])
+        if counts[4]:
+            raise TriangulationFailedError("duplicate points found")
+        # the open points, in index order, through Qhull on the host
+        U = torch.sort(open_pts[:nu])[0]
+        u_np = U.cpu().numpy()
+        simplices, nbr_u = qhull_tetrahedra(pts[U.long()].cpu().numpy())
+        hull_faces = int((nbr_u < 0).sum())
+        cand = torch.from_numpy(np.ascontiguousarray(u_np[simplices], dtype=np.int32)).to(dev)
+        m = int(cand.shape[0])
+        result = (C.c_uint64 * 4)()
+        tcap = nr // 3 + m + 4096
+        for _ in range(2):
+            tets = torch.empty((tcap, 4), dtype=torch.int32, device=dev)
+            nbr = torch.empty((tcap, 4), dtype=torch.int32, device=dev)
+            mbytes = int(L.sdf_delaunay_merge_scratch_bytes(n, nr, m, tcap))
+            if mbytes == 0:
+                raise RuntimeError("sdf_delaunay_merge_scratch_bytes failed")
+            mbuf, mptr = _aligned(mbytes, dev)
+            rc = L.sdf_delaunay_merge(ptr(pts), n, gptr, gbytes, ptr(reports), nr, ptr(cand), m,
+                                      ptr(tets), ptr(nbr), tcap, result, mptr, mbytes, stream)
+            if rc != 0 and result[0] > tcap and result[2] == 0:
+                tcap = int(result[0])
+                continue
+            if rc != 0 and result[2] != 0:
+                raise _Undecided(L.sdf_last_error().decode())
+            check(rc)
+            break
+    T = int(result[0])
+    if int(result[1]) != hull_faces:
+        raise _Undecided(f"{int(result[1])} faces without a neighbour, the hull has {hull_faces}")
+    stats = {"open": nu, "reports": nr, "candidates": m, "tets": T,
+             "undecided_cells": int(counts[2]), "overflow_cells": int(counts[3])}
+    return tets[:T], nbr[:T], stats
+
+
+def device_tables(points: torch.Tensor, simplices, neighbors) -> dict:
+    """sdf_delaunay_tables over the tetrahedra of `points` (CUDA float32
+    [N, 3]) as Qhull gives them (numpy or device int32 [T, 4]): the tables
+    as uint32 tensors on the points' device."""
     pts = points.contiguous()
     dev = pts.device
     n = pts.numel() // 3
     T = int(simplices.shape[0])
     L = _lib.lib()
-    tets_in = torch.from_numpy(np.ascontiguousarray(simplices, dtype=np.int32)).to(dev)
-    nbr_in = torch.from_numpy(np.ascontiguousarray(neighbors, dtype=np.int32)).to(dev)
+    if isinstance(simplices, torch.Tensor):
+        tets_in = simplices.to(dev, torch.int32).contiguous()
+        nbr_in = neighbors.to(dev, torch.int32).contiguous()
+    else:
+        tets_in = torch.from_numpy(np.ascontiguousarray(simplices, dtype=np.int32)).to(dev)
+        nbr_in = torch.from_numpy(np.ascontiguousarray(neighbors, dtype=np.int32)).to(dev)
     tets = torch.empty((T, 4), dtype=torch.int32, device=dev)
     tet_adj = torch.empty((T, 4), dtype=torch.int32, device=dev)
     v2t = torch.empty(n, dtype=torch.int32, device=dev)
@@ -184,8 +268,18 @@ def _check_points(points: torch.Tensor) -> None:
 
 
 class Triangulation:
-    def __init__(self, points: torch.Tensor):
+    """method "gpu": certified Voronoi cells on the GPU with Qhull on the few
+    open points (falls back to "qhull" when a sign is undecided); method
+    "qhull": Qhull on every point.  Both give the same tetrahedralisation for
+    points in general position; ``last_method`` says which one ran."""
+
+    def __init__(self, points: torch.Tensor, method: str = "gpu"):
         _check_points(points)
+        if method not in ("gpu", "qhull"):
+            raise ValueError(f"unknown triangulation method {method!r}")
+        self.method = method
+        self.last_method = None
+        self.last_stats = None
         self._num_points = 0
         self._perm_t = None
         self.rebuild(points, incremental=False)
@@ -204,10 +298,20 @@ class Triangulation:
             pts_dev = pts_dev[self._perm_t.view(torch.int32).long()]
             self._num_points = n
             sorted_now = True
+        if self.method == "gpu":
+            try:
+                simplices, neighbors, self.last_stats = gpu_tetrahedra(pts_dev)
+                self.last_method = "gpu"
+                self._tables = device_tables(pts_dev, simplices, neighbors)
+                return sorted_now
+            except _Undecided:
+                pass
         pts = pts_dev.cpu().numpy()
         if np.unique(pts, axis=0).shape[0] != n:
             raise TriangulationFailedError("duplicate points found")
         simplices, neighbors = qhull_tetrahedra(pts)
+        self.last_method = "qhull"
+        self.last_stats = None
         self._tables = device_tables(pts_dev, simplices, neighbors)
         return sorted_now
 

@@ -146,6 +146,33 @@ def test_triangulation_table_argument_errors():
     assert b"NULL pointer" in L.sdf_last_error()
 
 
+def test_gpu_delaunay_argument_errors():
+    from sdfoam_amd import _lib
+
+    L = _lib.lib()
+    buf = (C.c_uint64 * 128)()
+    p = C.cast(buf, C.c_void_p)
+    base = C.cast(buf, C.c_void_p).value
+    aligned = (base + 255) & ~255
+    counts = (C.c_uint64 * 5)()
+    rc = L.sdf_delaunay_certify(p, 31, p, 10, p, counts, aligned, 1 << 20, None)
+    assert rc == 1 and b"less than 32 points" in L.sdf_last_error()
+    rc = L.sdf_delaunay_certify(p, 100, p, 10, None, counts, aligned, 1 << 20, None)
+    assert rc == 1 and b"NULL pointer" in L.sdf_last_error()
+    rc = L.sdf_delaunay_certify(p, 100, p, 10, p, counts, aligned + 8, 1 << 20, None)
+    assert rc == 1 and b"256-byte aligned" in L.sdf_last_error()
+    result = (C.c_uint64 * 4)()
+    rc = L.sdf_delaunay_merge(p, 100, aligned, 1 << 20, None, 5, p, 1, p, p, 10, result,
+                              aligned, 1 << 20, None)
+    assert rc == 1 and b"NULL pointer" in L.sdf_last_error()
+    rc = L.sdf_delaunay_merge(p, 100, aligned + 16, 1 << 20, p, 5, p, 1, p, p, 10, result,
+                              aligned, 1 << 20, None)
+    assert rc == 1 and b"256-byte aligned" in L.sdf_last_error()
+    rc = L.sdf_delaunay_merge(p, 100, aligned, 1 << 20, p, 1 << 31, p, 1 << 31, p, p, 10,
+                              result, aligned, 1 << 20, None)
+    assert rc == 1 and b"too many reports" in L.sdf_last_error()
+
+
 def test_ray_order_and_plan_errors():
     from sdfoam_amd import _lib
 

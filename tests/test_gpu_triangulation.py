@@ -59,6 +59,7 @@ def test_triangulation_as_scene_uses_it(dev):
     rng = np.random.default_rng(21)
     raw = torch.from_numpy(rng.normal(size=(3000, 3)).astype(np.float32) * 0.6).to(dev)
     tri = sdfoam_amd.Triangulation(raw)
+    assert tri.last_method == "gpu"
     perm = tri.permutation().to(torch.long)
     assert np.array_equal(perm.cpu().numpy(), scenes.sort_points_order(raw.cpu().numpy()))
     pts = raw[perm]
@@ -141,3 +142,110 @@ def test_device_tables_match_host(dev, cfg):
     # the scene's own CSR adjacency is the same edge graph
     assert np.array_equal(_np(got["point_adjacency"]), w.adjacency)
     assert np.array_equal(_np(got["point_adjacency_offsets"]), w.offsets)
+
+
+def _gpu_sets():
+    rng = np.random.default_rng(8)
+    n = 60_000
+    c = rng.normal(size=(16, 3)) * 3
+    sh = rng.normal(size=(n, 3))
+    sh /= np.linalg.norm(sh, axis=1, keepdims=True)
+    return {
+        "C1": lambda: scene(1).points,
+        "C2": lambda: scene(2).points,
+        "gaussian": lambda: rng.normal(size=(n, 3)).astype(np.float32),
+        "clustered": lambda: (c[rng.integers(0, 16, n)] + rng.normal(size=(n, 3)) * 0.05).astype(np.float32),
+        "shell": lambda: (sh * (1 + 0.01 * rng.random((n, 1)))).astype(np.float32),
+    }
+
+
+def _face_neighbors(tets):
+    """[T, 4]: the tet across the face opposite vertex j (-1 if none), by
+    matching sorted vertex triples."""
+    T = tets.shape[0]
+    faces = np.stack([np.delete(tets, j, axis=1) for j in range(4)], axis=1).reshape(-1, 3)
+    key = np.sort(faces.astype(np.int64), axis=1)
+    key = (key[:, 0] << 42) | (key[:, 1] << 21) | key[:, 2]
+    order = np.argsort(key, kind="stable")
+    ks = key[order]
+    nbr = np.full(4 * T, -1, dtype=np.int64)
+    same = np.nonzero(ks[1:] == ks[:-1])[0]
+    assert not np.any(same[1:] == same[:-1] + 1)  # no face of three tets
+    a, b = order[same], order[same + 1]
+    nbr[a] = b // 4
+    nbr[b] = a // 4
+    return nbr.reshape(T, 4).astype(np.int32)
+
+
+@pytest.mark.parametrize("name", list(_gpu_sets()))
+def test_gpu_tetrahedra_match_qhull(dev, name):
+    """sdf_delaunay_certify + Qhull of the open points + sdf_delaunay_merge:
+    the same tetrahedra as Qhull on every point, and (through
+    sdf_delaunay_tables) every derived table bit-exact."""
+    import torch
+
+    from sdfoam_amd.triangulation import device_tables, gpu_tetrahedra, host_tables, qhull_tetrahedra
+
+    from scipy.spatial import ConvexHull
+
+    from test_delaunay_cells import assert_delaunay
+
+    import sdfoam_amd
+    from sdfoam_amd.triangulation import _Undecided
+
+    pts = np.ascontiguousarray(_gpu_sets()[name](), dtype=np.float32)
+    print(f"gpu_tetrahedra {name} n={pts.shape[0]}", flush=True)
+    pd = torch.from_numpy(pts).to(dev)
+    if name == "C1":
+        # C1 holds the cube's corners: each face of the cube is cospherical.
+        # A certified point on such a sphere leaves the split undecided, and
+        # Triangulation then runs Qhull on every point.
+        try:
+            tets, nbr, stats = gpu_tetrahedra(pd)
+        except _Undecided:
+            tri = sdfoam_amd.Triangulation(pd)
+            assert tri.last_method == "qhull"
+            return
+    else:
+        tets, nbr, stats = gpu_tetrahedra(pd)
+    tets_np, nbr_np = tets.cpu().numpy(), nbr.cpu().numpy()
+    # neighbours by face matching in numpy
+    assert np.array_equal(nbr_np, _face_neighbors(tets_np))
+    if name == "C1":
+        # C1 holds the cube's corners: each face of the cube is cospherical,
+        # and either split of it is Delaunay
+        assert_delaunay(pts, tets_np, ConvexHull(pts.astype(np.float64)).volume)
+        simplices, neighbors = tets_np, nbr_np
+    else:
+        simplices, neighbors = qhull_tetrahedra(pts)
+        got = np.sort(tets_np, axis=1)
+        ref = np.sort(simplices, axis=1)
+        assert got.shape == ref.shape
+        got = got[np.lexsort(got[:, ::-1].T)]
+        ref = ref[np.lexsort(ref[:, ::-1].T)]
+        assert np.array_equal(got, ref)
+        assert stats["tets"] == simplices.shape[0]
+    if name not in ("shell",):
+        # the hull layer is a larger share of a small set
+        assert stats["open"] < (0.2 if pts.shape[0] < 10_000 else 0.12) * pts.shape[0], stats
+    mine = device_tables(pd, tets, nbr)
+    host = host_tables(pts, simplices, neighbors)
+    for k, v in host.items():
+        assert np.array_equal(_np(mine[k]).reshape(v.shape), v), k
+
+
+def test_triangulation_methods_agree(dev):
+    import torch
+
+    import sdfoam_amd
+
+    w = scene(2)
+    pts = torch.from_numpy(w.points).to(dev)
+    a = sdfoam_amd.Triangulation(pts)
+    b = sdfoam_amd.Triangulation(pts, method="qhull")
+    assert a.last_method == "gpu" and b.last_method == "qhull"
+    assert a.last_stats["open"] < 0.05 * w.points.shape[0]
+    for k in ("tets", "tet_adjacency", "vert_to_tet", "point_adjacency", "point_adjacency_offsets"):
+        assert torch.equal(getattr(a, k)().view(torch.int32), getattr(b, k)().view(torch.int32)), k
+    with pytest.raises(ValueError, match="unknown triangulation method"):
+        sdfoam_amd.Triangulation(pts, method="cgal")

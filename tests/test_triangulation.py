@@ -42,6 +42,8 @@ def test_orientation_order_and_cover(small):
     a, b, c, d = (p[s[:, k]] for k in range(4))
     vol = np.einsum("ij,ij->i", np.cross(b - a, c - a), d - a)
     assert np.all(vol > 0)
+    # canonical vertex order: ascending but for the last two
+    assert np.all((s[:, 0] < s[:, 1]) & (s[:, 1] < s[:, 2]) & (s[:, 1] < s[:, 3]))
     key = np.sort(s, axis=1)
     assert all(tuple(key[i]) < tuple(key[i + 1]) for i in range(len(key) - 1))
     # the tets tile the convex hull

@@ -1,11 +1,30 @@
-// Host build of the GPU Delaunay's cell clipping (sdfoam_amd/csrc/voronoi_cell.h)
-// for the CPU tests: the same code the kernel runs, driven one cell at a time.
+// Host build of the GPU Delaunay's per-item code (sdfoam_amd/csrc/voronoi_cell.h,
+// sdfoam_amd/csrc/delaunay_grid.h) for the CPU tests: the same code the
+// kernels run, driven one cell or one candidate at a time.
 #include <cmath>
 #include <cstdint>
+#include <vector>
 
-#include "../sdfoam_amd/csrc/voronoi_cell.h"
+#include "../sdfoam_amd/csrc/delaunay_grid.h"
 
 using namespace sdfoam_hip::vcell;
+namespace dgrid = sdfoam_hip::dgrid;
+
+namespace {
+// the grids of the last vc_grid call
+dgrid::GridGeom g_geom;
+std::vector<uint32_t> g_start[dgrid::kLevels], g_sorted[dgrid::kLevels];
+
+dgrid::GridView view() {
+    dgrid::GridView v{};
+    v.g = g_geom;
+    for (int l = 0; l < dgrid::kLevels; ++l) {
+        v.start[l] = g_start[l].data();
+        v.sorted[l] = g_sorted[l].data();
+    }
+    return v;
+}
+} // namespace
 
 extern "C" {
 
@@ -65,4 +84,68 @@ int vc_box_unpaired(void) {
 int vc_insphere(const double *a, const double *b, const double *c, const double *q) {
     return in_sphere(a, b, c, q);
 }
+
+// The device's grids over n points (bounding box of the floats, each
+// level's cells by a stable counting sort); returns the cells of level 0
+// (dims: its dimensions), 0 if the box is degenerate.
+int vc_grid(const float *points, uint32_t n, uint32_t *dims) {
+    double lo[3] = {INFINITY, INFINITY, INFINITY}, hi[3] = {-INFINITY, -INFINITY, -INFINITY};
+    for (uint32_t i = 0; i < n; ++i)
+        for (int k = 0; k < 3; ++k) {
+            lo[k] = std::fmin(lo[k], (double)points[3 * i + k]);
+            hi[k] = std::fmax(hi[k], (double)points[3 * i + k]);
+        }
+    if (!dgrid::grid_geometry(lo, hi, n, g_geom)) return 0;
+    std::vector<uint32_t> id(n);
+    for (int l = 0; l < dgrid::kLevels; ++l) {
+        const uint32_t cells = g_geom.level[l].num_cells;
+        std::vector<uint32_t> &start = g_start[l];
+        start.assign(cells + 1, 0u);
+        for (uint32_t i = 0; i < n; ++i) {
+            id[i] = dgrid::cell_index(g_geom, l, points[3 * i], points[3 * i + 1],
+                                      points[3 * i + 2]);
+            ++start[id[i] + 1];
+        }
+        for (uint32_t c = 0; c < cells; ++c) start[c + 1] += start[c];
+        std::vector<uint32_t> cur(start.begin(), start.end() - 1);
+        g_sorted[l].assign(n, 0u);
+        for (uint32_t i = 0; i < n; ++i) g_sorted[l][cur[id[i]]++] = i;
+    }
+    for (int k = 0; k < 3; ++k) dims[k] = g_geom.level[0].dims[k];
+    return (int)g_geom.level[0].num_cells;
 }
+
+// certify_cell for every point on the last grid: status [n], coincident
+// count, and the report rows (point, a, b, c) of certified cells, up to
+// capacity; returns the number of rows asked for.
+long long vc_certify(const float *points, uint32_t n, uint32_t *status, uint32_t *reports,
+                     long long capacity, long long *coincident) {
+    static Cell cell;
+    const dgrid::GridView gv = view();
+    long long rows = 0;
+    *coincident = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        bool co = false;
+        status[i] = dgrid::certify_cell(points, i, gv, cell, co);
+        *coincident += co ? 1 : 0;
+        if (status[i] != kCertified) continue;
+        for (int v = 0; v < cell.num_verts; ++v, ++rows) {
+            if (rows >= capacity) continue;
+            reports[4 * rows] = i;
+            for (int k = 0; k < 3; ++k)
+                reports[4 * rows + 1 + k] = (uint32_t)cell.planes[cell.verts[v].p[k]].point;
+        }
+    }
+    return rows;
+}
+
+// sphere_empty for m candidates [m, 4] on the last grid (status: that of
+// vc_certify).
+void vc_sphere_empty(const float *points, const uint32_t *cand, long long m,
+                     const uint32_t *status, uint32_t *keep) {
+    const dgrid::GridView gv = view();
+    for (long long t = 0; t < m; ++t)
+        keep[t] = dgrid::sphere_empty(points, cand + 4 * t, gv, status);
+}
+}
+
