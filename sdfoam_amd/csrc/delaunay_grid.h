@@ -19,7 +19,7 @@ namespace dgrid {
 // sparse regions both see few candidates per cell.
 constexpr int kLevels = 3;
 constexpr double kLevelRatio = 4.0;
-constexpr double kFineCellsPerPoint = 8.0;
+constexpr double kFineCellsPerPoint = 27.0;
 constexpr int kMaxRing = 6;  // rings per level
 constexpr int kMinRing = 2;  // rings on a level before moving up
 constexpr int kBoxRing = 2;  // from here, a cell still reaching the box on a
@@ -118,6 +118,29 @@ SDF_HD uint32_t cell_index(const GridGeom &g, int l, double x, double y, double 
     return (cz * lv.dims[1] + cy) * lv.dims[0] + cx;
 }
 
+// Bounding box of the cell's vertices, grown by their error bounds: a
+// candidate q can cut the cell only if max over the box of x.q exceeds
+// |q|^2 / 2.
+SDF_HD void vertex_box(const vcell::Cell &cell, double *lo, double *hi) {
+    for (int k = 0; k < 3; ++k) {
+        lo[k] = cell.verts[0].x[k];
+        hi[k] = cell.verts[0].x[k];
+    }
+    double e = 0.0;
+    for (int i = 0; i < cell.num_verts; ++i) {
+        const vcell::Vert &v = cell.verts[i];
+        for (int k = 0; k < 3; ++k) {
+            lo[k] = v.x[k] < lo[k] ? v.x[k] : lo[k];
+            hi[k] = v.x[k] > hi[k] ? v.x[k] : hi[k];
+        }
+        e = v.e > e ? v.e : e;
+    }
+    for (int k = 0; k < 3; ++k) {
+        lo[k] -= e;
+        hi[k] += e;
+    }
+}
+
 SDF_HD bool touches_box(const vcell::Cell &cell) {
     for (int i = 0; i < cell.num_verts; ++i)
         for (int k = 0; k < 3; ++k)
@@ -160,6 +183,8 @@ SDF_HD uint32_t certify_cell(const float *p, uint32_t i, const GridView &gv, vce
         vcell::cell_init(cell, rlo, rhi);
     }
     double mr2 = vcell::max_r2(cell);
+    double blo[3], bhi[3];
+    vertex_box(cell, blo, bhi);
     int hc[kLevels][3];
     int rings[kLevels];
     for (int l = 0; l < kLevels; ++l) {
@@ -204,9 +229,22 @@ SDF_HD uint32_t certify_cell(const float *p, uint32_t i, const GridView &gv, vce
                                 return cell.status;
                             }
                             if (d2 > 4.0 * mr2 * (1.0 + 1e-9)) continue; // cannot cut
+                            // the bisector x.q = |q|^2 / 2 misses the vertices' box
+                            // (by more than the rounding of the sums)
+                            double reach_q = 0.0, mag = d2;
+                            for (int m = 0; m < 3; ++m) {
+                                const double b = q[m] > 0.0 ? bhi[m] : blo[m];
+                                reach_q += b * q[m];
+                                mag += vcell::dabs(b * q[m]);
+                            }
+                            if (reach_q < 0.5 * d2 - 1e-14 * mag) continue;
                             if (l > 0 && searched(g, l, x, hc, rings)) continue;
-                            if (!vcell::clip(cell, q, (int32_t)j)) return cell.status;
-                            mr2 = vcell::max_r2(cell);
+                            bool cut = false;
+                            if (!vcell::clip(cell, q, (int32_t)j, &cut)) return cell.status;
+                            if (cut) {
+                                mr2 = vcell::max_r2(cell);
+                                vertex_box(cell, blo, bhi);
+                            }
                         }
                     }
                 }

@@ -232,8 +232,10 @@ SDF_HD bool compact_planes(Cell &cell) {
 
 // Clips the cell by the bisector of o and candidate `point` at relative
 // position q.  Returns false when the cell became uncertain or overflowed
-// (cell.status says which).
-SDF_HD bool clip(Cell &cell, const double *q, int32_t point) {
+// (cell.status says which); *cut (if given) says whether the plane removed
+// any vertex.
+SDF_HD bool clip(Cell &cell, const double *q, int32_t point, bool *cut = nullptr) {
+    if (cut) *cut = false;
     if (cell.num_planes >= kMaxPlanes && !compact_planes(cell)) {
         cell.status = kOverflow;
         return false;
@@ -270,6 +272,7 @@ SDF_HD bool clip(Cell &cell, const double *q, int32_t point) {
         n_out += out[i] ? 1 : 0;
     }
     if (n_out == 0) return true; // the plane misses the cell
+    if (cut) *cut = true;
     if (n_out == cell.num_verts) {
         cell.status = kUncertain; // o itself would be cut off: impossible
         return false;
