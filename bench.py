@@ -44,6 +44,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "Mrays/s fwd+bwd at 1M pts/1600x1200 rays; % HBM roofline"
 RENDER_METRIC = "Mpixels/s inference render (trace_benchmark, RGBA8)"
 FETCH_METRIC = "GB/s of training batches delivered by BatchFetcher (rays + rgb)"
+TRI_METRIC = "Triangulation rebuilds/s (Delaunay + tables) at 1M points (C3 point set)"
 HOST_LINK_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
 
 
@@ -92,6 +93,10 @@ def main() -> int:
     ap.add_argument("--fetch", action="store_true",
                     help="time BatchFetcher feeding training batches (2^20 shuffled rows of "
                          "rays [M, 6] and colours [M, 3], M = 64 cameras x 960 x 640)")
+    ap.add_argument("--triangulate", action="store_true",
+                    help="time Triangulation.rebuild (sort, GPU Delaunay with Qhull on the "
+                         "open points, tables) on C3's 1M points, with Qhull on every point "
+                         "beside it")
     ap.add_argument("--render", action="store_true",
                     help="time the inference render (Pipeline.trace_benchmark, the reference's "
                          "benchmark.py) on the config's camera instead of the training step")
@@ -134,6 +139,8 @@ def main() -> int:
 
     if args.fetch:
         return fetch_bench(args, dev)
+    if args.triangulate:
+        return triangulate_bench(args, dev)
 
     t0 = time.time()
     if args.scene_cache and os.path.exists(args.scene_cache):
@@ -350,6 +357,77 @@ def main() -> int:
 
 
 CPU_SAMPLE_RAYS = 640_000
+
+
+def triangulate_bench(args, dev) -> int:
+    """Triangulation.rebuild(points, incremental=False) on the C3 point set
+    (850k noisy superquadric surface points and 150k uniform ones): the
+    reference's rebuild (src/delaunay/delaunay.cu:271-345) with the point
+    order, the tetrahedralisation and every table.  Each step is one
+    rebuild; the CPU baseline is Qhull (scipy) on every point, once.  The
+    certify kernel is latency-bound per-lane clipping in fp64, far from the
+    HBM roofline: the roofline entry reports its algorithmic bytes (points
+    in, report rows out) over the time of the certify call."""
+    import numpy as np
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import scenes
+    from sdfoam_amd.triangulation import qhull_tetrahedra
+
+    pts_np, _ = scenes._scene_c3(np.random.default_rng(0))
+    pts = torch.from_numpy(pts_np).to(dev)
+    n = pts.shape[0]
+    tri = sdfoam_amd.Triangulation(pts[:50_000].contiguous())  # warm the kernels
+    for _ in range(args.warmup):
+        tri.rebuild(pts, incremental=False)
+    torch.cuda.synchronize()
+    stats = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tri.rebuild(pts, incremental=False)
+        stats.append(tri.last_stats)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    if tri.last_method != "gpu":
+        raise RuntimeError("the GPU tetrahedralisation fell back to Qhull")
+    last = stats[-1]
+    certify = float(np.mean([s["certify_s"] for s in stats]))
+    sorted_pts = pts[tri.permutation().view(torch.int32).long()].cpu().numpy()
+    tq = time.perf_counter()
+    qhull_tetrahedra(sorted_pts)
+    t_qhull = time.perf_counter() - tq
+    algo_bytes = 12 * n + 16 * last["reports"]
+    achieved = algo_bytes / certify / 1e9
+    result = {
+        "metric": TRI_METRIC,
+        "value": 1.0 / dt,
+        "unit": "rebuilds/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dt * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": "Triangulation.rebuild of the C3 point set", "points": n,
+                   "tets": last["tets"]},
+        "phases_s": {"certify": certify,
+                     "open_points_qhull": float(np.mean([s["open_points_qhull_s"] for s in stats])),
+                     "merge": float(np.mean([s["merge_s"] for s in stats]))},
+        "open_points": last["open"],
+        "roofline": {"kernel": "certify_kernel", "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None},
+        "cpu_baseline": {"value": 1.0 / t_qhull, "unit": "rebuilds/s", "cores": 1,
+                         "kind": "library",
+                         "sample": "Qhull (scipy.spatial.Delaunay) on all 1M points, once; "
+                                   "tetrahedra only, no tables"},
+    }
+    print(json.dumps(result), flush=True)
+    return 0
 
 
 def fetch_bench(args, dev) -> int:

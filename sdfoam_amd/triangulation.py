@@ -32,6 +32,7 @@ statement of the same tables (the check of the device path).
 from __future__ import annotations
 
 import ctypes as C
+import time
 
 import numpy as np
 import torch
@@ -177,6 +178,7 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
     open_pts = torch.empty(n, dtype=torch.int32, device=dev)
     counts = (C.c_uint64 * 5)()
     cap = 28 * n + 4096
+    t0 = time.perf_counter()
     with torch.cuda.device(dev):
         for _ in range(2):
             reports = torch.empty((cap, 4), dtype=torch.int32, device=dev)
@@ -188,6 +190,7 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
         nr, nu = int(counts[0]), int(counts[1])
         if counts[4]:
             raise TriangulationFailedError("duplicate points found")
+        t1 = time.perf_counter()
         # the open points, in index order, through Qhull on the host
         U = torch.sort(open_pts[:nu])[0]
         u_np = U.cpu().numpy()
@@ -195,6 +198,7 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
         hull_faces = int((nbr_u < 0).sum())
         cand = torch.from_numpy(np.ascontiguousarray(u_np[simplices], dtype=np.int32)).to(dev)
         m = int(cand.shape[0])
+        t2 = time.perf_counter()
         result = (C.c_uint64 * 4)()
         tcap = nr // 3 + m + 4096
         for _ in range(2):
@@ -216,8 +220,10 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
     T = int(result[0])
     if int(result[1]) != hull_faces:
         raise _Undecided(f"{int(result[1])} faces without a neighbour, the hull has {hull_faces}")
+    t3 = time.perf_counter()
     stats = {"open": nu, "reports": nr, "candidates": m, "tets": T,
-             "undecided_cells": int(counts[2]), "overflow_cells": int(counts[3])}
+             "undecided_cells": int(counts[2]), "overflow_cells": int(counts[3]),
+             "certify_s": t1 - t0, "open_points_qhull_s": t2 - t1, "merge_s": t3 - t2}
     return tets[:T], nbr[:T], stats
 
 
