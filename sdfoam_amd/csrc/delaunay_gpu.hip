@@ -145,35 +145,492 @@ __global__ __launch_bounds__(256) void fill_kernel(uint32_t *__restrict__ v, uin
     if (i < n) v[i] = value;
 }
 
+// ---- certify: one wavefront per point ---------------------------------
+//
+// The cell of one point is shared by the 64 lanes of a wavefront: its
+// planes (at most 64) in LDS, its vertices (at most 128) two per lane in
+// registers.  Candidates are read 64 at a time (one grid cell per lane, the
+// cell's points in rounds), filtered per lane, and the survivors clipped
+// nearest first by the whole wavefront: each lane classifies its two
+// vertices, a 64 x 64 bitmap of the removed vertices' directed edges gives
+// the boundary edges (an edge is on the boundary when its reverse was not
+// removed), and the new vertices go through a staging list into free slots.
+// The decisions are those of dgrid::certify_cell and vcell::clip; every
+// branch that ends a cell is taken by the whole wavefront together.
+
+constexpr int kWavePlanes = 64;
+constexpr int kWaveVerts = 128;
+constexpr int kWaveNew = 64;    // new vertices one clip may make
+constexpr uint32_t kFree = 0xffffffffu;
+
+struct StagedVert {
+    uint32_t planes;
+    double x[3], e, r2;
+};
+
+struct WaveShared {
+    double pn[kWavePlanes][3]; // plane normals
+    double pc[kWavePlanes];    // plane offsets: x.n < c inside
+    int32_t pp[kWavePlanes];   // candidate index, -1 for a box face
+    uint32_t edges[kWavePlanes * kWavePlanes / 32];
+    uint32_t used[2];
+    uint8_t remap[kWavePlanes];
+    StagedVert stg[kWaveNew];
+};
+
+struct WaveCell {
+    uint32_t vp[2]; // plane indices a | b << 8 | c << 16 of this lane's two slots (kFree if none)
+    double vx[2][3], ve[2], vr2[2];
+    int np;                         // planes in use (same in every lane)
+    double mr2, blo[3], bhi[3];     // max |v|^2 and the vertices' box (same in every lane)
+};
+
+__device__ __forceinline__ uint32_t wlane() { return threadIdx.x & 63u; }
+__device__ __forceinline__ uint64_t wballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+// set bits of m in the lanes below this one
+__device__ __forceinline__ uint32_t wbelow(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+__device__ __forceinline__ double wmaxd(double v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmax(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ double wmind(double v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmin(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ uint32_t wsumu(uint32_t v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ uint32_t wmaxu(uint32_t v) {
+    for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t plane_of(uint32_t vp, int k) { return (vp >> (8 * k)) & 0xffu; }
+
+// max |v|^2 and the vertices' box grown by the largest error bound
+// (dgrid::vertex_box).
+__device__ void wave_bounds(WaveCell &c) {
+    double r2 = 0.0, e = 0.0, lo[3], hi[3];
+    for (int k = 0; k < 3; ++k) {
+        lo[k] = INFINITY;
+        hi[k] = -INFINITY;
+    }
+    for (int s = 0; s < 2; ++s) {
+        if (c.vp[s] == kFree) continue;
+        r2 = fmax(r2, c.vr2[s]);
+        e = fmax(e, c.ve[s]);
+        for (int k = 0; k < 3; ++k) {
+            lo[k] = fmin(lo[k], c.vx[s][k]);
+            hi[k] = fmax(hi[k], c.vx[s][k]);
+        }
+    }
+    c.mr2 = wmaxd(r2);
+    e = wmaxd(e);
+    for (int k = 0; k < 3; ++k) {
+        c.blo[k] = wmind(lo[k]) - e;
+        c.bhi[k] = wmaxd(hi[k]) + e;
+    }
+}
+
+__device__ void wave_init(WaveCell &c, WaveShared &sh, const double *rlo, const double *rhi) {
+    const uint32_t l = wlane();
+    if (l < 6) {
+        const int k = (int)(l >> 1);
+        for (int m = 0; m < 3; ++m) sh.pn[l][m] = 0.0;
+        sh.pn[l][k] = (l & 1u) ? -1.0 : 1.0;
+        sh.pc[l] = (l & 1u) ? -rlo[k] : rhi[k];
+        sh.pp[l] = -1;
+    }
+    c.np = 6;
+    c.vp[0] = c.vp[1] = kFree;
+    if (l < 8) {
+        // corners as vcell::cell_init makes them
+        const uint32_t sx = (l >> 2) & 1u, sy = (l >> 1) & 1u, sz = l & 1u;
+        const uint32_t px = sx, py = 2u + sy, pz = 4u + sz;
+        c.vp[0] = ((sx + sy + sz) & 1u) == 0 ? (px | py << 8 | pz << 16)
+                                              : (px | pz << 8 | py << 16);
+        c.vx[0][0] = sx ? rlo[0] : rhi[0];
+        c.vx[0][1] = sy ? rlo[1] : rhi[1];
+        c.vx[0][2] = sz ? rlo[2] : rhi[2];
+        c.ve[0] = 0.0;
+        c.vr2[0] = c.vx[0][0] * c.vx[0][0] + c.vx[0][1] * c.vx[0][1] + c.vx[0][2] * c.vx[0][2];
+    }
+    wave_bounds(c);
+    __syncthreads();
+}
+
+// Drops planes no vertex uses (vcell::compact_planes); false if all are used.
+__device__ bool wave_compact_planes(WaveCell &c, WaveShared &sh) {
+    const uint32_t l = wlane();
+    if (l < 2) sh.used[l] = 0u;
+    __syncthreads();
+    for (int s = 0; s < 2; ++s)
+        if (c.vp[s] != kFree)
+            for (int k = 0; k < 3; ++k) {
+                const uint32_t q = plane_of(c.vp[s], k);
+                atomicOr(&sh.used[q >> 5], 1u << (q & 31u));
+            }
+    __syncthreads();
+    const uint64_t used = (uint64_t)sh.used[0] | ((uint64_t)sh.used[1] << 32);
+    const bool mine = (used >> l) & 1ull;
+    const uint32_t to = wbelow(used);
+    double n0 = 0.0, n1 = 0.0, n2 = 0.0, pc = 0.0;
+    int32_t pp = 0;
+    if (mine) {
+        n0 = sh.pn[l][0];
+        n1 = sh.pn[l][1];
+        n2 = sh.pn[l][2];
+        pc = sh.pc[l];
+        pp = sh.pp[l];
+        sh.remap[l] = (uint8_t)to;
+    }
+    __syncthreads();
+    if (mine) {
+        sh.pn[to][0] = n0;
+        sh.pn[to][1] = n1;
+        sh.pn[to][2] = n2;
+        sh.pc[to] = pc;
+        sh.pp[to] = pp;
+    }
+    for (int s = 0; s < 2; ++s)
+        if (c.vp[s] != kFree)
+            c.vp[s] = (uint32_t)sh.remap[plane_of(c.vp[s], 0)] |
+                      (uint32_t)sh.remap[plane_of(c.vp[s], 1)] << 8 |
+                      (uint32_t)sh.remap[plane_of(c.vp[s], 2)] << 16;
+    c.np = __popcll(used);
+    __syncthreads();
+    return c.np < kWavePlanes;
+}
+
+// Clips the cell by the bisector of o and `point` (relative position q,
+// qc = |q|^2 / 2).  0: the plane misses the cell, 1: cut, 2: undecided,
+// 3: over capacity.  The whole wavefront calls it with the same arguments.
+__device__ int wave_clip(WaveCell &c, WaveShared &sh, const double *q, double qc,
+                         int32_t point) {
+    const uint32_t l = wlane();
+    if (c.np >= kWavePlanes && !wave_compact_planes(c, sh)) return 3;
+    const double qn = vcell::dabs(q[0]) + vcell::dabs(q[1]) + vcell::dabs(q[2]);
+    bool out[2] = {false, false}, undecided = false;
+    for (int s = 0; s < 2; ++s) {
+        if (c.vp[s] == kFree) continue;
+        const double *x = c.vx[s];
+        const double sd = x[0] * q[0] + x[1] * q[1] + x[2] * q[2] - qc;
+        const double bound =
+            c.ve[s] * qn + 4.0 * vcell::kEps *
+                               (vcell::dabs(x[0] * q[0]) + vcell::dabs(x[1] * q[1]) +
+                                vcell::dabs(x[2] * q[2]) + qc);
+        if (sd < -bound || sd > bound) {
+            out[s] = sd > 0.0;
+            continue;
+        }
+        // the exact decision (vcell::outside)
+        const uint32_t a = plane_of(c.vp[s], 0), b = plane_of(c.vp[s], 1),
+                       cc = plane_of(c.vp[s], 2);
+        int sg;
+        if (sh.pp[a] >= 0 && sh.pp[b] >= 0 && sh.pp[cc] >= 0) {
+            const double A[3] = {sh.pn[a][0], sh.pn[a][1], sh.pn[a][2]};
+            const double B[3] = {sh.pn[b][0], sh.pn[b][1], sh.pn[b][2]};
+            const double Cn[3] = {sh.pn[cc][0], sh.pn[cc][1], sh.pn[cc][2]};
+            sg = vcell::in_sphere(A, B, Cn, q);
+        } else {
+            const double scale =
+                (vcell::dabs(x[0]) + vcell::dabs(x[1]) + vcell::dabs(x[2])) * qn +
+                vcell::dabs(qc);
+            sg = vcell::dabs(sd) <= 1e-9 * scale ? 0 : (sd > 0.0 ? 1 : -1);
+        }
+        if (sg == 0) undecided = true;
+        out[s] = sg > 0;
+    }
+    if (wballot(undecided)) return 2;
+    const uint64_t o0 = wballot(out[0]), o1 = wballot(out[1]);
+    if ((o0 | o1) == 0ull) return 0;
+    const uint64_t a0 = wballot(c.vp[0] != kFree), a1 = wballot(c.vp[1] != kFree);
+    if (o0 == a0 && o1 == a1) return 2; // every vertex cut: o itself would go
+    // the removed vertices' directed edges
+    sh.edges[l] = 0u;
+    sh.edges[l + 64] = 0u;
+    __syncthreads();
+    for (int s = 0; s < 2; ++s)
+        if (out[s])
+            for (int k = 0; k < 3; ++k) {
+                const uint32_t ea = plane_of(c.vp[s], k), eb = plane_of(c.vp[s], (k + 1) % 3);
+                const uint32_t bit = ea * kWavePlanes + eb;
+                atomicOr(&sh.edges[bit >> 5], 1u << (bit & 31u));
+            }
+    __syncthreads();
+    // boundary edges (reverse not removed): one new vertex each
+    uint32_t fresh[6];
+    uint32_t nf = 0;
+    for (int s = 0; s < 2; ++s)
+        if (out[s])
+            for (int k = 0; k < 3; ++k) {
+                const uint32_t ea = plane_of(c.vp[s], k), eb = plane_of(c.vp[s], (k + 1) % 3);
+                const uint32_t rev = eb * kWavePlanes + ea;
+                if (!((sh.edges[rev >> 5] >> (rev & 31u)) & 1u)) fresh[nf++] = ea | eb << 8;
+            }
+    uint32_t incl = nf;
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = (uint32_t)__shfl_up((int)incl, off, 64);
+        if (l >= (uint32_t)off) incl += y;
+    }
+    const uint32_t total = (uint32_t)__shfl((int)incl, 63, 64);
+    const uint32_t base = incl - nf;
+    const uint32_t kept = __popcll(a0 & ~o0) + __popcll(a1 & ~o1);
+    if (total > (uint32_t)kWaveNew || kept + total > (uint32_t)kWaveVerts) return 3;
+    const uint32_t np = (uint32_t)c.np;
+    vcell::Plane P;
+    P.n[0] = q[0];
+    P.n[1] = q[1];
+    P.n[2] = q[2];
+    P.c = qc;
+    P.point = point;
+    bool bad = false;
+    for (uint32_t t = 0; t < nf; ++t) {
+        const uint32_t ea = fresh[t] & 0xffu, eb = fresh[t] >> 8;
+        vcell::Plane A, B;
+        for (int k = 0; k < 3; ++k) {
+            A.n[k] = sh.pn[ea][k];
+            B.n[k] = sh.pn[eb][k];
+        }
+        A.c = sh.pc[ea];
+        B.c = sh.pc[eb];
+        A.point = sh.pp[ea];
+        B.point = sh.pp[eb];
+        StagedVert &v = sh.stg[base + t];
+        double x[3], e = 0.0;
+        if (!vcell::meet(A, B, P, x, &e)) {
+            bad = true;
+            continue;
+        }
+        v.planes = ea | eb << 8 | np << 16;
+        v.x[0] = x[0];
+        v.x[1] = x[1];
+        v.x[2] = x[2];
+        v.e = e;
+        v.r2 = x[0] * x[0] + x[1] * x[1] + x[2] * x[2];
+    }
+    if (wballot(bad)) {
+        __syncthreads();
+        return 2;
+    }
+    for (int s = 0; s < 2; ++s)
+        if (out[s]) c.vp[s] = kFree;
+    if (l == 0) {
+        sh.pn[np][0] = q[0];
+        sh.pn[np][1] = q[1];
+        sh.pn[np][2] = q[2];
+        sh.pc[np] = qc;
+        sh.pp[np] = point;
+    }
+    c.np = (int)np + 1;
+    __syncthreads();
+    // free slots take the new vertices, slot 0 of every lane first
+    const uint64_t f0 = ~wballot(c.vp[0] != kFree), f1 = ~wballot(c.vp[1] != kFree);
+    for (int s = 0; s < 2; ++s) {
+        if (c.vp[s] != kFree) continue;
+        const uint32_t rank = s == 0 ? wbelow(f0) : (uint32_t)__popcll(f0) + wbelow(f1);
+        if (rank >= total) continue;
+        const StagedVert &v = sh.stg[rank];
+        c.vp[s] = v.planes;
+        c.vx[s][0] = v.x[0];
+        c.vx[s][1] = v.x[1];
+        c.vx[s][2] = v.x[2];
+        c.ve[s] = v.e;
+        c.vr2[s] = v.r2;
+    }
+    __syncthreads();
+    wave_bounds(c);
+    return 1;
+}
+
+__device__ bool wave_touches_box(const WaveCell &c, const WaveShared &sh) {
+    bool t = false;
+    for (int s = 0; s < 2; ++s)
+        if (c.vp[s] != kFree)
+            for (int k = 0; k < 3; ++k) t = t || sh.pp[plane_of(c.vp[s], k)] < 0;
+    return wballot(t) != 0ull;
+}
+
 // counters: 0 report rows asked for, 1 open points, 2 undecided cells,
 // 3 cells over the fixed capacity, 4 coincident point pairs seen (twice).
+// One 64-thread block per point.
 __global__ __launch_bounds__(64) void certify_kernel(const float *__restrict__ p, uint32_t n,
                                                      GridView gv, uint32_t *__restrict__ reports,
                                                      uint64_t report_capacity,
                                                      unsigned long long *__restrict__ counters,
                                                      uint32_t *__restrict__ open,
                                                      uint32_t *__restrict__ status_out) {
-    const uint32_t i = blockIdx.x * 64u + threadIdx.x;
+    __shared__ WaveShared sh;
+    const uint32_t i = blockIdx.x;
     if (i >= n) return;
-    vcell::Cell cell;
-    bool coincident = false;
-    const uint32_t st = dgrid::certify_cell(p, i, gv, cell, coincident);
-    if (coincident) atomicAdd(counters + 4, 1ull);
-    status_out[i] = st;
-    if (st == vcell::kCertified) {
-        const unsigned long long nv = (unsigned long long)cell.num_verts;
-        const unsigned long long at = atomicAdd(counters, nv);
-        if (at + nv <= report_capacity) {
-            for (int v = 0; v < cell.num_verts; ++v) {
-                const vcell::Vert &vx = cell.verts[v];
-                uint32_t *row = reports + 4ull * (at + (unsigned long long)v);
-                row[0] = i;
-                row[1] = (uint32_t)cell.planes[vx.p[0]].point;
-                row[2] = (uint32_t)cell.planes[vx.p[1]].point;
-                row[3] = (uint32_t)cell.planes[vx.p[2]].point;
-            }
+    const uint32_t l = wlane();
+    const GridGeom &g = gv.g;
+    const double o[3] = {(double)p[3ull * i], (double)p[3ull * i + 1], (double)p[3ull * i + 2]};
+    WaveCell c;
+    {
+        double rlo[3], rhi[3];
+        for (int k = 0; k < 3; ++k) {
+            rlo[k] = g.box_lo[k] - o[k];
+            rhi[k] = g.box_hi[k] - o[k];
         }
-    } else {
+        wave_init(c, sh, rlo, rhi);
+    }
+    int hc[dgrid::kLevels][3];
+    int rings[dgrid::kLevels];
+    for (int lev = 0; lev < dgrid::kLevels; ++lev) {
+        rings[lev] = -1;
+        for (int k = 0; k < 3; ++k)
+            hc[lev][k] = dgrid::axis_cell(o[k], g.lo[k], g.level[lev].inv_h, g.level[lev].dims[k]);
+    }
+    uint32_t st = vcell::kOpen, examined = 0;
+    bool decided = false, coincident = false;
+    for (int lev = 0; lev < dgrid::kLevels && !decided; ++lev) {
+        const dgrid::GridLevel &lv = g.level[lev];
+        const uint32_t *start = gv.start[lev];
+        const uint32_t *sorted = gv.sorted[lev];
+        const int *h = hc[lev];
+        for (int r = 0; r <= dgrid::kMaxRing && !decided; ++r) {
+            const int side = 2 * r + 1;
+            const uint32_t cube = (uint32_t)(side * side * side);
+            for (uint32_t base = 0; base < cube && !decided; base += 64) {
+                // one grid cell of the ring's shell per lane
+                const uint32_t t = base + l;
+                uint32_t b = 0, e = 0;
+                if (t < cube) {
+                    const int dx = (int)(t % (uint32_t)side) - r;
+                    const int dy = (int)((t / (uint32_t)side) % (uint32_t)side) - r;
+                    const int dz = (int)(t / (uint32_t)(side * side)) - r;
+                    const int cx = h[0] + dx, cy = h[1] + dy, cz = h[2] + dz;
+                    const bool shell = dx == -r || dx == r || dy == -r || dy == r || dz == -r ||
+                                       dz == r;
+                    if (shell && cx >= 0 && cx < (int)lv.dims[0] && cy >= 0 &&
+                        cy < (int)lv.dims[1] && cz >= 0 && cz < (int)lv.dims[2]) {
+                        const uint32_t cell = ((uint32_t)cz * lv.dims[1] + (uint32_t)cy) *
+                                                  lv.dims[0] +
+                                              (uint32_t)cx;
+                        b = start[cell];
+                        e = start[cell + 1];
+                    }
+                }
+                const uint32_t cnt = e - b;
+                examined += wsumu(cnt);
+                if (examined > dgrid::kMaxCandidates) {
+                    decided = true;
+                    break;
+                }
+                const uint32_t rounds = wmaxu(cnt);
+                for (uint32_t k = 0; k < rounds && !decided; ++k) {
+                    bool surv = false, dup = false;
+                    double q[3] = {0.0, 0.0, 0.0}, d2 = INFINITY;
+                    uint32_t j = 0;
+                    if (k < cnt) {
+                        j = sorted[b + k];
+                        if (j != i) {
+                            const double x[3] = {(double)p[3ull * j], (double)p[3ull * j + 1],
+                                                 (double)p[3ull * j + 2]};
+                            q[0] = x[0] - o[0];
+                            q[1] = x[1] - o[1];
+                            q[2] = x[2] - o[2];
+                            d2 = q[0] * q[0] + q[1] * q[1] + q[2] * q[2];
+                            if (d2 == 0.0) {
+                                dup = true;
+                            } else if (d2 <= 4.0 * c.mr2 * (1.0 + 1e-9)) {
+                                double reach_q = 0.0, mag = d2;
+                                for (int m = 0; m < 3; ++m) {
+                                    const double bb = q[m] > 0.0 ? c.bhi[m] : c.blo[m];
+                                    reach_q += bb * q[m];
+                                    mag += vcell::dabs(bb * q[m]);
+                                }
+                                surv = !(reach_q < 0.5 * d2 - 1e-14 * mag) &&
+                                       !(lev > 0 && dgrid::searched(g, lev, x, hc, rings));
+                            }
+                        }
+                    }
+                    if (wballot(dup)) {
+                        coincident = true;
+                        st = vcell::kUncertain;
+                        decided = true;
+                        break;
+                    }
+                    uint64_t m = wballot(surv);
+                    while (m) {
+                        // nearest first
+                        const bool mine = (m >> l) & 1ull;
+                        const double dm = wmind(mine ? d2 : INFINITY);
+                        const uint64_t hit = wballot(mine && d2 == dm);
+                        const int src = __builtin_ctzll(hit);
+                        m &= ~(1ull << src);
+                        const double qq[3] = {__shfl(q[0], src, 64), __shfl(q[1], src, 64),
+                                              __shfl(q[2], src, 64)};
+                        const double dd = __shfl(d2, src, 64);
+                        const int32_t jj = __shfl((int)j, src, 64);
+                        // the cell may have shrunk since the filter
+                        if (dd > 4.0 * c.mr2 * (1.0 + 1e-9)) continue;
+                        double reach_q = 0.0, mag = dd;
+                        for (int mm = 0; mm < 3; ++mm) {
+                            const double bb = qq[mm] > 0.0 ? c.bhi[mm] : c.blo[mm];
+                            reach_q += bb * qq[mm];
+                            mag += vcell::dabs(bb * qq[mm]);
+                        }
+                        if (reach_q < 0.5 * dd - 1e-14 * mag) continue;
+                        const int rc = wave_clip(c, sh, qq, 0.5 * dd, jj);
+                        if (rc >= 2) {
+                            st = rc == 2 ? vcell::kUncertain : vcell::kOverflow;
+                            decided = true;
+                            break;
+                        }
+                    }
+                }
+            }
+            if (decided) break;
+            rings[lev] = r;
+            // every point not yet seen lies r cells of this level away or more
+            const bool all = h[0] - r <= 0 && h[0] + r >= (int)lv.dims[0] - 1 && h[1] - r <= 0 &&
+                             h[1] + r >= (int)lv.dims[1] - 1 && h[2] - r <= 0 &&
+                             h[2] + r >= (int)lv.dims[2] - 1;
+            const double reach = (double)r * lv.h - g.slack;
+            const double reach2 = all ? INFINITY : (reach > 0.0 ? reach * reach : 0.0);
+            const bool box = wave_touches_box(c, sh);
+            if (4.0 * c.mr2 * (1.0 + 1e-9) < reach2) {
+                st = box ? vcell::kOpen : vcell::kCertified;
+                decided = true;
+                break;
+            }
+            if (r >= dgrid::kBoxRing && box) {
+                if (lev == 0) break;
+                decided = true;
+                break;
+            }
+            if (r >= dgrid::kMinRing &&
+                4.0 * c.mr2 * (1.0 + 1e-9) > (dgrid::kMaxRing * lv.h) * (dgrid::kMaxRing * lv.h))
+                break;
+        }
+    }
+    if (l == 0) {
+        status_out[i] = st;
+        if (coincident) atomicAdd(counters + 4, 1ull);
+    }
+    if (st == vcell::kCertified) {
+        const uint64_t a0 = wballot(c.vp[0] != kFree), a1 = wballot(c.vp[1] != kFree);
+        const unsigned long long nv = (unsigned long long)(__popcll(a0) + __popcll(a1));
+        unsigned long long at = 0;
+        if (l == 0) at = atomicAdd(counters, nv);
+        at = __shfl(at, 0, 64);
+        if (at + nv <= report_capacity)
+            for (int s = 0; s < 2; ++s) {
+                if (c.vp[s] == kFree) continue;
+                const uint32_t idx = s == 0 ? wbelow(a0) : (uint32_t)__popcll(a0) + wbelow(a1);
+                uint32_t *row = reports + 4ull * (at + idx);
+                row[0] = i;
+                row[1] = (uint32_t)sh.pp[plane_of(c.vp[s], 0)];
+                row[2] = (uint32_t)sh.pp[plane_of(c.vp[s], 1)];
+                row[3] = (uint32_t)sh.pp[plane_of(c.vp[s], 2)];
+            }
+    } else if (l == 0) {
         const unsigned long long at = atomicAdd(counters + 1, 1ull);
         open[at] = i;
         if (st == vcell::kUncertain) atomicAdd(counters + 2, 1ull);
@@ -406,7 +863,7 @@ hipError_t launch_delaunay_certify(const float *points, uint32_t n, uint32_t *re
         gv.start[l] = s.start[l];
         gv.sorted[l] = s.sorted[l];
     }
-    hipLaunchKernelGGL(certify_kernel, dim3((n + 63u) / 64u), dim3(64), 0, stream, points, n, gv,
+    hipLaunchKernelGGL(certify_kernel, dim3(n), dim3(64), 0, stream, points, n, gv,
                        reports, report_capacity, s.counters, open, s.status);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     unsigned long long hc[8];
