@@ -44,7 +44,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "Mrays/s fwd+bwd at 1M pts/1600x1200 rays; % HBM roofline"
 RENDER_METRIC = "Mpixels/s inference render (trace_benchmark, RGBA8)"
 FETCH_METRIC = "GB/s of training batches delivered by BatchFetcher (rays + rgb)"
-TRI_METRIC = "Triangulation rebuilds/s (Delaunay + tables) at 1M points (C3 point set)"
+TRI_METRIC = "Triangulation rebuilds/s (Delaunay + tables) on a config's point set"
 HOST_LINK_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
 
 
@@ -361,7 +361,8 @@ CPU_SAMPLE_RAYS = 640_000
 
 def triangulate_bench(args, dev) -> int:
     """Triangulation.rebuild(points, incremental=False) on the C3 point set
-    (850k noisy superquadric surface points and 150k uniform ones): the
+    (850k noisy superquadric surface points and 150k uniform ones; --config 4:
+    C4's 1.8M blob and 1.2M 1/r^2 shell points): the
     reference's rebuild (src/delaunay/delaunay.cu:271-345) with the point
     order, the tetrahedralisation and every table.  Each step is one
     rebuild; the CPU baseline is Qhull (scipy) on every point, once.  The
@@ -375,8 +376,13 @@ def triangulate_bench(args, dev) -> int:
     from sdfoam_amd import scenes
     from sdfoam_amd.triangulation import qhull_tetrahedra
 
-    pts_np, _ = scenes._scene_c3(np.random.default_rng(0))
-    pts = torch.from_numpy(pts_np).to(dev)
+    if args.config == 4:
+        pts_np, _ = scenes._scene_blobs_shell(np.random.default_rng(4), 1_800_000, 1_200_000)
+    elif args.config == 3:
+        pts_np, _ = scenes._scene_c3(np.random.default_rng(0))
+    else:
+        raise SystemExit("--triangulate takes --config 3 (default) or 4")
+    pts = torch.from_numpy(np.ascontiguousarray(pts_np, dtype=np.float32)).to(dev)
     n = pts.shape[0]
     tri = sdfoam_amd.Triangulation(pts[:50_000].contiguous())  # warm the kernels
     for _ in range(args.warmup):
@@ -412,8 +418,8 @@ def triangulate_bench(args, dev) -> int:
         "vs_baseline": None,
         "dtype": "f64",
         "data": "synthetic",
-        "config": {"workload": "Triangulation.rebuild of the C3 point set", "points": n,
-                   "tets": last["tets"]},
+        "config": {"workload": f"Triangulation.rebuild of the C{args.config} point set",
+                   "points": n, "tets": last["tets"]},
         "phases_s": {"certify": certify,
                      "open_points_qhull": float(np.mean([s["open_points_qhull_s"] for s in stats])),
                      "merge": float(np.mean([s["merge_s"] for s in stats]))},

@@ -39,8 +39,10 @@ using dgrid::GridView;
 struct GridScratch {
     GridGeom *geom;
     unsigned long long *counters;
-    uint32_t *mm, *counts, *ids, *ids_sorted, *index, *status;
-    uint32_t *start[dgrid::kLevels], *sorted[dgrid::kLevels];
+    uint32_t *mm, *index, *status;
+    uint64_t *keys, *keys_sorted;
+    dgrid::CellEntry *table[dgrid::kLevels];
+    uint32_t *sorted[dgrid::kLevels];
     void *temp;
     size_t temp_bytes;
     size_t total;
@@ -49,7 +51,7 @@ struct GridScratch {
 GridScratch carve_grid(void *base, uint32_t n, size_t temp_bytes) {
     GridScratch s{};
     char *p = static_cast<char *>(base);
-    const uint64_t cc = dgrid::level_cell_capacity(n);
+    const uint64_t slots = dgrid::table_slots(n);
     auto take = [&](size_t bytes) {
         char *q = p;
         p += a256(bytes);
@@ -59,12 +61,11 @@ GridScratch carve_grid(void *base, uint32_t n, size_t temp_bytes) {
     s.counters = reinterpret_cast<unsigned long long *>(take(8 * 8));
     s.mm = reinterpret_cast<uint32_t *>(take(6 * 4));
     for (int l = 0; l < dgrid::kLevels; ++l) {
-        s.start[l] = reinterpret_cast<uint32_t *>(take(4 * (cc + 1)));
+        s.table[l] = reinterpret_cast<dgrid::CellEntry *>(take(sizeof(dgrid::CellEntry) * slots));
         s.sorted[l] = reinterpret_cast<uint32_t *>(take(4ull * n));
     }
-    s.counts = reinterpret_cast<uint32_t *>(take(4 * (cc + 1)));
-    s.ids = reinterpret_cast<uint32_t *>(take(4ull * n));
-    s.ids_sorted = reinterpret_cast<uint32_t *>(take(4ull * n));
+    s.keys = reinterpret_cast<uint64_t *>(take(8ull * n));
+    s.keys_sorted = reinterpret_cast<uint64_t *>(take(8ull * n));
     s.index = reinterpret_cast<uint32_t *>(take(4ull * n));
     s.status = reinterpret_cast<uint32_t *>(take(4ull * n));
     s.temp = p;
@@ -74,15 +75,14 @@ GridScratch carve_grid(void *base, uint32_t n, size_t temp_bytes) {
 }
 
 size_t grid_temp_bytes(uint32_t n) {
-    size_t a = 0, b = 0;
-    const uint32_t *k = nullptr;
-    uint32_t *ko = nullptr;
-    if (rocprim::radix_sort_pairs(nullptr, a, k, ko, k, ko, (size_t)n, 0u, 32u) != hipSuccess)
+    size_t a = 0;
+    const uint64_t *k = nullptr;
+    uint64_t *ko = nullptr;
+    const uint32_t *v = nullptr;
+    uint32_t *vo = nullptr;
+    if (rocprim::radix_sort_pairs(nullptr, a, k, ko, v, vo, (size_t)n, 0u, 63u) != hipSuccess)
         return 0;
-    if (rocprim::exclusive_scan(nullptr, b, k, ko, 0u, (size_t)dgrid::level_cell_capacity(n) + 1,
-                                rocprim::plus<uint32_t>()) != hipSuccess)
-        return 0;
-    return std::max(a, b);
+    return a;
 }
 
 __device__ __forceinline__ uint32_t ordered(float x) {
@@ -125,24 +125,64 @@ __global__ __launch_bounds__(256) void bbox_kernel(const float *__restrict__ p, 
         }
 }
 
-__global__ __launch_bounds__(256) void cell_ids_kernel(const float *__restrict__ p, uint32_t n,
-                                                       GridGeom g, int level,
-                                                       uint32_t *__restrict__ ids,
-                                                       uint32_t *__restrict__ index,
-                                                       uint32_t *__restrict__ counts) {
+__global__ __launch_bounds__(256) void cell_keys_kernel(const float *__restrict__ p, uint32_t n,
+                                                        GridGeom g, int level,
+                                                        uint64_t *__restrict__ keys,
+                                                        uint32_t *__restrict__ index) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
     if (i >= n) return;
-    const uint32_t c =
-        dgrid::cell_index(g, level, p[3ull * i], p[3ull * i + 1], p[3ull * i + 2]);
-    ids[i] = c;
+    keys[i] = dgrid::point_key(g, level, p[3ull * i], p[3ull * i + 1], p[3ull * i + 2]);
     index[i] = i;
-    atomicAdd(counts + c, 1u);
 }
 
 __global__ __launch_bounds__(256) void fill_kernel(uint32_t *__restrict__ v, uint64_t n,
                                                    uint32_t value) {
     const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
     if (i < n) v[i] = value;
+}
+
+__global__ __launch_bounds__(256) void table_clear_kernel(dgrid::CellEntry *__restrict__ t,
+                                                          uint64_t slots) {
+    const uint64_t s = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (s < slots) t[s] = dgrid::CellEntry{dgrid::kEmptyKey, 0u, 0u};
+}
+
+// The first point of each run of equal keys claims a slot for its cell
+// (linear probing from the key's hash) and records where the run starts.
+__global__ __launch_bounds__(256) void table_insert_kernel(const uint64_t *__restrict__ ks,
+                                                           uint32_t n,
+                                                           dgrid::CellEntry *__restrict__ t,
+                                                           uint64_t mask) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n || (i > 0 && ks[i] == ks[i - 1])) return;
+    const uint64_t key = ks[i];
+    for (uint64_t s = dgrid::key_hash(key) & mask;; s = (s + 1) & mask) {
+        const unsigned long long prev = atomicCAS(
+            reinterpret_cast<unsigned long long *>(&t[s].key), (unsigned long long)dgrid::kEmptyKey,
+            (unsigned long long)key);
+        if (prev == dgrid::kEmptyKey || prev == key) {
+            t[s].start = i;
+            return;
+        }
+    }
+}
+
+// The last point of each run records where the run ends.
+__global__ __launch_bounds__(256) void table_end_kernel(const uint64_t *__restrict__ ks,
+                                                        uint32_t n,
+                                                        dgrid::CellEntry *__restrict__ t,
+                                                        uint64_t mask) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n || (i + 1 < n && ks[i + 1] == ks[i])) return;
+    const uint64_t key = ks[i];
+    for (uint64_t s = dgrid::key_hash(key) & mask;; s = (s + 1) & mask) {
+        const uint64_t k = t[s].key;
+        if (k == key) {
+            t[s].end = i + 1;
+            return;
+        }
+        if (k == dgrid::kEmptyKey) return; // (the insert pass placed every key)
+    }
 }
 
 // ---- certify: one wavefront per point ---------------------------------
@@ -488,9 +528,9 @@ __global__ __launch_bounds__(64) void certify_kernel(const float *__restrict__ p
     }
     uint32_t st = vcell::kOpen, examined = 0;
     bool decided = false, coincident = false;
-    for (int lev = 0; lev < dgrid::kLevels && !decided; ++lev) {
+    const int l0 = dgrid::first_level(gv, o);
+    for (int lev = l0; lev < dgrid::kLevels && !decided; ++lev) {
         const dgrid::GridLevel &lv = g.level[lev];
-        const uint32_t *start = gv.start[lev];
         const uint32_t *sorted = gv.sorted[lev];
         const int *h = hc[lev];
         for (int r = 0; r <= dgrid::kMaxRing && !decided; ++r) {
@@ -508,13 +548,9 @@ __global__ __launch_bounds__(64) void certify_kernel(const float *__restrict__ p
                     const bool shell = dx == -r || dx == r || dy == -r || dy == r || dz == -r ||
                                        dz == r;
                     if (shell && cx >= 0 && cx < (int)lv.dims[0] && cy >= 0 &&
-                        cy < (int)lv.dims[1] && cz >= 0 && cz < (int)lv.dims[2]) {
-                        const uint32_t cell = ((uint32_t)cz * lv.dims[1] + (uint32_t)cy) *
-                                                  lv.dims[0] +
-                                              (uint32_t)cx;
-                        b = start[cell];
-                        e = start[cell + 1];
-                    }
+                        cy < (int)lv.dims[1] && cz >= 0 && cz < (int)lv.dims[2])
+                        dgrid::cell_range(gv, lev, (uint32_t)cx, (uint32_t)cy, (uint32_t)cz, b,
+                                          e);
                 }
                 const uint32_t cnt = e - b;
                 examined += wsumu(cnt);
@@ -546,7 +582,7 @@ __global__ __launch_bounds__(64) void certify_kernel(const float *__restrict__ p
                                     mag += vcell::dabs(bb * q[m]);
                                 }
                                 surv = !(reach_q < 0.5 * d2 - 1e-14 * mag) &&
-                                       !(lev > 0 && dgrid::searched(g, lev, x, hc, rings));
+                                       !(lev > l0 && dgrid::searched(g, lev, x, hc, rings));
                             }
                         }
                     }
@@ -601,7 +637,7 @@ __global__ __launch_bounds__(64) void certify_kernel(const float *__restrict__ p
                 break;
             }
             if (r >= dgrid::kBoxRing && box) {
-                if (lev == 0) break;
+                if (lev == l0) break;
                 decided = true;
                 break;
             }
@@ -836,22 +872,23 @@ hipError_t launch_delaunay_certify(const float *points, uint32_t n, uint32_t *re
         hi[k] = (double)unordered(hm[3 + k]);
     }
     if (!dgrid::grid_geometry(lo, hi, n, g)) return hipErrorInvalidValue;
-    // each level: cell of every point, counts -> starts, points by cell
+    // each level: points sorted by cell key, then the table of occupied cells
+    const uint64_t slots = g.table_mask + 1;
     for (int l = 0; l < dgrid::kLevels; ++l) {
-        const uint64_t cells = g.level[l].num_cells;
-        hipLaunchKernelGGL(fill_kernel, grid1(cells + 1), dim3(256), 0, stream, s.counts,
-                           (uint64_t)cells + 1, 0u);
-        hipLaunchKernelGGL(cell_ids_kernel, grid1(n), dim3(256), 0, stream, points, n, g, l,
-                           s.ids, s.index, s.counts);
+        hipLaunchKernelGGL(cell_keys_kernel, grid1(n), dim3(256), 0, stream, points, n, g, l,
+                           s.keys, s.index);
+        hipLaunchKernelGGL(table_clear_kernel, grid1(slots), dim3(256), 0, stream, s.table[l],
+                           slots);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         size_t tb = s.temp_bytes;
-        e = rocprim::exclusive_scan(s.temp, tb, s.counts, s.start[l], 0u, (size_t)cells + 1,
-                                    rocprim::plus<uint32_t>(), stream);
+        e = rocprim::radix_sort_pairs(s.temp, tb, s.keys, s.keys_sorted, s.index, s.sorted[l],
+                                      (size_t)n, 0u, 63u, stream);
         if (e != hipSuccess) return e;
-        tb = s.temp_bytes;
-        e = rocprim::radix_sort_pairs(s.temp, tb, s.ids, s.ids_sorted, s.index, s.sorted[l],
-                                      (size_t)n, 0u, 32u, stream);
-        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(table_insert_kernel, grid1(n), dim3(256), 0, stream, s.keys_sorted, n,
+                           s.table[l], g.table_mask);
+        hipLaunchKernelGGL(table_end_kernel, grid1(n), dim3(256), 0, stream, s.keys_sorted, n,
+                           s.table[l], g.table_mask);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     // the geometry stays in the scratch for the merge (`g` lives until the
     // synchronisation below)
@@ -860,7 +897,7 @@ hipError_t launch_delaunay_certify(const float *points, uint32_t n, uint32_t *re
     GridView gv{};
     gv.g = g;
     for (int l = 0; l < dgrid::kLevels; ++l) {
-        gv.start[l] = s.start[l];
+        gv.table[l] = s.table[l];
         gv.sorted[l] = s.sorted[l];
     }
     hipLaunchKernelGGL(certify_kernel, dim3(n), dim3(64), 0, stream, points, n, gv,
@@ -900,7 +937,7 @@ hipError_t launch_delaunay_merge(const float *points, uint32_t n, void *grid_scr
     if (e != hipSuccess) return e;
     if ((e = hipStreamSynchronize(stream)) != hipSuccess) return e;
     for (int l = 0; l < dgrid::kLevels; ++l) {
-        gv.start[l] = gs.start[l];
+        gv.table[l] = gs.table[l];
         gv.sorted[l] = gs.sorted[l];
     }
     hipLaunchKernelGGL(init_kernel, dim3(1), dim3(64), 0, stream, nullptr, s.acc);

@@ -11,27 +11,37 @@
 namespace sdfoam_hip {
 namespace dgrid {
 
-// A hierarchy of uniform grids over the points: level 0 has about
-// kFineCellsPerPoint cells per point over the bounding box, each level above
-// is kLevelRatio times coarser per axis.  A cell is clipped ring by ring on
-// the finest level first and moves up a level when the rings it would still
-// need exceed kMaxRing (a point in a sparse region), so that dense and
-// sparse regions both see few candidates per cell.
-constexpr int kLevels = 3;
-constexpr double kLevelRatio = 4.0;
-constexpr double kFineCellsPerPoint = 27.0;
+// A hierarchy of sparse grids over the points, kLevelRatio times coarser
+// per axis from each level to the next: the coarsest has cells of about
+// twice the mean point spacing over the bounding box, the finest is
+// kLevelRatio^(kLevels-1) times finer, so that regions a million times denser
+// than the mean still have a level with a few points per cell.  Only
+// occupied cells are stored: a level is its points sorted by cell and an
+// open-addressing hash table from cell key to the cell's range of them.  A
+// cell starts on the finest level where its point's own grid cell holds
+// another point, is clipped ring by ring there, and moves up a level when
+// the rings it would still need exceed kMaxRing.
+constexpr int kLevels = 11;
+constexpr double kLevelRatio = 2.0;
 constexpr int kMaxRing = 6;  // rings per level
 constexpr int kMinRing = 2;  // rings on a level before moving up
 constexpr int kBoxRing = 2;  // from here, a cell still reaching the box on a
-                             // level above 0 is left open (hull points)
+                             // level above its first is left open (hull points)
 // Candidate points a cell may examine in all before it is left open (bounds
-// the slowest lane).
+// the slowest cell).
 constexpr uint32_t kMaxCandidates = 16384;
+constexpr uint32_t kAxisCells = (1u << 21) - 1; // cells per axis at most (21-bit keys)
+constexpr uint64_t kEmptyKey = ~0ull;
+
+struct alignas(16) CellEntry {
+    uint64_t key;        // cx | cy << 21 | cz << 42, kEmptyKey if the slot is free
+    uint32_t start, end; // the cell's points: sorted[start : end]
+};
 
 struct GridLevel {
     double h, inv_h; // cell edge
     uint32_t dims[3];
-    uint32_t num_cells;
+    uint32_t pad;
 };
 
 struct GridGeom {
@@ -40,18 +50,21 @@ struct GridGeom {
     double box_lo[3]; // clipping box: the bounding box grown by its extent
     double box_hi[3];
     GridLevel level[kLevels];
+    uint64_t table_mask; // hash table slots - 1 (the same for every level)
 };
 
 struct GridView {
     GridGeom g;
-    // level l: the points of cell c are sorted[l][start[l][c] : start[l][c + 1]]
-    const uint32_t *start[kLevels];
-    const uint32_t *sorted[kLevels];
+    const CellEntry *table[kLevels];
+    const uint32_t *sorted[kLevels]; // point ids by cell
 };
 
-// Cells of level 0 at most (every level has at most as many).
-inline uint64_t level_cell_capacity(uint32_t n) {
-    return (uint64_t)(kFineCellsPerPoint * 1.1 * (double)n) + 64;
+// Hash table slots: a power of two of at least twice the points, so that
+// every probe sequence meets a free slot.
+inline uint64_t table_slots(uint32_t n) {
+    uint64_t c = 64;
+    while (c < 2ull * n + 2) c <<= 1;
+    return c;
 }
 
 // The grids over the bounding box [lo, hi] of n points.  False if the box
@@ -71,30 +84,21 @@ inline bool grid_geometry(const double *lo, const double *hi, uint32_t n, GridGe
             vol *= hi[k] - lo[k];
             ++axes;
         }
-    double h = std::pow(vol / std::fmax(1.0, kFineCellsPerPoint * (double)n),
-                        1.0 / (double)(axes > 0 ? axes : 1));
-    h = std::fmax(h, ext * 1e-6);
-    const uint64_t cap = level_cell_capacity(n);
+    const double top = 2.0 * std::pow(vol / std::fmax(1.0, (double)n),
+                                      1.0 / (double)(axes > 0 ? axes : 1));
+    double h = std::fmax(top / std::pow(kLevelRatio, kLevels - 1), ext / (double)(kAxisCells - 1));
     for (int l = 0; l < kLevels; ++l) {
         GridLevel &lv = g.level[l];
-        for (;;) {
-            uint64_t cells = 1;
-            for (int k = 0; k < 3; ++k) {
-                const double d = std::ceil((hi[k] - lo[k]) / h);
-                lv.dims[k] = (uint32_t)std::fmax(1.0, std::fmin(d, 2097152.0));
-                cells *= lv.dims[k];
-            }
-            if (cells <= cap) {
-                lv.num_cells = (uint32_t)cells;
-                break;
-            }
-            h *= 1.05;
-        }
         lv.h = h;
         lv.inv_h = 1.0 / h;
+        for (int k = 0; k < 3; ++k)
+            lv.dims[k] = (uint32_t)std::fmax(1.0, std::fmin(std::ceil((hi[k] - lo[k]) / h),
+                                                          (double)kAxisCells));
+        lv.pad = 0;
         h *= kLevelRatio;
     }
     g.slack = 1e-12 * (mag + ext);
+    g.table_mask = table_slots(n) - 1;
     for (int k = 0; k < 3; ++k) {
         g.lo[k] = lo[k];
         g.box_lo[k] = lo[k] - ext;
@@ -110,12 +114,59 @@ SDF_HD int axis_cell(double x, double lo, double inv_h, uint32_t dim) {
     return (int)(u < dim ? u : dim - 1);
 }
 
-SDF_HD uint32_t cell_index(const GridGeom &g, int l, double x, double y, double z) {
+SDF_HD uint64_t cell_key(uint32_t cx, uint32_t cy, uint32_t cz) {
+    return (uint64_t)cx | ((uint64_t)cy << 21) | ((uint64_t)cz << 42);
+}
+
+SDF_HD uint64_t point_key(const GridGeom &g, int l, double x, double y, double z) {
     const GridLevel &lv = g.level[l];
-    const uint32_t cx = (uint32_t)axis_cell(x, g.lo[0], lv.inv_h, lv.dims[0]);
-    const uint32_t cy = (uint32_t)axis_cell(y, g.lo[1], lv.inv_h, lv.dims[1]);
-    const uint32_t cz = (uint32_t)axis_cell(z, g.lo[2], lv.inv_h, lv.dims[2]);
-    return (cz * lv.dims[1] + cy) * lv.dims[0] + cx;
+    return cell_key((uint32_t)axis_cell(x, g.lo[0], lv.inv_h, lv.dims[0]),
+                    (uint32_t)axis_cell(y, g.lo[1], lv.inv_h, lv.dims[1]),
+                    (uint32_t)axis_cell(z, g.lo[2], lv.inv_h, lv.dims[2]));
+}
+
+// 64-bit mixing (the splitmix64 finaliser) for the table slot.
+SDF_HD uint64_t key_hash(uint64_t k) {
+    k ^= k >> 30;
+    k *= 0xbf58476d1ce4e5b9ull;
+    k ^= k >> 27;
+    k *= 0x94d049bb133111ebull;
+    k ^= k >> 31;
+    return k;
+}
+
+// The points of cell (cx, cy, cz) of level l: sorted[l][b : e] (empty if
+// the cell holds none).
+SDF_HD void cell_range(const GridView &gv, int l, uint32_t cx, uint32_t cy, uint32_t cz,
+                       uint32_t &b, uint32_t &e) {
+    const uint64_t key = cell_key(cx, cy, cz);
+    const uint64_t mask = gv.g.table_mask;
+    const CellEntry *t = gv.table[l];
+    b = e = 0;
+    for (uint64_t s = key_hash(key) & mask;; s = (s + 1) & mask) {
+        const CellEntry en = t[s];
+        if (en.key == key) {
+            b = en.start;
+            e = en.end;
+            return;
+        }
+        if (en.key == kEmptyKey) return;
+    }
+}
+
+// The first level of point x: the finest whose grid cell around x holds
+// another point (the coarsest if none does).
+SDF_HD int first_level(const GridView &gv, const double *x) {
+    const GridGeom &g = gv.g;
+    for (int l = 0; l < kLevels - 1; ++l) {
+        const GridLevel &lv = g.level[l];
+        uint32_t b, e;
+        cell_range(gv, l, (uint32_t)axis_cell(x[0], g.lo[0], lv.inv_h, lv.dims[0]),
+                   (uint32_t)axis_cell(x[1], g.lo[1], lv.inv_h, lv.dims[1]),
+                   (uint32_t)axis_cell(x[2], g.lo[2], lv.inv_h, lv.dims[2]), b, e);
+        if (e - b >= 2) return l;
+    }
+    return kLevels - 1;
 }
 
 // Bounding box of the cell's vertices, grown by their error bounds: a
@@ -193,9 +244,9 @@ SDF_HD uint32_t certify_cell(const float *p, uint32_t i, const GridView &gv, vce
             hc[l][k] = axis_cell(o[k], g.lo[k], g.level[l].inv_h, g.level[l].dims[k]);
     }
     uint32_t examined = 0;
-    for (int l = 0; l < kLevels; ++l) {
+    const int l0 = first_level(gv, o);
+    for (int l = l0; l < kLevels; ++l) {
         const GridLevel &lv = g.level[l];
-        const uint32_t *start = gv.start[l];
         const uint32_t *sorted = gv.sorted[l];
         const int *h = hc[l];
         for (int r = 0; r <= kMaxRing; ++r) {
@@ -211,9 +262,8 @@ SDF_HD uint32_t certify_cell(const float *p, uint32_t i, const GridView &gv, vce
                     for (int dx = -r; dx <= r; dx += step) {
                         const int cx = h[0] + dx;
                         if (cx < 0 || cx >= (int)lv.dims[0]) continue;
-                        const uint32_t c = ((uint32_t)cz * lv.dims[1] + (uint32_t)cy) * lv.dims[0] +
-                                           (uint32_t)cx;
-                        const uint32_t begin = start[c], end = start[c + 1];
+                        uint32_t begin, end;
+                        cell_range(gv, l, (uint32_t)cx, (uint32_t)cy, (uint32_t)cz, begin, end);
                         examined += end - begin;
                         if (examined > kMaxCandidates) return vcell::kOpen;
                         for (uint32_t k = begin; k < end; ++k) {
@@ -238,7 +288,7 @@ SDF_HD uint32_t certify_cell(const float *p, uint32_t i, const GridView &gv, vce
                                 mag += vcell::dabs(b * q[m]);
                             }
                             if (reach_q < 0.5 * d2 - 1e-14 * mag) continue;
-                            if (l > 0 && searched(g, l, x, hc, rings)) continue;
+                            if (l > l0 && searched(g, l, x, hc, rings)) continue;
                             bool cut = false;
                             if (!vcell::clip(cell, q, (int32_t)j, &cut)) return cell.status;
                             if (cut) {
@@ -259,7 +309,7 @@ SDF_HD uint32_t certify_cell(const float *p, uint32_t i, const GridView &gv, vce
             const double reach2 = all ? INFINITY : (reach > 0.0 ? reach * reach : 0.0);
             if (4.0 * mr2 * (1.0 + 1e-9) < reach2) return vcell::settle(cell, reach2);
             if (r >= kBoxRing && touches_box(cell)) {
-                if (l == 0) break;
+                if (l == l0) break;
                 return vcell::kOpen;
             }
             // rings this level would still need if the cell shrank no more
@@ -307,10 +357,9 @@ SDF_HD uint32_t sphere_empty(const float *p, const uint32_t *v, const GridView &
             hi_c[k] = axis_cell(o[k] + ctr[k] + r, g.lo[k], lv.inv_h, lv.dims[k]);
             cells *= (double)(hi_c[k] - lo_c[k] + 1);
         }
-        if (cells <= 4096.0 || l == kLevels - 1) break;
+        if (cells <= 512.0 || l == kLevels - 1) break;
     }
     const GridLevel &lv = g.level[l];
-    const uint32_t *start = gv.start[l];
     const uint32_t *sorted = gv.sorted[l];
     for (int cz = lo_c[2]; cz <= hi_c[2]; ++cz)
         for (int cy = lo_c[1]; cy <= hi_c[1]; ++cy)
@@ -326,10 +375,9 @@ SDF_HD uint32_t sphere_empty(const float *p, const uint32_t *v, const GridView &
                     dd += e * e;
                 }
                 if (dd > r * r) continue;
-                const uint32_t c =
-                    ((uint32_t)cz * lv.dims[1] + (uint32_t)cy) * lv.dims[0] + (uint32_t)cx;
-                const uint32_t end = start[c + 1];
-                for (uint32_t k = start[c]; k < end; ++k) {
+                uint32_t begin, end;
+                cell_range(gv, l, (uint32_t)cx, (uint32_t)cy, (uint32_t)cz, begin, end);
+                for (uint32_t k = begin; k < end; ++k) {
                     const uint32_t j = sorted[k];
                     if (j == v[0] || j == v[1] || j == v[2] || j == v[3]) continue;
                     double q[3];

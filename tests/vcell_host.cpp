@@ -2,7 +2,9 @@
 // sdfoam_amd/csrc/delaunay_grid.h) for the CPU tests: the same code the
 // kernels run, driven one cell or one candidate at a time.
 #include <cmath>
+#include <algorithm>
 #include <cstdint>
+#include <utility>
 #include <vector>
 
 #include "../sdfoam_amd/csrc/delaunay_grid.h"
@@ -13,13 +15,14 @@ namespace dgrid = sdfoam_hip::dgrid;
 namespace {
 // the grids of the last vc_grid call
 dgrid::GridGeom g_geom;
-std::vector<uint32_t> g_start[dgrid::kLevels], g_sorted[dgrid::kLevels];
+std::vector<dgrid::CellEntry> g_table[dgrid::kLevels];
+std::vector<uint32_t> g_sorted[dgrid::kLevels];
 
 dgrid::GridView view() {
     dgrid::GridView v{};
     v.g = g_geom;
     for (int l = 0; l < dgrid::kLevels; ++l) {
-        v.start[l] = g_start[l].data();
+        v.table[l] = g_table[l].data();
         v.sorted[l] = g_sorted[l].data();
     }
     return v;
@@ -85,9 +88,10 @@ int vc_insphere(const double *a, const double *b, const double *c, const double 
     return in_sphere(a, b, c, q);
 }
 
-// The device's grids over n points (bounding box of the floats, each
-// level's cells by a stable counting sort); returns the cells of level 0
-// (dims: its dimensions), 0 if the box is degenerate.
+// The device's grids over n points (bounding box of the floats; each
+// level's points stably sorted by cell key, and the hash table of occupied
+// cells, filled by the same probing); returns the number of occupied cells
+// of level 0 (dims: its dimensions), 0 if the box is degenerate.
 int vc_grid(const float *points, uint32_t n, uint32_t *dims) {
     double lo[3] = {INFINITY, INFINITY, INFINITY}, hi[3] = {-INFINITY, -INFINITY, -INFINITY};
     for (uint32_t i = 0; i < n; ++i)
@@ -96,23 +100,34 @@ int vc_grid(const float *points, uint32_t n, uint32_t *dims) {
             hi[k] = std::fmax(hi[k], (double)points[3 * i + k]);
         }
     if (!dgrid::grid_geometry(lo, hi, n, g_geom)) return 0;
-    std::vector<uint32_t> id(n);
+    const uint64_t slots = g_geom.table_mask + 1;
+    std::vector<std::pair<uint64_t, uint32_t>> keyed(n);
+    int occupied0 = 0;
     for (int l = 0; l < dgrid::kLevels; ++l) {
-        const uint32_t cells = g_geom.level[l].num_cells;
-        std::vector<uint32_t> &start = g_start[l];
-        start.assign(cells + 1, 0u);
-        for (uint32_t i = 0; i < n; ++i) {
-            id[i] = dgrid::cell_index(g_geom, l, points[3 * i], points[3 * i + 1],
-                                      points[3 * i + 2]);
-            ++start[id[i] + 1];
+        for (uint32_t i = 0; i < n; ++i)
+            keyed[i] = {dgrid::point_key(g_geom, l, points[3 * i], points[3 * i + 1],
+                                         points[3 * i + 2]),
+                        i};
+        std::stable_sort(keyed.begin(), keyed.end(),
+                         [](const auto &a, const auto &b) { return a.first < b.first; });
+        g_sorted[l].resize(n);
+        for (uint32_t t = 0; t < n; ++t) g_sorted[l][t] = keyed[t].second;
+        std::vector<dgrid::CellEntry> &table = g_table[l];
+        table.assign(slots, dgrid::CellEntry{dgrid::kEmptyKey, 0u, 0u});
+        int occupied = 0;
+        for (uint32_t t = 0; t < n; ++t) {
+            if (t > 0 && keyed[t].first == keyed[t - 1].first) continue;
+            uint32_t e = t + 1;
+            while (e < n && keyed[e].first == keyed[t].first) ++e;
+            uint64_t sl = dgrid::key_hash(keyed[t].first) & g_geom.table_mask;
+            while (table[sl].key != dgrid::kEmptyKey) sl = (sl + 1) & g_geom.table_mask;
+            table[sl] = dgrid::CellEntry{keyed[t].first, t, e};
+            ++occupied;
         }
-        for (uint32_t c = 0; c < cells; ++c) start[c + 1] += start[c];
-        std::vector<uint32_t> cur(start.begin(), start.end() - 1);
-        g_sorted[l].assign(n, 0u);
-        for (uint32_t i = 0; i < n; ++i) g_sorted[l][cur[id[i]]++] = i;
+        if (l == 0) occupied0 = occupied;
     }
     for (int k = 0; k < 3; ++k) dims[k] = g_geom.level[0].dims[k];
-    return (int)g_geom.level[0].num_cells;
+    return occupied0;
 }
 
 // certify_cell for every point on the last grid: status [n], coincident
