@@ -12,6 +12,8 @@ import os
 from .build import LIB_PATH
 
 SDF_OK = 0
+SDF_E_INVALID = 1
+SDF_E_HIP = 2
 SDF_ALPHA_STANDARD = 0
 SDF_ALPHA_NEUS = 1
 SDF_ATTR_F32 = 0

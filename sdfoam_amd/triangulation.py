@@ -182,8 +182,12 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
     with torch.cuda.device(dev):
         for _ in range(2):
             reports = torch.empty((cap, 4), dtype=torch.int32, device=dev)
-            check(L.sdf_delaunay_certify(ptr(pts), n, ptr(reports), cap, ptr(open_pts), counts,
-                                         gptr, gbytes, stream))
+            rc = L.sdf_delaunay_certify(ptr(pts), n, ptr(reports), cap, ptr(open_pts), counts,
+                                        gptr, gbytes, stream)
+            if rc == _lib.SDF_E_INVALID:
+                # no volume or non-finite points: Qhull on every point decides
+                raise _Undecided(L.sdf_last_error().decode())
+            check(rc)
             if counts[0] <= cap:
                 break
             cap = int(counts[0])
@@ -194,7 +198,11 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
         # the open points, in index order, through Qhull on the host
         U = torch.sort(open_pts[:nu])[0]
         u_np = U.cpu().numpy()
-        simplices, nbr_u = qhull_tetrahedra(pts[U.long()].cpu().numpy())
+        try:
+            simplices, nbr_u = qhull_tetrahedra(pts[U.long()].cpu().numpy())
+        except TriangulationFailedError as e:
+            # a degenerate open subset: Qhull on every point decides
+            raise _Undecided(str(e)) from None
         hull_faces = int((nbr_u < 0).sum())
         cand = torch.from_numpy(np.ascontiguousarray(u_np[simplices], dtype=np.int32)).to(dev)
         m = int(cand.shape[0])

@@ -249,3 +249,41 @@ def test_triangulation_methods_agree(dev):
         assert torch.equal(getattr(a, k)().view(torch.int32), getattr(b, k)().view(torch.int32)), k
     with pytest.raises(ValueError, match="unknown triangulation method"):
         sdfoam_amd.Triangulation(pts, method="cgal")
+
+
+def test_gpu_delaunay_small_and_degenerate_inputs(dev):
+    """32 points (the minimum) on the GPU path; a cubic lattice, where every
+    cell is cospherical with its neighbours, still gives a Delaunay
+    tetrahedralisation (by whichever path); coplanar points fail as Qhull
+    does."""
+    import torch
+    from scipy.spatial import ConvexHull
+
+    import sdfoam_amd
+    from test_delaunay_cells import assert_delaunay
+
+    rng = np.random.default_rng(32)
+    pts = rng.normal(size=(32, 3)).astype(np.float32)
+    tri = sdfoam_amd.Triangulation(torch.from_numpy(pts).to(dev))
+    assert tri.last_method == "gpu"
+    perm = tri.permutation().to(torch.long).cpu().numpy()
+    tets = _np(tri.tets()).reshape(-1, 4).astype(np.int64)
+    assert_delaunay(pts[perm], tets, ConvexHull(pts.astype(np.float64)).volume)
+    g = np.arange(8, dtype=np.float32)
+    lattice = np.stack(np.meshgrid(g, g, g, indexing="ij"), axis=-1).reshape(-1, 3)
+    tri = sdfoam_amd.Triangulation(torch.from_numpy(lattice).to(dev))
+    assert tri.last_method in ("gpu", "qhull")
+    perm = tri.permutation().to(torch.long).cpu().numpy()
+    tets = _np(tri.tets()).reshape(-1, 4).astype(np.int64)
+    p = lattice[perm].astype(np.float64)
+    a, b, c, d = (p[tets[:, k]] for k in range(4))
+    vol = np.einsum("ij,ij->i", np.cross(b - a, c - a), d - a) / 6.0
+    # Qhull's triangulated output may hold flat tets on cospherical groups;
+    # the rest must tile the cube and have empty circumspheres
+    assert (vol >= 0).all() and abs(vol.sum() - 7.0 ** 3) < 1e-9
+    solid = vol > 0
+    assert_delaunay(lattice[perm], tets[solid], 7.0 ** 3)
+    flat = rng.normal(size=(100, 3)).astype(np.float32)
+    flat[:, 2] = 0.0
+    with pytest.raises(sdfoam_amd.TriangulationFailedError):
+        sdfoam_amd.Triangulation(torch.from_numpy(flat).to(dev))
