@@ -497,8 +497,10 @@ __device__ bool wave_touches_box(const WaveCell &c, const WaveShared &sh) {
 
 // counters: 0 report rows asked for, 1 open points, 2 undecided cells,
 // 3 cells over the fixed capacity, 4 coincident point pairs seen (twice).
-// One 64-thread block per point.
-__global__ __launch_bounds__(64) void certify_kernel(const float *__restrict__ p, uint32_t n,
+// One 64-thread block per point.  Four waves per SIMD (128 VGPRs, a few
+// hundred bytes of spills) run it ~20% faster than the two its natural
+// register count allows.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void certify_kernel(const float *__restrict__ p, uint32_t n,
                                                      GridView gv, uint32_t *__restrict__ reports,
                                                      uint64_t report_capacity,
                                                      unsigned long long *__restrict__ counters,
