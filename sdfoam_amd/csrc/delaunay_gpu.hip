@@ -1,12 +1,12 @@
 // The Delaunay tetrahedralisation on the GPU, by certified Voronoi cells.
 //
-// certify: a uniform grid over the points (about two points per grid cell),
-// then one lane per point clips its Voronoi cell (voronoi_cell.h) by the
-// points of the grid rings around it until every point within twice the
-// cell's farthest vertex has been seen.  A cell closed by bisectors alone,
-// every sign decided, is certified: each of its vertices is a Delaunay
-// tetrahedron, written as (point, a, b, c).  The other points (the hull, the
-// layer under it, undecided signs) are listed as open.
+// certify: sparse grids over the points (delaunay_grid.h), then one
+// wavefront per point clips its Voronoi cell by the points of the grid rings
+// around it, with the decisions of vcell::clip (voronoi_cell.h), until every
+// point within twice the cell's farthest vertex has been seen.  A cell closed
+// by bisectors alone, every sign decided, is certified: each of its vertices
+// is a Delaunay tetrahedron, written as (point, a, b, c).  The other points
+// (the hull, the layer under it, undecided signs) are listed as open.
 //
 // merge: the caller triangulates the open points on its own (a few percent
 // of them); a candidate tetrahedron whose circumsphere holds no point at all

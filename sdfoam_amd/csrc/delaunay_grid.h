@@ -1,6 +1,9 @@
 // The point grids of the GPU Delaunay and the two per-item steps that use
-// them (host and device): one point's certified Voronoi cell, and one
-// candidate tetrahedron's empty-circumsphere test.
+// them (host and device): one point's certified Voronoi cell (certify_cell:
+// the one-cell statement of the decisions certify_kernel makes with a whole
+// wavefront per cell, run by the host tests), and one candidate
+// tetrahedron's empty-circumsphere test (sphere_empty, run by
+// keep_empty_kernel and the host tests).
 #pragma once
 
 #include <cmath>
