@@ -32,7 +32,7 @@ constexpr int kBoxRing = 2;  // from here, a cell still reaching the box on a
                              // level above its first is left open (hull points)
 // Candidate points a cell may examine in all before it is left open (bounds
 // the slowest cell).
-constexpr uint32_t kMaxCandidates = 16384;
+constexpr uint32_t kMaxCandidates = 65536;
 constexpr uint32_t kAxisCells = (1u << 21) - 1; // cells per axis at most (21-bit keys)
 constexpr uint64_t kEmptyKey = ~0ull;
 
