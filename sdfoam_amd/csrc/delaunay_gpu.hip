@@ -676,28 +676,46 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
     }
 }
 
-// 1 if no point lies strictly inside the circumsphere of candidate t, 0 if
-// one does, 2 if the tetrahedron is invalid, flat, or a sign could not be
-// decided.
+// One 64-thread block per candidate t: 1 if no point lies strictly inside
+// its circumsphere, 0 if one does, 2 if the tetrahedron is invalid or flat
+// or, with none inside, a certified point's sign is undecided
+// (dgrid::sphere_empty).  The lanes take the sphere's cell columns in turn
+// and stop together once one finds a point inside.
 __global__ __launch_bounds__(64) void keep_empty_kernel(const float *__restrict__ p, uint32_t n,
                                                         GridView gv,
                                                         const uint32_t *__restrict__ cand,
                                                         uint32_t m,
                                                         const uint32_t *__restrict__ status,
                                                         uint32_t *__restrict__ keep) {
-    const uint32_t t = blockIdx.x * 64u + threadIdx.x;
+    const uint32_t t = blockIdx.x;
     if (t >= m) return;
+    const uint32_t l = threadIdx.x & 63u;
     uint32_t v[4];
     bool valid = true;
     for (int k = 0; k < 4; ++k) {
         v[k] = cand[4ull * t + k];
         valid = valid && v[k] < n;
     }
-    if (!valid) {
-        keep[t] = 2u;
+    dgrid::Sphere S;
+    if (!valid || !dgrid::sphere_setup(p, v, gv, S)) {
+        if (l == 0) keep[t] = 2u;
         return;
     }
-    keep[t] = dgrid::sphere_empty(p, v, gv, status);
+    const uint32_t cols = dgrid::sphere_columns(S);
+    bool inside = false, undecided = false;
+    for (uint32_t base = 0; base < cols; base += 64) {
+        if (base + l < cols) {
+            const uint32_t r = dgrid::sphere_scan_column(p, v, gv, status, S, base + l);
+            inside = r == 0u;
+            undecided = undecided || r == 2u;
+        }
+        if (__builtin_amdgcn_ballot_w64(inside)) {
+            inside = true;
+            break;
+        }
+    }
+    undecided = __builtin_amdgcn_ballot_w64(undecided) != 0ull;
+    if (l == 0) keep[t] = inside ? 0u : (undecided ? 2u : 1u);
 }
 
 // Row t of [reports; candidates] survives: a report (i, a, b, c) when i is
@@ -944,8 +962,8 @@ hipError_t launch_delaunay_merge(const float *points, uint32_t n, void *grid_scr
     }
     hipLaunchKernelGGL(init_kernel, dim3(1), dim3(64), 0, stream, nullptr, s.acc);
     if (m > 0)
-        hipLaunchKernelGGL(keep_empty_kernel, dim3((unsigned)((m + 63u) / 64u)), dim3(64), 0,
-                           stream, points, n, gv, cand, (uint32_t)m, gs.status, s.keep);
+        hipLaunchKernelGGL(keep_empty_kernel, dim3((unsigned)m), dim3(64), 0, stream, points, n,
+                           gv, cand, (uint32_t)m, gs.status, s.keep);
     const uint64_t rows = nr + m;
     uint32_t last[2] = {0, 0};
     if (rows > 0) {

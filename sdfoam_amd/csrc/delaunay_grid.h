@@ -323,76 +323,115 @@ SDF_HD uint32_t certify_cell(const float *p, uint32_t i, const GridView &gv, vce
     return vcell::kOpen;
 }
 
-// Candidate tetrahedron v[4] (ids below n): 1 if no point lies strictly
-// inside its circumsphere, 0 if one does, 2 if it is flat or a sign could
-// not be decided.  A point exactly on the sphere (cospherical with the
-// candidate) is passed over when it is open (status not certified): the
-// candidates' own triangulation of the open points already chose among
-// such points; a certified one is undecided.
-SDF_HD uint32_t sphere_empty(const float *p, const uint32_t *v, const GridView &gv,
-                             const uint32_t *status) {
+// The circumsphere of a candidate tetrahedron v[4] (ids below n) and the
+// part of a grid level to scan for points inside it: (y, z) columns of cells
+// over the sphere's box, each scanned along x over the cells the sphere
+// reaches in that column.
+struct Sphere {
+    double o[3];        // v[0]
+    vcell::Plane pl[3]; // bisectors of v[0] and v[1..3] (normals: relative positions)
+    double ctr[3];      // circumcentre relative to o
+    double r;           // radius, grown by the circumcentre's error bound
+    int l;              // grid level
+    int lo_c[3], hi_c[3];
+};
+
+// False if the tetrahedron is flat (no circumcentre).
+SDF_HD bool sphere_setup(const float *p, const uint32_t *v, const GridView &gv, Sphere &S) {
     const GridGeom &g = gv.g;
-    const double o[3] = {(double)p[3ull * v[0]], (double)p[3ull * v[0] + 1],
-                         (double)p[3ull * v[0] + 2]};
-    vcell::Plane pl[3];
+    for (int k = 0; k < 3; ++k) S.o[k] = (double)p[3ull * v[0] + k];
     for (int s = 0; s < 3; ++s) {
-        for (int k = 0; k < 3; ++k) pl[s].n[k] = (double)p[3ull * v[s + 1] + k] - o[k];
-        pl[s].c = 0.5 * (pl[s].n[0] * pl[s].n[0] + pl[s].n[1] * pl[s].n[1] +
-                         pl[s].n[2] * pl[s].n[2]);
-        pl[s].point = (int32_t)v[s + 1];
+        for (int k = 0; k < 3; ++k) S.pl[s].n[k] = (double)p[3ull * v[s + 1] + k] - S.o[k];
+        S.pl[s].c = 0.5 * (S.pl[s].n[0] * S.pl[s].n[0] + S.pl[s].n[1] * S.pl[s].n[1] +
+                           S.pl[s].n[2] * S.pl[s].n[2]);
+        S.pl[s].point = (int32_t)v[s + 1];
     }
     // the circumcentre (relative to o) is where the three bisectors meet;
     // its error grows with the conditioning of that system
-    double ctr[3];
-    if (!vcell::meet(pl[0], pl[1], pl[2], ctr)) return 2u;
+    if (!vcell::meet(S.pl[0], S.pl[1], S.pl[2], S.ctr)) return false;
     double perm;
-    const double d = vcell::det3(pl[0].n, pl[1].n, pl[2].n, perm);
+    const double d = vcell::det3(S.pl[0].n, S.pl[1].n, S.pl[2].n, perm);
     const double cond = perm / vcell::dabs(d);
-    const double r2 = ctr[0] * ctr[0] + ctr[1] * ctr[1] + ctr[2] * ctr[2];
-    const double r = sqrt(r2) * (1.0 + 1e-6 + 1e-13 * cond) + g.slack;
-    // the finest level that covers the sphere's box with few cells
-    int l = 0, lo_c[3], hi_c[3];
-    for (;; ++l) {
-        const GridLevel &lv = g.level[l];
-        double cells = 1.0;
+    const double r2 = S.ctr[0] * S.ctr[0] + S.ctr[1] * S.ctr[1] + S.ctr[2] * S.ctr[2];
+    S.r = sqrt(r2) * (1.0 + 1e-6 + 1e-13 * cond) + g.slack;
+    // the finest level whose cells cover the sphere's box in few columns
+    for (S.l = 0;; ++S.l) {
+        const GridLevel &lv = g.level[S.l];
         for (int k = 0; k < 3; ++k) {
-            lo_c[k] = axis_cell(o[k] + ctr[k] - r, g.lo[k], lv.inv_h, lv.dims[k]);
-            hi_c[k] = axis_cell(o[k] + ctr[k] + r, g.lo[k], lv.inv_h, lv.dims[k]);
-            cells *= (double)(hi_c[k] - lo_c[k] + 1);
+            S.lo_c[k] = axis_cell(S.o[k] + S.ctr[k] - S.r, g.lo[k], lv.inv_h, lv.dims[k]);
+            S.hi_c[k] = axis_cell(S.o[k] + S.ctr[k] + S.r, g.lo[k], lv.inv_h, lv.dims[k]);
         }
-        if (cells <= 512.0 || l == kLevels - 1) break;
+        const double cols =
+            (double)(S.hi_c[1] - S.lo_c[1] + 1) * (double)(S.hi_c[2] - S.lo_c[2] + 1);
+        if (cols <= 256.0 || S.l == kLevels - 1) break;
     }
-    const GridLevel &lv = g.level[l];
-    const uint32_t *sorted = gv.sorted[l];
-    for (int cz = lo_c[2]; cz <= hi_c[2]; ++cz)
-        for (int cy = lo_c[1]; cy <= hi_c[1]; ++cy)
-            for (int cx = lo_c[0]; cx <= hi_c[0]; ++cx) {
-                // skip grid cells the sphere does not reach
-                const int cc[3] = {cx, cy, cz};
-                double dd = 0.0;
-                for (int k = 0; k < 3; ++k) {
-                    const double blo = g.lo[k] + (double)cc[k] * lv.h - o[k] - g.slack;
-                    const double bhi = blo + lv.h + 2.0 * g.slack;
-                    const double e =
-                        ctr[k] < blo ? blo - ctr[k] : (ctr[k] > bhi ? ctr[k] - bhi : 0.0);
-                    dd += e * e;
-                }
-                if (dd > r * r) continue;
-                uint32_t begin, end;
-                cell_range(gv, l, (uint32_t)cx, (uint32_t)cy, (uint32_t)cz, begin, end);
-                for (uint32_t k = begin; k < end; ++k) {
-                    const uint32_t j = sorted[k];
-                    if (j == v[0] || j == v[1] || j == v[2] || j == v[3]) continue;
-                    double q[3];
-                    for (int m = 0; m < 3; ++m) q[m] = (double)p[3ull * j + m] - o[m];
-                    const double e0 = q[0] - ctr[0], e1 = q[1] - ctr[1], e2 = q[2] - ctr[2];
-                    if (e0 * e0 + e1 * e1 + e2 * e2 > r * r) continue; // clearly outside
-                    const int s = vcell::in_sphere(pl[0].n, pl[1].n, pl[2].n, q);
-                    if (s > 0) return 0u;
-                    if (s == 0 && status[j] == vcell::kCertified) return 2u;
-                }
-            }
-    return 1u;
+    return true;
+}
+
+SDF_HD uint32_t sphere_columns(const Sphere &S) {
+    return (uint32_t)(S.hi_c[1] - S.lo_c[1] + 1) * (uint32_t)(S.hi_c[2] - S.lo_c[2] + 1);
+}
+
+// Points of column `col` against the sphere: 0 if one lies strictly inside,
+// 2 if none does but one's sign is undecided and it is certified (an open
+// point exactly on the sphere is passed over: the candidates' own
+// triangulation of the open points already chose among such points), 1
+// otherwise.
+SDF_HD uint32_t sphere_scan_column(const float *p, const uint32_t *v, const GridView &gv,
+                                   const uint32_t *status, const Sphere &S, uint32_t col) {
+    const GridGeom &g = gv.g;
+    const GridLevel &lv = g.level[S.l];
+    const uint32_t ny = (uint32_t)(S.hi_c[1] - S.lo_c[1] + 1);
+    const int cy = S.lo_c[1] + (int)(col % ny), cz = S.lo_c[2] + (int)(col / ny);
+    // squared distance from the centre to the column's y and z extent
+    double rem = S.r * S.r;
+    const int cc[3] = {0, cy, cz};
+    for (int k = 1; k < 3; ++k) {
+        const double blo = g.lo[k] + (double)cc[k] * lv.h - S.o[k] - g.slack;
+        const double bhi = blo + lv.h + 2.0 * g.slack;
+        const double e =
+            S.ctr[k] < blo ? blo - S.ctr[k] : (S.ctr[k] > bhi ? S.ctr[k] - bhi : 0.0);
+        rem -= e * e;
+    }
+    if (rem < 0.0) return 1u;
+    const double w = sqrt(rem);
+    const int x0 = axis_cell(S.o[0] + S.ctr[0] - w - g.slack, g.lo[0], lv.inv_h, lv.dims[0]);
+    const int x1 = axis_cell(S.o[0] + S.ctr[0] + w + g.slack, g.lo[0], lv.inv_h, lv.dims[0]);
+    const uint32_t *sorted = gv.sorted[S.l];
+    uint32_t res = 1u;
+    for (int cx = x0 > S.lo_c[0] ? x0 : S.lo_c[0]; cx <= (x1 < S.hi_c[0] ? x1 : S.hi_c[0]); ++cx) {
+        uint32_t begin, end;
+        cell_range(gv, S.l, (uint32_t)cx, (uint32_t)cy, (uint32_t)cz, begin, end);
+        for (uint32_t k = begin; k < end; ++k) {
+            const uint32_t j = sorted[k];
+            if (j == v[0] || j == v[1] || j == v[2] || j == v[3]) continue;
+            double q[3];
+            for (int m = 0; m < 3; ++m) q[m] = (double)p[3ull * j + m] - S.o[m];
+            const double e0 = q[0] - S.ctr[0], e1 = q[1] - S.ctr[1], e2 = q[2] - S.ctr[2];
+            if (e0 * e0 + e1 * e1 + e2 * e2 > S.r * S.r) continue; // clearly outside
+            const int s = vcell::in_sphere(S.pl[0].n, S.pl[1].n, S.pl[2].n, q);
+            if (s > 0) return 0u;
+            if (s == 0 && status[j] == vcell::kCertified) res = 2u;
+        }
+    }
+    return res;
+}
+
+// Candidate tetrahedron v[4] (ids below n): 1 if no point lies strictly
+// inside its circumsphere, 0 if one does, 2 if it is flat or, with none
+// inside, a certified point's sign could not be decided.
+SDF_HD uint32_t sphere_empty(const float *p, const uint32_t *v, const GridView &gv,
+                             const uint32_t *status) {
+    Sphere S;
+    if (!sphere_setup(p, v, gv, S)) return 2u;
+    uint32_t res = 1u;
+    const uint32_t cols = sphere_columns(S);
+    for (uint32_t c = 0; c < cols; ++c) {
+        const uint32_t r = sphere_scan_column(p, v, gv, status, S, c);
+        if (r == 0u) return 0u;
+        if (r == 2u) res = 2u;
+    }
+    return res;
 }
 
 } // namespace dgrid
