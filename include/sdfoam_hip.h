@@ -369,7 +369,7 @@ int sdf_delaunay_tables(const float *points, uint32_t num_points,
  * lost but the rows past it; call again with room for counts[0]), open
  * points, undecided cells, cells over the fixed capacity, coincident
  * points seen (nonzero: duplicate points).  scratch 256-byte aligned, kept
- * for sdf_delaunay_merge.  Synchronizes the stream. */
+ * for sdf_delaunay_merge.  32 to 2^26 points.  Synchronizes the stream. */
 size_t sdf_delaunay_certify_scratch_bytes(uint32_t num_points);
 int sdf_delaunay_certify(const float *points, uint32_t num_points,
                          uint32_t *reports, uint64_t report_capacity,
@@ -384,7 +384,8 @@ int sdf_delaunay_certify(const float *points, uint32_t num_points,
  * (host): T, hull faces, invalid or undecided rows, faces of three tets.
  * certify_scratch: the scratch of the sdf_delaunay_certify call that made
  * the reports.  Fails when a candidate's sign cannot be decided or
- * T > tet_capacity (result[0] then holds T).  Synchronizes the stream. */
+ * T > tet_capacity (result[0] then holds T).  At most 2^26 candidates.
+ * Synchronizes the stream. */
 size_t sdf_delaunay_merge_scratch_bytes(uint32_t num_points, uint64_t num_reports,
                                         uint64_t num_candidates, uint64_t tet_capacity);
 int sdf_delaunay_merge(const float *points, uint32_t num_points,

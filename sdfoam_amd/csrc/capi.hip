@@ -606,6 +606,8 @@ int sdf_delaunay_certify(const float *points, uint32_t num_points, uint32_t *rep
         return fail(SDF_E_INVALID, "scratch must be 256-byte aligned");
     if (num_points < 32)
         return fail(SDF_E_INVALID, "Delaunay triangulation does not support less than 32 points");
+    if (num_points > (1u << 26))
+        return fail(SDF_E_INVALID, "sdf_delaunay_certify takes at most 2^26 points");
     const size_t need = delaunay_certify_scratch_bytes(num_points);
     if (need == 0) return fail(SDF_E_HIP, "delaunay_certify: no device to size the sorts for");
     if (scratch_bytes < need)
@@ -639,6 +641,8 @@ int sdf_delaunay_merge(const float *points, uint32_t num_points, void *certify_s
         return fail(SDF_E_INVALID, "Delaunay triangulation does not support less than 32 points");
     if (num_reports + num_candidates >= 0xffffffffull)
         return fail(SDF_E_INVALID, "too many reports and candidates");
+    if (num_points > (1u << 26) || num_candidates > (1ull << 26))
+        return fail(SDF_E_INVALID, "sdf_delaunay_merge takes at most 2^26 points and candidates");
     const size_t gneed = delaunay_certify_scratch_bytes(num_points);
     const size_t need =
         delaunay_merge_scratch_bytes(num_points, num_reports, num_candidates, tet_capacity);

@@ -157,6 +157,8 @@ def test_gpu_delaunay_argument_errors():
     counts = (C.c_uint64 * 5)()
     rc = L.sdf_delaunay_certify(p, 31, p, 10, p, counts, aligned, 1 << 20, None)
     assert rc == 1 and b"less than 32 points" in L.sdf_last_error()
+    rc = L.sdf_delaunay_certify(p, (1 << 26) + 1, p, 10, p, counts, aligned, 1 << 20, None)
+    assert rc == 1 and b"at most 2^26 points" in L.sdf_last_error()
     rc = L.sdf_delaunay_certify(p, 100, p, 10, None, counts, aligned, 1 << 20, None)
     assert rc == 1 and b"NULL pointer" in L.sdf_last_error()
     rc = L.sdf_delaunay_certify(p, 100, p, 10, p, counts, aligned + 8, 1 << 20, None)
@@ -171,6 +173,9 @@ def test_gpu_delaunay_argument_errors():
     rc = L.sdf_delaunay_merge(p, 100, aligned, 1 << 20, p, 1 << 31, p, 1 << 31, p, p, 10,
                               result, aligned, 1 << 20, None)
     assert rc == 1 and b"too many reports" in L.sdf_last_error()
+    rc = L.sdf_delaunay_merge(p, 100, aligned, 1 << 20, p, 5, p, (1 << 26) + 1, p, p, 10,
+                              result, aligned, 1 << 20, None)
+    assert rc == 1 and b"at most 2^26 points and candidates" in L.sdf_last_error()
 
 
 def test_ray_order_and_plan_errors():
