@@ -218,13 +218,17 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
             mbuf, mptr = _aligned(mbytes, dev)
             rc = L.sdf_delaunay_merge(ptr(pts), n, gptr, gbytes, ptr(reports), nr, ptr(cand), m,
                                       ptr(tets), ptr(nbr), tcap, result, mptr, mbytes, stream)
-            if rc != 0 and result[0] > tcap and result[2] == 0:
+            if rc == _lib.SDF_E_INVALID and result[0] > tcap and result[2] == 0:
                 tcap = int(result[0])
                 continue
-            if rc != 0 and result[2] != 0:
+            if rc == _lib.SDF_E_INVALID:
+                # an undecided candidate or an inconsistent union: Qhull on
+                # every point decides
                 raise _Undecided(L.sdf_last_error().decode())
             check(rc)
             break
+        else:
+            raise _Undecided("tets did not fit the merge's capacity")
     T = int(result[0])
     if int(result[1]) != hull_faces:
         raise _Undecided(f"{int(result[1])} faces without a neighbour, the hull has {hull_faces}")
