@@ -9,7 +9,8 @@ cameras, two quantiles), where the oracle would take minutes on every ray:
   finite;
 * oracle parity (the bars of test_gpu_parity) on a seeded subset of the
   same rays, forward and backward with the walk record, and the inference
-  render of a full C4 camera bit-exact.
+  render of a full C4 camera bit-exact;
+* the GPU triangulation of C3's 1M points against Qhull, every table.
 
 Scene generation (Qhull at 2-3M points) takes one to two minutes; progress
 lines are printed as each stage ends."""
@@ -157,3 +158,31 @@ def test_c4_render_full_camera(dev, oracle_lib, say):
     got, ref = _render_both(w, dev, oracle_lib, cam)
     assert np.array_equal(got, ref.rgba8)
     say("C4 full-camera render bit-exact")
+
+
+def test_c3_triangulation_matches_qhull(dev, say):
+    """Triangulation.rebuild at C3's 1M points: every table the GPU path
+    (certified cells, Qhull on the open points, merge) produces equals the
+    tables of Qhull's tetrahedralisation of all points, bit for bit."""
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import scenes
+    from sdfoam_amd.triangulation import host_tables, qhull_tetrahedra
+
+    pts_np, _ = scenes._scene_c3(np.random.default_rng(0))
+    pts = torch.from_numpy(pts_np).to(dev)
+    t = time.time()
+    tri = sdfoam_amd.Triangulation(pts)
+    torch.cuda.synchronize()
+    say(f"GPU triangulation of {pts_np.shape[0]} points: {time.time() - t:.2f}s, "
+        f"{tri.last_stats['open']} open points")
+    assert tri.last_method == "gpu"
+    sorted_pts = pts[tri.permutation().to(torch.long)].cpu().numpy()
+    t = time.time()
+    simplices, neighbors = qhull_tetrahedra(sorted_pts)
+    ref = host_tables(sorted_pts, simplices, neighbors)
+    say(f"Qhull + host tables: {time.time() - t:.1f}s")
+    for k, v in ref.items():
+        got = getattr(tri, k)().view(torch.int32).cpu().numpy().view(np.uint32)
+        assert np.array_equal(got.reshape(v.shape), v), k
