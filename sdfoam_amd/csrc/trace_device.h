@@ -335,8 +335,21 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
     const uint32_t nf = end - beg;
     const float t0 = ws.t0;
     float t1 = __builtin_bit_cast(float, 0x7f800000u);
-    float tmin_u = t1; // DUAL: smallest t over dp > 0 (NaN never taken)
+    float tmin_u = t1; // DUAL: smallest computed t over dp > 0 (NaN never taken)
+    bool below = false; // DUAL: a face with dp > 0 and t < t0 for certain
     uint32_t best = kNoIndex;
+    // t = num / dp (correctly rounded) is formed only for faces that could be
+    // taken.  Rounding is monotone and t0, t1 are floats, so t < t1 needs
+    // num < t1 dp and t > t0 needs num > t0 dp (dp > 0).  The bounds below
+    // are those products widened by 2^-21 of their size (more than the
+    // roundings of the widened factor and of the fused product, 2^-24 each)
+    // and by 2^-126 (for subnormal products and, as dp = diff . d < 2^17 for
+    // fp16 diffs and a unit direction, quotients that round to 0), so no face
+    // that the exact test takes is skipped and the exit face is the same bit
+    // for bit.  t0 >= 0; t1 may be negative in unsafe scans.
+    float t1m = t1;                             // t1 + |t1| 2^-21
+    const float t0m = t0 * (1.0f - 0x1p-21f);   // t0 (1 - 2^-21)
+    const float t0p = t0 * (1.0f + 0x1p-21f);   // t0 (1 + 2^-21), DUAL
     const uint2 *__restrict__ row = sc.diff + beg;
     // batches of 4: the table is padded, so the last batch may over-read
     for (uint32_t k0 = 0; k0 < nf; k0 += 4) {
@@ -355,24 +368,29 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
             const float fy = fmaf(dy, 0.5f, ws.xc[1]);
             const float fz = fmaf(dz, 0.5f, ws.xc[2]);
             const float dp = sdf_dot3(dx, dy, dz, ray.dx, ray.dy, ray.dz);
-            const float t = sdf_dot3(fx - ray.ox, fy - ray.oy, fz - ray.oz, dx, dy, dz) / dp;
-            bool take;
-            if constexpr (SAFE) {
-                take = dp > 0.0f && t > t0 && t < t1;
-            } else {
-                take = dp > 0.0f && t < t1;
-            }
-            if (take && k < nf) {
-                t1 = t;
-                best = k;
-            }
+            const float num = sdf_dot3(fx - ray.ox, fy - ray.oy, fz - ray.oz, dx, dy, dz);
+            const bool pos = dp > 0.0f && k < nf;
+            const float lo = fmaf(t0m, dp, -0x1p-126f); // < t0 dp
+            bool maybe = pos && num < fmaf(t1m, dp, 0x1p-126f) && (!SAFE || num > lo);
             if constexpr (DUAL) {
-                if (dp > 0.0f && k < nf) tmin_u = fminf(tmin_u, t);
+                // the unsafe exit differs when some t <= t0: certain below
+                // lo, certainly not above t0 (1 + 2^-21) dp, formed between
+                below = below || (pos && num < lo);
+                maybe = maybe || (pos && num >= lo && num <= fmaf(t0p, dp, 0x1p-126f));
+            }
+            if (maybe) {
+                const float t = num / dp;
+                if (SAFE ? (t > t0 && t < t1) : t < t1) {
+                    t1 = t;
+                    t1m = fmaf(fabsf(t), 0x1p-21f, t);
+                    best = k;
+                }
+                if constexpr (DUAL) tmin_u = fminf(tmin_u, t);
             }
         }
     }
     if constexpr (COUNT) wc.faces += nf;
-    if constexpr (DUAL) si.agrees = !(tmin_u <= t0);
+    if constexpr (DUAL) si.agrees = !(below || tmin_u <= t0);
     if (best == kNoIndex) {
         ws.alive = false;
         return;
