@@ -147,8 +147,9 @@ def main() -> int:
         log(f"loading scene from {args.scene_cache}")
         w = scenes.load_workload(args.scene_cache)
     else:
-        log(f"generating config C{args.config} (Delaunay via Qhull)")
-        w = scenes.make_config(args.config, mode=args.alpha_mode)
+        log(f"generating config C{args.config} (Delaunay on the GPU)")
+        w = scenes.make_config(args.config, mode=args.alpha_mode,
+                               tetrahedra=lambda p: gpu_simplices(p, dev))
         if args.scene_cache:
             scenes.save_workload(w, args.scene_cache)
     log(f"scene ready in {time.time() - t0:.1f}s: N={w.num_points} E={w.adjacency.size} R={w.num_rays}")
@@ -357,6 +358,21 @@ def main() -> int:
 
 
 CPU_SAMPLE_RAYS = 640_000
+
+
+def gpu_simplices(points, dev):
+    """Tetrahedra [T, 4] of float32 points by the library's GPU Delaunay
+    (Qhull on every point where it falls back)."""
+    import numpy as np
+    import torch
+
+    from sdfoam_amd.triangulation import _Undecided, gpu_tetrahedra, qhull_tetrahedra
+
+    pts = torch.from_numpy(np.ascontiguousarray(points, dtype=np.float32)).to(dev)
+    try:
+        return gpu_tetrahedra(pts)[0].cpu().numpy()
+    except _Undecided:
+        return qhull_tetrahedra(points)[0]
 
 
 def triangulate_bench(args, dev) -> int:

@@ -112,18 +112,21 @@ def fibonacci_sphere(n: int, radius: float) -> np.ndarray:
     return radius * np.stack([rxy * np.cos(phi), rxy * np.sin(phi), z], axis=1)
 
 
-def delaunay_adjacency(points: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+def delaunay_adjacency(points: np.ndarray, tetrahedra=None) -> tuple[np.ndarray, np.ndarray]:
     """CSR Delaunay adjacency with ascending rows.
 
     Edges of every tetrahedron, deduplicated, both directions, sorted by
     (row, neighbour): the layout of src/delaunay/delaunay.cu:146-226, where a
-    stable sort by row leaves each row ascending.
+    stable sort by row leaves each row ascending.  `tetrahedra(points)` gives
+    the tetrahedra [T, 4] (default: Qhull).
     """
-    from scipy.spatial import Delaunay
-
     n = int(points.shape[0])
-    tri = Delaunay(np.asarray(points, dtype=np.float64))
-    s = tri.simplices.astype(np.int64)
+    if tetrahedra is None:
+        from scipy.spatial import Delaunay
+
+        s = Delaunay(np.asarray(points, dtype=np.float64)).simplices.astype(np.int64)
+    else:
+        s = np.asarray(tetrahedra(points), dtype=np.int64)
     pairs = np.concatenate(
         [s[:, [0, 1]], s[:, [0, 2]], s[:, [0, 3]], s[:, [1, 2]], s[:, [1, 3]], s[:, [2, 3]]]
     )
@@ -296,12 +299,14 @@ def _scene_c3(rng):
 
 def make_config(index: int, *, mode: str = "sdfoam", inv_s: float | None = None,
                 image_scale: float = 1.0, point_scale: float = 1.0,
-                sh_degree: int | None = None) -> Workload:
+                sh_degree: int | None = None, tetrahedra=None) -> Workload:
     """Workload configuration C1-C5 (seed = config index).
 
     ``image_scale`` < 1 shrinks the image (same camera) for quick tests;
     ``point_scale`` < 1 shrinks the point counts of C4 / C5 (same proportions);
-    ``sh_degree`` replaces the configuration's SH degree (C1-C3).
+    ``sh_degree`` replaces the configuration's SH degree (C1-C3);
+    ``tetrahedra(points)`` replaces Qhull for the adjacency (the bench passes the
+    GPU tetrahedralisation).
     """
     rng = np.random.default_rng(index if index != 1 else 0)
     inv_s = math.exp(0.3) if inv_s is None else float(inv_s)
@@ -317,7 +322,7 @@ def make_config(index: int, *, mode: str = "sdfoam", inv_s: float | None = None,
         cam_pos = 3.0 * np.array([math.sin(th) * math.cos(ph), math.sin(th) * math.sin(ph), math.cos(th)])
         fov, w, h = math.radians(50.0), 400, 400
     elif index in (4, 5):
-        return _make_blob_config(index, rng, mode, inv_s, image_scale, point_scale)
+        return _make_blob_config(index, rng, mode, inv_s, image_scale, point_scale, tetrahedra)
     elif index == 3:
         pts, sq = _scene_c3(rng)
         degree = 3
@@ -354,7 +359,7 @@ def make_config(index: int, *, mode: str = "sdfoam", inv_s: float | None = None,
         last = np.logaddexp(0.0, 10.0 * logit) / 10.0  # softplus, beta = 10
     attrs[:, D - 1] = last.astype(np.float32)
 
-    adj, offs = delaunay_adjacency(pts)
+    adj, offs = delaunay_adjacency(pts, tetrahedra)
 
     if image_scale != 1.0:
         w = max(8, int(round(w * image_scale)))
@@ -382,7 +387,7 @@ def make_config(index: int, *, mode: str = "sdfoam", inv_s: float | None = None,
 
 
 def _make_blob_config(index: int, rng, mode: str, inv_s: float, image_scale: float,
-                      point_scale: float = 1.0) -> Workload:
+                      point_scale: float = 1.0, tetrahedra=None) -> Workload:
     """C4 (3M points, 8 ring cameras 1297x840, Q = 1) and C5 (2M points with
     positions perturbed N(0, 0.001) after the adjacency is built, rays of
     step 0: 2^20 (camera, pixel) samples over 64 cameras 960x640, Q = 2
@@ -406,7 +411,7 @@ def _make_blob_config(index: int, rng, mode: str, inv_s: float, image_scale: flo
     else:
         last = np.logaddexp(0.0, 10.0 * rng.normal(0.0, 1.0, size=n)) / 10.0
     attrs[:, D - 1] = last.astype(np.float32)
-    adj, offs = delaunay_adjacency(pts)
+    adj, offs = delaunay_adjacency(pts, tetrahedra)
     extra = {"permutation": perm, "centres": centres}
     if index == 4:
         w, h = 1297, 840
