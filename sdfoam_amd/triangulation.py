@@ -54,12 +54,18 @@ def _u32_cuda(a: np.ndarray, device) -> torch.Tensor:
 
 def qhull_tetrahedra(points: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """Delaunay tetrahedra of float32 points [N, 3] (Qhull, in double):
-    (simplices [T, 4] int32, neighbors [T, 4] int32, -1 on the hull)."""
+    (simplices [T, 4] int32, neighbors [T, 4] int32, -1 on the hull).  The
+    points are centred on their bounding box first: the triangulation does
+    not change, and Qhull's lifted coordinates (|x|^2) keep their precision
+    for clouds far from the origin."""
     from scipy.spatial import Delaunay
     from scipy.spatial import QhullError
 
+    p = np.asarray(points, dtype=np.float64)
+    if p.shape[0] > 0:
+        p = p - 0.5 * (p.min(axis=0) + p.max(axis=0))
     try:
-        tri = Delaunay(np.asarray(points, dtype=np.float64))
+        tri = Delaunay(p)
     except QhullError as e:
         raise TriangulationFailedError(f"Qhull failed: {str(e).splitlines()[0]}") from None
     return (np.ascontiguousarray(tri.simplices, dtype=np.int32),

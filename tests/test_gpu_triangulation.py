@@ -287,3 +287,24 @@ def test_gpu_delaunay_small_and_degenerate_inputs(dev):
     flat[:, 2] = 0.0
     with pytest.raises(sdfoam_amd.TriangulationFailedError):
         sdfoam_amd.Triangulation(torch.from_numpy(flat).to(dev))
+
+
+def test_gpu_delaunay_far_from_the_origin(dev):
+    """Points at 1000 + [0, 1)^3: the GPU tetrahedralisation works relative to
+    each cell's point and stays exactly Delaunay, where Qhull's lifted
+    coordinates lose precision (the two may differ here); every GPU tet has
+    an empty circumsphere and together they tile the hull."""
+    import torch
+    from scipy.spatial import ConvexHull
+
+    from sdfoam_amd.triangulation import gpu_tetrahedra
+    from test_delaunay_cells import assert_delaunay
+
+    rng = np.random.default_rng(99)
+    pts = np.unique((1000.0 + rng.random((20000, 3))).astype(np.float32), axis=0)
+    tets, nbr, stats = gpu_tetrahedra(torch.from_numpy(pts).to(dev))
+    t = tets.cpu().numpy()
+    assert np.array_equal(nbr.cpu().numpy(), _face_neighbors(t))
+    # volumes relative to the cloud's corner, in double
+    local = (pts.astype(np.float64) - 1000.0).astype(np.float64)
+    assert_delaunay(local, t, ConvexHull(local).volume)
