@@ -288,6 +288,17 @@ int sdf_batch_fetcher_destroy(sdf_batch_fetcher *fetcher);
 void sdf_batch_rows(uint32_t batch_index, size_t batch_size, size_t num_rows,
                     int shuffle, uint32_t *rows);
 
+/* Batch `batch_index` of a device-resident array `data` [num_rows] of
+ * `stride`-byte rows (a multiple of 4; 4-byte aligned) into `dst`
+ * [batch_size] on `stream`: the rows sdf_batch_rows selects (the
+ * reference's per-element seeding, src/utils/batch_fetcher.cpp:63-72),
+ * gathered by the GPU.  No counterpart in the reference, which keeps the
+ * array on the host (src/utils/batch_fetcher.cpp:29-157): for arrays that
+ * fit in HBM it replaces the host gather and upload of BatchFetcher::next. */
+int sdf_batch_gather(const void *data, size_t num_rows, size_t stride,
+                     uint32_t batch_index, size_t batch_size, int shuffle,
+                     void *dst, void *stream);
+
 /* Implicit AABB tree over consecutive point pairs, tree [pow2(N), 2, 3]
  * (node (d, i) at 2^td - 2^(d+1) + i; the last entry is zeroed).
  * Replaces build_aabb_tree (src/aabb_tree/aabb_tree.h:10-13,

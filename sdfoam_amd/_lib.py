@@ -40,6 +40,7 @@ EXPORTS = (
     "sdf_batch_fetcher_next",
     "sdf_batch_fetcher_destroy",
     "sdf_batch_rows",
+    "sdf_batch_gather",
     "sdf_build_aabb_tree",
     "sdf_farthest_neighbor",
     "sdf_sort_points_scratch_bytes",
@@ -181,6 +182,8 @@ def lib() -> C.CDLL:
     L.sdf_batch_fetcher_destroy.argtypes = [P]
     L.sdf_batch_rows.restype = None
     L.sdf_batch_rows.argtypes = [U32, SZ, SZ, C.c_int, P]
+    L.sdf_batch_gather.restype = C.c_int
+    L.sdf_batch_gather.argtypes = [P, SZ, SZ, U32, SZ, C.c_int, P, P]
     L.sdf_build_aabb_tree.restype = C.c_int
     L.sdf_build_aabb_tree.argtypes = [P, U32, P, P]
     L.sdf_farthest_neighbor.restype = C.c_int

@@ -29,7 +29,7 @@ constexpr int kSlots = 4;
 // 32-bit integer hash of the reference's RNG (src/utils/random.h:11-20; the
 // "triple32" construction of C. Wellons' hash-prospector) and its seeding
 // (src/utils/random.h:27-29).
-inline uint32_t mix32(uint32_t x) {
+__host__ __device__ inline uint32_t mix32(uint32_t x) {
     x ^= x >> 17;
     x *= 0xed5ad4bbu;
     x ^= x >> 11;
@@ -44,13 +44,29 @@ inline uint32_t mix32(uint32_t x) {
 // shuffle, the first draw of an RNG seeded with b * batch_size + j, scaled to
 // [0, n) as randint(rng, 0, n) does (src/utils/random.h:49-56); otherwise
 // the rows in order, wrapping around.
-inline uint32_t row_of(uint32_t b, size_t batch_size, size_t j, size_t n, bool shuffle) {
+__host__ __device__ inline uint32_t row_of(uint32_t b, size_t batch_size, size_t j, size_t n,
+                                           bool shuffle) {
     const size_t k = (size_t)b * batch_size + j;
     if (!shuffle) return (uint32_t)(k % n);
     const uint32_t draw = mix32((uint32_t)k ^ 0x2815db5bu);
     const uint32_t diff = (uint32_t)n;
     const uint32_t x = draw / (0xffffffffu / diff);
-    return std::min(x, diff - 1u);
+    return x < diff - 1u ? x : diff - 1u;
+}
+
+// One thread per 32-bit word of the batch: word w of element j is word w of
+// row row_of(b, ., j, .) of the device-resident array.
+__global__ __launch_bounds__(256) void batch_gather_kernel(const uint32_t *__restrict__ data,
+                                                           size_t num_rows, uint32_t row_words,
+                                                           uint32_t b, uint64_t batch_size,
+                                                           bool shuffle,
+                                                           uint32_t *__restrict__ dst) {
+    const uint64_t t = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (t >= batch_size * row_words) return;
+    const uint64_t j = t / row_words;
+    const uint32_t w = (uint32_t)(t - j * row_words);
+    const uint32_t row = row_of(b, (size_t)batch_size, (size_t)j, num_rows, shuffle);
+    dst[t] = data[(uint64_t)row * row_words + w];
 }
 
 struct Slot {
@@ -164,6 +180,27 @@ void sdf_batch_rows(uint32_t batch_index, size_t batch_size, size_t num_rows, in
     if (!rows || num_rows == 0) return;
     for (size_t j = 0; j < batch_size; ++j)
         rows[j] = row_of(batch_index, batch_size, j, num_rows, shuffle != 0);
+}
+
+int sdf_batch_gather(const void *data, size_t num_rows, size_t stride, uint32_t batch_index,
+                     size_t batch_size, int shuffle, void *dst, void *stream) {
+    if (batch_size == 0) return SDF_OK;
+    if (!data || !dst) return fail(SDF_E_INVALID, "NULL pointer argument");
+    if (num_rows == 0 || num_rows > 0xffffffffull)
+        return fail(SDF_E_INVALID, "num_rows must be in [1, 2^32)");
+    if (stride == 0 || stride % 4 != 0)
+        return fail(SDF_E_INVALID, "stride must be a positive multiple of 4 bytes");
+    if ((reinterpret_cast<uintptr_t>(data) | reinterpret_cast<uintptr_t>(dst)) & 3u)
+        return fail(SDF_E_INVALID, "data and dst must be 4-byte aligned");
+    const uint64_t words = (uint64_t)batch_size * (stride / 4);
+    if (words > (1ull << 40)) return fail(SDF_E_INVALID, "batch too large");
+    hipLaunchKernelGGL(batch_gather_kernel, dim3((unsigned)((words + 255u) / 256u)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint32_t *>(data),
+                       num_rows, (uint32_t)(stride / 4), batch_index, (uint64_t)batch_size,
+                       shuffle != 0, static_cast<uint32_t *>(dst));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "batch_gather");
+    return SDF_OK;
 }
 
 int sdf_batch_fetcher_create(const void *data, size_t num_bytes, size_t stride,

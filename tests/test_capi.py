@@ -224,6 +224,24 @@ def test_trace_benchmark_argument_errors():
     assert call(start=None) == 1 and b"start_point" in L.sdf_last_error()
 
 
+def test_batch_gather_argument_errors():
+    from sdfoam_amd import _lib
+
+    L = _lib.lib()
+    buf = (C.c_uint64 * 16)()
+    p = C.cast(buf, C.c_void_p)
+    assert L.sdf_batch_gather(p, 10, 24, 0, 0, 1, p, None) == 0  # empty batch
+    assert L.sdf_batch_gather(None, 10, 24, 0, 4, 1, p, None) == 1
+    assert b"NULL pointer" in L.sdf_last_error()
+    assert L.sdf_batch_gather(p, 0, 24, 0, 4, 1, p, None) == 1
+    assert b"num_rows" in L.sdf_last_error()
+    assert L.sdf_batch_gather(p, 10, 6, 0, 4, 1, p, None) == 1
+    assert b"multiple of 4" in L.sdf_last_error()
+    base = C.cast(buf, C.c_void_p).value
+    assert L.sdf_batch_gather(base + 2, 10, 24, 0, 4, 1, p, None) == 1
+    assert b"4-byte aligned" in L.sdf_last_error()
+
+
 def test_nn_and_tree_argument_errors():
     from sdfoam_amd import _lib
 
