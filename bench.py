@@ -286,10 +286,7 @@ def main() -> int:
     traffic = None
     variant = ("" if use_record else "_scan") + ("" if args.alpha_mode == "sdfoam" else "_standard") \
         + ("_f16" if half else "")
-    prof = os.path.join(ROOT, "profiles", f"traffic_{dominant}{variant}_C{args.config}.json")
-    if os.path.exists(prof):
-        with open(prof) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic = load_traffic(f"traffic_{dominant}{variant}_C{args.config}.json")
 
     if args.config == 5:
         rays_desc = f"{R} rays per step sampled from 64 cameras 960x640 (10 seeded batches)"
@@ -358,6 +355,16 @@ def main() -> int:
 
 
 CPU_SAMPLE_RAYS = 640_000
+
+
+def load_traffic(name):
+    """HBM bytes per launch that a committed rocprofv3 counter summary
+    (profiles/<name>) records, or None."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
 
 
 def gpu_simplices(points, dev):
@@ -483,18 +490,22 @@ def fetch_bench(args, dev) -> int:
             fr.next()
             fc.next()
         torch.cuda.synchronize()
+        # the gathers run on the current stream, where these events sit
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
+        e0.record()
         for _ in range(args.steps):
             fr.next()
             fc.next()
+        e1.record()
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / args.steps
         fr.close()
         fc.close()
-        return dt
+        return dt, e0.elapsed_time(e1) * 1e-3 / args.steps
 
-    dt = time_pairs(True)
-    dt_streamed = time_pairs(False)
+    dt, dt_kernels = time_pairs(True)
+    dt_streamed, _ = time_pairs(False)
     batch_bytes = B * (24 + 12)
     # naive host path for the same batch shape
     t0 = time.perf_counter()
@@ -507,7 +518,7 @@ def fetch_bench(args, dev) -> int:
     dt_naive = (time.perf_counter() - t0) / n_naive
     del ra, ca
     achieved = batch_bytes / dt / 1e9
-    hbm = 2 * batch_bytes / dt / 1e9
+    hbm = 2 * batch_bytes / dt_kernels / 1e9
     result = {
         "metric": FETCH_METRIC,
         "value": achieved,
@@ -527,7 +538,8 @@ def fetch_bench(args, dev) -> int:
                    "batch": B},
         "roofline": {"kernel": "batch_gather_kernel", "bound": "hbm", "achieved": hbm,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": hbm / HBM_PEAK_GBS,
-                     "traffic": None},
+                     "traffic": load_traffic("traffic_batch_gather_fetch.json")},
+        "kernel_ms_per_step": dt_kernels * 1e3,
         "streamed_ms_per_step": dt_streamed * 1e3,
         "streamed_GBps": batch_bytes / dt_streamed / 1e9,
         "streamed_host_link_frac": batch_bytes / dt_streamed / 1e9 / HOST_LINK_PEAK_GBS,
@@ -601,6 +613,9 @@ def render_bench(args, w, pts, attrs, adj, offs, inv, pipe, D) -> int:
     R = H * W
     bytes_frame = R * 4 + S * (8 + 4 + 12 + ab * D) + 8 * F_st
     achieved = bytes_frame / (render_ms * 1e-3) / 1e9
+    traffic = None
+    if args.alpha_mode == "sdfoam" and args.attr_dtype == "float32":
+        traffic = load_traffic(f"traffic_render_C{args.config}.json")
     result = {
         "metric": RENDER_METRIC,
         "value": R / (ms_frame * 1e-3) / 1e6,
@@ -626,7 +641,7 @@ def render_bench(args, w, pts, attrs, adj, offs, inv, pipe, D) -> int:
         "cell_steps_per_pixel": S / R,
         "roofline": {"kernel": "render", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None},
+                     "traffic": traffic},
     }
     if args.cpu_stride != 0:
         from oracle import oracle
