@@ -260,16 +260,16 @@ def main() -> int:
     N = w.num_points
     E = int(w.adjacency.size)
     # attribute elements (rows, contribution, gradient rows) at their storage
-    # width; with the walk record the backward reads 8 B per step instead of
-    # the stepped cell's face rows (standard mode: all but the rare steps
-    # where the unsafe walk leaves the recorded one)
+    # width; with the walk record the backward reads 24 B per step (the step
+    # and its colour) instead of the stepped cell's face rows and attribute
+    # row (standard mode: all but the rare steps where the unsafe walk leaves
+    # the recorded one)
     ab = 2 if half else 4
     recorded = use_record
     if recorded:
-        # the forward also writes 8 B per step; the backward reads them
-        # instead of the stepped cells' face rows
-        bytes_fwd = R * (48 + 12 * Q) + S * (28 + ab * D + ab + 8) + 8 * F_st
-        bytes_bwd = R * (60 + 12 * Q) + S * (36 + 2 * ab * D + 8)
+        # the forward also writes 24 B per step; the backward reads them
+        bytes_fwd = R * (48 + 12 * Q) + S * (28 + ab * D + ab + 24) + 8 * F_st
+        bytes_bwd = R * (60 + 12 * Q) + S * (36 + ab * D + 24)
     else:
         bytes_fwd = R * (48 + 12 * Q) + S * (28 + ab * D + ab) + 8 * F_st
         bytes_bwd = R * (60 + 12 * Q) + S * (36 + 2 * ab * D) + 8 * F_st

@@ -183,9 +183,11 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
  * points, scene and settings.  Results are identical with and without them.
  *
  * Walk record: the forward records each ray's steps (next cell and exit
- * distance, 8 bytes a step, `walk_budget` trips per wavefront of 64 rays);
- * the backward then reads the steps instead of scanning the cell faces
- * again.  In standard mode a step is recorded only while the density
+ * distance, and the step's colour and sdf/density value: 24 bytes a step,
+ * `walk_budget` trips per wavefront of 64 rays); the backward then reads
+ * the steps instead of scanning the cell faces again, and a recorded step's
+ * colour instead of the cell's attribute row, so the record is valid only
+ * for a backward over the attributes the forward traced.  In standard mode a step is recorded only while the density
  * backward's unsafe walk takes the same exit.  Rays past `walk_budget`
  * trips, or that walk further in the backward, scan as usual.
  * walk_record == NULL: no record.
@@ -204,7 +206,7 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
  * of a cell then touches fewer 64-byte memory segments than updates of the
  * three output arrays do.  grad_accum == NULL: updates go to the outputs. */
 typedef struct sdf_trace_plan {
-    void *walk_record;        /* device memory, 8-byte aligned, or NULL */
+    void *walk_record;        /* device memory, 16-byte aligned, or NULL */
     size_t walk_record_bytes; /* >= sdf_walk_record_bytes(num_rays, ray_image_width, walk_budget) */
     uint32_t walk_budget;
     const uint32_t *ray_order; /* device memory [num_rays], or NULL */

@@ -114,6 +114,7 @@ SceneView make_scene(uint32_t num_points, const float *points, const float *attr
 int check_plan(const sdf_trace_plan *plan, uint32_t num_rays, uint32_t ray_image_width,
                WalkRecordArgs &rec, const uint32_t *&order) {
     rec.entries = nullptr;
+    rec.colors = nullptr;
     rec.budget = 0;
     order = nullptr;
     if (!plan) return SDF_OK;
@@ -124,14 +125,17 @@ int check_plan(const sdf_trace_plan *plan, uint32_t num_rays, uint32_t ray_image
     }
     if (!plan->walk_record) return SDF_OK;
     if (plan->walk_budget == 0) return fail(SDF_E_INVALID, "walk record budget must be positive");
-    const uint64_t need =
-        walk_record_entries(num_ray_tiles(num_rays, ray_image_width), plan->walk_budget) * 8u;
+    const uint64_t count =
+        walk_record_entries(num_ray_tiles(num_rays, ray_image_width), plan->walk_budget);
+    const uint64_t need = count * kWalkRecordEntryBytes;
     if (plan->walk_record_bytes < need)
         return fail(SDF_E_INVALID, "walk record must hold %llu bytes (got %zu)",
                     (unsigned long long)need, plan->walk_record_bytes);
-    if ((reinterpret_cast<uintptr_t>(plan->walk_record) & 7u) != 0)
-        return fail(SDF_E_INVALID, "walk record must be 8-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(plan->walk_record) & 15u) != 0)
+        return fail(SDF_E_INVALID, "walk record must be 16-byte aligned");
     rec.entries = static_cast<uint2 *>(plan->walk_record);
+    // count is a multiple of 64, so the colours stay 16-byte aligned
+    rec.colors = reinterpret_cast<float4 *>(rec.entries + count);
     rec.budget = plan->walk_budget;
     return SDF_OK;
 }
@@ -466,7 +470,8 @@ int sdf_ray_order(uint32_t num_points, uint32_t num_rays, const float *rays,
 }
 
 size_t sdf_walk_record_bytes(uint32_t num_rays, uint32_t ray_image_width, uint32_t budget) {
-    return (size_t)walk_record_entries(num_ray_tiles(num_rays, ray_image_width), budget) * 8u;
+    return (size_t)walk_record_entries(num_ray_tiles(num_rays, ray_image_width), budget) *
+           kWalkRecordEntryBytes;
 }
 
 int sdf_trace_forward_planned(

@@ -17,11 +17,17 @@ int hip_fail(hipError_t e, const char *where);
 // walking.  Written by the forward of the sdfoam (safe) walk, replayed by
 // its backward, which then skips the face scans; a lane scans again from
 // its first unrecorded trip (past `budget`, or where it outlives the
-// forward's walk).
+// forward's walk).  Beside every entry, in a second array of the same
+// shape, the forward keeps the step's colour and density channel
+// {r, g, b, row[channel]} (channel: sdf_channel in sdfoam mode, D - 1 in
+// standard mode), so the backward of a recorded step reads 16 bytes instead
+// of the cell's attribute row and skips the SH sum.
 constexpr uint32_t kWalkUnrecorded = 0xfffffffeu;
+constexpr uint32_t kWalkRecordEntryBytes = 8u + 16u;
 
 struct WalkRecordArgs {
     uint2 *entries;  // NULL: no record
+    float4 *colors;  // entries' colours, same indexing
     uint32_t budget; // trips recorded per wavefront
 };
 

@@ -189,7 +189,11 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     WalkCounters wc = {0u, 0u, 0ull, 0ull};
     // walk record of this wavefront: one row of 64 entries per trip
     uint2 *wrec = nullptr;
-    if (!STATS && a.record.entries) wrec = walk_record_lane<kForwardChunk>(a.record, lane);
+    float4 *wcol = nullptr;
+    if (!STATS && a.record.entries) {
+        wrec = walk_record_lane<kForwardChunk>(a.record, lane);
+        wcol = a.record.colors + (wrec - a.record.entries);
+    }
     uint32_t trip = 0;
     FwdEntry held = {0u, 0.0f, 0.0f, false}; // step waiting for the next contribution pass
 
@@ -213,7 +217,12 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
                                        __builtin_bit_cast(uint32_t, si.t1));
             }
         }
-        if (wrec && trip < a.record.budget) wrec[(uint64_t)trip * 64] = entry;
+        // where this trip's colour goes (the step's, if the lane steps)
+        float4 *col = nullptr;
+        if (wrec && trip < a.record.budget) {
+            wrec[(uint64_t)trip * 64] = entry;
+            col = wcol + (uint64_t)trip * 64;
+        }
         ++trip;
 
         float alpha = 0.0f, w = 0.0f;
@@ -223,9 +232,11 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
             const float t0 = ws.t0, t1 = si.t1;
             const AT *__restrict__ row = static_cast<const AT *>(a.scene.attrs) + (uint64_t)cell * D;
             float s = (float)row[D - 1];
+            float chan = s; // the channel the backward reads (sdf value or density)
             const float dt = fmaxf(t1 - t0, 0.0f);
             if (neus_alpha) {
                 const float d = (float)row[sdf_ch];
+                chan = d;
                 const float phi = sdf_sigmoidf(-sha * d);
                 s = sha * phi * (1.0f - phi);
             }
@@ -242,6 +253,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
                 C0 = fmaf(w, r, C0);
                 C1 = fmaf(w, g, C1);
                 C2 = fmaf(w, b, C2);
+                if (col) *col = make_float4(r, g, b, chan);
                 const uint64_t qbase = (uint64_t)ray_idx * Q;
                 if (NEUS) {
                     const float drop = T - Tn;
@@ -712,7 +724,11 @@ backward_sdf_kernel(BwdArgs a) {
     // recorded, the step is read instead of scanned; from the first
     // unrecorded (or out-of-range) entry on, the lane scans.
     const uint2 *wrec = nullptr;
-    if (!STATS && a.record.entries) wrec = walk_record_lane<kBackwardChunk>(a.record, lane);
+    const float4 *wcol = nullptr;
+    if (!STATS && a.record.entries) {
+        wrec = walk_record_lane<kBackwardChunk>(a.record, lane);
+        wcol = a.record.colors + (wrec - a.record.entries);
+    }
     uint32_t trip = 0;
     StepEntries ents; // steps whose updates are not applied yet
     entries_init(ents);
@@ -721,9 +737,15 @@ backward_sdf_kernel(BwdArgs a) {
         StepInfo si;
         si.stepped = false;
         si.found = false;
+        // the recorded step's {r, g, b, channel}, valid when `replayed`
+        float4 rc4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        bool replayed = false;
         if (ws.alive) {
             uint2 e = make_uint2(kWalkUnrecorded, 0u);
-            if (wrec && trip < a.record.budget) e = wrec[(uint64_t)trip * 64];
+            if (wrec && trip < a.record.budget) {
+                e = wrec[(uint64_t)trip * 64];
+                rc4 = wcol[(uint64_t)trip * 64];
+            }
             if (e.x == kNoIndex) {
                 ++ws.n;
                 ws.alive = false;
@@ -736,6 +758,7 @@ backward_sdf_kernel(BwdArgs a) {
                 si.xn[1] = a.scene.points[3ull * e.x + 1];
                 si.xn[2] = a.scene.points[3ull * e.x + 2];
                 si.stepped = si.t1 > ws.t0;
+                replayed = true;
             } else {
                 wrec = nullptr;
                 walk_advance<true, STATS>(a.scene, ray, a.settings.max_intersections, ws, si, wc);
@@ -758,14 +781,20 @@ backward_sdf_kernel(BwdArgs a) {
             }
             const AT *__restrict__ row = static_cast<const AT *>(a.scene.attrs) + (uint64_t)cell * D;
             const float dt = fmaxf(t1 - t0, 0.0f);
-            const float d = (float)row[sdf_ch];
+            const float d = replayed ? rc4.w : (float)row[sdf_ch];
             const float phi = sdf_sigmoidf(-sha * d);
             const float s = sha * phi * (1.0f - phi);
             const float alpha = 1.0f - sdf_expf(-s * dt);
             const float Tn = T * (1.0f - alpha);
             if constexpr (!STATS) {
                 float r, g, b;
-                sh_rgb<L>(sh, kPitch, row, r, g, b);
+                if (replayed) {
+                    r = rc4.x;
+                    g = rc4.y;
+                    b = rc4.z;
+                } else {
+                    sh_rgb<L>(sh, kPitch, row, r, g, b);
+                }
                 const float w = T * alpha;
                 C0 = fmaf(w, r, C0);
                 C1 = fmaf(w, g, C1);
@@ -916,16 +945,26 @@ backward_density_kernel(BwdArgs a) {
     // replay of the forward's walk record as in backward_sdf; the forward
     // records a step only where the unsafe walk takes the same exit
     const uint2 *wrec = nullptr;
-    if (!STATS && a.record.entries) wrec = walk_record_lane<kBackwardChunk>(a.record, lane);
+    const float4 *wcol = nullptr;
+    if (!STATS && a.record.entries) {
+        wrec = walk_record_lane<kBackwardChunk>(a.record, lane);
+        wcol = a.record.colors + (wrec - a.record.entries);
+    }
     uint32_t trip = 0;
 
     while (__ballot(ws.alive) != 0ull) {
         StepInfo si;
         si.stepped = false;
         si.found = false;
+        // the recorded step's {r, g, b, channel}, valid when `replayed`
+        float4 rc4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        bool replayed = false;
         if (ws.alive) {
             uint2 e = make_uint2(kWalkUnrecorded, 0u);
-            if (wrec && trip < a.record.budget) e = wrec[(uint64_t)trip * 64];
+            if (wrec && trip < a.record.budget) {
+                e = wrec[(uint64_t)trip * 64];
+                rc4 = wcol[(uint64_t)trip * 64];
+            }
             if (e.x == kNoIndex) {
                 ++ws.n;
                 ws.alive = false;
@@ -938,6 +977,7 @@ backward_density_kernel(BwdArgs a) {
                 si.xn[1] = a.scene.points[3ull * e.x + 1];
                 si.xn[2] = a.scene.points[3ull * e.x + 2];
                 si.stepped = si.t1 > ws.t0;
+                replayed = true;
             } else {
                 wrec = nullptr;
                 walk_advance<false, STATS>(a.scene, ray, a.settings.max_intersections, ws, si,
@@ -960,13 +1000,18 @@ backward_density_kernel(BwdArgs a) {
                 ++rec;
             }
             const AT *__restrict__ row = static_cast<const AT *>(a.scene.attrs) + (uint64_t)cell * D;
-            const float s = (float)row[D - 1];
+            const float s = replayed ? rc4.w : (float)row[D - 1];
             const float dt = fmaxf(t1 - t0, 0.0f);
             const float alpha = 1.0f - sdf_expf(-s * dt);
             const float Tn = T * (1.0f - alpha);
             if constexpr (!STATS) {
                 float r, g, b;
-                if (s > 1e-6f) {
+                if (replayed) {
+                    // the forward's colour (zero where it found no density)
+                    r = rc4.x;
+                    g = rc4.y;
+                    b = rc4.z;
+                } else if (s > 1e-6f) {
                     sh_rgb<L>(sh, kPitch, row, r, g, b);
                 } else {
                     r = g = b = 0.0f;

@@ -103,15 +103,17 @@ class TracePlan:
 
     * ``order``: the launch order of the rays (sdf_ray_order), for rays in no
       particular order;
-    * ``entries``: the walk record, each ray's steps (8 bytes per step, up to
-      ``budget`` trips per wavefront of 64 rays);
+    * ``entries``: the walk record, each ray's steps and their colours and
+      sdf/density values (24 bytes per step, up to ``budget`` trips per
+      wavefront of 64 rays);
     * ``table``: the forward's fp16 offset table of the scene, which the
       backward reuses instead of rebuilding it while the points, adjacency
       and offsets tensors are the same and unmodified (same storage and
       version counter).
 
-    Valid for a backward over the same rays, start points, scene and
-    settings; the tracer checks the ray count, image width and walk limit."""
+    Valid for a backward over the same rays, start points, scene, attributes
+    and settings; the tracer checks the ray count, image width and walk
+    limit."""
 
     def __init__(self, num_rays: int, settings, device):
         self.num_rays = num_rays
