@@ -31,6 +31,18 @@ struct WalkRecordArgs {
     uint32_t budget; // trips recorded per wavefront
 };
 
+// Stores into the walk record.  It is written once by the forward and read
+// once by the backward, so the stores are non-temporal: they do not displace
+// the scene's cell data from L2 while the forward walks.
+__device__ inline void record_store(uint2 *p, uint2 v) {
+    __builtin_nontemporal_store(((uint64_t)v.y << 32) | v.x, reinterpret_cast<uint64_t *>(p));
+}
+__device__ inline void record_store(float4 *p, float4 v) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<f4v *>(p));
+}
+
 // entries for every block of the launch grid, the padding blocks included
 // (they write their "unrecorded" row)
 __host__ inline uint64_t walk_record_entries(uint32_t num_tiles, uint32_t budget) {

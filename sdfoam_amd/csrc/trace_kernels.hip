@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         // where this trip's colour goes (the step's, if the lane steps)
         float4 *col = nullptr;
         if (wrec && trip < a.record.budget) {
-            wrec[(uint64_t)trip * 64] = entry;
+            record_store(wrec + (uint64_t)trip * 64, entry);
             col = wcol + (uint64_t)trip * 64;
         }
         ++trip;
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
                 C0 = fmaf(w, r, C0);
                 C1 = fmaf(w, g, C1);
                 C2 = fmaf(w, b, C2);
-                if (col) *col = make_float4(r, g, b, chan);
+                if (col) record_store(col, make_float4(r, g, b, chan));
                 const uint64_t qbase = (uint64_t)ray_idx * Q;
                 if (NEUS) {
                     const float drop = T - Tn;
@@ -303,7 +303,8 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         if (ws.alive && si.found) walk_move(ws, si);
     }
     // a backward lane that outlives this wave's walk reads "unrecorded"
-    if (wrec && trip < a.record.budget) wrec[(uint64_t)trip * 64] = make_uint2(kWalkUnrecorded, 0u);
+    if (wrec && trip < a.record.budget)
+        record_store(wrec + (uint64_t)trip * 64, make_uint2(kWalkUnrecorded, 0u));
     if constexpr (!STATS) {
         if (a.contribution || a.alpha_out) {
             const FwdEntry none = {0u, 0.0f, 0.0f, false};
