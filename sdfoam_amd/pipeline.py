@@ -113,7 +113,9 @@ class TracePlan:
 
     Valid for a backward over the same rays, start points, scene, attributes
     and settings; the tracer checks the ray count, image width and walk
-    limit."""
+    limit, and uses the walk record only when the backward's rays, start
+    points, scene and attribute tensors are the forward's (same storage,
+    unmodified) with the same alpha mode and sdf channel."""
 
     def __init__(self, num_rays: int, settings, device):
         self.num_rays = num_rays
@@ -127,10 +129,19 @@ class TracePlan:
         self.table = None
         self.table_bytes = 0
         self.table_key = None
+        self.record_key = None
 
     @staticmethod
     def scene_key(points, adjacency, offsets) -> tuple:
         return tuple((t.data_ptr(), t._version, t.numel()) for t in (points, adjacency, offsets))
+
+    @staticmethod
+    def record_key(settings, *tensors) -> tuple:
+        """What the walk record depends on: the traced tensors (storage,
+        version counter, size) and the alpha mode and sdf channel (the record
+        holds each step's colour and sdf/density value)."""
+        return (int(settings.alpha_mode), int(settings.sdf_channel)) + tuple(
+            (t.data_ptr(), t._version, t.numel()) for t in tensors)
 
     def keep_table(self, table: torch.Tensor, nbytes: int, key: tuple) -> None:
         self.table, self.table_bytes, self.table_key = table, nbytes, key
@@ -169,9 +180,15 @@ class TracePlan:
         self.entries = torch.empty(max(1, self.nbytes // 8), dtype=torch.int64, device=self.device)
         self.budget = budget
 
-    def desc(self):
+    def desc(self, record_key=None):
+        """The C descriptor; the walk record is left out when `record_key`
+        (the backward's inputs) is not the one it was recorded for, so the
+        backward scans for itself."""
+        use_record = self.entries is not None and (record_key is None
+                                                   or record_key == self.record_key)
         return _lib.TracePlanDesc(
-            None if self.entries is None else self.entries.data_ptr(), self.nbytes, self.budget,
+            self.entries.data_ptr() if use_record else None, self.nbytes if use_record else 0,
+            self.budget if use_record else 0,
             None if self.order is None else self.order.data_ptr())
 
     def check_matches(self, num_rays: int, settings, device) -> None:
@@ -361,6 +378,9 @@ class Pipeline:
                 plan.sort_rays(num_points, rays_c, start_c)
             if want_record:
                 plan.allocate_record(walk_budget)
+                plan.record_key = TracePlan.record_key(settings, points, attributes,
+                                                       point_adjacency, point_adjacency_offsets,
+                                                       rays, start_point)
             plan.keep_table(scratch, nbytes, TracePlan.scene_key(points_c, adj_c, offs_c))
         args = (
             self._sh_degree, C.byref(settings), num_points, ptr(points_c), ptr(attributes_c),
@@ -501,7 +521,11 @@ class Pipeline:
             ptr(dq), ptr(didx), ptr(rgba), ptr(g), ptr(dgrad), ptr(rerr), ptr(points_grad),
             ptr(attr_grad), ptr(point_error), ptr(sharpness), ptr(sharpness_grad),
             ptr(scratch), nbytes, _lib.stream_handle(dev))
-        desc = trace_plan.desc() if trace_plan is not None else _lib.TracePlanDesc()
+        desc = _lib.TracePlanDesc()
+        if trace_plan is not None:
+            desc = trace_plan.desc(TracePlan.record_key(settings, points, attributes,
+                                                        point_adjacency, point_adjacency_offsets,
+                                                        rays, start_point))
         desc.scratch_ready = 1 if table_ready else 0
         accum = None
         if grad_accum and num_rays > 0:

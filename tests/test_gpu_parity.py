@@ -565,3 +565,37 @@ def test_trace_rays_autograd(torch_dev):
     assert torch.count_nonzero(inv.grad[1:]) == 0
     assert float(rgba.detach()[..., 3].max()) <= 1.0
     del contrib, nis, errbox, alpha
+
+
+def test_walk_record_other_attributes(torch_dev):
+    """A plan handed to a backward over other attributes than its forward's
+    (the record holds the forward's colours) leaves its walk record out: the
+    gradients equal those of the backward without a plan, not those the
+    forward's colours would give."""
+    import torch
+
+    import sdfoam_amd
+
+    w = scene(2)
+    g = gpu_scene(w, torch_dev)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    inv_t = torch.tensor([w.inv_s], device=torch_dev)
+    grad = to_dev(w.grad_rgba, torch_dev)
+    fwd = pipe.trace_forward(**g, alpha_mode="sdfoam", inv_s=inv_t, record_walk=True)
+    g2 = dict(g)
+    g2["attributes"] = g["attributes"] * 1.25 + 0.05
+
+    def backward(plan):
+        return pipe.trace_backward(**g2, rgb_out=fwd["rgba"], grad_in=grad, alpha_mode="sdfoam",
+                                   inv_s=inv_t, trace_plan=plan)
+
+    b_plan, b_plain = backward(fwd["trace_plan"]), backward(None)
+    b_own = pipe.trace_backward(**g, rgb_out=fwd["rgba"], grad_in=grad, alpha_mode="sdfoam",
+                                inv_s=inv_t, trace_plan=fwd["trace_plan"])
+    for k in ("points_grad", "attr_grad", "sharpness_grad"):
+        ref = b_plain[k].cpu().numpy()
+        np.testing.assert_allclose(b_plan[k].cpu().numpy(), ref, rtol=1e-4,
+                                   atol=1e-5 * float(np.abs(ref).max()))
+    # the other attributes change the gradients (the check above can fail)
+    a, b = b_own["attr_grad"].cpu().numpy(), b_plain["attr_grad"].cpu().numpy()
+    assert np.abs(a - b).max() > 1e-3 * np.abs(b).max()

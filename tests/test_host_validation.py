@@ -77,3 +77,28 @@ def test_trace_rays_signature():
     assert params == ["ctx", "pipeline", "_points", "_attributes", "_point_adjacency",
                       "_point_adjacency_offsets", "rays", "start_point", "depth_quantiles",
                       "return_contribution", "use_sdfoam", "inv_s", "eps", "sdf_channel"]
+
+
+def test_trace_plan_keeps_record_for_its_own_inputs():
+    """The walk record holds the forward's colours, so a plan hands it to the
+    backward only for the forward's tensors (same storage, unmodified) and
+    the same alpha mode and sdf channel; otherwise the backward scans."""
+    from sdfoam_amd import _lib
+    from sdfoam_amd.pipeline import TracePlan
+
+    pts, attrs, adj, offs, rays, start = scene()
+    s = _lib.TraceSettings(0.01, 100, 1, 48, 0, 0)
+    plan = TracePlan(5, s, "cpu")
+    plan.allocate_record(4)
+    plan.record_key = TracePlan.record_key(s, pts, attrs, adj, offs, rays, start)
+    same = plan.desc(TracePlan.record_key(s, pts, attrs, adj, offs, rays, start))
+    assert same.walk_record == plan.entries.data_ptr() and same.walk_budget == 4
+    assert same.walk_record_bytes == plan.nbytes > 0
+    others = [TracePlan.record_key(s, pts, attrs.clone(), adj, offs, rays, start)]
+    attrs.add_(0.0)  # same values, new version
+    others.append(TracePlan.record_key(s, pts, attrs, adj, offs, rays, start))
+    s2 = _lib.TraceSettings(0.01, 100, 1, 47, 0, 0)
+    others.append(TracePlan.record_key(s2, pts, attrs, adj, offs, rays, start))
+    for key in others:
+        d = plan.desc(key)
+        assert not d.walk_record and d.walk_record_bytes == 0 and d.walk_budget == 0
