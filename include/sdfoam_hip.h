@@ -187,9 +187,11 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
  * `walk_budget` trips per wavefront of 64 rays); the backward then reads
  * the steps instead of scanning the cell faces again, and a recorded step's
  * colour instead of the cell's attribute row, so the record is valid only
- * for a backward over the attributes the forward traced.  In standard mode a step is recorded only while the density
- * backward's unsafe walk takes the same exit.  Rays past `walk_budget`
- * trips, or that walk further in the backward, scan as usual.
+ * for a backward over the attributes the forward traced.  In standard mode
+ * the density backward walks in the unsafe mode: where it would take another
+ * exit the forward marks its step, and the backward scans from there until its
+ * walk meets the recorded one again.  Rays past `walk_budget` trips, or that
+ * walk further in the backward, scan as usual.
  * walk_record == NULL: no record.
  *
  * Ray order: a permutation of [0, num_rays) from sdf_ray_order; the kernels

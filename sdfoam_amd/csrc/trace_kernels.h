@@ -23,6 +23,13 @@ int hip_fail(hipError_t e, const char *where);
 // standard mode), so the backward of a recorded step reads 16 bytes instead
 // of the cell's attribute row and skips the SH sum.
 constexpr uint32_t kWalkUnrecorded = 0xfffffffeu;
+// Standard mode: where the density backward's unsafe walk would leave the
+// forward's safe one, the forward keeps its own step as {next | kWalkDiffers,
+// t1} (num_points < 2^31 - 1, so the mark leaves both sentinels free); the
+// backward scans from there and takes up the record again once its walk
+// stands where the forward stood after one of the next kSeekWindow steps.
+constexpr uint32_t kWalkDiffers = 0x80000000u;
+constexpr uint32_t kSeekWindow = 4;
 constexpr uint32_t kWalkRecordEntryBytes = 8u + 16u;
 
 struct WalkRecordArgs {

@@ -215,6 +215,9 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
                 if (si.agrees)
                     entry = make_uint2(si.found ? si.next : kNoIndex,
                                        __builtin_bit_cast(uint32_t, si.t1));
+                else if (si.found && a.scene.num_points < kWalkDiffers - 1u)
+                    entry = make_uint2(si.next | kWalkDiffers,
+                                       __builtin_bit_cast(uint32_t, si.t1));
             }
         }
         // where this trip's colour goes (the step's, if the lane steps)
@@ -952,6 +955,15 @@ backward_density_kernel(BwdArgs a) {
         wcol = a.record.colors + (wrec - a.record.entries);
     }
     uint32_t trip = 0;
+    // ridx: the forward trip whose entry the lane reads next.  After an entry
+    // marked kWalkDiffers the lane scans (`seeking`) until its walk stands
+    // where the forward stood after one of that entry's first kSeekWindow
+    // steps, then replays from the step after it.  From equal (cell, t0) the
+    // two walks take the same steps wherever the forward recorded agreement,
+    // so the replayed walk is the unsafe one; the step limit counts the
+    // lane's own steps.
+    uint32_t ridx = 0;
+    bool seeking = false;
 
     while (__ballot(ws.alive) != 0ull) {
         StepInfo si;
@@ -962,25 +974,34 @@ backward_density_kernel(BwdArgs a) {
         bool replayed = false;
         if (ws.alive) {
             uint2 e = make_uint2(kWalkUnrecorded, 0u);
-            if (wrec && trip < a.record.budget) {
-                e = wrec[(uint64_t)trip * 64];
-                rc4 = wcol[(uint64_t)trip * 64];
+            if (wrec && !seeking && ridx < a.record.budget) {
+                e = wrec[(uint64_t)ridx * 64];
+                rc4 = wcol[(uint64_t)ridx * 64];
+                ++ridx;
             }
             if (e.x == kNoIndex) {
                 ++ws.n;
                 ws.alive = false;
             } else if (e.x < a.scene.num_points) {
                 ++ws.n;
-                si.found = true;
-                si.next = e.x;
-                si.t1 = __builtin_bit_cast(float, e.y);
-                si.xn[0] = a.scene.points[3ull * e.x];
-                si.xn[1] = a.scene.points[3ull * e.x + 1];
-                si.xn[2] = a.scene.points[3ull * e.x + 2];
-                si.stepped = si.t1 > ws.t0;
-                replayed = true;
+                if (ws.n > a.settings.max_intersections) {
+                    ws.alive = false; // the step limit, as walk_advance applies it
+                } else {
+                    si.found = true;
+                    si.next = e.x;
+                    si.t1 = __builtin_bit_cast(float, e.y);
+                    si.xn[0] = a.scene.points[3ull * e.x];
+                    si.xn[1] = a.scene.points[3ull * e.x + 1];
+                    si.xn[2] = a.scene.points[3ull * e.x + 2];
+                    si.stepped = si.t1 > ws.t0;
+                    replayed = true;
+                }
             } else {
-                wrec = nullptr;
+                if (e.x != kWalkUnrecorded && (e.x & ~kWalkDiffers) < a.scene.num_points) {
+                    seeking = true; // entry ridx - 1: the forward's differing step
+                } else if (!seeking) {
+                    wrec = nullptr;
+                }
                 walk_advance<false, STATS>(a.scene, ray, a.settings.max_intersections, ws, si,
                                            wc);
             }
@@ -1069,6 +1090,23 @@ backward_density_kernel(BwdArgs a) {
             if (si.stepped) publish_step<L>(tb, ents, ws.cell, dr, dg, db, dds, pe);
         }
         if (ws.alive && si.found) walk_move(ws, si);
+        if (seeking && ws.alive) {
+            // the forward's states after its steps ridx - 1, ridx, ...: back on
+            // its path where one equals this lane's (cell, t0)
+#pragma unroll
+            for (uint32_t k = 0; k < kSeekWindow; ++k) {
+                const uint32_t f = ridx - 1u + k;
+                if (f >= a.record.budget) break;
+                const uint2 fe = wrec[(uint64_t)f * 64];
+                if (fe.x == kNoIndex || fe.x == kWalkUnrecorded) break;
+                if ((fe.x & ~kWalkDiffers) == ws.cell &&
+                    fe.y == __builtin_bit_cast(uint32_t, ws.t0)) {
+                    seeking = false;
+                    ridx = f + 1u;
+                    break;
+                }
+            }
+        }
     }
     if constexpr (!STATS) {
         const float zero3[3] = {0.0f, 0.0f, 0.0f};

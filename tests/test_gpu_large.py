@@ -186,3 +186,45 @@ def test_c3_triangulation_matches_qhull(dev, say):
     for k, v in ref.items():
         got = getattr(tri, k)().view(torch.int32).cpu().numpy().view(np.uint32)
         assert np.array_equal(got.reshape(v.shape), v), k
+
+
+def test_c3_standard_record_replays_the_unsafe_walk(dev, say):
+    """Standard mode at C3 (1M points, 1600x1200 rays): the backward that
+    replays the forward's record, leaving it where the unsafe walk differs and
+    taking it up again where the walks meet, gives the gradients of the
+    backward that scans every step (itself checked against the oracle on the
+    smaller configs).  A lane replaying from a wrong place would follow other
+    cells and move the sums far outside this tolerance."""
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import scenes
+
+    say("generating C3 (standard)")
+    w = scenes.make_config(3, mode="standard")
+    pts = torch.from_numpy(w.points).to(dev)
+    attrs = torch.from_numpy(w.attributes).to(dev)
+    adj, offs = _u32(w.adjacency, dev), _u32(w.offsets, dev)
+    rays = torch.from_numpy(w.rays).to(dev)
+    tree = sdfoam_amd.build_aabb_tree(pts)
+    start = sdfoam_amd.get_starting_point(rays, pts, tree)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    q = torch.from_numpy(w.quantiles).to(dev)
+    grad = torch.from_numpy(w.grad_rgba).to(dev)
+    dg = torch.from_numpy(w.depth_grad).to(dev)
+    fwd = pipe.trace_forward(pts, attrs, adj, offs, rays, start, depth_quantiles=q,
+                             alpha_mode="standard", record_walk=True)
+
+    def backward(plan):
+        return pipe.trace_backward(pts, attrs, adj, offs, rays, start, fwd["rgba"], grad, q,
+                                   fwd["depth_indices"], dg, alpha_mode="standard",
+                                   trace_plan=plan)
+
+    b_rec, b_scan = backward(fwd["trace_plan"]), backward(None)
+    torch.cuda.synchronize()
+    say("C3 standard backward with and without the record")
+    for k in ("points_grad", "attr_grad"):
+        a, b = b_rec[k].cpu().numpy(), b_scan[k].cpu().numpy()
+        scale = float(np.abs(b).max())
+        assert scale > 0, k
+        np.testing.assert_allclose(a, b, rtol=1e-3, atol=1e-5 * scale, err_msg=k)
