@@ -29,7 +29,7 @@ constexpr uint32_t kWalkUnrecorded = 0xfffffffeu;
 // backward scans from there and takes up the record again once its walk
 // stands where the forward stood after one of the next kSeekWindow steps.
 constexpr uint32_t kWalkDiffers = 0x80000000u;
-constexpr uint32_t kSeekWindow = 4;
+constexpr uint32_t kSeekWindow = 8;
 constexpr uint32_t kWalkRecordEntryBytes = 8u + 16u;
 
 struct WalkRecordArgs {
