@@ -11,20 +11,25 @@ A step is one training pass of the path through the drop-in API:
 ``Pipeline.trace_backward`` -- each runs the fp16 offset prepass and its
 kernel, as the reference does.
 
-Output: one JSON line on stdout.  ``roofline`` prices the dominant kernel's
-algorithmic bytes (the gather model below) against MI355X's 8 TB/s, with the
-kernel's average duration measured live by HIP events recorded on its launch
-stream.  ``cpu_baseline`` is the scalar host oracle (a port of the
-reference's algorithm) on a strided sample of the same rays, on this host's
-cores.
+Output: one JSON line on stdout.  ``roofline`` is the dominant kernel's HBM
+rate: the HBM bytes per launch that rocprofv3 counted for it (FETCH_SIZE and
+WRITE_SIZE, scaled by a copy kernel of known size; profiles/traffic_*.json)
+over its average duration, measured live by HIP events recorded on its launch
+stream, against MI355X's 8 TB/s.  Beside it, ``model_frac`` prices the
+kernel's algorithmic bytes (the gather model below, which counts every gather
+as an HBM access although L2 and the MALL serve most of them) the same way.
+``cpu_baseline`` is the scalar host oracle (a port of the reference's
+algorithm) on a strided sample of the same rays, on every CPU the process may
+use, plus a one-thread run.
 
-Byte model (per launch; D = attribute width, deg = CSR row length of the
+Gather model (per launch; D = attribute width, deg = CSR row length of the
 stepped cell, Q = quantiles):
   forward : per ray 48 + 12Q; per step 28 + 4D + 4 (contribution) + 8 deg
   backward: per ray 60 + 12Q; per step 36 + 8D + 8 deg
   prepass : 12 E + 16 N
-With the walk record (default, as TraceRays runs it) the forward writes 8 B
-per step more and the backward reads those 8 B instead of 8 deg.
+With the walk record (default, as TraceRays runs it) the forward also writes
+24 B per step and the backward reads them instead of the face rows and the
+attribute row.
 """
 
 from __future__ import annotations
@@ -52,12 +57,40 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_threads() -> int:
+def cpu_affinity() -> int:
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        return os.cpu_count() or 1
+
+
+def cpu_quota():
+    """CPUs this process's cgroup may use (cgroup v2 cpu.max or v1 CFS
+    quota), or None when unlimited."""
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+            if q != "max":
+                return max(1, int(int(q) / int(period)))
+            return None
+    except (OSError, ValueError):
+        pass
+    try:
+        with open("/sys/fs/cgroup/cpu/cpu.cfs_quota_us") as f:
+            q = int(f.read())
+        with open("/sys/fs/cgroup/cpu/cpu.cfs_period_us") as f:
+            period = int(f.read())
+        return max(1, q // period) if q > 0 else None
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_threads() -> int:
+    """Every CPU the process may run on: its affinity set, bounded by its
+    cgroup's CPU quota."""
+    n = cpu_affinity()
+    q = cpu_quota()
+    return max(1, min(n, q) if q else n)
 
 
 def cpu_model() -> str:
@@ -260,33 +293,35 @@ def main() -> int:
     N = w.num_points
     E = int(w.adjacency.size)
     # attribute elements (rows, contribution, gradient rows) at their storage
-    # width; with the walk record the backward reads 24 B per step (the step
-    # and its colour) instead of the stepped cell's face rows and attribute
-    # row (standard mode: all but the rare steps where the unsafe walk leaves
-    # the recorded one)
+    # width.  The gather model prices every access as an HBM access, whether
+    # or not the walk record replaces it (the record's own 24 B per step,
+    # written by the forward and read by the backward, are counted apart).
     ab = 2 if half else 4
     recorded = use_record
-    if recorded:
-        # the forward also writes 24 B per step; the backward reads them
-        bytes_fwd = R * (48 + 12 * Q) + S * (28 + ab * D + ab + 24) + 8 * F_st
-        bytes_bwd = R * (60 + 12 * Q) + S * (36 + ab * D + 24)
-    else:
-        bytes_fwd = R * (48 + 12 * Q) + S * (28 + ab * D + ab) + 8 * F_st
-        bytes_bwd = R * (60 + 12 * Q) + S * (36 + 2 * ab * D) + 8 * F_st
+    gather_fwd = R * (48 + 12 * Q) + S * (28 + ab * D + ab) + 8 * F_st
+    gather_bwd = R * (60 + 12 * Q) + S * (36 + 2 * ab * D) + 8 * F_st
+    record_bytes = 24 * S if recorded else 0
     bytes_pre = 12 * E + 16 * N
     # offset-table builds per step (the backward reuses the forward's table
     # when it gets the forward's trace plan)
     pre_per_step = len(per_kernel.get("prefetch_adjacent_diff", [])) / args.steps
-    bytes_step = bytes_fwd + bytes_bwd + pre_per_step * bytes_pre
-
-    kernel_bytes = {"forward": bytes_fwd, "backward": bytes_bwd, "prefetch_adjacent_diff": bytes_pre}
+    bytes_step = gather_fwd + gather_bwd + pre_per_step * bytes_pre
+    kernel_bytes = {"forward": gather_fwd, "backward": gather_bwd,
+                    "prefetch_adjacent_diff": bytes_pre}
     dominant = max((k for k in avg if k in kernel_bytes), key=lambda k: avg[k] * len(per_kernel[k]))
-    achieved = kernel_bytes[dominant] / (avg[dominant] * 1e-3) / 1e9
+    kernel_s = avg[dominant] * 1e-3
+    model_gbps = kernel_bytes[dominant] / kernel_s / 1e9
 
-    traffic = None
     variant = ("" if use_record else "_scan") + ("" if args.alpha_mode == "sdfoam" else "_standard") \
         + ("_f16" if half else "")
-    traffic = load_traffic(f"traffic_{dominant}{variant}_C{args.config}.json")
+    counters = load_counters(f"traffic_{dominant}{variant}_C{args.config}.json")
+    traffic = counters.get("hbm_bytes_per_launch") if counters else None
+    if traffic:
+        # measured HBM bytes of this kernel (rocprofv3 FETCH_SIZE / WRITE_SIZE,
+        # calibrated) over its live duration
+        achieved, basis = traffic / kernel_s / 1e9, "rocprof HBM bytes per launch / live kernel time"
+    else:
+        achieved, basis = model_gbps, "gather model (no rocprof counters for this workload)"
 
     if args.config == 5:
         rays_desc = f"{R} rays per step sampled from 64 cameras 960x640 (10 seeded batches)"
@@ -327,8 +362,8 @@ def main() -> int:
         "faces_per_step": F_st / max(S, 1),
         "faces_scanned": F_all,
         "kernel_ms": avg,
-        "algorithmic_bytes": {"forward": bytes_fwd, "backward": bytes_bwd, "prefetch": bytes_pre,
-                              "step": bytes_step},
+        "algorithmic_bytes": {"forward": gather_fwd, "backward": gather_bwd, "prefetch": bytes_pre,
+                              "step": bytes_step, "walk_record_each_way": record_bytes},
         "step_algorithmic_GBps": bytes_step / (ms_per_step * 1e-3) / 1e9,
         "roofline": {
             "kernel": dominant,
@@ -338,6 +373,13 @@ def main() -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic,
+            "basis": basis,
+            "kernel_ms": avg[dominant],
+            "l2_hit": counters.get("l2_hit") if counters else None,
+            "counters": counters.get("source") if counters else None,
+            "algorithmic_bytes": kernel_bytes[dominant],
+            "model_achieved": model_gbps,
+            "model_frac": model_gbps / HBM_PEAK_GBS,
         },
     }
 
@@ -357,14 +399,21 @@ def main() -> int:
 CPU_SAMPLE_RAYS = 640_000
 
 
-def load_traffic(name):
-    """HBM bytes per launch that a committed rocprofv3 counter summary
-    (profiles/<name>) records, or None."""
+def load_counters(name):
+    """A committed rocprofv3 counter summary of one kernel (profiles/<name>):
+    HBM bytes per launch, L2 hit rate, source table; or None."""
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        return json.load(f)
+
+
+def load_traffic(name):
+    """HBM bytes per launch that a committed rocprofv3 counter summary
+    (profiles/<name>) records, or None."""
+    c = load_counters(name)
+    return c.get("hbm_bytes_per_launch") if c else None
 
 
 def gpu_simplices(points, dev):
@@ -677,29 +726,43 @@ def cpu_baseline(w, rays, start, quantiles, grad_rgba, depth_grad, stride: int,
 
     oracle.build()
     threads = cpu_threads()
-    rays = rays.reshape(-1, 6)[::stride]
-    sp = start.reshape(-1)[::stride]
-    qv = quantiles.reshape(-1, quantiles.shape[-1])[::stride]
-    g = grad_rgba.reshape(-1, 4)[::stride]
-    dg = depth_grad.reshape(-1, depth_grad.shape[-1])[::stride]
-    log(f"CPU baseline: {rays.shape[0]} rays on {threads} threads")
-    t0 = time.perf_counter()
-    f = oracle.trace_forward(w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, rays, sp,
-                             qv, alpha_mode=alpha_mode, inv_s=w.inv_s, threads=threads)
-    oracle.trace_backward(w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, rays, sp,
-                          f.rgba, g, qv, f.depth_indices, dg, alpha_mode=alpha_mode,
-                          inv_s=w.inv_s,
-                          threads=threads, side_buffers=False)
-    dt = time.perf_counter() - t0
-    log(f"CPU baseline: {dt:.1f}s")
+
+    def run(step, nthreads):
+        r = rays.reshape(-1, 6)[::step]
+        sp = start.reshape(-1)[::step]
+        qv = quantiles.reshape(-1, quantiles.shape[-1])[::step]
+        g = grad_rgba.reshape(-1, 4)[::step]
+        dg = depth_grad.reshape(-1, depth_grad.shape[-1])[::step]
+        log(f"CPU baseline: {r.shape[0]} rays on {nthreads} threads")
+        t0 = time.perf_counter()
+        f = oracle.trace_forward(w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, r,
+                                 sp, qv, alpha_mode=alpha_mode, inv_s=w.inv_s, threads=nthreads)
+        oracle.trace_backward(w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, r, sp,
+                              f.rgba, g, qv, f.depth_indices, dg, alpha_mode=alpha_mode,
+                              inv_s=w.inv_s, threads=nthreads, side_buffers=False)
+        dt = time.perf_counter() - t0
+        log(f"CPU baseline: {dt:.1f}s")
+        return r.shape[0], int(np.sum(f.steps)), dt
+
+    n, steps, dt = run(stride, threads)
+    # one thread on a sample a sixteenth the size (about as long)
+    n1, steps1, dt1 = run(stride * 16, 1)
     return {
-        "value": rays.shape[0] / dt / 1e6,
+        "value": n / dt / 1e6,
         "unit": "Mrays/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"1 ray in {stride} of the same workload ({rays.shape[0]} rays, "
-                  f"{int(np.sum(f.steps))} cell steps), forward + backward, {dt:.1f}s on "
-                  f"{threads} threads of {cpu_model()}",
+        "sample": f"1 ray in {stride} of the same workload ({n} rays, {steps} cell steps), "
+                  f"forward + backward, {dt:.1f}s on {threads} threads (every CPU the process "
+                  f"may use) of {cpu_model()}",
+        "cell_steps_per_s": steps / dt,
+        "cpu_model": cpu_model(),
+        "affinity_cpus": cpu_affinity(),
+        "cgroup_cpu_quota": cpu_quota(),
+        "single_thread": {"value": n1 / dt1 / 1e6, "unit": "Mrays/s", "cores": 1,
+                          "cell_steps_per_s": steps1 / dt1,
+                          "sample": f"1 ray in {stride * 16} ({n1} rays, {steps1} cell steps), "
+                                    f"{dt1:.1f}s on one thread"},
     }
 
 

@@ -191,11 +191,31 @@ class TracePlan:
             self.budget if use_record else 0,
             None if self.order is None else self.order.data_ptr())
 
+    def matches(self, num_rays: int, settings, device) -> bool:
+        return (num_rays == self.num_rays
+                and int(settings.ray_image_width) == self.ray_image_width
+                and int(settings.max_intersections) == self.max_intersections
+                and self.device == torch.device(device))
+
     def check_matches(self, num_rays: int, settings, device) -> None:
-        if (num_rays != self.num_rays or int(settings.ray_image_width) != self.ray_image_width
-                or int(settings.max_intersections) != self.max_intersections
-                or self.device != torch.device(device)):
+        if not self.matches(num_rays, settings, device):
             raise RuntimeError("trace_plan does not belong to these rays and settings")
+
+
+def _backward_can_follow(points, attributes, inv_s) -> bool:
+    """Whether autograd can ask for this trace's backward: some traced input
+    requires grad.  Under ``torch.no_grad()`` the reference's scene builds its
+    attribute rows and sharpness without grad (sdfoam_model/scene.py:259-265,
+    252-254), so evaluation renders fall outside this even though the points
+    are parameters."""
+    return bool(attributes.requires_grad
+                or (isinstance(inv_s, torch.Tensor) and inv_s.requires_grad)
+                or (points.requires_grad and torch.is_grad_enabled()))
+
+
+# attribute of a forward's rgba tensor that carries its trace plan to the
+# backward over it (the reference's TraceRays hands the backward that tensor)
+_PLAN_ATTR = "_sdfoam_trace_plan"
 
 
 def _auto_sort(sort_rays, settings, num_rays: int) -> bool:
@@ -314,7 +334,7 @@ class Pipeline:
     def trace_forward(self, points, attributes, point_adjacency, point_adjacency_offsets, rays,
                       start_point, depth_quantiles=None, weight_threshold=None,
                       max_intersections=None, return_contribution=False, alpha_mode=None,
-                      inv_s=None, eps=None, sdf_channel=None, record_walk=False,
+                      inv_s=None, eps=None, sdf_channel=None, record_walk=None,
                       walk_budget=None, sort_rays=None):
         """Reference arguments and outputs, plus (no counterpart in the
         reference):
@@ -323,14 +343,19 @@ class Pipeline:
           skips its face scans (standard mode: the steps where the density
           backward's unsafe walk takes the same exit, which is all of them
           but for degenerate ties); ``walk_budget`` bounds the recorded trips
-          per wavefront;
+          per wavefront.  ``None`` (the default) records when a backward can
+          follow: the attributes or ``inv_s`` require grad (or the points do
+          with grad mode on), which is how the reference's scene calls it in
+          training and not under ``torch.no_grad()``;
         * ``sort_rays``: trace rays of shape [R, 6] in sorted order
           (sdf_ray_order); None sorts from 32768 rays on.  Outputs stay in
           the caller's order.
 
         When either applies, the result holds ``"trace_plan"``, which
         ``trace_backward(trace_plan=...)`` over the same rays and settings
-        takes."""
+        takes.  The plan also rides on the returned ``rgba`` tensor, so a
+        ``trace_backward`` handed that tensor as ``rgb_out`` (as the
+        reference's ``TraceRays`` does) uses it without being given it."""
         points_c = points.contiguous()
         attributes_c = attributes.contiguous()
         adj_c = point_adjacency.contiguous()
@@ -370,9 +395,12 @@ class Pipeline:
         alpha = torch.zeros((num_points, 1), dtype=torch.float32, device=dev)
         scratch, nbytes = self._scratch(num_points, num_adj, dev)
         plan = None
-        want_record = bool(record_walk)
+        if record_walk is None:
+            want_record = num_rays > 0 and _backward_can_follow(points, attributes, inv_s)
+        else:
+            want_record = bool(record_walk)
         want_sort = num_rays > 0 and _auto_sort(sort_rays, settings, num_rays)
-        if record_walk or want_sort:
+        if want_record or want_sort:
             plan = TracePlan(num_rays, settings, dev)
             if want_sort:
                 plan.sort_rays(num_points, rays_c, start_c)
@@ -381,7 +409,10 @@ class Pipeline:
                 plan.record_key = TracePlan.record_key(settings, points, attributes,
                                                        point_adjacency, point_adjacency_offsets,
                                                        rays, start_point)
-            plan.keep_table(scratch, nbytes, TracePlan.scene_key(points_c, adj_c, offs_c))
+            # keyed on the caller's tensors: a contiguous copy made above is
+            # freed after this call and its storage may be handed out again
+            plan.keep_table(scratch, nbytes,
+                            TracePlan.scene_key(points, point_adjacency, point_adjacency_offsets))
         args = (
             self._sh_degree, C.byref(settings), num_points, ptr(points_c), ptr(attributes_c),
             num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c), ptr(start_c), num_q,
@@ -402,6 +433,7 @@ class Pipeline:
         out["alpha"] = alpha
         if plan is not None:
             out["trace_plan"] = plan
+            setattr(rgba, _PLAN_ATTR, plan)
         return out
 
     # -- trace_backward (torch_bindings/pipeline_bindings.cpp:336-607) ------
@@ -411,7 +443,8 @@ class Pipeline:
                        max_intersections=None, alpha_mode=None, inv_s=None, eps=None,
                        sdf_channel=None, trace_plan=None, sort_rays=None, grad_accum=True):
         """Reference arguments and outputs, plus ``trace_plan`` (the
-        forward's "trace_plan": its ray order and walk record),
+        forward's "trace_plan": its ray order and walk record; by default the
+        plan the forward attached to ``rgb_out``, which this call detaches),
         ``sort_rays`` (as in trace_forward, when no plan is given) and
         ``grad_accum``: accumulate each cell's gradients in one aligned fp32
         row of a temporary buffer (256 bytes per cell at SH degree 3) before
@@ -505,9 +538,17 @@ class Pipeline:
         ray_grad = torch.zeros_like(rays_c)
         sharpness_grad = torch.zeros_like(sharpness, dtype=torch.float32)
         table_ready = False
+        # the plan of the forward that produced rgb_out, used by one backward
+        # (detached here, so the record does not outlive it with the tensor)
+        carried = getattr(rgb_out, _PLAN_ATTR, None)
+        if carried is not None:
+            delattr(rgb_out, _PLAN_ATTR)
+            if trace_plan is None and carried.matches(num_rays, settings, dev):
+                trace_plan = carried
         if trace_plan is not None:
             trace_plan.check_matches(num_rays, settings, dev)
-            kept = trace_plan.table_for(TracePlan.scene_key(points_c, adj_c, offs_c))
+            kept = trace_plan.table_for(
+                TracePlan.scene_key(points, point_adjacency, point_adjacency_offsets))
             if kept is not None:
                 scratch, nbytes, table_ready = kept, trace_plan.table_bytes, True
         if not table_ready:

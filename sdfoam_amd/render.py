@@ -3,10 +3,14 @@
 Same forward/backward contract as the reference's ``TraceRays``
 (sdfoam_model/render.py:10-189): forward returns
 ``(rgba, depth, contribution, num_intersections, ErrorBox, alpha)``; backward
-calls ``trace_backward`` with the saved forward outputs (and the forward's
-trace plan: ray order, walk record and offset table), zeroes non-finite
+calls ``trace_backward`` with the saved forward outputs, zeroes non-finite
 gradients and returns gradients for ``points``, ``attributes`` and, in
-sdfoam mode, ``inv_s``.
+sdfoam mode, ``inv_s``.  The calls to the pipeline are the reference's: the
+forward's trace plan (ray order, walk record, offset table) reaches the
+backward on the saved ``rgba`` tensor, as it does when the reference's own
+``TraceRays`` drives this build's pipeline.  The walk is recorded only when
+a backward can follow (the attributes or ``inv_s`` require grad), so an
+evaluation render under ``torch.no_grad()`` records nothing.
 """
 
 from __future__ import annotations
@@ -51,12 +55,8 @@ class TraceRays(torch.autograd.Function):
             inv_s=ctx.inv_s,
             eps=ctx.eps,
             sdf_channel=ctx.sdf_channel,
-            record_walk=True,
         )
         ctx.rgba = results["rgba"]
-        # the forward's ray order, walk steps (sdfoam mode) and offset table,
-        # reused by the backward (no counterpart in the reference)
-        ctx.trace_plan = results.get("trace_plan", None)
         ctx.depth_indices = results.get("depth_indices", None)
         errbox = ErrorBox()
         ctx.errbox = errbox
@@ -81,7 +81,6 @@ class TraceRays(torch.autograd.Function):
             inv_s=ctx.inv_s,
             eps=ctx.eps,
             sdf_channel=ctx.sdf_channel,
-            trace_plan=ctx.trace_plan,
         )
         points_grad = results["points_grad"].contiguous()
         attr_grad = results["attr_grad"].contiguous()
@@ -94,8 +93,7 @@ class TraceRays(torch.autograd.Function):
         if sharpness_grad is not None:
             sharpness_grad[~sharpness_grad.isfinite()] = 0
         del (ctx.rays, ctx.start_point, ctx.pipeline, ctx.rgba, ctx.points, ctx.attributes,
-             ctx.point_adjacency, ctx.point_adjacency_offsets, ctx.depth_quantiles,
-             ctx.trace_plan)
+             ctx.point_adjacency, ctx.point_adjacency_offsets, ctx.depth_quantiles)
         return (
             None,
             points_grad,

@@ -148,6 +148,49 @@ def test_c4_cameras(dev, oracle_lib, say):
     say("C4 subset backward parity")
 
 
+def test_c3_headline_parity(dev, oracle_lib, say):
+    """The headline workload as bench.py times it (C3: 1M points near a
+    superquadric, SH degree 3, sdfoam alpha, inv_s = e^0.3, 1600x1200 rays,
+    forward with the walk record, backward replaying it):
+
+    * the full batch's start cells, contribution sum, loop counts, depth
+      indices and gradient finiteness;
+    * every one of the 1.92M rays against the oracle forward: visit hash,
+      step count, faces scanned, num_intersections and depth indices
+      bit-exact; rgba and depth within 1e-4 / 1e-5; contribution within the
+      summation bound;
+    * the backward's walk of every ray equals the oracle's (the sdfoam
+      backward walks in the forward's safe mode);
+    * the backward's gradients against the oracle on the image-shaped subset
+      of every 4th row and column (120k rays through the tile path)."""
+    import torch
+
+    from test_gpu_parity import (_backward_both, _check_backward, _check_forward,
+                                 _forward_both, gpu_scene)
+
+    w = big_scene(3, say)
+    start = _full_batch_properties(w, dev, say, w.rays, w.quantiles, w.grad_rgba, w.depth_grad)
+    full = dataclasses.replace(w, extra={"start": np.ascontiguousarray(start)})
+    out, st, ref = _forward_both(full, dev, oracle_lib, "sdfoam", record=0, record_walk=True)
+    _check_forward(out, st, ref, full, 0)
+    say(f"C3 forward parity on all {full.num_rays} rays "
+        f"({float(ref.steps.mean()):.1f} steps per ray)")
+    import sdfoam_amd
+
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    bst = pipe.walk_stats(**gpu_scene(full, dev), backward=True, alpha_mode="sdfoam",
+                          inv_s=torch.tensor([w.inv_s], device=dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(bst["visit_hash"].cpu().numpy().view(np.uint64),
+                          ref.visit_hash.reshape(-1)), "backward walk"
+    del out, st, ref, bst
+    sl = (slice(None, None, 4), slice(None, None, 4))
+    sub = _subset(w, w.rays[sl], w.quantiles[sl], w.grad_rgba[sl], w.depth_grad[sl], start[sl])
+    bwd, st, ref = _backward_both(sub, dev, oracle_lib, "sdfoam", walk=True)
+    _check_backward(bwd, st, ref, sub)
+    say(f"C3 backward parity on the {sub.num_rays}-ray image subset")
+
+
 def test_c4_render_full_camera(dev, oracle_lib, say):
     from test_gpu_render import _render_both
 

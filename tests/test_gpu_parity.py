@@ -161,7 +161,8 @@ def test_prefetch_diff_bitexact(torch_dev, oracle_lib, cfg):
     assert np.array_equal(got, ref)
 
 
-def _forward_both(w, dev, oracle_lib, mode, record=0, inv_s=None, sort_rays=None):
+def _forward_both(w, dev, oracle_lib, mode, record=0, inv_s=None, sort_rays=None,
+                  record_walk=False):
     import torch
 
     import sdfoam_amd
@@ -171,7 +172,8 @@ def _forward_both(w, dev, oracle_lib, mode, record=0, inv_s=None, sort_rays=None
     pipe = sdfoam_amd.create_pipeline(w.sh_degree)
     q = to_dev(w.quantiles, dev)
     out = pipe.trace_forward(**g, depth_quantiles=q, return_contribution=True, alpha_mode=mode,
-                             inv_s=torch.tensor([inv], device=dev), sort_rays=sort_rays)
+                             inv_s=torch.tensor([inv], device=dev), sort_rays=sort_rays,
+                             record_walk=record_walk)
     st = pipe.walk_stats(**g, alpha_mode=mode, inv_s=torch.tensor([inv], device=dev),
                          record_cells=record)
     torch.cuda.synchronize()
@@ -385,6 +387,32 @@ def test_walk_record_standard_mode_c2(torch_dev, oracle_lib):
     w = scene(2, mode="standard")
     bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, "standard", walk=True)
     _check_backward(bwd, st, ref, w)
+
+
+@pytest.mark.parametrize("cfg", [1, 2])
+def test_walk_record_standard_marks_differing_steps(torch_dev, cfg):
+    """The standard-mode parity tests above cover the backward's re-meet
+    replay only if their scenes hold steps where the unsafe walk leaves the
+    forward's: count the entries the forward marks {next | 2^31, t1}.  C2 has
+    them (asserted); C1's count is reported."""
+    import torch
+
+    import sdfoam_amd
+
+    w = scene(cfg, mode="standard")
+    g = gpu_scene(w, torch_dev)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    fwd = pipe.trace_forward(**g, alpha_mode="standard", record_walk=True)
+    plan = fwd["trace_plan"]
+    torch.cuda.synchronize()
+    n = plan.nbytes // 24  # 8-byte {next, t1} entries first, then the 16-byte colours
+    nxt = plan.entries[:n].cpu().numpy().view(np.uint64) & np.uint64(0xFFFFFFFF)
+    marked = int(np.count_nonzero(((nxt & np.uint64(0x80000000)) != 0)
+                                  & (nxt < np.uint64(0xFFFFFFFE))))
+    stepped = int(np.count_nonzero(nxt < np.uint64(w.num_points)))
+    print(f"C{cfg} standard: {marked} marked of {stepped + marked} recorded steps")
+    if cfg == 2:
+        assert marked > 0
 
 
 def test_walk_record_mismatch_raises(torch_dev):

@@ -102,3 +102,37 @@ def test_trace_plan_keeps_record_for_its_own_inputs():
     for key in others:
         d = plan.desc(key)
         assert not d.walk_record and d.walk_record_bytes == 0 and d.walk_budget == 0
+
+
+def test_sdfoam_import_name():
+    """`import sdfoam` (the reference's module name, sdfoam_model/scene.py:8)
+    gives this build's objects for every name the reference's scripts use."""
+    import sdfoam
+
+    for name in ("create_pipeline", "build_aabb_tree", "nn", "Triangulation",
+                 "TriangulationFailedError", "farthest_neighbor", "BatchFetcher"):
+        assert getattr(sdfoam, name) is getattr(sdfoam_amd, name), name
+    with pytest.raises(RuntimeError, match="viewer"):
+        sdfoam.run_with_viewer(None, None)
+
+
+def test_record_walk_default_follows_autograd():
+    """record_walk=None records only when a backward can follow: the
+    attributes or inv_s require grad, or the points do with grad mode on
+    (inside an autograd Function's forward grad mode is off, so there the
+    points alone do not count: the reference's scene builds its attributes
+    without grad under torch.no_grad())."""
+    from sdfoam_amd.pipeline import _backward_can_follow
+
+    pts = torch.nn.Parameter(torch.zeros(4, 3))
+    att = torch.nn.Parameter(torch.zeros(4, 49))
+    attributes = torch.cat([att[:, :48], att[:, 48:]], dim=-1)
+    assert _backward_can_follow(pts, attributes, 1.0)
+    with torch.no_grad():
+        frozen = torch.cat([att[:, :48], att[:, 48:]], dim=-1)
+        assert not _backward_can_follow(pts, frozen, torch.ones(4, 1))
+    assert _backward_can_follow(pts, frozen, 1.0)  # grad mode on: the points count
+    inv = torch.ones(4, 1, requires_grad=True)
+    with torch.no_grad():
+        assert _backward_can_follow(pts, frozen, inv)
+    assert not _backward_can_follow(pts.detach(), frozen, 50.0)
