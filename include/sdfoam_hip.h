@@ -135,6 +135,34 @@ int sdf_trace_backward(int sh_degree, const sdf_trace_settings *settings,
                        float *sharpness_grad, void *scratch,
                        size_t scratch_bytes, void *stream);
 
+/* sdf_trace_forward without caller scratch.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * call allocates nothing: the fp16 offset table lives in a static device
+ * array of SDF_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it
+ * runs on until the process ends (its first call on a device looks up the
+ * array's address there).  Scenes are limited to
+ * SDF_NOALLOC_SCRATCH_BYTES / 8 - 32 = 16,777,184 adjacency entries (about
+ * one million Delaunay points); larger ones fail with SDF_E_INVALID before
+ * any work is queued.  All calls on one GPU share the array, so calls that
+ * overlap on one GPU (on other streams or threads) race: the caller must
+ * serialise them.  Arguments and results are sdf_trace_forward's. */
+#define SDF_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+int sdf_trace_forward_noalloc(int sh_degree, const sdf_trace_settings *settings,
+                              uint32_t num_points, const float *points,
+                              const float *attributes, uint32_t adjacency_size,
+                              const uint32_t *point_adjacency,
+                              const uint32_t *point_adjacency_offsets,
+                              uint32_t num_rays, const float *rays,
+                              const uint32_t *start_point_index,
+                              uint32_t num_depth_quantiles,
+                              const float *depth_quantiles, float *ray_rgba,
+                              float *quantile_depths,
+                              uint32_t *quantile_point_indices,
+                              uint32_t *num_intersections,
+                              float *point_contribution, const float *sharpness,
+                              float *alpha_output, void *stream);
+
 /* Camera of the inference render (src/tracing/camera.h:17-27). */
 #define SDF_CAMERA_PINHOLE 0
 #define SDF_CAMERA_FISHEYE 1

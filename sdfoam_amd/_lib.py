@@ -27,6 +27,7 @@ EXPORTS = (
     "sdf_trace_scratch_bytes",
     "sdf_prefetch_adjacent_diff",
     "sdf_trace_forward",
+    "sdf_trace_forward_noalloc",
     "sdf_trace_backward",
     "sdf_trace_benchmark",
     "sdf_walk_record_bytes",
@@ -152,6 +153,8 @@ def lib() -> C.CDLL:
     L.sdf_trace_forward.argtypes = [
         C.c_int, C.POINTER(TraceSettings), U32, P, P, U32, P, P, U32, P, P, U32, P,
         P, P, P, P, P, P, P, P, SZ, P]
+    L.sdf_trace_forward_noalloc.restype = C.c_int
+    L.sdf_trace_forward_noalloc.argtypes = L.sdf_trace_forward.argtypes[:-3] + [P]
     L.sdf_trace_backward.restype = C.c_int
     L.sdf_trace_backward.argtypes = [
         C.c_int, C.POINTER(TraceSettings), U32, P, P, U32, P, P, U32, P, P, U32, P, P,

@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "trace_kernels.h"
 
@@ -300,6 +301,45 @@ int trace_backward_impl(const sdf_trace_plan *plan, int sh_degree,
 
 } // namespace
 
+// ---- the forward for callers that cannot allocate -------------------------
+// sdf_trace_forward_noalloc keeps the fp16 offset table in this file-scope
+// device array instead of caller scratch: every GPU the library runs on holds
+// its own copy until the process ends.  In host code the array's name is only
+// a host-side stand-in; kernels get the device address hipGetSymbolAddress
+// gives for the current device, looked up on the entry point's first call on
+// that device and kept per device.  The prefetch pass rewrites every entry
+// the walk reads (the padding included) on each call, so nothing has to start
+// at zero.
+static __device__ __align__(256) uint8_t noalloc_scratch[SDF_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void *g_noalloc_ptr[kMaxDevices] = {};
+
+// Device address of noalloc_scratch on the current device.
+int noalloc_scratch_ptr(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(SDF_E_INVALID, "device %d: the library keeps scratch for devices 0..%d", dev,
+                    kMaxDevices - 1);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(noalloc_scratch)");
+        if (!p) return fail(SDF_E_HIP, "hipGetSymbolAddress(noalloc_scratch) gave NULL");
+        g_noalloc_ptr[dev] = p;
+    }
+    *out = g_noalloc_ptr[dev];
+    return SDF_OK;
+}
+
+} // namespace
+
 extern "C" {
 
 const char *sdf_version(void) { return "sdfoam_hip 0.1 (gfx950)"; }
@@ -354,6 +394,35 @@ int sdf_trace_forward(int sh_degree, const sdf_trace_settings *settings, uint32_
                               ray_rgba, quantile_depths, quantile_point_indices,
                               num_intersections, point_contribution, sharpness, alpha_output,
                               scratch, scratch_bytes, stream);
+}
+
+int sdf_trace_forward_noalloc(int sh_degree, const sdf_trace_settings *settings,
+                              uint32_t num_points, const float *points, const float *attributes,
+                              uint32_t adjacency_size, const uint32_t *point_adjacency,
+                              const uint32_t *point_adjacency_offsets, uint32_t num_rays,
+                              const float *rays, const uint32_t *start_point_index,
+                              uint32_t num_depth_quantiles, const float *depth_quantiles,
+                              float *ray_rgba, float *quantile_depths,
+                              uint32_t *quantile_point_indices, uint32_t *num_intersections,
+                              float *point_contribution, const float *sharpness,
+                              float *alpha_output, void *stream) {
+    const size_t need = sdf_trace_scratch_bytes(num_points, adjacency_size);
+    if (need > SDF_NOALLOC_SCRATCH_BYTES)
+        return fail(SDF_E_INVALID,
+                    "sdf_trace_forward_noalloc: %u adjacency entries need %zu bytes of offset "
+                    "table, more than its %zu-byte static scratch (at most %zu entries); use "
+                    "sdf_trace_forward with caller scratch",
+                    adjacency_size, need, (size_t)SDF_NOALLOC_SCRATCH_BYTES,
+                    (size_t)SDF_NOALLOC_SCRATCH_BYTES / 8 - kDiffPad);
+    void *table = nullptr;
+    const int rc = noalloc_scratch_ptr(&table);
+    if (rc != SDF_OK) return rc;
+    return trace_forward_impl(nullptr, sh_degree, settings, num_points, points, attributes,
+                              adjacency_size, point_adjacency, point_adjacency_offsets, num_rays,
+                              rays, start_point_index, num_depth_quantiles, depth_quantiles,
+                              ray_rgba, quantile_depths, quantile_point_indices,
+                              num_intersections, point_contribution, sharpness, alpha_output,
+                              table, SDF_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int sdf_trace_backward(int sh_degree, const sdf_trace_settings *settings, uint32_t num_points,
