@@ -415,11 +415,13 @@ struct WaveTables {
     __device__ float *rec() { return buf + kRec; }
 };
 
-// Next member of a lane mask (64 = padding once the mask is empty).
-__device__ __forceinline__ int pop_member(uint64_t &mm) {
-    if (!mm) return 64;
-    const int m = first_lane(mm);
-    mm &= mm - 1;
+// Next member of a lane mask (64 = padding once the mask is empty).  Three
+// scalar instructions: s_ff1 and s_min (s_ff1 gives -1 for an empty mask)
+// and s_bitset0, which takes bit m mod 64 (bit 0 of an already empty mask
+// for the padding member).
+__device__ __forceinline__ uint32_t pop_member(uint64_t &mm) {
+    const uint32_t m = mm ? (uint32_t)__builtin_ctzll(mm) : 64u;
+    asm("s_bitset0_b64 %0, %1" : "+s"(mm) : "s"(m));
     return m;
 }
 
@@ -482,7 +484,7 @@ __device__ __forceinline__ float sum_members(uint64_t mm, const float *__restric
     const float *gb = buf + ow.g_base + slot * ow.g_slot;
     float acc = 0.0f;
     while (mm) {
-        int m[4];
+        uint32_t m[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) m[u] = pop_member(mm);
         float y[4], g[4];
@@ -595,31 +597,30 @@ __device__ __forceinline__ void grouped_pass(StepEntries &e, const OwnerLane &ow
         todo[s] = __ballot((e.ready >> s) & 1u);
         flushing[s] = __ballot((e.flushed >> s) & 1u);
     }
+    static_assert(kWindow == 2, "the leader selection below takes two slots");
     while (true) {
-        // leader: the first entry left, in slot order
-        uint32_t c = 0u;
-        bool found = false;
+        // leader: the first entry left, in slot order (selects, no branches)
+        const uint64_t lead = todo[0] ? todo[0] : todo[1];
+        if (!lead) break;
+        const uint32_t c = readlane_u(todo[0] ? e.key[0] : e.key[1], first_lane(lead));
+        // every ready entry of cell c is still in todo[s]
+        uint64_t grp[kWindow];
+        uint64_t flush_any = 0ull;
 #pragma unroll
         for (int s = 0; s < kWindow; ++s) {
-            if (!found && todo[s]) {
-                c = readlane_u(e.key[s], first_lane(todo[s]));
-                found = true;
-            }
+            grp[s] = todo[s] & lane_mask(e.key[s] == c);
+            todo[s] &= ~grp[s];
+            flush_any |= grp[s] & flushing[s];
         }
-        if (!found) break;
+        const bool pos = flush_any != 0ull;
+        // an empty group half sums to +0 in no iterations, as the product
+        // sums of the nonempty ones are added to 0 in slot order
         float acc = 0.0f;
-        bool pos = false;
 #pragma unroll
         for (int s = 0; s < kWindow; ++s) {
-            // every ready entry of cell c is still in todo[s]
-            const uint64_t grp = todo[s] & lane_mask(e.key[s] == c);
-            if (grp) {
-                todo[s] &= ~grp;
-                pos = pos || (grp & flushing[s]) != 0ull;
-                const float *ls = last + s * WaveTables<L>::kSlot;
-                acc = acc + (any_also_last ? sum_members<true>(grp, tb.buf, ow, s, ls)
-                                           : sum_members<false>(grp, tb.buf, ow, s, ls));
-            }
+            const float *ls = last + s * WaveTables<L>::kSlot;
+            acc = acc + (any_also_last ? sum_members<true>(grp[s], tb.buf, ow, s, ls)
+                                       : sum_members<false>(grp[s], tb.buf, ow, s, ls));
         }
         if (accum) {
             // one atomic instruction into the cell's fp32 row (for either
