@@ -437,10 +437,10 @@ struct OwnerLane {
     int g_slot;         // g of slot s is s * g_slot further (0 on the zero row)
     bool also_last;     // last_ch is an SH component too: add dL/dlast as well
     // gradient accumulator row: this lane's float in a cell's row, and whether
-    // it adds to it always (attribute components) or only when a member
-    // flushed a position gradient (position components)
+    // the lane adds to it (attribute and position components; the point
+    // error when it is asked for)
     uint32_t row_off;
-    bool row_always, row_pos;
+    bool row_active;
 };
 
 template <int L>
@@ -452,8 +452,7 @@ __device__ __forceinline__ OwnerLane owner_lane(int last_ch, bool point_error) {
     OwnerLane o;
     o.also_last = false;
     o.row_off = lane < D ? (uint32_t)lane : lane >= 60 ? (uint32_t)(D + lane - 60) : 0u;
-    o.row_always = lane < D || (lane == 63 && point_error);
-    o.row_pos = lane >= 60 && lane < 63;
+    o.row_active = lane < D || (lane >= 60 && lane < 63) || (lane == 63 && point_error);
     if (lane < 3 * nsh) {
         o.y_base = (lane / 3) * kPitch;
         o.g_base = T::kRec + (lane % 3) * kPitch;
@@ -476,7 +475,7 @@ __device__ __forceinline__ OwnerLane owner_lane(int last_ch, bool point_error) {
 
 // Sum over the members in `mm` (entries in slot `slot`) of
 // buf[y_base + m] * buf[g_base + slot * g_slot + m] (+ the last channel on
-// the also_last lane), four members at a time.
+// the also_last lane), two members at a time.
 template <bool ALSO_LAST>
 __device__ __forceinline__ float sum_members(uint64_t mm, const float *__restrict__ buf,
                                              const OwnerLane &ow, int slot, const float *last) {
@@ -484,20 +483,20 @@ __device__ __forceinline__ float sum_members(uint64_t mm, const float *__restric
     const float *gb = buf + ow.g_base + slot * ow.g_slot;
     float acc = 0.0f;
     while (mm) {
-        uint32_t m[4];
+        uint32_t m[2];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) m[u] = pop_member(mm);
-        float y[4], g[4];
+        for (int u = 0; u < 2; ++u) m[u] = pop_member(mm);
+        float y[2], g[2];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < 2; ++u) {
             y[u] = yb[m[u]];
             g[u] = gb[m[u]];
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc = acc + y[u] * g[u];
+        for (int u = 0; u < 2; ++u) acc = acc + y[u] * g[u];
         if constexpr (ALSO_LAST) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < 2; ++u) {
                 if (ow.also_last) acc = acc + last[m[u]];
             }
         }
@@ -573,29 +572,34 @@ __device__ __forceinline__ void publish_step(WaveTables<L> &tb, StepEntries &e, 
 // active).  For every distinct cell among them, owner lane i < D adds the
 // sum of its component over the cell's entries to the cell's attribute row
 // (one coalesced atomic instruction per cell), lanes 60..62 add the summed
-// flushed position gradient (if an entry carries one) and lane 63 the point
-// error.  The owner lanes read the entries four at a time, two LDS reads and
-// one fma per entry.  With an accumulator (fp32), the instruction's targets
-// are one row of accum_stride(L) floats per cell: an atomic add costs about
-// one memory transaction per 64-byte segment it touches, and the row spans
-// ceil((D + 4) / 16) of them where the three output arrays span up to
-// ceil(D / 16) + 3.
-template <int L, typename AT>
-__device__ __forceinline__ void grouped_pass(StepEntries &e, const OwnerLane &ow,
-                                             WaveTables<L> &tb, void *__restrict__ attr_grad,
-                                             void *__restrict__ point_error,
-                                             float *__restrict__ points_grad,
-                                             float *__restrict__ accum) {
+// flushed position gradient and lane 63 the point error.  The owner lanes
+// read the entries two at a time, two LDS reads and one product per entry.
+//
+// ACC: the sums go to the cell's row of the fp32 accumulator (for either
+// attribute type), one row of accum_stride(L) floats per cell: an atomic add
+// costs about one memory transaction per 64-byte segment it touches, and the
+// row spans ceil((D + 4) / 16) of them where the three output arrays span up
+// to ceil(D / 16) + 3.  The position lanes add their sums whether or not an
+// entry flushed a position (then they add zeros, which leave a row as it is
+// for the finalize pass: it skips zero elements), and `row` is this lane's
+// element of cell 0's row, so a group costs one address add.
+// !ACC: straight into attr_grad, points_grad (only when an entry of the
+// group flushed a position) and point_error.
+// ALSO_LAST: the last channel is an SH component too (sdf_channel < 3 nsh).
+template <int L, typename AT, bool ACC, bool ALSO_LAST>
+__device__ __forceinline__ void grouped_pass_impl(StepEntries &e, const OwnerLane &ow,
+                                                  WaveTables<L> &tb, void *__restrict__ attr_grad,
+                                                  void *__restrict__ point_error,
+                                                  float *__restrict__ points_grad,
+                                                  float *__restrict__ row) {
     constexpr int D = 1 + 3 * (L + 1) * (L + 1);
     const uint32_t lane = lane_id();
     const float *last = tb.rec() + 3 * kPitch;
-    __builtin_amdgcn_wave_barrier();
-    const bool any_also_last = __ballot(ow.also_last) != 0ull;
     uint64_t todo[kWindow], flushing[kWindow];
 #pragma unroll
     for (int s = 0; s < kWindow; ++s) {
         todo[s] = __ballot((e.ready >> s) & 1u);
-        flushing[s] = __ballot((e.flushed >> s) & 1u);
+        flushing[s] = ACC ? 0ull : __ballot((e.flushed >> s) & 1u);
     }
     static_assert(kWindow == 2, "the leader selection below takes two slots");
     while (true) {
@@ -610,44 +614,83 @@ __device__ __forceinline__ void grouped_pass(StepEntries &e, const OwnerLane &ow
         for (int s = 0; s < kWindow; ++s) {
             grp[s] = todo[s] & lane_mask(e.key[s] == c);
             todo[s] &= ~grp[s];
-            flush_any |= grp[s] & flushing[s];
+            if constexpr (!ACC) flush_any |= grp[s] & flushing[s];
         }
-        const bool pos = flush_any != 0ull;
         // an empty group half sums to +0 in no iterations, as the product
         // sums of the nonempty ones are added to 0 in slot order
         float acc = 0.0f;
 #pragma unroll
         for (int s = 0; s < kWindow; ++s) {
             const float *ls = last + s * WaveTables<L>::kSlot;
-            acc = acc + (any_also_last ? sum_members<true>(grp[s], tb.buf, ow, s, ls)
-                                       : sum_members<false>(grp[s], tb.buf, ow, s, ls));
+            acc = acc + sum_members<ALSO_LAST>(grp[s], tb.buf, ow, s, ls);
         }
-        if (accum) {
-            // one atomic instruction into the cell's fp32 row (for either
-            // attribute type): uniform row base + this lane's precomputed offset
-            if (ow.row_always || (pos && ow.row_pos))
-                atomicAdd(accum + (uint64_t)c * accum_stride(L) + ow.row_off, acc);
-        } else if constexpr (sizeof(AT) == 4) {
-            // one atomic instruction: the row, the position and the point error
-            float *dst = nullptr;
-            if (lane < (uint32_t)D) {
-                dst = static_cast<float *>(attr_grad) + (uint64_t)c * D + lane;
-            } else if (lane >= 60u && lane < 63u) {
-                if (pos) dst = points_grad + 3ull * c + (lane - 60u);
-            } else if (lane == 63u && point_error) {
-                dst = static_cast<float *>(point_error) + c;
-            }
-            if (dst) atomicAdd(dst, acc);
+        if constexpr (ACC) {
+            if (ow.row_active) atomicAdd(row + (uint64_t)c * accum_stride(L), acc);
         } else {
-            atomic_add_row<AT>(attr_grad, c, lane, (uint32_t)D, acc);
-            if (point_error && lane == 63u) atomic_add_elem<AT>(point_error, c, acc);
-            if (pos && lane >= 60u && lane < 63u)
-                atomicAdd(points_grad + 3ull * c + (lane - 60u), acc);
+            const bool pos = flush_any != 0ull;
+            if constexpr (sizeof(AT) == 4) {
+                // one atomic instruction: the row, the position and the point error
+                float *dst = nullptr;
+                if (lane < (uint32_t)D) {
+                    dst = static_cast<float *>(attr_grad) + (uint64_t)c * D + lane;
+                } else if (lane >= 60u && lane < 63u) {
+                    if (pos) dst = points_grad + 3ull * c + (lane - 60u);
+                } else if (lane == 63u && point_error) {
+                    dst = static_cast<float *>(point_error) + c;
+                }
+                if (dst) atomicAdd(dst, acc);
+            } else {
+                atomic_add_row<AT>(attr_grad, c, lane, (uint32_t)D, acc);
+                if (point_error && lane == 63u) atomic_add_elem<AT>(point_error, c, acc);
+                if (pos && lane >= 60u && lane < 63u)
+                    atomicAdd(points_grad + 3ull * c + (lane - 60u), acc);
+            }
         }
     }
     e.ready = 0u;
     e.flushed = 0u;
+}
+
+// Where a wave's grouped passes send their sums (decided once per kernel).
+struct PassTarget {
+    void *attr_grad;
+    void *point_error;
+    float *points_grad;
+    float *row;         // accumulator: this lane's element of cell 0's row, or nullptr
+    bool also_last;     // some owner lane adds the last channel to an SH component
+};
+
+template <int L, typename AT>
+__device__ __forceinline__ void grouped_pass(StepEntries &e, const OwnerLane &ow,
+                                             WaveTables<L> &tb, const PassTarget &t) {
     __builtin_amdgcn_wave_barrier();
+    if (t.row) {
+        if (t.also_last)
+            grouped_pass_impl<L, AT, true, true>(e, ow, tb, t.attr_grad, t.point_error,
+                                                 t.points_grad, t.row);
+        else
+            grouped_pass_impl<L, AT, true, false>(e, ow, tb, t.attr_grad, t.point_error,
+                                                  t.points_grad, t.row);
+    } else {
+        if (t.also_last)
+            grouped_pass_impl<L, AT, false, true>(e, ow, tb, t.attr_grad, t.point_error,
+                                                  t.points_grad, t.row);
+        else
+            grouped_pass_impl<L, AT, false, false>(e, ow, tb, t.attr_grad, t.point_error,
+                                                   t.points_grad, t.row);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+template <int L>
+__device__ __forceinline__ PassTarget pass_target(const BwdArgs &a, const OwnerLane &ow) {
+    PassTarget t;
+    t.attr_grad = a.attr_grad;
+    t.point_error = a.point_error;
+    t.points_grad = a.points_grad;
+    t.row = a.accum ? a.accum + ow.row_off : nullptr;
+    t.also_last = __ballot(ow.also_last) != 0ull;
+    return t;
 }
 
 template <int L>
@@ -697,6 +740,7 @@ backward_sdf_kernel(BwdArgs a) {
     const int32_t sdf_ch = a.settings.sdf_channel >= 0 ? a.settings.sdf_channel : D - 1;
     const bool write_sdf = a.settings.sdf_channel >= 0;
     const OwnerLane owner = owner_lane<L>(write_sdf ? sdf_ch : -1, a.point_error != nullptr);
+    const PassTarget target = pass_target<L>(a, owner);
     const float thr = a.settings.weight_threshold;
     const uint32_t Q = a.num_quantiles;
     const float *rq = (valid && a.quantiles) ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
@@ -858,9 +902,7 @@ backward_sdf_kernel(BwdArgs a) {
             // steps go out every kWindow trips
             if (ents.pend && (si.stepped || !ws.alive))
                 complete_entry<L>(ents, si.stepped && flush, flush_g, tb);
-            if (trip % kWindow == 0)
-                grouped_pass<L, AT>(ents, owner, tb, a.attr_grad, a.point_error, a.points_grad,
-                                    a.accum);
+            if (trip % kWindow == 0) grouped_pass<L, AT>(ents, owner, tb, target);
             if (si.stepped) publish_step<L>(tb, ents, ws.cell, dr, dg, db, dsdf, pe);
         }
         if (ws.alive && si.found) walk_move(ws, si);
@@ -869,7 +911,7 @@ backward_sdf_kernel(BwdArgs a) {
         // steps not applied when the walks ended
         const float zero3[3] = {0.0f, 0.0f, 0.0f};
         if (ents.pend) complete_entry<L>(ents, false, zero3, tb);
-        grouped_pass<L, AT>(ents, owner, tb, a.attr_grad, a.point_error, a.points_grad, a.accum);
+        grouped_pass<L, AT>(ents, owner, tb, target);
     }
 
     if constexpr (STATS) {
@@ -912,6 +954,7 @@ backward_density_kernel(BwdArgs a) {
     const float *sh = tb.y() + lane; // this ray's SH basis, in LDS (stride kPitch)
 
     const OwnerLane owner = owner_lane<L>(D - 1, a.point_error != nullptr);
+    const PassTarget target = pass_target<L>(a, owner);
     const float thr = a.settings.weight_threshold;
     const uint32_t Q = a.num_quantiles;
     const float *rq = (valid && a.quantiles) ? a.quantiles + (uint64_t)ray_idx * Q : nullptr;
@@ -1085,9 +1128,7 @@ backward_density_kernel(BwdArgs a) {
         if constexpr (!STATS) {
             if (ents.pend && (si.stepped || !ws.alive))
                 complete_entry<L>(ents, si.stepped && flush, flush_g, tb);
-            if (trip % kWindow == 0)
-                grouped_pass<L, AT>(ents, owner, tb, a.attr_grad, a.point_error, a.points_grad,
-                                    a.accum);
+            if (trip % kWindow == 0) grouped_pass<L, AT>(ents, owner, tb, target);
             if (si.stepped) publish_step<L>(tb, ents, ws.cell, dr, dg, db, dds, pe);
         }
         if (ws.alive && si.found) walk_move(ws, si);
@@ -1112,7 +1153,7 @@ backward_density_kernel(BwdArgs a) {
     if constexpr (!STATS) {
         const float zero3[3] = {0.0f, 0.0f, 0.0f};
         if (ents.pend) complete_entry<L>(ents, false, zero3, tb);
-        grouped_pass<L, AT>(ents, owner, tb, a.attr_grad, a.point_error, a.points_grad, a.accum);
+        grouped_pass<L, AT>(ents, owner, tb, target);
     }
 
     if constexpr (STATS) {
