@@ -141,6 +141,10 @@ def main() -> int:
     ap.add_argument("--calibrate-copy-gib", type=float, default=0.0,
                     help="only run a device-to-device copy of this many GiB (a kernel of known "
                          "traffic, to scale rocprof FETCH_SIZE / WRITE_SIZE) and exit")
+    ap.add_argument("--calibrate-gather-gib", type=float, default=0.0,
+                    help="only run a gather of this many GiB of 128-byte rows in a random "
+                         "order, each row read once (a gather of known traffic, to scale rocprof "
+                         "FETCH_SIZE for the tracer's gathers) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
@@ -168,6 +172,18 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibration_copy_bytes": 4 * n, "launches": 3}), flush=True)
+        return 0
+
+    if args.calibrate_gather_gib > 0:
+        rows = int(args.calibrate_gather_gib * (1 << 30)) // 128
+        src = torch.ones((rows, 32), dtype=torch.float32, device=dev)
+        perm = torch.randperm(rows, device=dev, generator=torch.Generator(device=dev).manual_seed(1))
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.index_select(src, 0, perm, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration_gather_rows": rows, "row_bytes": 128,
+                          "index_bytes": 8 * rows, "launches": 3}), flush=True)
         return 0
 
     if args.fetch:
