@@ -136,6 +136,9 @@ def main() -> int:
     ap.add_argument("--walk-record", type=int, default=1, choices=[0, 1],
                     help="1: the forward records each ray's steps and the backward replays "
                          "them (TraceRays does this); 0: the backward scans the faces again")
+    ap.add_argument("--cell-table", type=int, default=1, choices=[0, 1],
+                    help="1: the forward walks over its cell table (the default of "
+                         "trace_forward); 0: over the caller's arrays")
     ap.add_argument("--scene-cache", default="",
                     help="npz file to load the generated scene from / save it to")
     ap.add_argument("--calibrate-copy-gib", type=float, default=0.0,
@@ -259,7 +262,8 @@ def main() -> int:
                  else b["start"])
         out = pipe.trace_forward(pts, attrs, adj, offs, b["rays"], start, depth_quantiles=b["q"],
                                  return_contribution=True, alpha_mode=args.alpha_mode,
-                                 inv_s=inv, record_walk=use_record)
+                                 inv_s=inv, record_walk=use_record,
+                                 cell_table=bool(args.cell_table))
         bwd = pipe.trace_backward(pts, attrs, adj, offs, b["rays"], start, out["rgba"], b["g"],
                                   b["q"], out["depth_indices"], b["dg"],
                                   alpha_mode=args.alpha_mode, inv_s=inv,

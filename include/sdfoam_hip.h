@@ -234,7 +234,13 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
  * then adds each row into attribute_grad, points_grad and point_error (fp16
  * outputs of an fp16 pipeline get the fp32 sums rounded once).  A wavefront's atomic update
  * of a cell then touches fewer 64-byte memory segments than updates of the
- * three output arrays do.  grad_accum == NULL: updates go to the outputs. */
+ * three output arrays do.  grad_accum == NULL: updates go to the outputs.
+ *
+ * Cell table (forward): the forward first copies, per cell, its position,
+ * CSR row bounds and attribute row into one aligned record (64-256 bytes,
+ * sdf_cell_table_bytes), then walks over the records, so a step reads one or
+ * two whole cache lines of the cell instead of parts of three arrays.
+ * cell_table == NULL: the forward reads the arrays. */
 typedef struct sdf_trace_plan {
     void *walk_record;        /* device memory, 16-byte aligned, or NULL */
     size_t walk_record_bytes; /* >= sdf_walk_record_bytes(num_rays, ray_image_width, walk_budget) */
@@ -246,10 +252,15 @@ typedef struct sdf_trace_plan {
                                   scene's offset table (the forward over the same
                                   scene filled it); the backward then skips
                                   rebuilding it */
+    void *cell_table;          /* forward: device memory, 256-byte aligned, or NULL */
+    size_t cell_table_bytes;   /* >= sdf_cell_table_bytes(sh_degree, attr_type, num_points) */
 } sdf_trace_plan;
 
 size_t sdf_walk_record_bytes(uint32_t num_rays, uint32_t ray_image_width,
                              uint32_t budget);
+
+/* Bytes of the forward's cell table (0 for an invalid degree or type). */
+size_t sdf_cell_table_bytes(int sh_degree, int attr_type, uint32_t num_points);
 
 /* Bytes of the backward's gradient accumulator (0 for an invalid degree). */
 size_t sdf_grad_accum_bytes(int sh_degree, uint32_t num_points);
@@ -480,6 +491,7 @@ int sdf_debug_fpmath(int op, const float *in, void *out, uint64_t n,
 #define SDF_KERNEL_RAY_ORDER 6
 #define SDF_KERNEL_GRAD_CLEAR 7
 #define SDF_KERNEL_GRAD_FINALIZE 8
+#define SDF_KERNEL_CELL_TABLE 9
 int sdf_set_timing(int enable);
 int sdf_timing_collect(int *kinds, float *ms, int max_n, int *n_out);
 

@@ -32,6 +32,7 @@ EXPORTS = (
     "sdf_trace_benchmark",
     "sdf_walk_record_bytes",
     "sdf_grad_accum_bytes",
+    "sdf_cell_table_bytes",
     "sdf_ray_order_scratch_bytes",
     "sdf_ray_order",
     "sdf_trace_forward_planned",
@@ -61,7 +62,7 @@ EXPORTS = (
 )
 
 KERNEL_NAMES = {0: "prefetch_adjacent_diff", 1: "forward", 2: "backward", 3: "build_aabb_tree", 4: "nn",
-                5: "render", 6: "ray_order", 7: "grad_clear", 8: "grad_finalize"}
+                5: "render", 6: "ray_order", 7: "grad_clear", 8: "grad_finalize", 9: "cell_table"}
 
 SDF_CAMERA_PINHOLE = 0
 SDF_CAMERA_FISHEYE = 1
@@ -103,8 +104,8 @@ class Visualization(C.Structure):
 
 
 class TracePlanDesc(C.Structure):
-    """sdf_trace_plan: the forward's walk record, the rays' launch order and
-    the backward's gradient accumulator."""
+    """sdf_trace_plan: the forward's walk record, the rays' launch order,
+    the backward's gradient accumulator and the forward's cell table."""
 
     _fields_ = [
         ("walk_record", C.c_void_p),
@@ -114,6 +115,8 @@ class TracePlanDesc(C.Structure):
         ("grad_accum", C.c_void_p),
         ("grad_accum_bytes", C.c_size_t),
         ("scratch_ready", C.c_uint32),
+        ("cell_table", C.c_void_p),
+        ("cell_table_bytes", C.c_size_t),
     ]
 
 
@@ -167,6 +170,8 @@ def lib() -> C.CDLL:
     L.sdf_walk_record_bytes.argtypes = [U32, U32, U32]
     L.sdf_grad_accum_bytes.restype = SZ
     L.sdf_grad_accum_bytes.argtypes = [C.c_int, U32]
+    L.sdf_cell_table_bytes.restype = SZ
+    L.sdf_cell_table_bytes.argtypes = [C.c_int, C.c_int, U32]
     L.sdf_ray_order_scratch_bytes.restype = SZ
     L.sdf_ray_order_scratch_bytes.argtypes = [U32, U32]
     L.sdf_ray_order.restype = C.c_int

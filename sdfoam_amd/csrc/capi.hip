@@ -104,6 +104,7 @@ SceneView make_scene(uint32_t num_points, const float *points, const float *attr
     sc.adj = adj;
     sc.offs = offs;
     sc.diff = static_cast<const uint2 *>(scratch);
+    sc.cells = nullptr;
     sc.num_points = num_points;
     sc.num_adj = adjacency_size;
     return sc;
@@ -167,6 +168,16 @@ int trace_forward_impl(const sdf_trace_plan *plan, int sh_degree,
     const uint32_t *order = nullptr;
     rc = check_plan(plan, num_rays, settings->ray_image_width, rec, order);
     if (rc != SDF_OK) return rc;
+    uint32_t *cells = nullptr;
+    if (plan && plan->cell_table) {
+        const size_t need = sdf_cell_table_bytes(sh_degree, settings->attr_type, num_points);
+        if (plan->cell_table_bytes < need)
+            return fail(SDF_E_INVALID, "cell table must hold %zu bytes (got %zu)", need,
+                        plan->cell_table_bytes);
+        if ((reinterpret_cast<uintptr_t>(plan->cell_table) & 255u) != 0)
+            return fail(SDF_E_INVALID, "cell table must be 256-byte aligned");
+        cells = static_cast<uint32_t *>(plan->cell_table);
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     tbegin(SDF_KERNEL_PREFETCH, s);
     hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
@@ -179,6 +190,13 @@ int trace_forward_impl(const sdf_trace_plan *plan, int sh_degree,
     a.order = order;
     a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
                          point_adjacency_offsets, scratch);
+    if (cells) {
+        tbegin(SDF_KERNEL_CELL_TABLE, s);
+        e = launch_cell_table(sh_degree, half, a.scene, cells, s);
+        tend(s);
+        if (e != hipSuccess) return hip_fail(e, "cell_table");
+        a.scene.cells = cells;
+    }
     a.settings = *settings;
     a.rays = rays;
     a.num_rays = num_rays;
@@ -349,6 +367,12 @@ const char *sdf_last_error(void) { return g_err; }
 int sdf_attribute_dim(int sh_degree) {
     if (sh_degree < 0 || sh_degree > 3) return -1;
     return 1 + 3 * (sh_degree + 1) * (sh_degree + 1);
+}
+
+size_t sdf_cell_table_bytes(int sh_degree, int attr_type, uint32_t num_points) {
+    if (sh_degree < 0 || sh_degree > 3) return 0;
+    if (attr_type != SDF_ATTR_F32 && attr_type != SDF_ATTR_F16) return 0;
+    return (size_t)num_points * cell_record_bytes(sh_degree, attr_type == SDF_ATTR_F16 ? 2 : 4);
 }
 
 size_t sdf_grad_accum_bytes(int sh_degree, uint32_t num_points) {

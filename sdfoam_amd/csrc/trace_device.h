@@ -253,12 +253,29 @@ __device__ __forceinline__ void sh_rgb(const float *sh, int sh_stride, const AT 
     b = fmaxf(a2, 0.0f);
 }
 
+// Cell table (optional; the forward builds it from the caller's arrays before
+// it walks): one record per cell holding what a step of the forward reads of
+// that cell: words 0-2 the position (fp32 bits), word 3 the CSR row begin,
+// word 4 its end, then from byte 20 the cell's attribute row in the
+// pipeline's attribute type, zero-padded to a power of two of at least 64
+// bytes.  A step then touches the record's one or two whole cache lines
+// instead of the lines of three arrays (position, offsets, a 196-byte row at
+// any 4-byte alignment).
+constexpr uint32_t kCellAttrByte = 20;
+__host__ __device__ constexpr uint32_t cell_record_bytes(int L, uint32_t attr_size) {
+    const uint32_t need = kCellAttrByte + (1u + 3u * (L + 1) * (L + 1)) * attr_size;
+    uint32_t b = 64;
+    while (b < need) b *= 2;
+    return b;
+}
+
 struct SceneView {
     const float *__restrict__ points;
     const void *__restrict__ attrs; // [N, D] of the pipeline's attribute type
     const uint32_t *__restrict__ adj;
     const uint32_t *__restrict__ offs;
     const uint2 *__restrict__ diff; // fp16 x, y | z, 0 per CSR entry
+    const uint32_t *__restrict__ cells; // cell table or NULL
     uint32_t num_points;
     uint32_t num_adj;
 };
@@ -276,6 +293,7 @@ struct WalkState {
     float xc[3];   // position of `cell`
     float t0;      // entry distance into `cell`
     uint32_t n;    // loop iterations so far (the reference's return value)
+    uint32_t beg, end; // CSR row of `cell` (walks over a cell table)
     bool alive;
 };
 
@@ -287,19 +305,39 @@ struct StepInfo {
     uint32_t next;
     float t1;
     float xn[3];
+    uint32_t beg, end; // CSR row of `next` (walks over a cell table)
 };
 
+// Position and CSR row of cell i: from the cell table when RB (its record
+// bytes) is nonzero, else from the points and offsets arrays.
+template <uint32_t RB>
+__device__ __forceinline__ void load_cell(const SceneView &sc, uint32_t i, float *x, uint32_t &beg,
+                                          uint32_t &end) {
+    if constexpr (RB != 0) {
+        const uint32_t *r = sc.cells + (uint64_t)i * (RB / 4);
+        const uint4 h = *reinterpret_cast<const uint4 *>(r);
+        x[0] = __builtin_bit_cast(float, h.x);
+        x[1] = __builtin_bit_cast(float, h.y);
+        x[2] = __builtin_bit_cast(float, h.z);
+        beg = h.w;
+        end = r[4];
+    } else {
+        x[0] = sc.points[3ull * i];
+        x[1] = sc.points[3ull * i + 1];
+        x[2] = sc.points[3ull * i + 2];
+        beg = end = 0;
+    }
+}
+
+template <uint32_t RB = 0>
 __device__ __forceinline__ void walk_init(const SceneView &sc, uint32_t start, WalkState &ws) {
     ws.cell = start;
     ws.t0 = 0.0f;
     ws.n = 0;
     ws.alive = start < sc.num_points;
     ws.xc[0] = ws.xc[1] = ws.xc[2] = 0.0f;
-    if (ws.alive) {
-        ws.xc[0] = sc.points[3ull * start];
-        ws.xc[1] = sc.points[3ull * start + 1];
-        ws.xc[2] = sc.points[3ull * start + 2];
-    }
+    ws.beg = ws.end = 0;
+    if (ws.alive) load_cell<RB>(sc, start, ws.xc, ws.beg, ws.end);
 }
 
 // One iteration of the walk: exit face = the first minimum t over the cell's
@@ -313,7 +351,8 @@ __device__ __forceinline__ void walk_init(const SceneView &sc, uint32_t start, W
 // minimum t over dp > 0 alone) is the same face: it is unless the smallest
 // such t is <= t0 (then it lies outside the safe set, or the safe set is
 // empty while the unsafe one is not); sets si.agrees.
-template <bool SAFE, bool COUNT, bool GUARD = false, bool DUAL = false>
+// RB: walk over a cell table of RB-byte records (0: the scene's arrays).
+template <bool SAFE, bool COUNT, bool GUARD = false, bool DUAL = false, uint32_t RB = 0>
 __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ray,
                                              uint32_t max_steps, WalkState &ws, StepInfo &si,
                                              WalkCounters &wc) {
@@ -326,8 +365,8 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
         ws.alive = false;
         return;
     }
-    const uint32_t beg = sc.offs[ws.cell];
-    const uint32_t end = sc.offs[ws.cell + 1];
+    const uint32_t beg = RB ? ws.beg : sc.offs[ws.cell];
+    const uint32_t end = RB ? ws.end : sc.offs[ws.cell + 1];
     if (beg > end || end > sc.num_adj) {
         ws.alive = false;
         return;
@@ -403,9 +442,7 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
     si.found = true;
     si.next = next;
     si.t1 = t1;
-    si.xn[0] = sc.points[3ull * next];
-    si.xn[1] = sc.points[3ull * next + 1];
-    si.xn[2] = sc.points[3ull * next + 2];
+    load_cell<RB>(sc, next, si.xn, si.beg, si.end);
     si.stepped = t1 > t0;
     if constexpr (COUNT) {
         if (si.stepped) {
@@ -421,6 +458,8 @@ __device__ __forceinline__ void walk_move(WalkState &ws, const StepInfo &si) {
     ws.xc[0] = si.xn[0];
     ws.xc[1] = si.xn[1];
     ws.xc[2] = si.xn[2];
+    ws.beg = si.beg;
+    ws.end = si.end;
 }
 
 // cell_intersection_grad (src/tracing/tracing_utils.cuh:112-124):

@@ -153,9 +153,15 @@ hipError_t launch_ray_order(uint32_t num_points, uint32_t num_rays, const float 
 hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32_t num_adj,
                                 const uint32_t *adj, const uint32_t *offs, uint2 *diff,
                                 hipStream_t stream);
-// half: fp16 attributes (settings.attr_type == SDF_ATTR_F16)
+// half: fp16 attributes (settings.attr_type == SDF_ATTR_F16).  With
+// a.scene.cells set, the forward (not its statistics instantiation) walks
+// over that cell table, which launch_cell_table filled.
 hipError_t launch_forward(int L, const FwdArgs &a, bool neus, bool stats, bool half,
                           hipStream_t stream);
+// Fills the cell table (cell_record_bytes(L, attribute size) per cell) from
+// sc's points, offsets and attributes.
+hipError_t launch_cell_table(int L, bool half, const SceneView &sc, uint32_t *cells,
+                             hipStream_t stream);
 // Floats per cell row of the backward's gradient accumulator: the next
 // power of two >= D + 4 (attribute row, position, point error), at least 8,
 // so that a row spans the fewest 64-byte segments.

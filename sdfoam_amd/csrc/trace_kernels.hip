@@ -16,6 +16,8 @@
 // forms; only the order of the sums differs (fp32 atomics have no order).
 #include "trace_kernels.h"
 
+#include <algorithm>
+
 namespace sdfoam_hip {
 
 // ---------------------------------------------------------------------------
@@ -144,8 +146,10 @@ __device__ __forceinline__ void contribution_pass(FwdSlots &fs, const FwdEntry &
 // ---------------------------------------------------------------------------
 // forward (src/tracing/pipeline.cu:36-264)
 
-template <int L, bool NEUS, bool STATS, typename AT>
+// CT: walk over the cell table (a.scene.cells) and read attribute rows from it.
+template <int L, bool NEUS, bool STATS, typename AT, bool CT = false>
 __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
+    constexpr uint32_t RB = CT ? cell_record_bytes(L, sizeof(AT)) : 0u;
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
     // SH basis of each lane's ray, in LDS (frees nsh VGPRs)
@@ -185,7 +189,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     uint32_t rec = 0;
 
     WalkState ws;
-    walk_init(a.scene, valid ? a.start[ray_idx] : kNoIndex, ws);
+    walk_init<RB>(a.scene, valid ? a.start[ray_idx] : kNoIndex, ws);
     WalkCounters wc = {0u, 0u, 0ull, 0ull};
     // walk record of this wavefront: one row of 64 entries per trip
     uint2 *wrec = nullptr;
@@ -204,14 +208,14 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         uint2 entry = make_uint2(kWalkUnrecorded, 0u);
         if (ws.alive) {
             if constexpr (NEUS || STATS) {
-                walk_advance<true, STATS>(a.scene, ray, max_steps, ws, si, wc);
+                walk_advance<true, STATS, false, false, RB>(a.scene, ray, max_steps, ws, si, wc);
                 entry = make_uint2(si.found ? si.next : kNoIndex,
                                    __builtin_bit_cast(uint32_t, si.t1));
             } else {
                 // the density backward walks in the unsafe mode: a step is
                 // recorded while that walk takes the same exit; from the first
                 // step where it would not, the backward scans for itself
-                walk_advance<true, false, false, true>(a.scene, ray, max_steps, ws, si, wc);
+                walk_advance<true, false, false, true, RB>(a.scene, ray, max_steps, ws, si, wc);
                 if (si.agrees)
                     entry = make_uint2(si.found ? si.next : kNoIndex,
                                        __builtin_bit_cast(uint32_t, si.t1));
@@ -233,7 +237,10 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         if (si.stepped) {
             const uint32_t cell = ws.cell;
             const float t0 = ws.t0, t1 = si.t1;
-            const AT *__restrict__ row = static_cast<const AT *>(a.scene.attrs) + (uint64_t)cell * D;
+            const AT *__restrict__ row =
+                CT ? reinterpret_cast<const AT *>(reinterpret_cast<const char *>(a.scene.cells) +
+                                                  (uint64_t)cell * RB + kCellAttrByte)
+                   : static_cast<const AT *>(a.scene.attrs) + (uint64_t)cell * D;
             float s = (float)row[D - 1];
             float chan = s; // the channel the backward reads (sdf value or density)
             const float dt = fmaxf(t1 - t0, 0.0f);
@@ -1182,20 +1189,79 @@ hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32
 template <int L, typename AT>
 static hipError_t launch_forward_L(const FwdArgs &a, bool neus, bool stats, hipStream_t stream) {
     const dim3 grid(grid_blocks_for_tiles(a.num_tiles));
+    const bool ct = a.scene.cells != nullptr;
     if (neus) {
         if (stats) {
             hipLaunchKernelGGL((forward_kernel<L, true, true, AT>), grid, dim3(kBlock), 0, stream, a);
+        } else if (ct) {
+            hipLaunchKernelGGL((forward_kernel<L, true, false, AT, true>), grid, dim3(kBlock), 0,
+                               stream, a);
         } else {
             hipLaunchKernelGGL((forward_kernel<L, true, false, AT>), grid, dim3(kBlock), 0, stream, a);
         }
     } else {
         if (stats) {
             hipLaunchKernelGGL((forward_kernel<L, false, true, AT>), grid, dim3(kBlock), 0, stream, a);
+        } else if (ct) {
+            hipLaunchKernelGGL((forward_kernel<L, false, false, AT, true>), grid, dim3(kBlock), 0,
+                               stream, a);
         } else {
             hipLaunchKernelGGL((forward_kernel<L, false, false, AT>), grid, dim3(kBlock), 0, stream, a);
         }
     }
     return hipGetLastError();
+}
+
+// Cell table: one thread per 4-byte word of the table (layout at
+// cell_record_bytes), so the writes are coalesced and each record's
+// attribute words are read from one row.
+template <int L, typename AT>
+__global__ __launch_bounds__(kBlock) void cell_table_kernel(const SceneView sc, uint32_t *cells) {
+    constexpr uint32_t D = 1 + 3 * (L + 1) * (L + 1);
+    constexpr uint32_t W = cell_record_bytes(L, sizeof(AT)) / 4;
+    constexpr uint32_t A = kCellAttrByte / 4;
+    const uint64_t total = (uint64_t)sc.num_points * W;
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < total;
+         i += (uint64_t)gridDim.x * kBlock) {
+        const uint64_t c = i / W;
+        const uint32_t w = (uint32_t)(i - c * W);
+        uint32_t v = 0;
+        if (w < 3) {
+            v = __builtin_bit_cast(uint32_t, sc.points[3 * c + w]);
+        } else if (w < A) {
+            v = sc.offs[c + (w - 3)];
+        } else if constexpr (sizeof(AT) == 4) {
+            if (w - A < D) v = static_cast<const uint32_t *>(sc.attrs)[c * D + (w - A)];
+        } else {
+            const uint16_t *row = static_cast<const uint16_t *>(sc.attrs) + c * D;
+            const uint32_t k = 2 * (w - A);
+            if (k < D) v = row[k];
+            if (k + 1 < D) v |= (uint32_t)row[k + 1] << 16;
+        }
+        cells[i] = v;
+    }
+}
+
+template <typename AT>
+static hipError_t launch_cell_table_T(int L, const SceneView &sc, uint32_t *cells,
+                                      hipStream_t stream) {
+    const uint64_t words = (uint64_t)sc.num_points * (cell_record_bytes(L, sizeof(AT)) / 4);
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((words + kBlock - 1) / kBlock, 1u << 20);
+    switch (L) {
+    case 0: hipLaunchKernelGGL((cell_table_kernel<0, AT>), dim3(blocks), dim3(kBlock), 0, stream, sc, cells); break;
+    case 1: hipLaunchKernelGGL((cell_table_kernel<1, AT>), dim3(blocks), dim3(kBlock), 0, stream, sc, cells); break;
+    case 2: hipLaunchKernelGGL((cell_table_kernel<2, AT>), dim3(blocks), dim3(kBlock), 0, stream, sc, cells); break;
+    case 3: hipLaunchKernelGGL((cell_table_kernel<3, AT>), dim3(blocks), dim3(kBlock), 0, stream, sc, cells); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_cell_table(int L, bool half, const SceneView &sc, uint32_t *cells,
+                             hipStream_t stream) {
+    if (sc.num_points == 0) return hipSuccess;
+    return half ? launch_cell_table_T<_Float16>(L, sc, cells, stream)
+                : launch_cell_table_T<float>(L, sc, cells, stream);
 }
 
 template <typename AT>

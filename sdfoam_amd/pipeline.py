@@ -335,7 +335,7 @@ class Pipeline:
                       start_point, depth_quantiles=None, weight_threshold=None,
                       max_intersections=None, return_contribution=False, alpha_mode=None,
                       inv_s=None, eps=None, sdf_channel=None, record_walk=None,
-                      walk_budget=None, sort_rays=None):
+                      walk_budget=None, sort_rays=None, cell_table=True):
         """Reference arguments and outputs, plus (no counterpart in the
         reference):
 
@@ -349,7 +349,11 @@ class Pipeline:
           training and not under ``torch.no_grad()``;
         * ``sort_rays``: trace rays of shape [R, 6] in sorted order
           (sdf_ray_order); None sorts from 32768 rays on.  Outputs stay in
-          the caller's order.
+          the caller's order;
+        * ``cell_table``: copy each cell's position, CSR row bounds and
+          attribute row into one aligned record before walking (a temporary
+          of 64-256 bytes per point, sdf_cell_table_bytes); False walks over
+          the caller's arrays.  Results are the same.
 
         When either applies, the result holds ``"trace_plan"``, which
         ``trace_backward(trace_plan=...)`` over the same rays and settings
@@ -418,11 +422,24 @@ class Pipeline:
             num_adj, ptr(adj_c), ptr(offs_c), num_rays, ptr(rays_c), ptr(start_c), num_q,
             ptr(dq), ptr(rgba), ptr(depth), ptr(didx), ptr(nisect), ptr(contribution),
             ptr(sharpness), ptr(alpha), ptr(scratch), nbytes, _lib.stream_handle(dev))
+        desc = plan.desc() if plan is not None else None
+        cells = None
+        if cell_table and num_rays > 0:
+            cbytes = int(_lib.lib().sdf_cell_table_bytes(self._sh_degree, settings.attr_type,
+                                                         num_points))
+            cells = torch.empty(cbytes + 256, dtype=torch.uint8, device=dev)
+            if desc is None:
+                desc = _lib.TracePlanDesc()
+            desc.cell_table = (cells.data_ptr() + 255) & ~255
+            desc.cell_table_bytes = cbytes
         with torch.cuda.device(dev):
-            if plan is None:
+            if desc is None:
                 check(_lib.lib().sdf_trace_forward(*args))
             else:
-                check(_lib.lib().sdf_trace_forward_planned(C.byref(plan.desc()), *args))
+                check(_lib.lib().sdf_trace_forward_planned(C.byref(desc), *args))
+        # `cells` may be freed now: torch reuses it only for later work on
+        # this stream, which runs after the forward
+        del cells
         out = {"rgba": rgba}
         if return_depth:
             out["depth"] = depth

@@ -130,6 +130,32 @@ def test_grad_accum_sizes_and_errors():
         assert rc == 1 and msg in L.sdf_last_error()
 
 
+def test_cell_table_sizes_and_errors():
+    from sdfoam_amd import _lib
+
+    L = _lib.lib()
+    # per cell: position, CSR begin and end (20 bytes), then the attribute
+    # row (D = 4, 13, 28, 49 values), rounded up to a power of two >= 64
+    assert [L.sdf_cell_table_bytes(d, 0, 10) for d in range(4)] == [640, 1280, 2560, 2560]
+    assert [L.sdf_cell_table_bytes(d, 1, 10) for d in range(4)] == [640, 640, 1280, 1280]
+    assert L.sdf_cell_table_bytes(4, 0, 10) == 0
+    assert L.sdf_cell_table_bytes(3, 2, 10) == 0
+    assert L.sdf_cell_table_bytes(3, 0, 1 << 20) == 256 << 20
+    s = _settings()
+    buf = (C.c_uint64 * 512)()
+    p = C.cast(buf, C.c_void_p)
+    nb = L.sdf_trace_scratch_bytes(10, 4)
+    base = C.cast(buf, C.c_void_p).value
+    aligned = (base + 255) & ~255
+    for addr, nbytes, msg in ((aligned, 2559, b"cell table must hold 2560 bytes"),
+                              (aligned + 16, 2560, b"cell table must be 256-byte aligned")):
+        plan = _lib.TracePlanDesc()
+        plan.cell_table, plan.cell_table_bytes = addr, nbytes
+        rc = L.sdf_trace_forward_planned(C.byref(plan), 3, C.byref(s), 10, p, p, 4, p, p, 1, p,
+                                         p, 0, None, p, None, None, p, None, p, p, p, nb, None)
+        assert rc == 1 and msg in L.sdf_last_error()
+
+
 def test_triangulation_table_argument_errors():
     from sdfoam_amd import _lib
 

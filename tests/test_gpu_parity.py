@@ -472,6 +472,60 @@ def test_backward_reuses_forward_table(torch_dev):
                                        atol=1e-5 * float(np.abs(ref).max()))
 
 
+@pytest.mark.parametrize("mode,dtype", [("sdfoam", "float32"), ("standard", "float32"),
+                                        ("sdfoam", "float16"), ("standard", "float16")])
+def test_cell_table_same_results(torch_dev, mode, dtype, monkeypatch):
+    """The forward over the cell table (the default) and over the caller's
+    arrays give the same bits: rgba, depths, depth indices, loop counts and
+    the walk record (steps and their colours; the records are zeroed first,
+    since a wave writes only the rows it walks) are per ray and
+    deterministic.  Contribution is summed by fp32 atomics in any order, so
+    it is compared to the summation bound used against the oracle."""
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import pipeline
+
+    allocate = pipeline.TracePlan.allocate_record
+
+    def allocate_zeroed(self, budget):
+        allocate(self, budget)
+        self.entries.zero_()
+
+    monkeypatch.setattr(pipeline.TracePlan, "allocate_record", allocate_zeroed)
+
+    w = scene(2, mode=mode)
+    g = gpu_scene(w, torch_dev)
+    tdt = torch.float16 if dtype == "float16" else torch.float32
+    g["attributes"] = g["attributes"].to(tdt)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree, dtype)
+    q = to_dev(w.quantiles, torch_dev)
+    inv_t = torch.tensor([w.inv_s], device=torch_dev)
+    outs = [pipe.trace_forward(**g, depth_quantiles=q, return_contribution=True, alpha_mode=mode,
+                               inv_s=inv_t, record_walk=True, walk_budget=64, cell_table=ct)
+            for ct in (False, True)]
+    torch.cuda.synchronize()
+    a, b = outs
+
+    def bits(t):
+        return t.contiguous().view(torch.uint8).cpu().numpy()
+
+    for k in ("rgba", "depth", "depth_indices", "num_intersections"):
+        assert np.array_equal(bits(a[k]), bits(b[k])), k
+    assert np.array_equal(bits(a["trace_plan"].entries), bits(b["trace_plan"].entries)), \
+        "walk record"
+    ca = a["contribution"].double().cpu().numpy().ravel()
+    cb = b["contribution"].double().cpu().numpy().ravel()
+    if dtype == "float32":
+        # the same fp32 weights (>= 0) summed in two orders, at most one per
+        # ray: each sum is within gamma_R of the exact one
+        tol = 2 * gamma(w.num_rays) * np.abs(ca) + 1e-30
+        assert (np.abs(ca - cb) <= tol).all(), "contribution"
+    else:
+        # fp16 atomics round every add: compare the totals
+        assert abs(ca.sum() - cb.sum()) <= 1e-2 * abs(ca.sum()) + 1e-3, "contribution"
+
+
 def flat(w):
     """The workload with its rays as a flat [R, 6] batch (no image layout)."""
     import dataclasses
