@@ -279,14 +279,27 @@ def main() -> int:
     _lib.set_timing(True)
     torch.cuda.synchronize()
     t_start = time.perf_counter()
+    last = None
     for k in range(args.steps):
-        step(args.warmup + k)
+        last = step(args.warmup + k)
     torch.cuda.synchronize()
     t_end = time.perf_counter()
     launches = _lib.collect_timings()
     _lib.set_timing(False)
     ms_per_step = (t_end - t_start) * 1e3 / args.steps
     log(f"{ms_per_step:.3f} ms/step")
+    # the last step's walk record: its pool (sized by the steps before it)
+    # and the chunks its walk asked for
+    record = None
+    plan = last[0].get("trace_plan") if last is not None else None
+    if plan is not None and plan.entries is not None:
+        asked = plan.record_counters().cpu().numpy()
+        record = {"bytes": int(plan.nbytes), "pool_chunks": int(plan.chunks),
+                  "chunks_asked": int(asked.sum()), "chunks_asked_max_xcd": int(asked.max()),
+                  "budget_trips": int(plan.budget),
+                  "full_bytes": int(_lib.lib().sdf_walk_record_bytes(plan.num_rays,
+                                                                     plan.ray_image_width,
+                                                                     plan.budget))}
 
     per_kernel: dict[str, list[float]] = {}
     for name, ms in launches:
@@ -382,6 +395,7 @@ def main() -> int:
         "faces_per_step": F_st / max(S, 1),
         "faces_scanned": F_all,
         "kernel_ms": avg,
+        "walk_record": record,
         "algorithmic_bytes": {"forward": gather_fwd, "backward": gather_bwd, "prefetch": bytes_pre,
                               "step": bytes_step, "walk_record_each_way": record_bytes},
         "step_algorithmic_GBps": bytes_step / (ms_per_step * 1e-3) / 1e9,

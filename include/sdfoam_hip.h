@@ -212,7 +212,7 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
  *
  * Walk record: the forward records each ray's steps (next cell and exit
  * distance, and the step's colour and sdf/density value: 24 bytes a step,
- * `walk_budget` trips per wavefront of 64 rays); the backward then reads
+ * up to `walk_budget` trips per wavefront of 64 rays); the backward then reads
  * the steps instead of scanning the cell faces again, and a recorded step's
  * colour instead of the cell's attribute row, so the record is valid only
  * for a backward over the attributes the forward traced.  In standard mode
@@ -221,6 +221,13 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
  * walk meets the recorded one again.  Rays past `walk_budget` trips, or that
  * walk further in the backward, scan as usual.
  * walk_record == NULL: no record.
+ * Storage is sized by need: a wavefront takes chunks of 16 trips from a
+ * pool of `walk_record_chunks` as its walk gets there, and records nothing
+ * more once the pool (split in 8 parts, one per XCD) has none left for it.
+ * The record starts with 8 counters, 256 bytes apart (uint32 at byte offsets
+ * 0, 256, ..., 1792): after the forward their sum is the number of chunks
+ * the walk asked for, pool or not, i.e. the pool a forward over the same
+ * rays needs to record every trip up to `walk_budget`.
  *
  * Ray order: a permutation of [0, num_rays) from sdf_ray_order; the kernels
  * trace rays in that order (outputs stay in the caller's order).  For rays
@@ -242,9 +249,10 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
  * two whole cache lines of the cell instead of parts of three arrays.
  * cell_table == NULL: the forward reads the arrays. */
 typedef struct sdf_trace_plan {
-    void *walk_record;        /* device memory, 16-byte aligned, or NULL */
-    size_t walk_record_bytes; /* >= sdf_walk_record_bytes(num_rays, ray_image_width, walk_budget) */
-    uint32_t walk_budget;
+    void *walk_record;        /* device memory, 256-byte aligned, or NULL */
+    size_t walk_record_bytes; /* >= sdf_walk_record_pool_bytes(num_rays, ray_image_width,
+                                 walk_budget, walk_record_chunks) */
+    uint32_t walk_budget;     /* trips recorded per wavefront at most */
     const uint32_t *ray_order; /* device memory [num_rays], or NULL */
     void *grad_accum;          /* device memory, 256-byte aligned, or NULL */
     size_t grad_accum_bytes;   /* >= sdf_grad_accum_bytes(sh_degree, num_points) */
@@ -254,10 +262,19 @@ typedef struct sdf_trace_plan {
                                   rebuilding it */
     void *cell_table;          /* forward: device memory, 256-byte aligned, or NULL */
     size_t cell_table_bytes;   /* >= sdf_cell_table_bytes(sh_degree, attr_type, num_points) */
+    uint32_t walk_record_chunks; /* chunks of 16 trips in the record's pool, rounded up to
+                                    a multiple of 8; 0: every wavefront's `walk_budget`
+                                    trips (sdf_walk_record_full_chunks) */
 } sdf_trace_plan;
 
+/* Bytes of a walk record for every wavefront's `budget` trips (a pool that
+ * never runs out), and for a pool of `chunks` chunks (0: the same). */
 size_t sdf_walk_record_bytes(uint32_t num_rays, uint32_t ray_image_width,
                              uint32_t budget);
+size_t sdf_walk_record_pool_bytes(uint32_t num_rays, uint32_t ray_image_width,
+                                  uint32_t budget, uint32_t chunks);
+uint32_t sdf_walk_record_full_chunks(uint32_t num_rays, uint32_t ray_image_width,
+                                     uint32_t budget);
 
 /* Bytes of the forward's cell table (0 for an invalid degree or type). */
 size_t sdf_cell_table_bytes(int sh_degree, int attr_type, uint32_t num_points);

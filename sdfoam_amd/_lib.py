@@ -31,6 +31,8 @@ EXPORTS = (
     "sdf_trace_backward",
     "sdf_trace_benchmark",
     "sdf_walk_record_bytes",
+    "sdf_walk_record_pool_bytes",
+    "sdf_walk_record_full_chunks",
     "sdf_grad_accum_bytes",
     "sdf_cell_table_bytes",
     "sdf_ray_order_scratch_bytes",
@@ -117,6 +119,7 @@ class TracePlanDesc(C.Structure):
         ("scratch_ready", C.c_uint32),
         ("cell_table", C.c_void_p),
         ("cell_table_bytes", C.c_size_t),
+        ("walk_record_chunks", C.c_uint32),
     ]
 
 
@@ -168,6 +171,10 @@ def lib() -> C.CDLL:
         C.POINTER(Visualization), P, P, P, P]
     L.sdf_walk_record_bytes.restype = SZ
     L.sdf_walk_record_bytes.argtypes = [U32, U32, U32]
+    L.sdf_walk_record_pool_bytes.restype = SZ
+    L.sdf_walk_record_pool_bytes.argtypes = [U32, U32, U32, U32]
+    L.sdf_walk_record_full_chunks.restype = U32
+    L.sdf_walk_record_full_chunks.argtypes = [U32, U32, U32]
     L.sdf_grad_accum_bytes.restype = SZ
     L.sdf_grad_accum_bytes.argtypes = [C.c_int, U32]
     L.sdf_cell_table_bytes.restype = SZ

@@ -111,13 +111,11 @@ SceneView make_scene(uint32_t num_points, const float *points, const float *attr
 }
 
 // plan == NULL: neither aid.  A walk record must hold
-// sdf_walk_record_bytes(num_rays, ray_image_width, walk_budget) bytes; a ray
-// order needs ray_image_width == 0.
+// sdf_walk_record_pool_bytes(num_rays, ray_image_width, walk_budget,
+// walk_record_chunks) bytes; a ray order needs ray_image_width == 0.
 int check_plan(const sdf_trace_plan *plan, uint32_t num_rays, uint32_t ray_image_width,
                WalkRecordArgs &rec, const uint32_t *&order) {
-    rec.entries = nullptr;
-    rec.colors = nullptr;
-    rec.budget = 0;
+    rec = WalkRecordArgs{};
     order = nullptr;
     if (!plan) return SDF_OK;
     if (plan->ray_order) {
@@ -127,18 +125,24 @@ int check_plan(const sdf_trace_plan *plan, uint32_t num_rays, uint32_t ray_image
     }
     if (!plan->walk_record) return SDF_OK;
     if (plan->walk_budget == 0) return fail(SDF_E_INVALID, "walk record budget must be positive");
-    const uint64_t count =
-        walk_record_entries(num_ray_tiles(num_rays, ray_image_width), plan->walk_budget);
-    const uint64_t need = count * kWalkRecordEntryBytes;
+    const uint32_t tiles = num_ray_tiles(num_rays, ray_image_width);
+    const uint64_t pool = record_pool_chunks(tiles, plan->walk_budget, plan->walk_record_chunks);
+    if (pool >= kNoIndex) return fail(SDF_E_INVALID, "walk record pool too large");
+    const uint64_t need = walk_record_bytes_for(tiles, plan->walk_budget, pool);
     if (plan->walk_record_bytes < need)
         return fail(SDF_E_INVALID, "walk record must hold %llu bytes (got %zu)",
                     (unsigned long long)need, plan->walk_record_bytes);
-    if ((reinterpret_cast<uintptr_t>(plan->walk_record) & 15u) != 0)
-        return fail(SDF_E_INVALID, "walk record must be 16-byte aligned");
-    rec.entries = static_cast<uint2 *>(plan->walk_record);
-    // count is a multiple of 64, so the colours stay 16-byte aligned
-    rec.colors = reinterpret_cast<float4 *>(rec.entries + count);
+    if ((reinterpret_cast<uintptr_t>(plan->walk_record) & 255u) != 0)
+        return fail(SDF_E_INVALID, "walk record must be 256-byte aligned");
+    char *base = static_cast<char *>(plan->walk_record);
+    rec.counters = reinterpret_cast<uint32_t *>(base);
+    rec.chunks = reinterpret_cast<uint32_t *>(base + kRecordHeadBytes);
+    rec.entries =
+        reinterpret_cast<uint2 *>(base + kRecordHeadBytes + walk_record_table_bytes(tiles, plan->walk_budget));
+    // the pool is a multiple of 8 chunks of 8 KB, so the colours stay aligned
+    rec.colors = reinterpret_cast<float4 *>(rec.entries + pool * kChunkEntries);
     rec.budget = plan->walk_budget;
+    rec.pool = (uint32_t)pool;
     return SDF_OK;
 }
 
@@ -190,6 +194,12 @@ int trace_forward_impl(const sdf_trace_plan *plan, int sh_degree,
     a.order = order;
     a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
                          point_adjacency_offsets, scratch);
+    if (rec.entries) {
+        const uint64_t words =
+            walk_record_waves(num_ray_tiles(num_rays, settings->ray_image_width)) * chunk_slots(rec.budget);
+        e = launch_record_reset(rec, words, s);
+        if (e != hipSuccess) return hip_fail(e, "walk record reset");
+    }
     if (cells) {
         tbegin(SDF_KERNEL_CELL_TABLE, s);
         e = launch_cell_table(sh_degree, half, a.scene, cells, s);
@@ -563,8 +573,20 @@ int sdf_ray_order(uint32_t num_points, uint32_t num_rays, const float *rays,
 }
 
 size_t sdf_walk_record_bytes(uint32_t num_rays, uint32_t ray_image_width, uint32_t budget) {
-    return (size_t)walk_record_entries(num_ray_tiles(num_rays, ray_image_width), budget) *
-           kWalkRecordEntryBytes;
+    return sdf_walk_record_pool_bytes(num_rays, ray_image_width, budget, 0);
+}
+
+size_t sdf_walk_record_pool_bytes(uint32_t num_rays, uint32_t ray_image_width, uint32_t budget,
+                                  uint32_t chunks) {
+    if (budget == 0) return 0;
+    const uint32_t tiles = num_ray_tiles(num_rays, ray_image_width);
+    return (size_t)walk_record_bytes_for(tiles, budget, record_pool_chunks(tiles, budget, chunks));
+}
+
+uint32_t sdf_walk_record_full_chunks(uint32_t num_rays, uint32_t ray_image_width,
+                                     uint32_t budget) {
+    const uint64_t c = walk_record_full_chunks(num_ray_tiles(num_rays, ray_image_width), budget);
+    return c >= kNoIndex ? kNoIndex : (uint32_t)c;
 }
 
 int sdf_trace_forward_planned(

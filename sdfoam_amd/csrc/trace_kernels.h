@@ -11,17 +11,26 @@ namespace sdfoam_hip {
 int fail(int code, const char *fmt, ...);
 int hip_fail(hipError_t e, const char *where);
 
-// Walk record: for every wavefront, `budget` trips of 64 entries (one per
-// lane) of {next cell, bits of t1}, with next = kNoIndex where the lane's
-// walk ended on that trip and kWalkUnrecorded where the lane was not
+// Walk record: for every wavefront, up to `budget` trips of 64 entries (one
+// per lane) of {next cell, bits of t1}, with next = kNoIndex where the
+// lane's walk ended on that trip and kWalkUnrecorded where the lane was not
 // walking.  Written by the forward of the sdfoam (safe) walk, replayed by
 // its backward, which then skips the face scans; a lane scans again from
-// its first unrecorded trip (past `budget`, or where it outlives the
-// forward's walk).  Beside every entry, in a second array of the same
-// shape, the forward keeps the step's colour and density channel
-// {r, g, b, row[channel]} (channel: sdf_channel in sdfoam mode, D - 1 in
-// standard mode), so the backward of a recorded step reads 16 bytes instead
-// of the cell's attribute row and skips the SH sum.
+// its first unrecorded trip (past `budget`, past the wavefront's last
+// recorded chunk, or where it outlives the forward's walk).  Beside every
+// entry, in a second array of the same shape, the forward keeps the step's
+// colour and density channel {r, g, b, row[channel]} (channel: sdf_channel
+// in sdfoam mode, D - 1 in standard mode), so the backward of a recorded
+// step reads 16 bytes instead of the cell's attribute row and skips the SH
+// sum.
+//
+// Storage is sized by need: trips are stored in chunks of kChunkTrips rows
+// that a wavefront claims from a shared pool as it walks (a counter per
+// XCD, each with its own eighth of the pool, so the claims of one XCD stay
+// in its L2); its chunk table lists them in trip order.  A wavefront whose
+// claim finds its sub-pool empty records nothing from there on.  The
+// counters keep counting past their sub-pools, so after the forward their
+// sum is the number of chunks the walk asked for.
 constexpr uint32_t kWalkUnrecorded = 0xfffffffeu;
 // Standard mode: where the density backward's unsafe walk would leave the
 // forward's safe one, the forward keeps its own step as {next | kWalkDiffers,
@@ -31,12 +40,24 @@ constexpr uint32_t kWalkUnrecorded = 0xfffffffeu;
 constexpr uint32_t kWalkDiffers = 0x80000000u;
 constexpr uint32_t kSeekWindow = 8;
 constexpr uint32_t kWalkRecordEntryBytes = 8u + 16u;
+constexpr uint32_t kChunkTrips = 16;
+constexpr uint32_t kChunkEntries = kChunkTrips * 64;
+// record layout: kXcds counters (one 256-byte line each), the chunk tables
+// (rounded up to 256 bytes), the pool's entries, then their colours
+constexpr uint32_t kRecordHeadBytes = kXcds * 256;
 
 struct WalkRecordArgs {
-    uint2 *entries;  // NULL: no record
-    float4 *colors;  // entries' colours, same indexing
-    uint32_t budget; // trips recorded per wavefront
+    uint2 *entries;     // NULL: no record; chunk k is entries [k, k + 1) * kChunkEntries
+    float4 *colors;     // entries' colours, same indexing
+    uint32_t *chunks;   // per wavefront, chunk_slots(budget) chunk numbers (kNoIndex: none)
+    uint32_t *counters; // chunks asked for, per XCD (64 words apart)
+    uint32_t budget;    // trips recorded per wavefront at most
+    uint32_t pool;      // chunks in the pool (a multiple of kXcds)
 };
+
+__host__ __device__ inline uint32_t chunk_slots(uint32_t budget) {
+    return (budget + kChunkTrips - 1) / kChunkTrips;
+}
 
 // Stores into the walk record.  It is written once by the forward and read
 // once by the backward, so the stores are non-temporal: they do not displace
@@ -50,18 +71,51 @@ __device__ inline void record_store(float4 *p, float4 v) {
     __builtin_nontemporal_store(w, reinterpret_cast<f4v *>(p));
 }
 
-// entries for every block of the launch grid, the padding blocks included
-// (they write their "unrecorded" row)
-__host__ inline uint64_t walk_record_entries(uint32_t num_tiles, uint32_t budget) {
-    return (uint64_t)grid_blocks_for_tiles(num_tiles) * (kBlock / 64) * budget * 64;
+// wavefronts of the launch grid, the padding blocks included (they write
+// their "unrecorded" row)
+__host__ inline uint64_t walk_record_waves(uint32_t num_tiles) {
+    return (uint64_t)grid_blocks_for_tiles(num_tiles) * (kBlock / 64);
 }
 
-// this lane's entry of trip 0; trip k is 64 * k entries further.  Rows
-// belong to tiles, not blocks, so kernels with different tile runs share them.
+// chunks for `budget` trips of every wavefront (what a pool that can never
+// run out holds), a multiple of kXcds
+__host__ inline uint64_t walk_record_full_chunks(uint32_t num_tiles, uint32_t budget) {
+    const uint64_t c = walk_record_waves(num_tiles) * chunk_slots(budget);
+    return (c + kXcds - 1) / kXcds * kXcds;
+}
+
+// the pool of a plan asking for `chunks` (0: the full pool), rounded up to
+// a multiple of kXcds
+__host__ inline uint64_t record_pool_chunks(uint32_t num_tiles, uint32_t budget, uint32_t chunks) {
+    if (chunks == 0) return walk_record_full_chunks(num_tiles, budget);
+    return ((uint64_t)chunks + kXcds - 1) / kXcds * kXcds;
+}
+
+__host__ inline uint64_t walk_record_table_bytes(uint32_t num_tiles, uint32_t budget) {
+    return (walk_record_waves(num_tiles) * chunk_slots(budget) * 4 + 255) / 256 * 256;
+}
+
+__host__ inline uint64_t walk_record_bytes_for(uint32_t num_tiles, uint32_t budget,
+                                               uint64_t chunks) {
+    return kRecordHeadBytes + walk_record_table_bytes(num_tiles, budget) +
+           chunks * kChunkEntries * kWalkRecordEntryBytes;
+}
+
+// this wavefront's chunk table.  Tables belong to tiles, not blocks, so
+// kernels with different tile runs share them.
 template <uint32_t CHUNK>
-__device__ inline uint2 *walk_record_lane(const WalkRecordArgs &r, uint32_t lane) {
+__device__ inline uint32_t *walk_record_table(const WalkRecordArgs &r) {
     const uint64_t wave = (uint64_t)block_tile<CHUNK>() * (kBlock / 64) + (threadIdx.x >> 6);
-    return r.entries + wave * r.budget * 64 + lane;
+    return r.chunks + wave * chunk_slots(r.budget);
+}
+
+// This lane's entry of trip `trip` (< budget) of the wavefront with chunk
+// table `tab`, or NULL where that trip has no chunk.
+__device__ inline uint64_t record_slot(const WalkRecordArgs &r, const uint32_t *tab,
+                                       uint32_t trip, uint32_t lane) {
+    const uint32_t c = tab[trip / kChunkTrips];
+    return c == kNoIndex ? ~0ull
+                         : (uint64_t)c * kChunkEntries + (trip % kChunkTrips) * 64u + lane;
 }
 
 struct FwdArgs {
@@ -153,6 +207,9 @@ hipError_t launch_ray_order(uint32_t num_points, uint32_t num_rays, const float 
 hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32_t num_adj,
                                 const uint32_t *adj, const uint32_t *offs, uint2 *diff,
                                 hipStream_t stream);
+// Before a forward that records: the counters to 0 and every chunk table
+// entry to kNoIndex.
+hipError_t launch_record_reset(const WalkRecordArgs &r, uint64_t table_words, hipStream_t stream);
 // half: fp16 attributes (settings.attr_type == SDF_ATTR_F16).  With
 // a.scene.cells set, the forward (not its statistics instantiation) walks
 // over that cell table, which launch_cell_table filled.

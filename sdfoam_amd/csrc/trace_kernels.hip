@@ -77,6 +77,22 @@ __device__ __forceinline__ int first_lane(uint64_t mask) { return __builtin_ctzl
 // already is (no widening to a 0/1 integer first).
 __device__ __forceinline__ uint64_t lane_mask(bool p) { return __builtin_amdgcn_ballot_w64(p); }
 
+// The forward's claim of chunk `slot` of its wavefront's walk record: the
+// first active lane takes the next chunk of its XCD's sub-pool (none once
+// that is used up; the counter still counts the claim) and enters it in the
+// chunk table.  The result is uniform over the wave.
+__device__ inline uint32_t record_claim(const WalkRecordArgs &r, uint32_t *tab, uint32_t slot) {
+    const uint32_t x = blockIdx.x % kXcds;
+    const uint32_t per = r.pool / kXcds;
+    uint32_t got = kNoIndex;
+    if (lane_id() == (uint32_t)first_lane(__ballot(1))) {
+        const uint32_t k = atomicAdd(r.counters + 64u * x, 1u);
+        got = k < per ? x * per + k : kNoIndex;
+        tab[slot] = got;
+    }
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)got);
+}
+
 // Groups of lanes per forward slot round.
 constexpr int kSlots = 16;
 
@@ -191,13 +207,12 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     WalkState ws;
     walk_init<RB>(a.scene, valid ? a.start[ray_idx] : kNoIndex, ws);
     WalkCounters wc = {0u, 0u, 0ull, 0ull};
-    // walk record of this wavefront: one row of 64 entries per trip
-    uint2 *wrec = nullptr;
-    float4 *wcol = nullptr;
-    if (!STATS && a.record.entries) {
-        wrec = walk_record_lane<kForwardChunk>(a.record, lane);
-        wcol = a.record.colors + (wrec - a.record.entries);
-    }
+    // walk record of this wavefront: one row of 64 entries per trip, in
+    // chunks of kChunkTrips rows claimed as the walk gets there; wslot is
+    // this lane's entry in the current chunk's first row (~0: no chunk)
+    uint32_t *wtab = nullptr;
+    uint64_t wslot = ~0ull;
+    if (!STATS && a.record.entries) wtab = walk_record_table<kForwardChunk>(a.record);
     uint32_t trip = 0;
     FwdEntry held = {0u, 0.0f, 0.0f, false}; // step waiting for the next contribution pass
 
@@ -226,9 +241,16 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         }
         // where this trip's colour goes (the step's, if the lane steps)
         float4 *col = nullptr;
-        if (wrec && trip < a.record.budget) {
-            record_store(wrec + (uint64_t)trip * 64, entry);
-            col = wcol + (uint64_t)trip * 64;
+        if (wtab && trip < a.record.budget) {
+            if (trip % kChunkTrips == 0) {
+                const uint32_t c = record_claim(a.record, wtab, trip / kChunkTrips);
+                wslot = c == kNoIndex ? ~0ull : (uint64_t)c * kChunkEntries + lane;
+            }
+            if (wslot != ~0ull) {
+                const uint64_t i = wslot + (trip % kChunkTrips) * 64u;
+                record_store(a.record.entries + i, entry);
+                col = a.record.colors + i;
+            }
         }
         ++trip;
 
@@ -312,9 +334,12 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         if (si.stepped && !keep) ws.alive = false;
         if (ws.alive && si.found) walk_move(ws, si);
     }
-    // a backward lane that outlives this wave's walk reads "unrecorded"
-    if (wrec && trip < a.record.budget)
-        record_store(wrec + (uint64_t)trip * 64, make_uint2(kWalkUnrecorded, 0u));
+    // a backward lane that outlives this wave's walk reads "unrecorded": this
+    // row, or (when the next trip would open a chunk) the chunk table's
+    // kNoIndex, which the table starts out with
+    if (wtab && trip < a.record.budget && trip % kChunkTrips != 0 && wslot != ~0ull)
+        record_store(a.record.entries + wslot + (trip % kChunkTrips) * 64u,
+                     make_uint2(kWalkUnrecorded, 0u));
     if constexpr (!STATS) {
         if (a.contribution || a.alpha_out) {
             const FwdEntry none = {0u, 0.0f, 0.0f, false};
@@ -778,12 +803,14 @@ backward_sdf_kernel(BwdArgs a) {
     WalkCounters wc = {0u, 0u, 0ull, 0ull};
     // replay of the forward's walk record: while this lane's entries are
     // recorded, the step is read instead of scanned; from the first
-    // unrecorded (or out-of-range) entry on, the lane scans.
-    const uint2 *wrec = nullptr;
-    const float4 *wcol = nullptr;
+    // unrecorded (or out-of-range) entry on, the lane scans.  wslot: this
+    // lane's entry in the first row of the trip's chunk (~0: no chunk).
+    const uint32_t *wtab = nullptr;
+    uint64_t wslot = ~0ull;
+    bool replaying = false;
     if (!STATS && a.record.entries) {
-        wrec = walk_record_lane<kBackwardChunk>(a.record, lane);
-        wcol = a.record.colors + (wrec - a.record.entries);
+        wtab = walk_record_table<kBackwardChunk>(a.record);
+        replaying = true;
     }
     uint32_t trip = 0;
     StepEntries ents; // steps whose updates are not applied yet
@@ -796,11 +823,16 @@ backward_sdf_kernel(BwdArgs a) {
         // the recorded step's {r, g, b, channel}, valid when `replayed`
         float4 rc4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         bool replayed = false;
+        if (wtab && trip < a.record.budget && trip % kChunkTrips == 0) {
+            const uint32_t c = wtab[trip / kChunkTrips];
+            wslot = c == kNoIndex ? ~0ull : (uint64_t)c * kChunkEntries + lane;
+        }
         if (ws.alive) {
             uint2 e = make_uint2(kWalkUnrecorded, 0u);
-            if (wrec && trip < a.record.budget) {
-                e = wrec[(uint64_t)trip * 64];
-                rc4 = wcol[(uint64_t)trip * 64];
+            if (replaying && trip < a.record.budget && wslot != ~0ull) {
+                const uint64_t i = wslot + (trip % kChunkTrips) * 64u;
+                e = a.record.entries[i];
+                rc4 = a.record.colors[i];
             }
             if (e.x == kNoIndex) {
                 ++ws.n;
@@ -816,7 +848,7 @@ backward_sdf_kernel(BwdArgs a) {
                 si.stepped = si.t1 > ws.t0;
                 replayed = true;
             } else {
-                wrec = nullptr;
+                replaying = false;
                 walk_advance<true, STATS>(a.scene, ray, a.settings.max_intersections, ws, si, wc);
             }
         }
@@ -999,11 +1031,11 @@ backward_density_kernel(BwdArgs a) {
     entries_init(ents);
     // replay of the forward's walk record as in backward_sdf; the forward
     // records a step only where the unsafe walk takes the same exit
-    const uint2 *wrec = nullptr;
-    const float4 *wcol = nullptr;
+    const uint32_t *wtab = nullptr;
+    bool replaying = false;
     if (!STATS && a.record.entries) {
-        wrec = walk_record_lane<kBackwardChunk>(a.record, lane);
-        wcol = a.record.colors + (wrec - a.record.entries);
+        wtab = walk_record_table<kBackwardChunk>(a.record);
+        replaying = true;
     }
     uint32_t trip = 0;
     // ridx: the forward trip whose entry the lane reads next.  After an entry
@@ -1025,9 +1057,12 @@ backward_density_kernel(BwdArgs a) {
         bool replayed = false;
         if (ws.alive) {
             uint2 e = make_uint2(kWalkUnrecorded, 0u);
-            if (wrec && !seeking && ridx < a.record.budget) {
-                e = wrec[(uint64_t)ridx * 64];
-                rc4 = wcol[(uint64_t)ridx * 64];
+            if (replaying && !seeking && ridx < a.record.budget) {
+                const uint64_t i = record_slot(a.record, wtab, ridx, lane);
+                if (i != ~0ull) {
+                    e = a.record.entries[i];
+                    rc4 = a.record.colors[i];
+                }
                 ++ridx;
             }
             if (e.x == kNoIndex) {
@@ -1051,7 +1086,7 @@ backward_density_kernel(BwdArgs a) {
                 if (e.x != kWalkUnrecorded && (e.x & ~kWalkDiffers) < a.scene.num_points) {
                     seeking = true; // entry ridx - 1: the forward's differing step
                 } else if (!seeking) {
-                    wrec = nullptr;
+                    replaying = false;
                 }
                 walk_advance<false, STATS>(a.scene, ray, a.settings.max_intersections, ws, si,
                                            wc);
@@ -1146,7 +1181,9 @@ backward_density_kernel(BwdArgs a) {
             for (uint32_t k = 0; k < kSeekWindow; ++k) {
                 const uint32_t f = ridx - 1u + k;
                 if (f >= a.record.budget) break;
-                const uint2 fe = wrec[(uint64_t)f * 64];
+                const uint64_t i = record_slot(a.record, wtab, f, lane);
+                if (i == ~0ull) break;
+                const uint2 fe = a.record.entries[i];
                 if (fe.x == kNoIndex || fe.x == kWalkUnrecorded) break;
                 if ((fe.x & ~kWalkDiffers) == ws.cell &&
                     fe.y == __builtin_bit_cast(uint32_t, ws.t0)) {
@@ -1209,6 +1246,21 @@ static hipError_t launch_forward_L(const FwdArgs &a, bool neus, bool stats, hipS
             hipLaunchKernelGGL((forward_kernel<L, false, false, AT>), grid, dim3(kBlock), 0, stream, a);
         }
     }
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(kBlock) void record_reset_kernel(WalkRecordArgs r,
+                                                              uint64_t table_words) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < table_words;
+         i += (uint64_t)gridDim.x * kBlock)
+        r.chunks[i] = kNoIndex;
+    if (blockIdx.x == 0 && threadIdx.x < kXcds) r.counters[64u * threadIdx.x] = 0u;
+}
+
+hipError_t launch_record_reset(const WalkRecordArgs &r, uint64_t table_words, hipStream_t stream) {
+    const uint32_t blocks =
+        (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>((table_words + kBlock - 1) / kBlock, 4096));
+    hipLaunchKernelGGL(record_reset_kernel, dim3(blocks), dim3(kBlock), 0, stream, r, table_words);
     return hipGetLastError();
 }
 

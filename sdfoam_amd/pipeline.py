@@ -18,6 +18,7 @@ undefined or wasteful:
 from __future__ import annotations
 
 import ctypes as C
+import math
 
 import torch
 
@@ -92,7 +93,14 @@ def _inv_s_to_tensor(inv_s, like: torch.Tensor) -> torch.Tensor:
     return s
 
 
-DEFAULT_WALK_BUDGET = 256
+# a wavefront's first pool of walk-record chunks, when no earlier forward
+# over rays of this count and layout tells what the walk needs: this many
+# trips per wavefront on average
+RECORD_INITIAL_TRIPS = 256
+# pools after that: per XCD, the chunks the last such forward asked for
+# there, plus an eighth and one
+RECORD_MARGIN = 1.125
+RECORD_COUNTERS = 8  # uint32 at 256-byte strides at the start of a record
 # rays in no particular order are traced in sorted order from this many on
 AUTO_SORT_MIN_RAYS = 32768
 
@@ -105,7 +113,9 @@ class TracePlan:
       particular order;
     * ``entries``: the walk record, each ray's steps and their colours and
       sdf/density values (24 bytes per step, up to ``budget`` trips per
-      wavefront of 64 rays);
+      wavefront of 64 rays), in a pool of ``chunks`` chunks of 16 trips that
+      the wavefronts claim as they walk (``record_ptr``: its 256-byte
+      aligned start in ``entries``);
     * ``table``: the forward's fp16 offset table of the scene, which the
       backward reuses instead of rebuilding it while the points, adjacency
       and offsets tensors are the same and unmodified (same storage and
@@ -124,8 +134,10 @@ class TracePlan:
         self.device = torch.device(device)
         self.order = None
         self.entries = None
+        self.record_ptr = 0
         self.nbytes = 0
         self.budget = 0
+        self.chunks = 0
         self.table = None
         self.table_bytes = 0
         self.table_key = None
@@ -167,18 +179,35 @@ class TracePlan:
         # `scratch` may be freed now: torch reuses it only for later work on
         # this stream, which runs after the sort
 
-    def allocate_record(self, budget) -> None:
+    def allocate_record(self, budget, chunks: int = 0) -> None:
+        """A record for up to ``budget`` trips per wavefront (default: every
+        trip the walk limit allows, max_intersections + 1, plus the
+        terminating row) in a pool of ``chunks`` chunks (0: the pool of
+        RECORD_INITIAL_TRIPS trips per wavefront, or every trip if that is
+        less)."""
         if budget is None:
-            # a wavefront walks at most max_intersections + 1 trips, plus the
-            # terminating row
-            budget = min(self.max_intersections + 2, DEFAULT_WALK_BUDGET)
+            budget = self.max_intersections + 2
         budget = int(budget)
         if budget <= 0:
             raise RuntimeError("walk_budget must be positive")
-        self.nbytes = int(_lib.lib().sdf_walk_record_bytes(self.num_rays, self.ray_image_width,
-                                                           budget))
-        self.entries = torch.empty(max(1, self.nbytes // 8), dtype=torch.int64, device=self.device)
+        L = _lib.lib()
+        full = int(L.sdf_walk_record_full_chunks(self.num_rays, self.ray_image_width, budget))
+        if chunks <= 0:
+            chunks = int(L.sdf_walk_record_full_chunks(self.num_rays, self.ray_image_width,
+                                                       min(budget, RECORD_INITIAL_TRIPS)))
+        chunks = max(1, min(int(chunks), full))
+        self.nbytes = int(L.sdf_walk_record_pool_bytes(self.num_rays, self.ray_image_width,
+                                                       budget, chunks))
+        self.entries = torch.empty(self.nbytes + 256, dtype=torch.uint8, device=self.device)
+        self.record_ptr = (self.entries.data_ptr() + 255) & ~255
         self.budget = budget
+        self.chunks = chunks
+
+    def record_counters(self) -> torch.Tensor:
+        """The record's chunk counters (int32 [8], on the device): their sum
+        is the number of chunks the last forward asked for."""
+        off = self.record_ptr - self.entries.data_ptr()
+        return self.entries[off:off + 256 * RECORD_COUNTERS].view(torch.int32)[::64]
 
     def desc(self, record_key=None):
         """The C descriptor; the walk record is left out when `record_key`
@@ -186,10 +215,12 @@ class TracePlan:
         backward scans for itself."""
         use_record = self.entries is not None and (record_key is None
                                                    or record_key == self.record_key)
-        return _lib.TracePlanDesc(
-            self.entries.data_ptr() if use_record else None, self.nbytes if use_record else 0,
+        d = _lib.TracePlanDesc(
+            self.record_ptr if use_record else None, self.nbytes if use_record else 0,
             self.budget if use_record else 0,
             None if self.order is None else self.order.data_ptr())
+        d.walk_record_chunks = self.chunks if use_record else 0
+        return d
 
     def matches(self, num_rays: int, settings, device) -> bool:
         return (num_rays == self.num_rays
@@ -200,6 +231,33 @@ class TracePlan:
     def check_matches(self, num_rays: int, settings, device) -> None:
         if not self.matches(num_rays, settings, device):
             raise RuntimeError("trace_plan does not belong to these rays and settings")
+
+
+class _RecordNeed:
+    """What the walk records of one ray count and layout needed: the chunk
+    counters of the last forward, copied to pinned host memory behind the
+    forward and read once that copy has completed (no synchronisation)."""
+
+    def __init__(self):
+        self.host = torch.zeros(RECORD_COUNTERS, dtype=torch.int32).pin_memory()
+        self.event = None
+        self.per_xcd = 0  # the most chunks one XCD asked for
+
+    def observe(self, plan: "TracePlan") -> None:
+        self.host.copy_(plan.record_counters(), non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record()
+
+    def estimate(self) -> int:
+        """Chunks for the next pool (0: no forward has told yet).  Each XCD
+        claims from its own eighth of the pool, so the eighths are sized for
+        the XCD that asked for most."""
+        if self.event is not None and self.event.query():
+            self.per_xcd = int(self.host.max())
+            self.event = None
+        if self.per_xcd <= 0:
+            return 0
+        return (int(math.ceil(self.per_xcd * RECORD_MARGIN)) + 1) * RECORD_COUNTERS
 
 
 def _backward_can_follow(points, attributes, inv_s) -> bool:
@@ -233,6 +291,8 @@ class Pipeline:
     def __init__(self, sh_degree: int, attr_dtype: torch.dtype):
         self._sh_degree = int(sh_degree)
         self._attr_dtype = attr_dtype
+        # (rays, image width, budget, device) -> _RecordNeed
+        self._record_need = {}
 
     # -- src/tracing/pipeline.h:158-160 -------------------------------------
     def attribute_dim(self) -> int:
@@ -343,7 +403,12 @@ class Pipeline:
           skips its face scans (standard mode: the steps where the density
           backward's unsafe walk takes the same exit, which is all of them
           but for degenerate ties); ``walk_budget`` bounds the recorded trips
-          per wavefront.  ``None`` (the default) records when a backward can
+          per wavefront (default: all the walk limit allows).  The record's
+          storage is sized by need: the first forward over rays of this
+          count and layout gets room for 256 trips per wavefront on
+          average, later ones what the last one asked for plus an eighth;
+          trips the pool has no room for are scanned again by the backward.
+          ``None`` (the default) records when a backward can
           follow: the attributes or ``inv_s`` require grad (or the points do
           with grad mode on), which is how the reference's scene calls it in
           training and not under ``torch.no_grad()``;
@@ -408,8 +473,12 @@ class Pipeline:
             plan = TracePlan(num_rays, settings, dev)
             if want_sort:
                 plan.sort_rays(num_points, rays_c, start_c)
+            need = None
             if want_record:
-                plan.allocate_record(walk_budget)
+                budget = plan.max_intersections + 2 if walk_budget is None else int(walk_budget)
+                need = self._record_need.setdefault(
+                    (num_rays, plan.ray_image_width, budget, str(dev)), _RecordNeed())
+                plan.allocate_record(budget, need.estimate())
                 plan.record_key = TracePlan.record_key(settings, points, attributes,
                                                        point_adjacency, point_adjacency_offsets,
                                                        rays, start_point)
@@ -440,6 +509,9 @@ class Pipeline:
         # `cells` may be freed now: torch reuses it only for later work on
         # this stream, which runs after the forward
         del cells
+        if plan is not None and plan.entries is not None:
+            with torch.cuda.device(dev):
+                need.observe(plan)
         out = {"rgba": rgba}
         if return_depth:
             out["depth"] = depth

@@ -80,22 +80,30 @@ def test_walk_record_sizes_and_errors():
     from sdfoam_amd import _lib
 
     L = _lib.lib()
-    # one row of 64 entries (24 bytes: the step and its colour) per trip and
-    # wavefront, 4 wavefronts a block, blocks padded to a multiple of 8 (one
-    # per XCD)
-    assert L.sdf_walk_record_bytes(256, 0, 10) == 8 * 4 * 10 * 64 * 24
-    assert L.sdf_walk_record_bytes(8 * 256 + 1, 0, 3) == 16 * 4 * 3 * 64 * 24
-    # 1600 x 1200 image: 100 x 75 tiles of 16 x 16
-    assert L.sdf_walk_record_bytes(1600 * 1200, 1600, 1) == 7504 * 4 * 64 * 24
+    # 8 counters (256 bytes apart), the chunk tables (one uint32 per 16 trips
+    # and wavefront, rounded up to 256 bytes), then the pool: chunks of 16
+    # rows of 64 entries of 24 bytes (the step and its colour), a multiple of
+    # 8 chunks.  Wavefronts: 4 a block, blocks padded to a multiple of 8
+    chunk = 16 * 64 * 24
+    assert L.sdf_walk_record_bytes(256, 0, 10) == 2048 + 256 + 32 * chunk
+    assert L.sdf_walk_record_full_chunks(256, 0, 10) == 32
+    assert L.sdf_walk_record_full_chunks(256, 0, 40) == 96
+    assert L.sdf_walk_record_bytes(8 * 256 + 1, 0, 3) == 2048 + 256 + 64 * chunk
+    # 1600 x 1200 image: 100 x 75 tiles of 16 x 16, 7504 blocks
+    assert L.sdf_walk_record_bytes(1600 * 1200, 1600, 1) == 2048 + 120064 + 30016 * chunk
+    assert L.sdf_walk_record_pool_bytes(256, 0, 10, 5) == 2048 + 256 + 8 * chunk
+    assert L.sdf_walk_record_pool_bytes(256, 0, 10, 0) == L.sdf_walk_record_bytes(256, 0, 10)
+    assert L.sdf_walk_record_pool_bytes(256, 0, 0, 5) == 0
     s = _settings()
     buf = (C.c_uint64 * 64)()
     p = C.cast(buf, C.c_void_p)
     nb = L.sdf_trace_scratch_bytes(10, 4)
     base = C.cast(buf, C.c_void_p).value
-    off16 = base + 8 if base % 16 == 0 else base  # 8 mod 16
-    for addr, budget, nbytes, msg in ((base, 0, 1 << 20, b"budget must be positive"),
-                                      (base, 2, 100, b"walk record must hold"),
-                                      (off16, 2, 1 << 20, b"walk record must be 16-byte aligned")):
+    aligned = (base + 255) & ~255
+    for addr, budget, nbytes, msg in ((aligned, 0, 1 << 20, b"budget must be positive"),
+                                      (aligned, 2, 100, b"walk record must hold"),
+                                      (aligned + 16, 2, 1 << 20,
+                                       b"walk record must be 256-byte aligned")):
         rec = _lib.TracePlanDesc(addr, nbytes, budget, None)
         rc = L.sdf_trace_forward_planned(C.byref(rec), 3, C.byref(s), 10, p, p, 4, p, p, 1, p,
                                           p, 0, None, p, None, None, p, None, p, p, p, nb, None)

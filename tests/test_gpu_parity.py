@@ -261,9 +261,7 @@ def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False, walk=F
     fwd = pipe.trace_forward(**g, depth_quantiles=q, alpha_mode=mode, inv_s=inv_t,
                              record_walk=walk, walk_budget=walk_budget, sort_rays=sort_rays)
     if walk and mode == "sdfoam":
-        from sdfoam_amd.pipeline import DEFAULT_WALK_BUDGET
-
-        assert fwd["trace_plan"].budget == (walk_budget or min(1024 + 2, DEFAULT_WALK_BUDGET))
+        assert fwd["trace_plan"].budget == (walk_budget or 1024 + 2)
     rerr = None
     if ray_error:
         rerr_np = np.random.default_rng(11).uniform(0, 1, w.rays.shape[:-1]).astype(np.float32)
@@ -283,6 +281,33 @@ def _backward_both(w, dev, oracle_lib, mode, inv_s=None, ray_error=False, walk=F
         None if rerr is None else rerr.cpu().numpy(), alpha_mode=mode, inv_s=inv,
         threads=_threads())
     return bwd, st, ref
+
+
+def record_rows(plan):
+    """A walk record's trips in wavefront order, from its chunk tables and
+    pool: entries {next, t1} [waves, trips, 64] (uint64), colours
+    [waves, trips, 64, 4] and which trips have a chunk [waves, trips];
+    trips without one read as 0."""
+    from sdfoam_amd import _lib
+
+    slots = -(-plan.budget // 16)
+    waves = int(_lib.lib().sdf_walk_record_full_chunks(plan.num_rays, plan.ray_image_width,
+                                                       plan.budget)) // slots
+    pool = -(-plan.chunks // 8) * 8
+    off = plan.record_ptr - plan.entries.data_ptr()
+    raw = plan.entries[off:off + plan.nbytes].cpu().numpy()
+    head = 8 * 256
+    tbytes = -(-waves * slots * 4 // 256) * 256
+    table = raw[head:head + waves * slots * 4].view(np.uint32).reshape(waves, slots)
+    e0 = head + tbytes
+    ents = raw[e0:e0 + pool * 1024 * 8].view(np.uint64).reshape(pool, 16, 64)
+    cols = raw[e0 + pool * 1024 * 8:e0 + pool * 1024 * 24].view(np.float32).reshape(pool, 16, 64, 4)
+    have = table != 0xFFFFFFFF
+    assert (table[have] < pool).all()
+    idx = np.where(have, table, 0)
+    E = np.where(have[:, :, None, None], ents[idx], 0).reshape(waves, slots * 16, 64)
+    Cc = np.where(have[:, :, None, None, None], cols[idx], 0).reshape(waves, slots * 16, 64, 4)
+    return E, Cc, np.repeat(have, 16, axis=1)
 
 
 def _check_backward(bwd, st, ref, w):
@@ -348,6 +373,59 @@ def test_backward_direct_updates_c2(torch_dev, oracle_lib):
     _check_backward(bwd, st, ref, w)
 
 
+@pytest.mark.parametrize("mode", ["sdfoam", "standard"])
+@pytest.mark.parametrize("pool", ["one chunk per XCD", "a third"])
+def test_backward_walk_record_small_pool(torch_dev, oracle_lib, mode, pool, monkeypatch):
+    """Walk records whose chunk pool runs out: wavefronts that find none
+    left record nothing from there on and the backward scans those trips
+    (8 chunks: most wavefronts get none; a third of the chunks every trip
+    needs: the pool runs out part way through the launch)."""
+    from sdfoam_amd import _lib, pipeline
+
+    w = scene(2, mode=mode)
+    full = int(_lib.lib().sdf_walk_record_full_chunks(w.num_rays, w.rays.shape[-2], 1026))
+    n = 8 if pool == "one chunk per XCD" else full // 3
+    monkeypatch.setattr(pipeline._RecordNeed, "estimate", lambda self: n)
+    bwd, st, ref = _backward_both(w, torch_dev, oracle_lib, mode, walk=True)
+    _check_backward(bwd, st, ref, w)
+
+
+def test_walk_record_sized_by_need(torch_dev):
+    """The record's counters hold the chunks the walk asked for: every
+    wavefront claims one chunk per 16 trips it walks (its longest lane's
+    loop count, num_intersections).  The next forward's pool has, for each
+    of the 8 XCDs, the most one XCD asked for plus an eighth and one."""
+    import math
+
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import _lib, pipeline
+
+    w = scene(1)
+    g = gpu_scene(w, torch_dev)
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree)
+    inv_t = torch.tensor([w.inv_s], device=torch_dev)
+    fwd = pipe.trace_forward(**g, alpha_mode="sdfoam", inv_s=inv_t, record_walk=True)
+    torch.cuda.synchronize()
+    plan = fwd["trace_plan"]
+    counters = plan.record_counters().cpu().numpy()
+    asked = int(counters.sum())
+    H, W = w.rays.shape[:2]
+    ni = np_u32(fwd["num_intersections"]).reshape(H, W).astype(np.int64)
+    want = 0
+    for ty in range(0, H, 8):
+        for tx in range(0, W, 8):
+            want += -(-min(int(ni[ty:ty + 8, tx:tx + 8].max()), plan.budget) // 16)
+    assert asked == want
+    _, _, have = record_rows(plan)
+    assert int(have.sum()) // 16 == asked  # the first pool had room for every claim
+    fwd2 = pipe.trace_forward(**g, alpha_mode="sdfoam", inv_s=inv_t, record_walk=True)
+    per = math.ceil(int(counters.max()) * pipeline.RECORD_MARGIN) + 1
+    full = int(_lib.lib().sdf_walk_record_full_chunks(w.num_rays, W, plan.budget))
+    assert fwd2["trace_plan"].chunks == min(8 * per, full)
+
+
 @pytest.mark.parametrize("budget", [None, 2, 7])
 def test_backward_walk_record_c1(torch_dev, oracle_lib, budget):
     """Backward replaying the forward's walk record: full record, and budgets
@@ -405,8 +483,8 @@ def test_walk_record_standard_marks_differing_steps(torch_dev, cfg):
     fwd = pipe.trace_forward(**g, alpha_mode="standard", record_walk=True)
     plan = fwd["trace_plan"]
     torch.cuda.synchronize()
-    n = plan.nbytes // 24  # 8-byte {next, t1} entries first, then the 16-byte colours
-    nxt = plan.entries[:n].cpu().numpy().view(np.uint64) & np.uint64(0xFFFFFFFF)
+    E, _, have = record_rows(plan)
+    nxt = E[have] & np.uint64(0xFFFFFFFF)
     marked = int(np.count_nonzero(((nxt & np.uint64(0x80000000)) != 0)
                                   & (nxt < np.uint64(0xFFFFFFFE))))
     stepped = int(np.count_nonzero(nxt < np.uint64(w.num_points)))
@@ -488,8 +566,8 @@ def test_cell_table_same_results(torch_dev, mode, dtype, monkeypatch):
 
     allocate = pipeline.TracePlan.allocate_record
 
-    def allocate_zeroed(self, budget):
-        allocate(self, budget)
+    def allocate_zeroed(self, budget, chunks=0):
+        allocate(self, budget, chunks)
         self.entries.zero_()
 
     monkeypatch.setattr(pipeline.TracePlan, "allocate_record", allocate_zeroed)
@@ -512,8 +590,9 @@ def test_cell_table_same_results(torch_dev, mode, dtype, monkeypatch):
 
     for k in ("rgba", "depth", "depth_indices", "num_intersections"):
         assert np.array_equal(bits(a[k]), bits(b[k])), k
-    assert np.array_equal(bits(a["trace_plan"].entries), bits(b["trace_plan"].entries)), \
-        "walk record"
+    for x, y, name in zip(record_rows(a["trace_plan"]), record_rows(b["trace_plan"]),
+                          ("record entries", "record colours", "record chunks")):
+        assert np.array_equal(np.asarray(x).view(np.uint8), np.asarray(y).view(np.uint8)), name
     ca = a["contribution"].double().cpu().numpy().ravel()
     cb = b["contribution"].double().cpu().numpy().ravel()
     if dtype == "float32":

@@ -92,7 +92,8 @@ def test_trace_plan_keeps_record_for_its_own_inputs():
     plan.allocate_record(4)
     plan.record_key = TracePlan.record_key(s, pts, attrs, adj, offs, rays, start)
     same = plan.desc(TracePlan.record_key(s, pts, attrs, adj, offs, rays, start))
-    assert same.walk_record == plan.entries.data_ptr() and same.walk_budget == 4
+    assert same.walk_record == plan.record_ptr and same.walk_budget == 4
+    assert plan.record_ptr % 256 == 0 and same.walk_record_chunks == plan.chunks > 0
     assert same.walk_record_bytes == plan.nbytes > 0
     others = [TracePlan.record_key(s, pts, attrs.clone(), adj, offs, rays, start)]
     attrs.add_(0.0)  # same values, new version
