@@ -216,13 +216,13 @@ struct WaveShared {
     uint32_t used[2];
     uint8_t remap[kWavePlanes];
     StagedVert stg[kWaveNew];
+    double mr2, blo[3], bhi[3]; // max |v|^2 and the vertices' box (the cell's bounds)
 };
 
 struct WaveCell {
     uint32_t vp[2]; // plane indices a | b << 8 | c << 16 of this lane's two slots (kFree if none)
     double vx[2][3], ve[2], vr2[2];
     int np;                         // planes in use (same in every lane)
-    double mr2, blo[3], bhi[3];     // max |v|^2 and the vertices' box (same in every lane)
 };
 
 __device__ __forceinline__ uint32_t wlane() { return threadIdx.x & 63u; }
@@ -253,7 +253,7 @@ __device__ __forceinline__ uint32_t plane_of(uint32_t vp, int k) { return (vp >>
 
 // max |v|^2 and the vertices' box grown by the largest error bound
 // (dgrid::vertex_box).
-__device__ void wave_bounds(WaveCell &c) {
+__device__ void wave_bounds(WaveCell &c, WaveShared &sh) {
     double r2 = 0.0, e = 0.0, lo[3], hi[3];
     for (int k = 0; k < 3; ++k) {
         lo[k] = INFINITY;
@@ -268,11 +268,12 @@ __device__ void wave_bounds(WaveCell &c) {
             hi[k] = fmax(hi[k], c.vx[s][k]);
         }
     }
-    c.mr2 = wmaxd(r2);
+    // every lane stores the same values; the wave's own later reads see them
+    sh.mr2 = wmaxd(r2);
     e = wmaxd(e);
     for (int k = 0; k < 3; ++k) {
-        c.blo[k] = wmind(lo[k]) - e;
-        c.bhi[k] = wmaxd(hi[k]) + e;
+        sh.blo[k] = wmind(lo[k]) - e;
+        sh.bhi[k] = wmaxd(hi[k]) + e;
     }
 }
 
@@ -299,7 +300,7 @@ __device__ void wave_init(WaveCell &c, WaveShared &sh, const double *rlo, const 
         c.ve[0] = 0.0;
         c.vr2[0] = c.vx[0][0] * c.vx[0][0] + c.vx[0][1] * c.vx[0][1] + c.vx[0][2] * c.vx[0][2];
     }
-    wave_bounds(c);
+    wave_bounds(c, sh);
     __syncthreads();
 }
 
@@ -402,15 +403,23 @@ __device__ int wave_clip(WaveCell &c, WaveShared &sh, const double *q, double qc
                 atomicOr(&sh.edges[bit >> 5], 1u << (bit & 31u));
             }
     __syncthreads();
-    // boundary edges (reverse not removed): one new vertex each
-    uint32_t fresh[6];
-    uint32_t nf = 0;
+    // boundary edges (reverse not removed): one new vertex each, listed as
+    // 16-bit {ea, eb} fields of one register (no indexed array: it would
+    // live in scratch memory)
+    uint64_t fresh = 0;
+    uint32_t fresh5 = 0, nf = 0;
     for (int s = 0; s < 2; ++s)
         if (out[s])
             for (int k = 0; k < 3; ++k) {
                 const uint32_t ea = plane_of(c.vp[s], k), eb = plane_of(c.vp[s], (k + 1) % 3);
                 const uint32_t rev = eb * kWavePlanes + ea;
-                if (!((sh.edges[rev >> 5] >> (rev & 31u)) & 1u)) fresh[nf++] = ea | eb << 8;
+                if (!((sh.edges[rev >> 5] >> (rev & 31u)) & 1u)) {
+                    if (nf < 5)
+                        fresh |= (uint64_t)(ea | eb << 6) << (12u * nf);
+                    else
+                        fresh5 = ea | eb << 6;
+                    ++nf;
+                }
             }
     uint32_t incl = nf;
     for (int off = 1; off < 64; off <<= 1) {
@@ -430,7 +439,8 @@ __device__ int wave_clip(WaveCell &c, WaveShared &sh, const double *q, double qc
     P.point = point;
     bool bad = false;
     for (uint32_t t = 0; t < nf; ++t) {
-        const uint32_t ea = fresh[t] & 0xffu, eb = fresh[t] >> 8;
+        const uint32_t f = t < 5 ? (uint32_t)(fresh >> (12u * t)) & 0xfffu : fresh5;
+        const uint32_t ea = f & 63u, eb = f >> 6;
         vcell::Plane A, B;
         for (int k = 0; k < 3; ++k) {
             A.n[k] = sh.pn[ea][k];
@@ -483,7 +493,7 @@ __device__ int wave_clip(WaveCell &c, WaveShared &sh, const double *q, double qc
         c.vr2[s] = v.r2;
     }
     __syncthreads();
-    wave_bounds(c);
+    wave_bounds(c, sh);
     return 1;
 }
 
@@ -497,9 +507,12 @@ __device__ bool wave_touches_box(const WaveCell &c, const WaveShared &sh) {
 
 // counters: 0 report rows asked for, 1 open points, 2 undecided cells,
 // 3 cells over the fixed capacity, 4 coincident point pairs seen (twice).
-// One 64-thread block per point.  Four waves per SIMD (128 VGPRs, a few
-// hundred bytes of spills) run it ~20% faster than the two its natural
-// register count allows.
+// One 64-thread block per point.  Four waves per SIMD (128 VGPRs, 200 bytes
+// of spills per lane) run it ~20% faster than the two its natural register
+// count (203) allows; three (168 VGPRs, 40 bytes) run it ~10% slower than
+// four.  What is uniform over the wave and indexed at run time (the grid
+// cell and searched rings per level) or needed by every lane (the cell's
+// bounds) lives in LDS, not in per-lane registers or scratch.
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void certify_kernel(const float *__restrict__ p, uint32_t n,
                                                      GridView gv, uint32_t *__restrict__ reports,
                                                      uint64_t report_capacity,
@@ -507,6 +520,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                                                      uint32_t *__restrict__ open,
                                                      uint32_t *__restrict__ status_out) {
     __shared__ WaveShared sh;
+    // the point's grid cell and searched rings per level (uniform over the
+    // wave; indexed by level, so kept in LDS rather than scratch memory)
+    __shared__ int hc[dgrid::kLevels][3];
+    __shared__ int rings[dgrid::kLevels];
     const uint32_t i = blockIdx.x;
     if (i >= n) return;
     const uint32_t l = wlane();
@@ -521,13 +538,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
         }
         wave_init(c, sh, rlo, rhi);
     }
-    int hc[dgrid::kLevels][3];
-    int rings[dgrid::kLevels];
-    for (int lev = 0; lev < dgrid::kLevels; ++lev) {
-        rings[lev] = -1;
+    if (l < (uint32_t)dgrid::kLevels) {
+        rings[l] = -1;
         for (int k = 0; k < 3; ++k)
-            hc[lev][k] = dgrid::axis_cell(o[k], g.lo[k], g.level[lev].inv_h, g.level[lev].dims[k]);
+            hc[l][k] = dgrid::axis_cell(o[k], g.lo[k], g.level[l].inv_h, g.level[l].dims[k]);
     }
+    __syncthreads();
     uint32_t st = vcell::kOpen, examined = 0;
     bool decided = false, coincident = false;
     const int l0 = dgrid::first_level(gv, o);
@@ -576,10 +592,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                             d2 = q[0] * q[0] + q[1] * q[1] + q[2] * q[2];
                             if (d2 == 0.0) {
                                 dup = true;
-                            } else if (d2 <= 4.0 * c.mr2 * (1.0 + 1e-9)) {
+                            } else if (d2 <= 4.0 * sh.mr2 * (1.0 + 1e-9)) {
                                 double reach_q = 0.0, mag = d2;
                                 for (int m = 0; m < 3; ++m) {
-                                    const double bb = q[m] > 0.0 ? c.bhi[m] : c.blo[m];
+                                    const double bb = q[m] > 0.0 ? sh.bhi[m] : sh.blo[m];
                                     reach_q += bb * q[m];
                                     mag += vcell::dabs(bb * q[m]);
                                 }
@@ -607,10 +623,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                         const double dd = __shfl(d2, src, 64);
                         const int32_t jj = __shfl((int)j, src, 64);
                         // the cell may have shrunk since the filter
-                        if (dd > 4.0 * c.mr2 * (1.0 + 1e-9)) continue;
+                        if (dd > 4.0 * sh.mr2 * (1.0 + 1e-9)) continue;
                         double reach_q = 0.0, mag = dd;
                         for (int mm = 0; mm < 3; ++mm) {
-                            const double bb = qq[mm] > 0.0 ? c.bhi[mm] : c.blo[mm];
+                            const double bb = qq[mm] > 0.0 ? sh.bhi[mm] : sh.blo[mm];
                             reach_q += bb * qq[mm];
                             mag += vcell::dabs(bb * qq[mm]);
                         }
@@ -625,7 +641,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                 }
             }
             if (decided) break;
-            rings[lev] = r;
+            if (l == 0) rings[lev] = r;
+            __syncthreads();
             // every point not yet seen lies r cells of this level away or more
             const bool all = h[0] - r <= 0 && h[0] + r >= (int)lv.dims[0] - 1 && h[1] - r <= 0 &&
                              h[1] + r >= (int)lv.dims[1] - 1 && h[2] - r <= 0 &&
@@ -633,7 +650,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
             const double reach = (double)r * lv.h - g.slack;
             const double reach2 = all ? INFINITY : (reach > 0.0 ? reach * reach : 0.0);
             const bool box = wave_touches_box(c, sh);
-            if (4.0 * c.mr2 * (1.0 + 1e-9) < reach2) {
+            if (4.0 * sh.mr2 * (1.0 + 1e-9) < reach2) {
                 st = box ? vcell::kOpen : vcell::kCertified;
                 decided = true;
                 break;
@@ -644,7 +661,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                 break;
             }
             if (r >= dgrid::kMinRing &&
-                4.0 * c.mr2 * (1.0 + 1e-9) > (dgrid::kMaxRing * lv.h) * (dgrid::kMaxRing * lv.h))
+                4.0 * sh.mr2 * (1.0 + 1e-9) > (dgrid::kMaxRing * lv.h) * (dgrid::kMaxRing * lv.h))
                 break;
         }
     }
