@@ -12,8 +12,8 @@ A step is one training pass of the path through the drop-in API:
 kernel, as the reference does.
 
 Output: one JSON line on stdout.  ``roofline`` is the dominant kernel's HBM
-rate: the HBM bytes per launch that rocprofv3 counted for it (FETCH_SIZE and
-WRITE_SIZE, scaled by a copy kernel of known size; profiles/traffic_*.json)
+rate: the HBM bytes per launch that rocprofv3 counted for it (L2-to-memory
+read and write requests weighted by their sizes; profiles/traffic_*.json)
 over its average duration, measured live by HIP events recorded on its launch
 stream, against MI355X's 8 TB/s.  Beside it, ``model_frac`` prices the
 kernel's algorithmic bytes (the gather model below, which counts every gather
