@@ -532,7 +532,7 @@ def triangulate_bench(args, dev) -> int:
         "open_points": last["open"],
         "roofline": {"kernel": "certify_kernel", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None},
+                     "traffic": load_traffic(f"traffic_certify_C{args.config}.json")},
         "cpu_baseline": {"value": 1.0 / t_qhull, "unit": "rebuilds/s", "cores": 1,
                          "kind": "library",
                          "sample": "Qhull (scipy.spatial.Delaunay) on all 1M points, once; "
