@@ -338,9 +338,14 @@ def main() -> int:
     # offset-table builds per step (the backward reuses the forward's table
     # when it gets the forward's trace plan)
     pre_per_step = len(per_kernel.get("prefetch_adjacent_diff", [])) / args.steps
-    bytes_step = gather_fwd + gather_bwd + pre_per_step * bytes_pre
+    # the forward's one-pass offset table + cell table: the table's bytes, each
+    # cell's position, offsets and attribute row read and its record written
+    bytes_prep = bytes_pre + N * (12 + 8 + ab * D) + int(
+        _lib.lib().sdf_cell_table_bytes(w.sh_degree, 1 if half else 0, N))
+    prep_per_step = len(per_kernel.get("scene_prep", [])) / args.steps
+    bytes_step = gather_fwd + gather_bwd + pre_per_step * bytes_pre + prep_per_step * bytes_prep
     kernel_bytes = {"forward": gather_fwd, "backward": gather_bwd,
-                    "prefetch_adjacent_diff": bytes_pre}
+                    "prefetch_adjacent_diff": bytes_pre, "scene_prep": bytes_prep}
     dominant = max((k for k in avg if k in kernel_bytes), key=lambda k: avg[k] * len(per_kernel[k]))
     kernel_s = avg[dominant] * 1e-3
     model_gbps = kernel_bytes[dominant] / kernel_s / 1e9

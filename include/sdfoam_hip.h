@@ -245,9 +245,10 @@ int sdf_trace_benchmark(int sh_degree, const sdf_trace_settings *settings,
  *
  * Cell table (forward): the forward first copies, per cell, its position,
  * CSR row bounds and attribute row into one aligned record (64-256 bytes,
- * sdf_cell_table_bytes), then walks over the records, so a step reads one or
- * two whole cache lines of the cell instead of parts of three arrays.
- * cell_table == NULL: the forward reads the arrays. */
+ * sdf_cell_table_bytes), in the same pass that fills the offset table, then
+ * walks over the records, so a step reads one or two whole cache lines of the
+ * cell instead of parts of three arrays.  cell_table == NULL: the forward
+ * reads the arrays. */
 typedef struct sdf_trace_plan {
     void *walk_record;        /* device memory, 256-byte aligned, or NULL */
     size_t walk_record_bytes; /* >= sdf_walk_record_pool_bytes(num_rays, ray_image_width,
@@ -508,7 +509,7 @@ int sdf_debug_fpmath(int op, const float *in, void *out, uint64_t n,
 #define SDF_KERNEL_RAY_ORDER 6
 #define SDF_KERNEL_GRAD_CLEAR 7
 #define SDF_KERNEL_GRAD_FINALIZE 8
-#define SDF_KERNEL_CELL_TABLE 9
+#define SDF_KERNEL_SCENE_PREP 9 /* offset table + cell table, one pass */
 int sdf_set_timing(int enable);
 int sdf_timing_collect(int *kinds, float *ms, int max_n, int *n_out);
 

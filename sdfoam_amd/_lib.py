@@ -64,7 +64,7 @@ EXPORTS = (
 )
 
 KERNEL_NAMES = {0: "prefetch_adjacent_diff", 1: "forward", 2: "backward", 3: "build_aabb_tree", 4: "nn",
-                5: "render", 6: "ray_order", 7: "grad_clear", 8: "grad_finalize", 9: "cell_table"}
+                5: "render", 6: "ray_order", 7: "grad_clear", 8: "grad_finalize", 9: "scene_prep"}
 
 SDF_CAMERA_PINHOLE = 0
 SDF_CAMERA_FISHEYE = 1

@@ -183,29 +183,32 @@ int trace_forward_impl(const sdf_trace_plan *plan, int sh_degree,
         cells = static_cast<uint32_t *>(plan->cell_table);
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
-    tbegin(SDF_KERNEL_PREFETCH, s);
-    hipError_t e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
-                                        point_adjacency_offsets, static_cast<uint2 *>(scratch), s);
-    tend(s);
-    if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
-    if (num_rays == 0) return SDF_OK;
     FwdArgs a = {};
-    a.record = rec;
-    a.order = order;
     a.scene = make_scene(num_points, points, attributes, adjacency_size, point_adjacency,
                          point_adjacency_offsets, scratch);
+    hipError_t e;
+    if (cells) {
+        // the offset table and the cell table in one pass
+        tbegin(SDF_KERNEL_SCENE_PREP, s);
+        e = launch_scene_prep(sh_degree, half, a.scene, cells, static_cast<uint2 *>(scratch), s);
+        tend(s);
+        if (e != hipSuccess) return hip_fail(e, "scene preparation");
+        a.scene.cells = cells;
+    } else {
+        tbegin(SDF_KERNEL_PREFETCH, s);
+        e = launch_prefetch_diff(points, num_points, adjacency_size, point_adjacency,
+                                 point_adjacency_offsets, static_cast<uint2 *>(scratch), s);
+        tend(s);
+        if (e != hipSuccess) return hip_fail(e, "prefetch_adjacent_diff");
+    }
+    if (num_rays == 0) return SDF_OK;
+    a.record = rec;
+    a.order = order;
     if (rec.entries) {
         const uint64_t words =
             walk_record_waves(num_ray_tiles(num_rays, settings->ray_image_width)) * chunk_slots(rec.budget);
         e = launch_record_reset(rec, words, s);
         if (e != hipSuccess) return hip_fail(e, "walk record reset");
-    }
-    if (cells) {
-        tbegin(SDF_KERNEL_CELL_TABLE, s);
-        e = launch_cell_table(sh_degree, half, a.scene, cells, s);
-        tend(s);
-        if (e != hipSuccess) return hip_fail(e, "cell_table");
-        a.scene.cells = cells;
     }
     a.settings = *settings;
     a.rays = rays;

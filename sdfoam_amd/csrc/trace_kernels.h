@@ -215,9 +215,10 @@ hipError_t launch_record_reset(const WalkRecordArgs &r, uint64_t table_words, hi
 // over that cell table, which launch_cell_table filled.
 hipError_t launch_forward(int L, const FwdArgs &a, bool neus, bool stats, bool half,
                           hipStream_t stream);
-// Fills the cell table (cell_record_bytes(L, attribute size) per cell) from
-// sc's points, offsets and attributes.
-hipError_t launch_cell_table(int L, bool half, const SceneView &sc, uint32_t *cells,
+// Fills the fp16 offset table `diff` (as launch_prefetch_diff) and the cell
+// table (cell_record_bytes(L, attribute size) per cell) from sc's points,
+// adjacency, offsets and attributes, in one pass.
+hipError_t launch_scene_prep(int L, bool half, const SceneView &sc, uint32_t *cells, uint2 *diff,
                              hipStream_t stream);
 // Floats per cell row of the backward's gradient accumulator: the next
 // power of two >= D + 4 (attribute row, position, point error), at least 8,

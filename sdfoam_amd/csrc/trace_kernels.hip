@@ -1264,56 +1264,107 @@ hipError_t launch_record_reset(const WalkRecordArgs &r, uint64_t table_words, hi
     return hipGetLastError();
 }
 
-// Cell table: one thread per 4-byte word of the table (layout at
-// cell_record_bytes), so the writes are coalesced and each record's
-// attribute words are read from one row.
+// The forward's scene preparation in one pass: the fp16 offset table (the
+// values prefetch_diff_kernel writes) and the cell table (layout at
+// cell_record_bytes).  One wavefront per 64 consecutive cells: their CSR rows
+// are one contiguous run of entries, so the row of an entry is found among
+// the 64 row starts the wavefront holds (six cross-lane reads) instead of by a
+// search of the whole offsets array.  The first wavefront also takes entries
+// before offs[0], the last one those from offs[N] up to num_adj and the
+// table's zero padding, as prefetch_diff_kernel does.  Record words past the
+// attribute row are left unwritten (nothing reads them).
 template <int L, typename AT>
-__global__ __launch_bounds__(kBlock) void cell_table_kernel(const SceneView sc, uint32_t *cells) {
+__global__ __launch_bounds__(kBlock) void scene_prep_kernel(const SceneView sc, uint32_t *cells,
+                                                            uint2 *diff) {
     constexpr uint32_t D = 1 + 3 * (L + 1) * (L + 1);
-    constexpr uint32_t W = cell_record_bytes(L, sizeof(AT)) / 4;
+    constexpr uint32_t RW = cell_record_bytes(L, sizeof(AT)) / 4;
     constexpr uint32_t A = kCellAttrByte / 4;
-    const uint64_t total = (uint64_t)sc.num_points * W;
-    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < total;
-         i += (uint64_t)gridDim.x * kBlock) {
-        const uint64_t c = i / W;
-        const uint32_t w = (uint32_t)(i - c * W);
-        uint32_t v = 0;
-        if (w < 3) {
-            v = __builtin_bit_cast(uint32_t, sc.points[3 * c + w]);
-        } else if (w < A) {
-            v = sc.offs[c + (w - 3)];
-        } else if constexpr (sizeof(AT) == 4) {
-            if (w - A < D) v = static_cast<const uint32_t *>(sc.attrs)[c * D + (w - A)];
-        } else {
-            const uint16_t *row = static_cast<const uint16_t *>(sc.attrs) + c * D;
-            const uint32_t k = 2 * (w - A);
-            if (k < D) v = row[k];
-            if (k + 1 < D) v |= (uint32_t)row[k + 1] << 16;
-        }
-        cells[i] = v;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t c0 = (blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6)) * 64u;
+    if (c0 >= sc.num_points) return; // the whole wavefront
+    const uint32_t n = min(64u, sc.num_points - c0);
+    const bool last = c0 + n == sc.num_points;
+    // lanes past the last cell hold a row start no entry reaches
+    uint32_t beg = 0xffffffffu, end = 0u;
+    float x = 0.0f, y = 0.0f, z = 0.0f;
+    if (lane < n) {
+        const uint32_t c = c0 + lane;
+        beg = sc.offs[c];
+        end = sc.offs[c + 1];
+        x = sc.points[3ull * c];
+        y = sc.points[3ull * c + 1];
+        z = sc.points[3ull * c + 2];
+        uint32_t *r = cells + (uint64_t)c * RW;
+        *reinterpret_cast<uint4 *>(r) = make_uint4(__builtin_bit_cast(uint32_t, x),
+                                                   __builtin_bit_cast(uint32_t, y),
+                                                   __builtin_bit_cast(uint32_t, z), beg);
+        r[4] = end;
     }
+    // attribute rows c0 .. c0 + n - 1: contiguous in the caller's array
+    if constexpr (sizeof(AT) == 4) {
+        const uint32_t *src = static_cast<const uint32_t *>(sc.attrs) + (uint64_t)c0 * D;
+        for (uint32_t j = lane; j < n * D; j += 64u) {
+            const uint32_t cc = j / D;
+            cells[(uint64_t)(c0 + cc) * RW + A + (j - cc * D)] = src[j];
+        }
+    } else {
+        const uint16_t *src = static_cast<const uint16_t *>(sc.attrs) + (uint64_t)c0 * D;
+        uint16_t *dst = reinterpret_cast<uint16_t *>(cells);
+        for (uint32_t j = lane; j < n * D; j += 64u) {
+            const uint32_t cc = j / D;
+            dst[((uint64_t)(c0 + cc) * RW + A) * 2u + (j - cc * D)] = src[j];
+        }
+    }
+    // the offset table entries of these rows
+    const uint32_t first = (uint32_t)__shfl((int)beg, 0);
+    const uint32_t e0 = c0 == 0 ? 0u : min(first, sc.num_adj);
+    const uint32_t e1 = last ? sc.num_adj : min((uint32_t)__shfl((int)end, (int)n - 1), sc.num_adj);
+    for (uint32_t k0 = e0; k0 < e1; k0 += 64u) {
+        const uint32_t k = k0 + lane;
+        // the last row i < n with beg_i <= k (row 0 if none)
+        uint32_t row = 0;
+#pragma unroll
+        for (uint32_t step = 32; step > 0; step >>= 1) {
+            const uint32_t probe = row + step;
+            const uint32_t b = (uint32_t)__shfl((int)beg, (int)min(probe, 63u));
+            if (probe < n && b <= k) row = probe;
+        }
+        const float px = __shfl(x, (int)row), py = __shfl(y, (int)row), pz = __shfl(z, (int)row);
+        if (k < e1) {
+            const uint32_t a = sc.adj[k];
+            if (a >= sc.num_points) {
+                diff[k] = make_uint2(0x7e007e00u, 0x7e00u); // NaN plane
+            } else {
+                const float qx = sc.points[3ull * a], qy = sc.points[3ull * a + 1],
+                            qz = sc.points[3ull * a + 2];
+                diff[k] = make_uint2(f32_to_f16(qx - px) | (f32_to_f16(qy - py) << 16),
+                                     f32_to_f16(qz - pz));
+            }
+        }
+    }
+    if (last && lane < kDiffPad) diff[sc.num_adj + lane] = make_uint2(0u, 0u);
 }
 
 template <typename AT>
-static hipError_t launch_cell_table_T(int L, const SceneView &sc, uint32_t *cells,
+static hipError_t launch_scene_prep_T(int L, const SceneView &sc, uint32_t *cells, uint2 *diff,
                                       hipStream_t stream) {
-    const uint64_t words = (uint64_t)sc.num_points * (cell_record_bytes(L, sizeof(AT)) / 4);
-    const uint32_t blocks = (uint32_t)std::min<uint64_t>((words + kBlock - 1) / kBlock, 1u << 20);
+    const uint32_t waves = (sc.num_points + 63u) / 64u;
+    const dim3 grid((waves + kBlock / 64 - 1) / (kBlock / 64));
     switch (L) {
-    case 0: hipLaunchKernelGGL((cell_table_kernel<0, AT>), dim3(blocks), dim3(kBlock), 0, stream, sc, cells); break;
-    case 1: hipLaunchKernelGGL((cell_table_kernel<1, AT>), dim3(blocks), dim3(kBlock), 0, stream, sc, cells); break;
-    case 2: hipLaunchKernelGGL((cell_table_kernel<2, AT>), dim3(blocks), dim3(kBlock), 0, stream, sc, cells); break;
-    case 3: hipLaunchKernelGGL((cell_table_kernel<3, AT>), dim3(blocks), dim3(kBlock), 0, stream, sc, cells); break;
+    case 0: hipLaunchKernelGGL((scene_prep_kernel<0, AT>), grid, dim3(kBlock), 0, stream, sc, cells, diff); break;
+    case 1: hipLaunchKernelGGL((scene_prep_kernel<1, AT>), grid, dim3(kBlock), 0, stream, sc, cells, diff); break;
+    case 2: hipLaunchKernelGGL((scene_prep_kernel<2, AT>), grid, dim3(kBlock), 0, stream, sc, cells, diff); break;
+    case 3: hipLaunchKernelGGL((scene_prep_kernel<3, AT>), grid, dim3(kBlock), 0, stream, sc, cells, diff); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_cell_table(int L, bool half, const SceneView &sc, uint32_t *cells,
+hipError_t launch_scene_prep(int L, bool half, const SceneView &sc, uint32_t *cells, uint2 *diff,
                              hipStream_t stream) {
     if (sc.num_points == 0) return hipSuccess;
-    return half ? launch_cell_table_T<_Float16>(L, sc, cells, stream)
-                : launch_cell_table_T<float>(L, sc, cells, stream);
+    return half ? launch_scene_prep_T<_Float16>(L, sc, cells, diff, stream)
+                : launch_scene_prep_T<float>(L, sc, cells, diff, stream);
 }
 
 template <typename AT>

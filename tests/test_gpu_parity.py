@@ -161,6 +161,30 @@ def test_prefetch_diff_bitexact(torch_dev, oracle_lib, cfg):
     assert np.array_equal(got, ref)
 
 
+@pytest.mark.parametrize("cfg,dtype", [(1, "float32"), (2, "float32"), (2, "float16")])
+def test_forward_offset_table_bitexact(torch_dev, oracle_lib, cfg, dtype):
+    """The forward builds its fp16 offset table in the same pass as its cell
+    table; the table it keeps for the backward equals the oracle's
+    prefetch_adjacent_diff bit for bit, with its 32 padding entries zero."""
+    import torch
+
+    import sdfoam_amd
+
+    w = scene(cfg)
+    g = gpu_scene(w, torch_dev)
+    if dtype == "float16":
+        g["attributes"] = g["attributes"].half()
+    pipe = sdfoam_amd.create_pipeline(w.sh_degree, dtype)
+    fwd = pipe.trace_forward(**g, alpha_mode="sdfoam", inv_s=torch.tensor([w.inv_s], device=torch_dev),
+                             record_walk=True)
+    torch.cuda.synchronize()
+    E = w.adjacency.size
+    table = fwd["trace_plan"].table.view(torch.uint8)[:(E + 32) * 8].cpu().numpy().view(np.uint16)
+    ref = oracle_lib.prefetch_adjacent_diff(w.points, w.adjacency, w.offsets)
+    assert np.array_equal(table[:4 * E], ref.reshape(-1))
+    assert not table[4 * E:].any()
+
+
 def _forward_both(w, dev, oracle_lib, mode, record=0, inv_s=None, sort_rays=None,
                   record_walk=False):
     import torch
