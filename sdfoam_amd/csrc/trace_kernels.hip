@@ -21,9 +21,10 @@
 namespace sdfoam_hip {
 
 // ---------------------------------------------------------------------------
-// prefetch_adjacent_diff (src/tracing/pipeline.cu:1202-1242): one lane per
-// CSR entry (coalesced over the adjacency array) instead of one per row; the
-// row of entry k is found by a binary search of the offsets.
+// prefetch_adjacent_diff (src/tracing/pipeline.cu:1202-1242) by one lane per
+// CSR entry, the row of entry k found by a binary search of the offsets.  Used
+// for scenes without points only (every entry is then a NaN plane); otherwise
+// scene_prep_kernel builds the table by rows.
 
 __global__ __launch_bounds__(kBlock) void prefetch_diff_kernel(
     const float *__restrict__ points, uint32_t num_points, uint32_t num_adj,
@@ -1215,13 +1216,6 @@ backward_density_kernel(BwdArgs a) {
 
 static inline dim3 grid_for(uint64_t n) { return dim3((unsigned)((n + kBlock - 1) / kBlock)); }
 
-hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32_t num_adj,
-                                const uint32_t *adj, const uint32_t *offs, uint2 *diff,
-                                hipStream_t stream) {
-    hipLaunchKernelGGL(prefetch_diff_kernel, grid_for((uint64_t)num_adj + kDiffPad), dim3(kBlock), 0,
-                       stream, points, num_points, num_adj, adj, offs, diff);
-    return hipGetLastError();
-}
 
 template <int L, typename AT>
 static hipError_t launch_forward_L(const FwdArgs &a, bool neus, bool stats, hipStream_t stream) {
@@ -1272,8 +1266,9 @@ hipError_t launch_record_reset(const WalkRecordArgs &r, uint64_t table_words, hi
 // search of the whole offsets array.  The first wavefront also takes entries
 // before offs[0], the last one those from offs[N] up to num_adj and the
 // table's zero padding, as prefetch_diff_kernel does.  Record words past the
-// attribute row are left unwritten (nothing reads them).
-template <int L, typename AT>
+// attribute row are left unwritten (nothing reads them).  CELLS = false: the
+// offset table alone.
+template <int L, typename AT, bool CELLS = true>
 __global__ __launch_bounds__(kBlock) void scene_prep_kernel(const SceneView sc, uint32_t *cells,
                                                             uint2 *diff) {
     constexpr uint32_t D = 1 + 3 * (L + 1) * (L + 1);
@@ -1294,14 +1289,17 @@ __global__ __launch_bounds__(kBlock) void scene_prep_kernel(const SceneView sc, 
         x = sc.points[3ull * c];
         y = sc.points[3ull * c + 1];
         z = sc.points[3ull * c + 2];
-        uint32_t *r = cells + (uint64_t)c * RW;
-        *reinterpret_cast<uint4 *>(r) = make_uint4(__builtin_bit_cast(uint32_t, x),
-                                                   __builtin_bit_cast(uint32_t, y),
-                                                   __builtin_bit_cast(uint32_t, z), beg);
-        r[4] = end;
+        if constexpr (CELLS) {
+            uint32_t *r = cells + (uint64_t)c * RW;
+            *reinterpret_cast<uint4 *>(r) = make_uint4(__builtin_bit_cast(uint32_t, x),
+                                                       __builtin_bit_cast(uint32_t, y),
+                                                       __builtin_bit_cast(uint32_t, z), beg);
+            r[4] = end;
+        }
     }
     // attribute rows c0 .. c0 + n - 1: contiguous in the caller's array
-    if constexpr (sizeof(AT) == 4) {
+    if constexpr (!CELLS) {
+    } else if constexpr (sizeof(AT) == 4) {
         const uint32_t *src = static_cast<const uint32_t *>(sc.attrs) + (uint64_t)c0 * D;
         for (uint32_t j = lane; j < n * D; j += 64u) {
             const uint32_t cc = j / D;
@@ -1343,6 +1341,26 @@ __global__ __launch_bounds__(kBlock) void scene_prep_kernel(const SceneView sc, 
         }
     }
     if (last && lane < kDiffPad) diff[sc.num_adj + lane] = make_uint2(0u, 0u);
+}
+
+hipError_t launch_prefetch_diff(const float *points, uint32_t num_points, uint32_t num_adj,
+                                const uint32_t *adj, const uint32_t *offs, uint2 *diff,
+                                hipStream_t stream) {
+    if (num_points == 0) {
+        hipLaunchKernelGGL(prefetch_diff_kernel, grid_for((uint64_t)num_adj + kDiffPad), dim3(kBlock),
+                           0, stream, points, num_points, num_adj, adj, offs, diff);
+        return hipGetLastError();
+    }
+    SceneView sc = {};
+    sc.points = points;
+    sc.adj = adj;
+    sc.offs = offs;
+    sc.num_points = num_points;
+    sc.num_adj = num_adj;
+    const uint32_t waves = (num_points + 63u) / 64u;
+    hipLaunchKernelGGL((scene_prep_kernel<0, float, false>), dim3((waves + kBlock / 64 - 1) / (kBlock / 64)),
+                       dim3(kBlock), 0, stream, sc, nullptr, diff);
+    return hipGetLastError();
 }
 
 template <typename AT>
