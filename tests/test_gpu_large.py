@@ -189,6 +189,15 @@ def test_c3_headline_parity(dev, oracle_lib, say):
     bwd, st, ref = _backward_both(sub, dev, oracle_lib, "sdfoam", walk=True)
     _check_backward(bwd, st, ref, sub)
     say(f"C3 backward parity on the {sub.num_rays}-ray image subset")
+    # the backward that scans every face again (no walk record), on every
+    # 8th row and column
+    del bwd, st, ref
+    sl8 = (slice(None, None, 8), slice(None, None, 8))
+    sub8 = _subset(w, w.rays[sl8], w.quantiles[sl8], w.grad_rgba[sl8], w.depth_grad[sl8],
+                   start[sl8])
+    bwd, st, ref = _backward_both(sub8, dev, oracle_lib, "sdfoam", walk=False)
+    _check_backward(bwd, st, ref, sub8)
+    say(f"C3 scanning backward parity on the {sub8.num_rays}-ray image subset")
 
 
 def test_c4_render_full_camera(dev, oracle_lib, say):
