@@ -185,6 +185,46 @@ def test_forward_offset_table_bitexact(torch_dev, oracle_lib, cfg, dtype):
     assert not table[4 * E:].any()
 
 
+def test_offset_table_with_empty_rows(torch_dev, oracle_lib):
+    """CSR rows may be empty (a point whose row was cleared): the tables are
+    built by runs of 64 rows, so an entry's row is the last one starting at or
+    before it.  Every 7th point of C1 loses its row (and runs of empty rows
+    occur); the forward's table, the plain table and the forward itself
+    still equal the oracle's."""
+    import dataclasses
+
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import prefetch_adjacent_diff
+
+    w = scene(1)
+    offs = w.offsets.astype(np.int64)
+    deg = np.diff(offs)
+    keep_row = np.ones(w.points.shape[0], dtype=bool)
+    keep_row[::7] = False
+    keep_row[100:140] = False  # a run of empty rows
+    deg = np.where(keep_row, deg, 0)
+    rows = np.repeat(np.arange(w.points.shape[0]), np.diff(offs))
+    adj = w.adjacency[keep_row[rows]]
+    new_offs = np.concatenate([[0], np.cumsum(deg)]).astype(np.uint32)
+    w2 = dataclasses.replace(w, adjacency=np.ascontiguousarray(adj, dtype=np.uint32),
+                             offsets=new_offs)
+    ref_table = oracle_lib.prefetch_adjacent_diff(w2.points, w2.adjacency, w2.offsets)
+    g = gpu_scene(w2, torch_dev)
+    plain = prefetch_adjacent_diff(g["points"], g["point_adjacency"], g["point_adjacency_offsets"])
+    pipe = sdfoam_amd.create_pipeline(w2.sh_degree)
+    fwd = pipe.trace_forward(**g, alpha_mode="sdfoam",
+                             inv_s=torch.tensor([w2.inv_s], device=torch_dev), record_walk=True)
+    torch.cuda.synchronize()
+    E = w2.adjacency.size
+    assert np.array_equal(plain.cpu().numpy().view(np.uint16)[:E].reshape(-1), ref_table.reshape(-1))
+    table = fwd["trace_plan"].table.view(torch.uint8)[:(E + 32) * 8].cpu().numpy().view(np.uint16)
+    assert np.array_equal(table[:4 * E], ref_table.reshape(-1))
+    out, st, ref = _forward_both(w2, torch_dev, oracle_lib, "sdfoam")
+    _check_forward(out, st, ref, w2, 0)
+
+
 def _forward_both(w, dev, oracle_lib, mode, record=0, inv_s=None, sort_rays=None,
                   record_walk=False):
     import torch
