@@ -375,6 +375,20 @@ int sdf_nn(const float *points, const float *aabb_tree, const float *queries,
            uint32_t num_points, uint32_t num_queries, uint32_t *indices,
            void *stream);
 
+/* Start cell of each ray: the nearest point to its origin (rays [num_rays, 6],
+ * origin first), as sdf_nn over the distinct origins gives it for finite
+ * points and origins (ties: smallest index), without a host synchronisation:
+ * the origins are deduplicated on the GPU by their bits, and each distinct
+ * one is searched once (a scan over all points when there are at most 256,
+ * else the tree).  scratch: sdf_start_points_scratch_bytes(num_rays),
+ * 256-byte aligned; num_points >= 32.
+ * Replaces get_starting_point (sdfoam_model/scene.py:272-282: torch.unique
+ * over the origins, then nn). */
+size_t sdf_start_points_scratch_bytes(uint32_t num_rays);
+int sdf_start_points(const float *rays, uint32_t num_rays, const float *points,
+                     uint32_t num_points, const float *aabb_tree, uint32_t *start,
+                     void *scratch, size_t scratch_bytes, void *stream);
+
 /* Per point: the farthest CSR neighbour (UINT32_MAX if none is farther
  * than 0) and cell_radius = sum of half the neighbour distances / row length.
  * Neighbours out of range are skipped.

@@ -35,6 +35,8 @@ EXPORTS = (
     "sdf_walk_record_full_chunks",
     "sdf_grad_accum_bytes",
     "sdf_cell_table_bytes",
+    "sdf_start_points_scratch_bytes",
+    "sdf_start_points",
     "sdf_ray_order_scratch_bytes",
     "sdf_ray_order",
     "sdf_trace_forward_planned",
@@ -177,6 +179,9 @@ def lib() -> C.CDLL:
     L.sdf_walk_record_full_chunks.argtypes = [U32, U32, U32]
     L.sdf_grad_accum_bytes.restype = SZ
     L.sdf_grad_accum_bytes.argtypes = [C.c_int, U32]
+    L.sdf_start_points_scratch_bytes.restype = SZ
+    L.sdf_start_points_scratch_bytes.argtypes = [U32]
+    L.sdf_start_points.argtypes = [P, U32, P, U32, P, P, P, SZ, P]
     L.sdf_cell_table_bytes.restype = SZ
     L.sdf_cell_table_bytes.argtypes = [C.c_int, C.c_int, U32]
     L.sdf_ray_order_scratch_bytes.restype = SZ

@@ -16,6 +16,8 @@
 // the smallest index.
 #include "trace_kernels.h"
 
+#include <algorithm>
+
 namespace sdfoam_hip {
 
 __device__ __forceinline__ uint32_t ilog2_u32(uint32_t x) { return x ? 31u - __clz(x) : 0u; }
@@ -129,18 +131,13 @@ __device__ __forceinline__ void wave_argmin(float &v, uint32_t &idx) {
     }
 }
 
-__global__ __launch_bounds__(kBlock) void nn_kernel(const float *__restrict__ points,
-                                                    const float *__restrict__ tree,
-                                                    const float *__restrict__ queries,
-                                                    uint32_t num_points, uint32_t num_queries,
-                                                    uint32_t *__restrict__ indices) {
-    __shared__ NNItem stack_all[kNNWaves][kNNStack];
-    const uint32_t wave = threadIdx.x >> 6;
+// Nearest point to q for the whole wavefront (the result is uniform): a
+// depth-first search over groups of up to 64 sibling nodes six levels apart,
+// the group under the best lane first, groups whose lower bound exceeds the
+// best distance skipped.  0 when no point has a distance (NaN query).
+__device__ uint32_t nn_wave(const float *__restrict__ points, const float *__restrict__ tree,
+                            uint32_t num_points, float qx, float qy, float qz, NNItem *st) {
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t qi = blockIdx.x * kNNWaves + wave;
-    if (qi >= num_queries) return; // uniform per wave
-    NNItem *st = stack_all[wave];
-    const float qx = queries[3ull * qi], qy = queries[3ull * qi + 1], qz = queries[3ull * qi + 2];
     const uint32_t td = ilog2_u32(pow2_up(num_points));
     const uint64_t n2 = 1ull << td;
     const float kInf = __builtin_bit_cast(float, 0x7f800000u);
@@ -194,7 +191,22 @@ __global__ __launch_bounds__(kBlock) void nn_kernel(const float *__restrict__ po
         sp += npush;
         __builtin_amdgcn_wave_barrier();
     }
-    if (lane == 0) indices[qi] = best_idx == kNoIndex ? 0u : best_idx;
+    const uint32_t r = (uint32_t)__builtin_amdgcn_readfirstlane((int)best_idx);
+    return r == kNoIndex ? 0u : r;
+}
+
+__global__ __launch_bounds__(kBlock) void nn_kernel(const float *__restrict__ points,
+                                                    const float *__restrict__ tree,
+                                                    const float *__restrict__ queries,
+                                                    uint32_t num_points, uint32_t num_queries,
+                                                    uint32_t *__restrict__ indices) {
+    __shared__ NNItem stack_all[kNNWaves][kNNStack];
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t qi = blockIdx.x * kNNWaves + wave;
+    if (qi >= num_queries) return; // uniform per wave
+    const uint32_t r = nn_wave(points, tree, num_points, queries[3ull * qi], queries[3ull * qi + 1],
+                               queries[3ull * qi + 2], stack_all[wave]);
+    if ((threadIdx.x & 63u) == 0) indices[qi] = r;
 }
 
 hipError_t launch_nn(const float *points, const float *tree, const float *queries,
@@ -203,6 +215,219 @@ hipError_t launch_nn(const float *points, const float *tree, const float *querie
     if (num_queries == 0) return hipSuccess;
     hipLaunchKernelGGL(nn_kernel, dim3((num_queries + kNNWaves - 1) / kNNWaves), dim3(kBlock), 0,
                        stream, points, tree, queries, num_points, num_queries, indices);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Start cells of a ray batch (get_starting_point, sdfoam_model/scene.py:
+// 272-282): the nearest point to each ray's origin.  A batch's rays come from
+// few camera positions, so the origins are deduplicated on the GPU in an
+// open-addressing hash table keyed on their bits (the reference sorts them
+// with torch.unique, which synchronises with the host), each distinct
+// origin's nearest point is found once, and every ray takes its origin's.
+// With at most kStartBrute distinct origins the search is a scan over all
+// points (one pass over the points for all of them: the same fp32 distances
+// as nn_wave, ties to the smallest index), else nn_wave per origin.  Equal
+// results to nn over the distinct origins for finite points and origins.
+
+constexpr uint32_t kStartBrute = 256;
+constexpr uint32_t kStartPts = 8;          // points per thread in the scan
+constexpr uint32_t kStartTreeBlocks = 1024; // waves that share the tree searches
+
+__host__ StartLayout start_layout(uint32_t num_rays) {
+    StartLayout l;
+    uint64_t t = 64;
+    while (t < 2ull * num_rays) t *= 2;
+    l.table_slots = t;
+    auto up = [](uint64_t x) { return (x + 255u) / 256u * 256u; };
+    l.table = 256;
+    l.uid = l.table + up(4 * t);
+    l.ray_slot = l.uid + up(4 * t);
+    l.uq_ray = l.ray_slot + up(4ull * num_rays);
+    l.best = l.uq_ray + up(4ull * num_rays);
+    l.bytes = l.best + up(8ull * num_rays);
+    return l;
+}
+
+__device__ __forceinline__ uint32_t origin_hash(uint32_t x, uint32_t y, uint32_t z) {
+    uint32_t h = x * 0x9e3779b1u ^ (y + 0x7f4a7c15u) * 0x85ebca77u ^ (z + 0x165667b1u) * 0xc2b2ae3du;
+    h ^= h >> 15;
+    h *= 0x2c1b3c6du;
+    h ^= h >> 12;
+    return h;
+}
+
+__device__ __forceinline__ bool same_origin(const float *__restrict__ rays, uint32_t a, uint32_t b) {
+    const uint32_t *ra = reinterpret_cast<const uint32_t *>(rays + 6ull * a);
+    const uint32_t *rb = reinterpret_cast<const uint32_t *>(rays + 6ull * b);
+    return ra[0] == rb[0] && ra[1] == rb[1] && ra[2] == rb[2];
+}
+
+__global__ __launch_bounds__(kBlock) void start_init_kernel(uint32_t *__restrict__ counter,
+                                                            uint32_t *__restrict__ table,
+                                                            uint64_t slots) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < slots;
+         i += (uint64_t)gridDim.x * kBlock)
+        table[i] = kNoIndex;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *counter = 0u;
+}
+
+// Each ray claims the first free slot of its probe sequence or finds the
+// slot of an equal origin there.  The table has at least twice as many slots
+// as rays, so every probe sequence reaches a free slot or its origin's.
+__global__ __launch_bounds__(kBlock) void start_hash_kernel(const float *__restrict__ rays,
+                                                            uint32_t num_rays,
+                                                            uint32_t *__restrict__ table,
+                                                            uint64_t slots,
+                                                            uint32_t *__restrict__ ray_slot) {
+    const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= num_rays) return;
+    const uint32_t *o = reinterpret_cast<const uint32_t *>(rays + 6ull * i);
+    uint64_t h = origin_hash(o[0], o[1], o[2]) & (slots - 1);
+    for (uint64_t probe = 0; probe < slots; ++probe) {
+        uint32_t s = table[h];
+        if (s == kNoIndex) {
+            s = atomicCAS(table + h, kNoIndex, i);
+            if (s == kNoIndex) break; // claimed
+        }
+        if (same_origin(rays, s, i)) break;
+        h = (h + 1) & (slots - 1);
+    }
+    ray_slot[i] = (uint32_t)h;
+}
+
+// Numbers the claimed slots (the distinct origins) and resets their results.
+__global__ __launch_bounds__(kBlock) void start_unique_kernel(const uint32_t *__restrict__ table,
+                                                              uint64_t slots,
+                                                              uint32_t *__restrict__ counter,
+                                                              uint32_t *__restrict__ uid,
+                                                              uint32_t *__restrict__ uq_ray,
+                                                              uint64_t *__restrict__ best) {
+    for (uint64_t h = (uint64_t)blockIdx.x * kBlock + threadIdx.x; h < slots;
+         h += (uint64_t)gridDim.x * kBlock) {
+        const uint32_t r = table[h];
+        if (r == kNoIndex) continue;
+        const uint32_t u = atomicAdd(counter, 1u);
+        uid[h] = u;
+        uq_ray[u] = r;
+        best[u] = ~0ull;
+    }
+}
+
+// At most kStartBrute distinct origins: every block scans kBlock * kStartPts
+// points for all of them; per origin the smallest (distance bits, index)
+// of the block goes into `best` with one atomic.
+__global__ __launch_bounds__(kBlock) void start_brute_kernel(const float *__restrict__ points,
+                                                             uint32_t num_points,
+                                                             const float *__restrict__ rays,
+                                                             const uint32_t *__restrict__ counter,
+                                                             const uint32_t *__restrict__ uq_ray,
+                                                             uint64_t *__restrict__ best) {
+    __shared__ float q[kStartBrute][3];
+    __shared__ unsigned long long slot[kStartBrute];
+    const uint32_t count = *counter;
+    if (count == 0 || count > kStartBrute) return; // the whole grid
+    for (uint32_t u = threadIdx.x; u < count; u += kBlock) {
+        const float *o = rays + 6ull * uq_ray[u];
+        q[u][0] = o[0];
+        q[u][1] = o[1];
+        q[u][2] = o[2];
+        slot[u] = ~0ull;
+    }
+    __syncthreads();
+    const uint64_t p0 = (uint64_t)blockIdx.x * kBlock * kStartPts;
+    float px[kStartPts], py[kStartPts], pz[kStartPts];
+#pragma unroll
+    for (uint32_t k = 0; k < kStartPts; ++k) {
+        const uint64_t j = p0 + (uint64_t)k * kBlock + threadIdx.x;
+        const bool ok = j < num_points;
+        px[k] = ok ? points[3 * j] : 0.0f;
+        py[k] = ok ? points[3 * j + 1] : 0.0f;
+        pz[k] = ok ? points[3 * j + 2] : 0.0f;
+    }
+    for (uint32_t u = 0; u < count; ++u) {
+        const float qx = q[u][0], qy = q[u][1], qz = q[u][2];
+        unsigned long long key = ~0ull;
+#pragma unroll
+        for (uint32_t k = 0; k < kStartPts; ++k) {
+            const uint64_t j = p0 + (uint64_t)k * kBlock + threadIdx.x;
+            const float dx = px[k] - qx, dy = py[k] - qy, dz = pz[k] - qz;
+            const float d = sqrtf(sdf_dot3(dx, dy, dz, dx, dy, dz));
+            const unsigned long long c =
+                ((unsigned long long)__builtin_bit_cast(uint32_t, d) << 32) | (uint32_t)j;
+            if (j < num_points && d == d && c < key) key = c; // NaN: no candidate
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned long long o = __shfl_xor(key, off, 64);
+            key = o < key ? o : key;
+        }
+        if ((threadIdx.x & 63u) == 0 && key != ~0ull) atomicMin(slot + u, key);
+    }
+    __syncthreads();
+    for (uint32_t u = threadIdx.x; u < count; u += kBlock)
+        if (slot[u] != ~0ull) atomicMin(reinterpret_cast<unsigned long long *>(best) + u, slot[u]);
+}
+
+// More distinct origins: one tree search per origin, the waves of the grid
+// taking the origins in turn.
+__global__ __launch_bounds__(kBlock) void start_tree_kernel(const float *__restrict__ points,
+                                                            uint32_t num_points,
+                                                            const float *__restrict__ tree,
+                                                            const float *__restrict__ rays,
+                                                            const uint32_t *__restrict__ counter,
+                                                            const uint32_t *__restrict__ uq_ray,
+                                                            uint64_t *__restrict__ best) {
+    __shared__ NNItem stack_all[kNNWaves][kNNStack];
+    const uint32_t count = *counter;
+    if (count <= kStartBrute) return; // the whole grid
+    const uint32_t wave = threadIdx.x >> 6;
+    for (uint32_t u = blockIdx.x * kNNWaves + wave; u < count; u += gridDim.x * kNNWaves) {
+        const float *o = rays + 6ull * uq_ray[u];
+        const uint32_t r = nn_wave(points, tree, num_points, o[0], o[1], o[2], stack_all[wave]);
+        if ((threadIdx.x & 63u) == 0) best[u] = r;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void start_scatter_kernel(uint32_t num_rays,
+                                                               const uint32_t *__restrict__ ray_slot,
+                                                               const uint32_t *__restrict__ uid,
+                                                               const uint64_t *__restrict__ best,
+                                                               uint32_t *__restrict__ start) {
+    const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= num_rays) return;
+    const uint64_t b = best[uid[ray_slot[i]]];
+    start[i] = b == ~0ull ? 0u : (uint32_t)b;
+}
+
+hipError_t launch_start_points(const float *rays, uint32_t num_rays, const float *points,
+                               uint32_t num_points, const float *tree, uint32_t *start,
+                               void *scratch, hipStream_t stream) {
+    if (num_rays == 0) return hipSuccess;
+    const StartLayout l = start_layout(num_rays);
+    char *base = static_cast<char *>(scratch);
+    uint32_t *counter = reinterpret_cast<uint32_t *>(base);
+    uint32_t *table = reinterpret_cast<uint32_t *>(base + l.table);
+    uint32_t *uid = reinterpret_cast<uint32_t *>(base + l.uid);
+    uint32_t *ray_slot = reinterpret_cast<uint32_t *>(base + l.ray_slot);
+    uint32_t *uq_ray = reinterpret_cast<uint32_t *>(base + l.uq_ray);
+    uint64_t *best = reinterpret_cast<uint64_t *>(base + l.best);
+    const uint32_t slot_blocks = (uint32_t)std::min<uint64_t>((l.table_slots + kBlock - 1) / kBlock, 4096);
+    const uint32_t ray_blocks = (num_rays + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL(start_init_kernel, dim3(slot_blocks), dim3(kBlock), 0, stream, counter, table,
+                       l.table_slots);
+    hipLaunchKernelGGL(start_hash_kernel, dim3(ray_blocks), dim3(kBlock), 0, stream, rays, num_rays,
+                       table, l.table_slots, ray_slot);
+    hipLaunchKernelGGL(start_unique_kernel, dim3(slot_blocks), dim3(kBlock), 0, stream, table,
+                       l.table_slots, counter, uid, uq_ray, best);
+    const uint32_t point_blocks = (uint32_t)(((uint64_t)num_points + kBlock * kStartPts - 1) /
+                                             (kBlock * kStartPts));
+    hipLaunchKernelGGL(start_brute_kernel, dim3(point_blocks), dim3(kBlock), 0, stream, points,
+                       num_points, rays, counter, uq_ray, best);
+    hipLaunchKernelGGL(start_tree_kernel, dim3(kStartTreeBlocks), dim3(kBlock), 0, stream, points,
+                       num_points, tree, rays, counter, uq_ray, best);
+    hipLaunchKernelGGL(start_scatter_kernel, dim3(ray_blocks), dim3(kBlock), 0, stream, num_rays,
+                       ray_slot, uid, best, start);
     return hipGetLastError();
 }
 

@@ -807,6 +807,30 @@ int sdf_nn(const float *points, const float *aabb_tree, const float *queries, ui
     return SDF_OK;
 }
 
+size_t sdf_start_points_scratch_bytes(uint32_t num_rays) {
+    return start_layout(num_rays).bytes;
+}
+
+int sdf_start_points(const float *rays, uint32_t num_rays, const float *points,
+                     uint32_t num_points, const float *aabb_tree, uint32_t *start, void *scratch,
+                     size_t scratch_bytes, void *stream) {
+    if (num_points < 32) return fail(SDF_E_INVALID, "number of points must be at least 32");
+    if (!points || !aabb_tree || (num_rays > 0 && (!rays || !start)))
+        return fail(SDF_E_INVALID, "NULL pointer argument");
+    const size_t need = sdf_start_points_scratch_bytes(num_rays);
+    if (num_rays > 0 && (!scratch || scratch_bytes < need))
+        return fail(SDF_E_INVALID, "scratch must hold %zu bytes (got %zu)", need, scratch_bytes);
+    if ((reinterpret_cast<uintptr_t>(scratch) & 255u) != 0)
+        return fail(SDF_E_INVALID, "scratch must be 256-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    tbegin(SDF_KERNEL_NN, s);
+    hipError_t e = launch_start_points(rays, num_rays, points, num_points, aabb_tree, start,
+                                       scratch, s);
+    tend(s);
+    if (e != hipSuccess) return hip_fail(e, "start points");
+    return SDF_OK;
+}
+
 int sdf_trace_walk_stats(int sh_degree, const sdf_trace_settings *settings, int backward,
                          uint32_t num_points, const float *points, const float *attributes,
                          uint32_t adjacency_size, const uint32_t *point_adjacency,

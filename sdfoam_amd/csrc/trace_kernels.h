@@ -280,6 +280,18 @@ hipError_t launch_delaunay_merge(const float *points, uint32_t num_points, void 
 
 hipError_t launch_build_aabb_tree(const float *points, uint32_t num_points, float *tree,
                                   hipStream_t stream);
+// Scratch of launch_start_points: a counter, the origin hash table (uid
+// beside it), each ray's slot, the distinct origins' rays and results.
+struct StartLayout {
+    uint64_t table_slots;
+    size_t table, uid, ray_slot, uq_ray, best, bytes;
+};
+StartLayout start_layout(uint32_t num_rays);
+// start[i] = the nearest point to ray i's origin (as nn over the distinct
+// origins), without a host synchronisation.
+hipError_t launch_start_points(const float *rays, uint32_t num_rays, const float *points,
+                               uint32_t num_points, const float *tree, uint32_t *start,
+                               void *scratch, hipStream_t stream);
 hipError_t launch_nn(const float *points, const float *tree, const float *queries,
                      uint32_t num_points, uint32_t num_queries, uint32_t *indices,
                      hipStream_t stream);

@@ -67,14 +67,33 @@ def nn(points: torch.Tensor, tree: torch.Tensor, queries: torch.Tensor) -> torch
 
 
 def get_starting_point(rays: torch.Tensor, points: torch.Tensor, aabb_tree: torch.Tensor):
-    """Start cell per ray: nearest point to each distinct ray origin, looked up
-    once per origin (sdfoam_model/scene.py:272-282)."""
-    with torch.no_grad():
-        camera_origins = rays[..., :3]
-        unique_cameras, inverse_indices = torch.unique(camera_origins, dim=0, return_inverse=True)
-        nn_inds = nn(points, aabb_tree, unique_cameras).long()
-        start_point = nn_inds[inverse_indices]
-        return start_point.to(torch.uint32)
+    """Start cell per ray: the nearest point to each distinct ray origin,
+    looked up once per origin (sdfoam_model/scene.py:272-282).  The
+    reference deduplicates the origins with torch.unique, which waits for the
+    GPU; here sdf_start_points deduplicates them on the GPU, so the call
+    queues its work and returns.  The result equals nn over the distinct
+    origins for finite points and origins."""
+    if rays.size(-1) != 6:
+        raise RuntimeError("rays must have 6 as the last dimension")
+    if rays.dtype != torch.float32 or points.dtype != torch.float32 or aabb_tree.dtype != torch.float32:
+        raise RuntimeError("unsupported scalar type")
+    if rays.device.type != "cuda" or points.device.type != "cuda" or aabb_tree.device.type != "cuda":
+        raise RuntimeError("rays, points and tree must be on CUDA device")
+    num_points = points.numel() // 3
+    if num_points < 32:
+        raise RuntimeError("number of points must be at least 32")
+    r = rays.detach().contiguous()
+    num_rays = r.numel() // 6
+    start = torch.empty(tuple(r.shape[:-1]), dtype=torch.uint32, device=r.device)
+    L = _lib.lib()
+    nbytes = int(L.sdf_start_points_scratch_bytes(num_rays))
+    scratch = torch.empty(nbytes + 256, dtype=torch.uint8, device=r.device)
+    base = (scratch.data_ptr() + 255) & ~255
+    with torch.cuda.device(r.device):
+        check(L.sdf_start_points(ptr(r), num_rays, ptr(points.detach().contiguous()), num_points,
+                                 ptr(aabb_tree.detach().contiguous()), ptr(start), base, nbytes,
+                                 _lib.stream_handle(r.device)))
+    return start
 
 
 __all__ = ["build_aabb_tree", "nn", "get_starting_point", "pow2_round_up", "_c10"]

@@ -164,6 +164,33 @@ def test_cell_table_sizes_and_errors():
         assert rc == 1 and msg in L.sdf_last_error()
 
 
+def test_start_points_sizes_and_errors():
+    from sdfoam_amd import _lib
+
+    L = _lib.lib()
+    # a counter line, the hash table and its slot numbers (4 bytes per slot,
+    # a power of two >= 2 rays and >= 64), 4 + 4 + 8 bytes per ray; every
+    # part 256-byte aligned
+    def up(x):
+        return -(-x // 256) * 256
+
+    for rays in (1, 100, 1000):
+        slots = max(64, 1 << (2 * rays - 1).bit_length())
+        want = 256 + 2 * up(4 * slots) + 2 * up(4 * rays) + up(8 * rays)
+        assert L.sdf_start_points_scratch_bytes(rays) == want
+    buf = (C.c_uint64 * 4096)()
+    p = C.cast(buf, C.c_void_p)
+    base = C.cast(buf, C.c_void_p).value
+    aligned = (base + 255) & ~255
+    need = L.sdf_start_points_scratch_bytes(10)
+    assert L.sdf_start_points(p, 10, p, 31, p, p, aligned, need, None) == 1
+    assert b"at least 32" in L.sdf_last_error()
+    assert L.sdf_start_points(p, 10, p, 40, p, p, aligned, need - 1, None) == 1
+    assert b"scratch must hold" in L.sdf_last_error()
+    assert L.sdf_start_points(p, 10, p, 40, p, p, aligned + 8, need, None) == 1
+    assert b"256-byte aligned" in L.sdf_last_error()
+
+
 def test_triangulation_table_argument_errors():
     from sdfoam_amd import _lib
 

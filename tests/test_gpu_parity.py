@@ -764,6 +764,43 @@ def test_get_starting_point_matches_nn(torch_dev, oracle_lib):
     assert np.array_equal(np_u32(sp), w.extra["start"])
 
 
+@pytest.mark.parametrize("origins", [1, 64, 255, 256, 3000])
+def test_start_points_batch(torch_dev, oracle_lib, origins):
+    """get_starting_point on a batch of random rays from `origins` distinct
+    positions (drawn with replacement, so every origin repeats), some inside
+    the point cloud and some far outside it, the first one at the origin with
+    x = +0 or -0 (two bit patterns, so origins + 1 keys): equal to nn over
+    the distinct origins (the reference's torch.unique + nn) and to the
+    host's exact nearest neighbour.  Up to 256 keys are searched by the scan
+    over all points (255 origins: exactly 256), more by the tree (256)."""
+    import torch
+
+    import sdfoam_amd
+
+    w = scene(2)
+    pts = to_dev(w.points, torch_dev)
+    tree = sdfoam_amd.build_aabb_tree(pts)
+    rng = np.random.default_rng(origins)
+    cams = rng.normal(0.0, 1.0, (origins, 3)).astype(np.float32)
+    cams *= rng.choice([0.3, 4.0], size=(origins, 1)).astype(np.float32)
+    cams[0] = 0.0
+    R = 20000
+    pick = rng.integers(0, origins, R)
+    rays = np.zeros((R, 6), dtype=np.float32)
+    rays[:, :3] = cams[pick]
+    rays[:, 3:] = rng.normal(size=(R, 3)).astype(np.float32)
+    rays[pick == 0, 0] = np.where(rng.random((pick == 0).sum()) < 0.5, 0.0, -0.0)
+    rd = to_dev(rays, torch_dev)
+    sp = sdfoam_amd.get_starting_point(rd, pts, tree)
+    uniq, inv = torch.unique(rd[:, :3], dim=0, return_inverse=True)
+    ref = sdfoam_amd.nn(pts, tree, uniq).long()[inv]
+    torch.cuda.synchronize()
+    got = np_u32(sp)
+    assert np.array_equal(got, ref.cpu().numpy().astype(np.uint32))
+    host = oracle_lib.nn(w.points, cams, threads=_threads())
+    assert np.array_equal(got, host[pick])
+
+
 def test_trace_rays_autograd(torch_dev):
     import torch
 
