@@ -7,13 +7,15 @@
 // consecutive point pairs, the last point repeated as padding.
 //
 // The search gives one wave64 to a query.  The wave tests a group of up to
-// 64 sibling nodes per step (one per lane), six tree levels apart, and keeps a
-// depth-first stack of node groups in LDS: the group under the best lane is
-// visited first, so the first leaf visit already gives a tight bound, and
-// every group whose lower bound exceeds the best distance is skipped.  The fp32
-// box distance is a lower bound of the fp32 point distance (rounding is
-// monotone), so the result is the exact fp32 nearest neighbour; ties go to
-// the smallest index.
+// 64 sibling nodes per step (one per lane), six tree levels apart (depths 6,
+// 12, 18, ...), and descends depth first: at each level the children are
+// taken in the order of their lower bounds, so the first leaf visit already
+// gives a tight bound, and every node whose lower bound exceeds the best
+// distance is skipped.  The top two group levels (depth 6: 64 boxes, depth 12:
+// 4,096 boxes) are copied into LDS once per block, so a search reads global
+// memory only below depth 12.  The fp32 box distance is a lower bound of the
+// fp32 point distance (rounding is monotone), so the result is the exact fp32
+// nearest neighbour; ties go to the smallest index.
 #include "trace_kernels.h"
 
 #include <algorithm>
@@ -90,16 +92,20 @@ hipError_t launch_build_aabb_tree(const float *points, uint32_t num_points, floa
 
 // ---------------------------------------------------------------------------
 
-constexpr int kNNWaves = kBlock / 64;
-// The stack holds, per tree depth visited (at most ceil(32 / 6) of them), the
-// <= 63 pending sibling groups of the group being expanded, plus one.
-constexpr int kNNStack = 512;
+// Blocks of 16 waves share one copy of the top levels (1 block per CU).
+constexpr int kNNBlock = 1024;
+constexpr int kNNWaves = kNNBlock / 64;
+constexpr uint32_t kNNTopA = 64;           // boxes at depth 6
+constexpr uint32_t kNNTopB = 4096;         // boxes at depth 12
+constexpr uint32_t kNNTop = kNNTopA + kNNTopB;
+// Group levels of a descent: depths 6, 12, ..., 30 below the root (tree
+// depth <= 32); the points are tested without a level of their own.
+constexpr int kNNLevels = 6;
+constexpr uint32_t kNNMaxBlocks = 256;
 
-struct NNItem {
-    uint32_t depth_size; // depth | (group size << 8)
-    uint32_t first;      // first node of the group
-    float lb;            // lower bound of the parent node
-    uint32_t pad;
+struct NNShared {
+    float top[6][kNNTop];              // min x, y, z, max x, y, z (SoA: no bank conflicts)
+    float lb[kNNWaves][kNNLevels][64]; // lower bounds of each level's pending nodes
 };
 
 __device__ __forceinline__ float point_dist(const float *__restrict__ p, float qx, float qy,
@@ -131,90 +137,127 @@ __device__ __forceinline__ void wave_argmin(float &v, uint32_t &idx) {
     }
 }
 
-// Nearest point to q for the whole wavefront (the result is uniform): a
-// depth-first search over groups of up to 64 sibling nodes six levels apart,
-// the group under the best lane first, groups whose lower bound exceeds the
-// best distance skipped.  0 when no point has a distance (NaN query).
+__device__ __forceinline__ float box_dist_top(const NNShared &sh, uint32_t b, float qx, float qy,
+                                             float qz) {
+    const float dx = fmaxf(fmaxf(sh.top[0][b] - qx, 0.0f), qx - sh.top[3][b]);
+    const float dy = fmaxf(fmaxf(sh.top[1][b] - qy, 0.0f), qy - sh.top[4][b]);
+    const float dz = fmaxf(fmaxf(sh.top[2][b] - qz, 0.0f), qz - sh.top[5][b]);
+    return sqrtf(sdf_dot3(dx, dy, dz, dx, dy, dz));
+}
+
+// Copies the boxes of depths 6 and 12 (those above the points) into LDS.
+// Every thread of the block calls it; it ends with a block barrier.
+__device__ void nn_load_top(const float *__restrict__ tree, uint32_t td, NNShared &sh) {
+    const uint64_t n2 = 1ull << td;
+    for (uint32_t t = threadIdx.x; t < kNNTop; t += kNNBlock) {
+        const uint32_t d = t < kNNTopA ? 6u : 12u;
+        const uint32_t i = t < kNNTopA ? t : t - kNNTopA;
+        if (d >= td) continue; // no boxes at that depth: never read
+        const float *b = tree + 6ull * ((n2 - (2ull << d)) + i);
+#pragma unroll
+        for (int c = 0; c < 6; ++c) sh.top[c][t] = b[c];
+    }
+    __syncthreads();
+}
+
+// Nearest point to q for the whole wavefront (the result is uniform), over
+// the tree of depth td (points padded to 2^td).  NaN lower bounds mark nodes
+// that are taken, outside the group or not comparable (NaN query): a node is
+// pending while lb <= best.  0 when no point has a distance (NaN query).
 __device__ uint32_t nn_wave(const float *__restrict__ points, const float *__restrict__ tree,
-                            uint32_t num_points, float qx, float qy, float qz, NNItem *st) {
+                            uint32_t num_points, uint32_t td, float qx, float qy, float qz,
+                            NNShared &sh, uint32_t wave) {
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t td = ilog2_u32(pow2_up(num_points));
     const uint64_t n2 = 1ull << td;
     const float kInf = __builtin_bit_cast(float, 0x7f800000u);
-
+    const float kNaN = __builtin_bit_cast(float, 0x7fc00000u);
     float best = kInf;
     uint32_t best_idx = kNoIndex;
-    int sp = 0;
-    {
-        const uint32_t d0 = td < 6 ? td : 6;
-        if (lane == 0) st[0] = NNItem{d0 | ((1u << d0) << 8), 0u, 0.0f, 0u};
-        sp = 1;
+
+    // the points of a group: one per lane
+    auto test_points = [&](uint32_t first, uint32_t size) {
+        const uint32_t p = first + lane;
+        const bool ok = lane < size && p < num_points;
+        float dist = ok ? point_dist(points + 3ull * p, qx, qy, qz) : kInf;
+        uint32_t idx = ok ? p : kNoIndex;
+        wave_argmin(dist, idx);
+        if (dist < best || (dist == best && idx < best_idx)) {
+            best = dist;
+            best_idx = idx;
+        }
+    };
+    // lower bound of node `first + lane` of depth d (NaN outside the group)
+    auto bound = [&](uint32_t d, uint32_t first, uint32_t size) {
+        const uint32_t node = first + lane;
+        if (lane >= size) return kNaN;
+        if (d == 6) return box_dist_top(sh, node, qx, qy, qz);
+        if (d == 12) return box_dist_top(sh, kNNTopA + node, qx, qy, qz);
+        return box_dist(tree + 6ull * ((n2 - (2ull << d)) + node), qx, qy, qz);
+    };
+
+    if (td <= 6) { // a single group of points
+        test_points(0, 1u << td);
+        const uint32_t r = (uint32_t)__builtin_amdgcn_readfirstlane((int)best_idx);
+        return r == kNoIndex ? 0u : r;
     }
-    __builtin_amdgcn_wave_barrier();
-    while (sp > 0) {
-        --sp;
-        const NNItem it = st[sp];
+    float(*lbs)[64] = sh.lb[wave];
+    // lane k holds the first node of level k's group (level k at depth
+    // min(6 (k + 1), td), all of it below the points' depth)
+    uint32_t first_of = 0;
+    lbs[0][lane] = bound(6, 0, 64);
+    int k = 0;
+    while (k >= 0) {
         __builtin_amdgcn_wave_barrier();
-        if (it.lb > best) continue;
-        const uint32_t d = it.depth_size & 0xffu;
-        const uint32_t size = it.depth_size >> 8;
-        const uint32_t node = it.first + lane;
-        bool valid = lane < size;
-        if (d == td) {
-            valid = valid && node < num_points;
-            float dist = valid ? point_dist(points + 3ull * node, qx, qy, qz) : kInf;
-            uint32_t idx = valid ? node : kNoIndex;
-            wave_argmin(dist, idx);
-            if (dist < best || (dist == best && idx < best_idx)) {
-                best = dist;
-                best_idx = idx;
-            }
+        const float lb = lbs[k][lane];
+        const bool pending = lb <= best;
+        float bl = pending ? lb : kInf;
+        uint32_t bi = pending ? lane : 64u;
+        wave_argmin(bl, bi);
+        if (bi >= 64u) { // level done
+            --k;
             continue;
         }
-        const float *box = tree + 6ull * ((n2 - (2ull << d)) + node);
-        const float lb = valid ? box_dist(box, qx, qy, qz) : kInf;
-        const bool keep = valid && !(lb > best);
-        float bl = keep ? lb : kInf;
-        uint32_t bi = keep ? lane : 64u;
-        wave_argmin(bl, bi);
-        const uint32_t dc = (d + 6 < td) ? d + 6 : td;
-        const uint32_t csize = 1u << (dc - d);
+        if (lane == bi) lbs[k][lane] = kNaN; // taken
+        const uint32_t d = 6u * (uint32_t)(k + 1);
+        const uint32_t node = (uint32_t)__builtin_amdgcn_readlane((int)first_of, k) + bi;
+        const uint32_t dc = d + 6 < td ? d + 6 : td;
         const uint32_t cfirst = node << (dc - d);
-        const bool push = keep && lane != bi;
-        const uint64_t pm = __ballot(push);
-        const uint64_t below = (lane == 0) ? 0ull : (pm & (~0ull >> (64 - lane)));
-        const int pos = sp + (int)__popcll(below);
-        const int npush = (int)__popcll(pm) + (bi < 64u ? 1 : 0);
-        if (sp + npush > kNNStack) break; // unreachable: the stack bound is kNNStack
-        if (push) st[pos] = NNItem{dc | (csize << 8), cfirst, lb, 0u};
-        if (bi < 64u && lane == bi) st[sp + npush - 1] = NNItem{dc | (csize << 8), cfirst, lb, 0u};
-        sp += npush;
-        __builtin_amdgcn_wave_barrier();
+        const uint32_t csize = 1u << (dc - d);
+        if (dc == td) {
+            test_points(cfirst, csize);
+            continue;
+        }
+        ++k; // k + 1 < kNNLevels: dc < td <= 32 makes dc <= 30
+        if (lane == (uint32_t)k) first_of = cfirst;
+        lbs[k][lane] = bound(dc, cfirst, csize);
     }
     const uint32_t r = (uint32_t)__builtin_amdgcn_readfirstlane((int)best_idx);
     return r == kNoIndex ? 0u : r;
 }
 
-__global__ __launch_bounds__(kBlock) void nn_kernel(const float *__restrict__ points,
-                                                    const float *__restrict__ tree,
-                                                    const float *__restrict__ queries,
-                                                    uint32_t num_points, uint32_t num_queries,
-                                                    uint32_t *__restrict__ indices) {
-    __shared__ NNItem stack_all[kNNWaves][kNNStack];
+__global__ __launch_bounds__(kNNBlock) void nn_kernel(const float *__restrict__ points,
+                                                      const float *__restrict__ tree,
+                                                      const float *__restrict__ queries,
+                                                      uint32_t num_points, uint32_t num_queries,
+                                                      uint32_t *__restrict__ indices) {
+    __shared__ NNShared sh;
+    const uint32_t td = ilog2_u32(pow2_up(num_points));
+    nn_load_top(tree, td, sh);
     const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t qi = blockIdx.x * kNNWaves + wave;
-    if (qi >= num_queries) return; // uniform per wave
-    const uint32_t r = nn_wave(points, tree, num_points, queries[3ull * qi], queries[3ull * qi + 1],
-                               queries[3ull * qi + 2], stack_all[wave]);
-    if ((threadIdx.x & 63u) == 0) indices[qi] = r;
+    for (uint32_t qi = blockIdx.x * kNNWaves + wave; qi < num_queries; qi += gridDim.x * kNNWaves) {
+        const uint32_t r = nn_wave(points, tree, num_points, td, queries[3ull * qi],
+                                   queries[3ull * qi + 1], queries[3ull * qi + 2], sh, wave);
+        if ((threadIdx.x & 63u) == 0) indices[qi] = r;
+    }
 }
 
 hipError_t launch_nn(const float *points, const float *tree, const float *queries,
                      uint32_t num_points, uint32_t num_queries, uint32_t *indices,
                      hipStream_t stream) {
     if (num_queries == 0) return hipSuccess;
-    hipLaunchKernelGGL(nn_kernel, dim3((num_queries + kNNWaves - 1) / kNNWaves), dim3(kBlock), 0,
-                       stream, points, tree, queries, num_points, num_queries, indices);
+    const uint32_t blocks = std::min<uint32_t>((num_queries + kNNWaves - 1) / kNNWaves, kNNMaxBlocks);
+    hipLaunchKernelGGL(nn_kernel, dim3(blocks), dim3(kNNBlock), 0, stream, points, tree, queries,
+                       num_points, num_queries, indices);
     return hipGetLastError();
 }
 
@@ -232,7 +275,6 @@ hipError_t launch_nn(const float *points, const float *tree, const float *querie
 
 constexpr uint32_t kStartBrute = 256;
 constexpr uint32_t kStartPts = 8;          // points per thread in the scan
-constexpr uint32_t kStartTreeBlocks = 1024; // waves that share the tree searches
 
 __host__ StartLayout start_layout(uint32_t num_rays) {
     StartLayout l;
@@ -371,20 +413,22 @@ __global__ __launch_bounds__(kBlock) void start_brute_kernel(const float *__rest
 
 // More distinct origins: one tree search per origin, the waves of the grid
 // taking the origins in turn.
-__global__ __launch_bounds__(kBlock) void start_tree_kernel(const float *__restrict__ points,
-                                                            uint32_t num_points,
-                                                            const float *__restrict__ tree,
-                                                            const float *__restrict__ rays,
-                                                            const uint32_t *__restrict__ counter,
-                                                            const uint32_t *__restrict__ uq_ray,
-                                                            uint64_t *__restrict__ best) {
-    __shared__ NNItem stack_all[kNNWaves][kNNStack];
+__global__ __launch_bounds__(kNNBlock) void start_tree_kernel(const float *__restrict__ points,
+                                                              uint32_t num_points,
+                                                              const float *__restrict__ tree,
+                                                              const float *__restrict__ rays,
+                                                              const uint32_t *__restrict__ counter,
+                                                              const uint32_t *__restrict__ uq_ray,
+                                                              uint64_t *__restrict__ best) {
+    __shared__ NNShared sh;
     const uint32_t count = *counter;
     if (count <= kStartBrute) return; // the whole grid
+    const uint32_t td = ilog2_u32(pow2_up(num_points));
+    nn_load_top(tree, td, sh);
     const uint32_t wave = threadIdx.x >> 6;
     for (uint32_t u = blockIdx.x * kNNWaves + wave; u < count; u += gridDim.x * kNNWaves) {
         const float *o = rays + 6ull * uq_ray[u];
-        const uint32_t r = nn_wave(points, tree, num_points, o[0], o[1], o[2], stack_all[wave]);
+        const uint32_t r = nn_wave(points, tree, num_points, td, o[0], o[1], o[2], sh, wave);
         if ((threadIdx.x & 63u) == 0) best[u] = r;
     }
 }
@@ -424,7 +468,7 @@ hipError_t launch_start_points(const float *rays, uint32_t num_rays, const float
                                              (kBlock * kStartPts));
     hipLaunchKernelGGL(start_brute_kernel, dim3(point_blocks), dim3(kBlock), 0, stream, points,
                        num_points, rays, counter, uq_ray, best);
-    hipLaunchKernelGGL(start_tree_kernel, dim3(kStartTreeBlocks), dim3(kBlock), 0, stream, points,
+    hipLaunchKernelGGL(start_tree_kernel, dim3(kNNMaxBlocks), dim3(kNNBlock), 0, stream, points,
                        num_points, tree, rays, counter, uq_ray, best);
     hipLaunchKernelGGL(start_scatter_kernel, dim3(ray_blocks), dim3(kBlock), 0, stream, num_rays,
                        ray_slot, uid, best, start);

@@ -749,6 +749,36 @@ def test_aabb_tree_and_nn_exact(torch_dev, oracle_lib):
     assert np.array_equal(np_u32(idx), ref)
 
 
+@pytest.mark.parametrize("n", [32, 33, 64, 65, 129, 4096, 4097, 70_000, 300_000])
+def test_nn_tree_depths(torch_dev, oracle_lib, n):
+    """nn over trees of every shape the search distinguishes: one group of
+    points (n <= 64), the depth-6 boxes over points (n <= 4096), the depth-6
+    and depth-12 boxes held in LDS over points, and boxes below depth 12 read
+    from the tree (n > 262,144).  Duplicated points make ties, which go to
+    the smaller index; the host's exact nearest neighbour is the reference."""
+    import torch
+
+    import sdfoam_amd
+
+    rng = np.random.default_rng(n)
+    pts = rng.uniform(-1, 1, (n, 3)).astype(np.float32)
+    pts[n // 2] = pts[n // 3]
+    pts[n - 1] = pts[0]
+    queries = np.concatenate([
+        rng.uniform(-1.3, 1.3, (2000, 3)),
+        rng.normal(0, 5, (100, 3)),
+        pts[rng.integers(0, n, 100)],
+        pts[[n // 2, n // 3, 0, n - 1]],
+    ]).astype(np.float32)
+    p = to_dev(pts, torch_dev)
+    tree = sdfoam_amd.build_aabb_tree(p)
+    idx = sdfoam_amd.nn(p, tree, to_dev(queries, torch_dev))
+    torch.cuda.synchronize()
+    ref = oracle_lib.nn(pts, queries, threads=_threads())
+    assert np.array_equal(np_u32(idx), ref)
+    assert ref[-4] == ref[-3] == n // 3 and ref[-2] == ref[-1] == 0
+
+
 def test_get_starting_point_matches_nn(torch_dev, oracle_lib):
     import torch
 
