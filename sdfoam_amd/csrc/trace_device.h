@@ -269,6 +269,16 @@ __host__ __device__ constexpr uint32_t cell_record_bytes(int L, uint32_t attr_si
     return b;
 }
 
+// Fourth half of an offset-table entry built with the cell table: the
+// neighbour a of the row's cell i as a - i in int16, or kDeltaNone when it
+// does not fit (the walk then reads the adjacency).  Every delta but
+// kDeltaNone decodes to a exactly.
+constexpr uint32_t kDeltaNone = 0x8000u;
+__host__ __device__ inline uint32_t neighbour_delta(uint32_t i, uint32_t a) {
+    const int64_t d = (int64_t)a - (int64_t)i;
+    return (d >= -32767 && d <= 32767) ? (uint32_t)(uint16_t)(int16_t)d : kDeltaNone;
+}
+
 struct SceneView {
     const float *__restrict__ points;
     const void *__restrict__ attrs; // [N, D] of the pipeline's attribute type
@@ -386,6 +396,7 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
     // fp16 diffs and a unit direction, quotients that round to 0), so no face
     // that the exact test takes is skipped and the exit face is the same bit
     // for bit.  t0 >= 0; t1 may be negative in unsafe scans.
+    uint32_t bw = kDeltaNone; // RB: the exit entry's neighbour delta
     float t1m = t1;                             // t1 + |t1| 2^-21
     const float t0m = t0 * (1.0f - 0x1p-21f);   // t0 (1 - 2^-21)
     const float t0p = t0 * (1.0f + 0x1p-21f);   // t0 (1 + 2^-21), DUAL
@@ -423,6 +434,7 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
                     t1 = t;
                     t1m = fmaf(fabsf(t), 0x1p-21f, t);
                     best = k;
+                    if constexpr (RB != 0) bw = h[u].y >> 16;
                 }
                 if constexpr (DUAL) tmin_u = fminf(tmin_u, t);
             }
@@ -434,7 +446,11 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
         ws.alive = false;
         return;
     }
-    const uint32_t next = sc.adj[beg + best];
+    // over the cell table the entry names the neighbour (but for the rare
+    // deltas beyond int16); the adjacency array otherwise
+    const uint32_t next = (RB != 0 && bw != kDeltaNone)
+                              ? (uint32_t)((int32_t)ws.cell + (int32_t)(int16_t)(uint16_t)bw)
+                              : sc.adj[beg + best];
     if (next >= sc.num_points) {
         ws.alive = false;
         return;

@@ -1266,8 +1266,11 @@ hipError_t launch_record_reset(const WalkRecordArgs &r, uint64_t table_words, hi
 // search of the whole offsets array.  The first wavefront also takes entries
 // before offs[0], the last one those from offs[N] up to num_adj and the
 // table's zero padding, as prefetch_diff_kernel does.  Record words past the
-// attribute row are left unwritten (nothing reads them).  CELLS = false: the
-// offset table alone.
+// attribute row are left unwritten (nothing reads them).  The offset table
+// built with the cell table carries each entry's neighbour in its fourth
+// half (`neighbour_delta`), so the walk over the cell table reads the exit
+// face's neighbour from the entry it already holds.  CELLS = false: the
+// offset table alone, as prefetch_adjacent_diff gives it (fourth half 0).
 template <int L, typename AT, bool CELLS = true>
 __global__ __launch_bounds__(kBlock) void scene_prep_kernel(const SceneView sc, uint32_t *cells,
                                                             uint2 *diff) {
@@ -1330,13 +1333,16 @@ __global__ __launch_bounds__(kBlock) void scene_prep_kernel(const SceneView sc, 
         const float px = __shfl(x, (int)row), py = __shfl(y, (int)row), pz = __shfl(z, (int)row);
         if (k < e1) {
             const uint32_t a = sc.adj[k];
+            // with the cell table, the entry's fourth half (0 in the plain
+            // table) holds the neighbour relative to the row's cell
+            const uint32_t w = CELLS ? neighbour_delta(c0 + row, a) : 0u;
             if (a >= sc.num_points) {
-                diff[k] = make_uint2(0x7e007e00u, 0x7e00u); // NaN plane
+                diff[k] = make_uint2(0x7e007e00u, 0x7e00u | (w << 16)); // NaN plane
             } else {
                 const float qx = sc.points[3ull * a], qy = sc.points[3ull * a + 1],
                             qz = sc.points[3ull * a + 2];
                 diff[k] = make_uint2(f32_to_f16(qx - px) | (f32_to_f16(qy - py) << 16),
-                                     f32_to_f16(qz - pz));
+                                     f32_to_f16(qz - pz) | (w << 16));
             }
         }
     }

@@ -161,11 +161,38 @@ def test_prefetch_diff_bitexact(torch_dev, oracle_lib, cfg):
     assert np.array_equal(got, ref)
 
 
+def with_neighbour_deltas(ref, adjacency, offsets):
+    """The oracle's prefetch_adjacent_diff entries [E, 4] (fourth half 0) with
+    the fourth half the table built beside the cell table carries: the
+    neighbour minus the row's point as int16, 0x8000 where that does not fit."""
+    offs = np.asarray(offsets, dtype=np.int64)
+    rows = np.repeat(np.arange(offs.size - 1), np.diff(offs))
+    d = np.asarray(adjacency, dtype=np.int64) - rows
+    fourth = np.where(np.abs(d) <= 32767, d & 0xFFFF, 0x8000).astype(np.uint16)
+    out = np.array(ref, dtype=np.uint16).reshape(-1, 4)
+    assert not out[:, 3].any()
+    out[:, 3] = fourth
+    return out
+
+
+def test_neighbour_delta_encoding():
+    """The host restatement of the fourth half on hand cases: in-range deltas
+    of both signs, the int16 limits and beyond (0x8000 = read the adjacency)."""
+    # rows 0, 0, 1, 1, 2, 3, 3, then 40000, 40000 (rows 4..39999 empty)
+    adj = np.array([1, 0, 32769, 40000, 5, 2, 32770, 7232, 7233], dtype=np.uint32)
+    offs = np.array([0, 2, 4, 5] + [7] * 39997 + [9], dtype=np.uint32)
+    got = with_neighbour_deltas(np.zeros((9, 4), np.uint16), adj, offs)[:, 3]
+    # deltas 1, 0, 32768, 39999, 3, -1, 32767, -32768, -32767
+    assert got.tolist() == [1, 0, 0x8000, 0x8000, 3, 0xFFFF, 32767, 0x8000, 0x8001]
+
+
 @pytest.mark.parametrize("cfg,dtype", [(1, "float32"), (2, "float32"), (2, "float16")])
 def test_forward_offset_table_bitexact(torch_dev, oracle_lib, cfg, dtype):
     """The forward builds its fp16 offset table in the same pass as its cell
     table; the table it keeps for the backward equals the oracle's
-    prefetch_adjacent_diff bit for bit, with its 32 padding entries zero."""
+    prefetch_adjacent_diff bit for bit in the offset halves, carries each
+    entry's neighbour delta in the fourth, and has its 32 padding entries
+    zero."""
     import torch
 
     import sdfoam_amd
@@ -181,7 +208,7 @@ def test_forward_offset_table_bitexact(torch_dev, oracle_lib, cfg, dtype):
     E = w.adjacency.size
     table = fwd["trace_plan"].table.view(torch.uint8)[:(E + 32) * 8].cpu().numpy().view(np.uint16)
     ref = oracle_lib.prefetch_adjacent_diff(w.points, w.adjacency, w.offsets)
-    assert np.array_equal(table[:4 * E], ref.reshape(-1))
+    assert np.array_equal(table[:4 * E], with_neighbour_deltas(ref, w.adjacency, w.offsets).reshape(-1))
     assert not table[4 * E:].any()
 
 
@@ -220,7 +247,8 @@ def test_offset_table_with_empty_rows(torch_dev, oracle_lib):
     E = w2.adjacency.size
     assert np.array_equal(plain.cpu().numpy().view(np.uint16)[:E].reshape(-1), ref_table.reshape(-1))
     table = fwd["trace_plan"].table.view(torch.uint8)[:(E + 32) * 8].cpu().numpy().view(np.uint16)
-    assert np.array_equal(table[:4 * E], ref_table.reshape(-1))
+    assert np.array_equal(table[:4 * E],
+                          with_neighbour_deltas(ref_table, w2.adjacency, w2.offsets).reshape(-1))
     out, st, ref = _forward_both(w2, torch_dev, oracle_lib, "sdfoam")
     _check_forward(out, st, ref, w2, 0)
 
