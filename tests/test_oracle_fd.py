@@ -10,8 +10,9 @@ Not covered here, and pinned elsewhere: position gradients (the walk uses
 fp16 planes, so positions are pinned on an exact lattice,
 test_oracle_lattice.py); the depth terms of sdfoam mode, whose coupling
 through g_logT follows the reference's code (src/tracing/pipeline.cu:405-469)
-and is not the derivative of the linearised depth -- parity unpinned beyond
-the differential GPU-vs-oracle tests.
+and is not the derivative of the linearised depth, so finite differences
+cannot pin it: test_oracle_depth_coupling.py restates those equations in
+closed form on the exact lattice.
 """
 
 import numpy as np
