@@ -317,6 +317,9 @@ __global__ __launch_bounds__(kBlock) void start_init_kernel(uint32_t *__restrict
 // Each ray claims the first free slot of its probe sequence or finds the
 // slot of an equal origin there.  The table has at least twice as many slots
 // as rays, so every probe sequence reaches a free slot or its origin's.
+// Rays of one wavefront with the bits of its first ray's origin take that
+// ray's slot without probing: a batch from one camera then makes one probe
+// per wavefront instead of every ray contending for the same slot.
 __global__ __launch_bounds__(kBlock) void start_hash_kernel(const float *__restrict__ rays,
                                                             uint32_t num_rays,
                                                             uint32_t *__restrict__ table,
@@ -325,17 +328,29 @@ __global__ __launch_bounds__(kBlock) void start_hash_kernel(const float *__restr
     const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
     if (i >= num_rays) return;
     const uint32_t *o = reinterpret_cast<const uint32_t *>(rays + 6ull * i);
-    uint64_t h = origin_hash(o[0], o[1], o[2]) & (slots - 1);
-    for (uint64_t probe = 0; probe < slots; ++probe) {
-        uint32_t s = table[h];
-        if (s == kNoIndex) {
-            s = atomicCAS(table + h, kNoIndex, i);
-            if (s == kNoIndex) break; // claimed
+    const uint32_t ox = o[0], oy = o[1], oz = o[2];
+    // the first active lane's id and origin, read by every lane (before any
+    // branch: a cross-lane read in a branch sees only the lanes in it)
+    const uint32_t lead = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x & 63u));
+    const uint32_t lx = (uint32_t)__builtin_amdgcn_readfirstlane((int)ox);
+    const uint32_t ly = (uint32_t)__builtin_amdgcn_readfirstlane((int)oy);
+    const uint32_t lz = (uint32_t)__builtin_amdgcn_readfirstlane((int)oz);
+    const bool follower = ((threadIdx.x & 63u) != lead) & (ox == lx) & (oy == ly) & (oz == lz);
+    uint64_t h = origin_hash(ox, oy, oz) & (slots - 1);
+    if (!follower) {
+        for (uint64_t probe = 0; probe < slots; ++probe) {
+            uint32_t s = table[h];
+            if (s == kNoIndex) {
+                s = atomicCAS(table + h, kNoIndex, i);
+                if (s == kNoIndex) break; // claimed
+            }
+            if (same_origin(rays, s, i)) break;
+            h = (h + 1) & (slots - 1);
         }
-        if (same_origin(rays, s, i)) break;
-        h = (h + 1) & (slots - 1);
     }
-    ray_slot[i] = (uint32_t)h;
+    // the first ray's slot (its probe has ended: the loop above is done)
+    const uint32_t lead_slot = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)h);
+    ray_slot[i] = follower ? lead_slot : (uint32_t)h;
 }
 
 // Numbers the claimed slots (the distinct origins) and resets their results.
