@@ -361,7 +361,8 @@ int sdf_batch_gather(const void *data, size_t num_rows, size_t stride,
                      void *dst, void *stream);
 
 /* Implicit AABB tree over consecutive point pairs, tree [pow2(N), 2, 3]
- * (node (d, i) at 2^td - 2^(d+1) + i; the last entry is zeroed).
+ * (node (d, i) at 2^td - 2^(d+1) + i; the last entry is zeroed);
+ * 1 <= N <= 2^31 (here and for sdf_nn and sdf_start_points).
  * Replaces build_aabb_tree (src/aabb_tree/aabb_tree.h:10-13,
  * src/aabb_tree/aabb_tree.cu:294-341). */
 int sdf_build_aabb_tree(const float *points, uint32_t num_points,

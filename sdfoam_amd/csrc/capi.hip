@@ -626,10 +626,15 @@ int sdf_trace_backward_planned(
                                sharpness, sharpness_grad, scratch, scratch_bytes, stream);
 }
 
+// The tree has pow2(N) boxes (N rounded up to a power of two in 32 bits).
+constexpr uint32_t kMaxTreePoints = 1u << 31;
+
 int sdf_build_aabb_tree(const float *points, uint32_t num_points, float *aabb_tree,
                         void *stream) {
     if (!points || !aabb_tree) return fail(SDF_E_INVALID, "NULL pointer argument");
     if (num_points == 0) return fail(SDF_E_INVALID, "num_points must be positive");
+    if (num_points > kMaxTreePoints)
+        return fail(SDF_E_INVALID, "at most %u points (got %u)", kMaxTreePoints, num_points);
     hipStream_t s = static_cast<hipStream_t>(stream);
     tbegin(SDF_KERNEL_AABB_TREE, s);
     hipError_t e = launch_build_aabb_tree(points, num_points, aabb_tree, s);
@@ -797,6 +802,8 @@ int sdf_delaunay_merge(const float *points, uint32_t num_points, void *certify_s
 int sdf_nn(const float *points, const float *aabb_tree, const float *queries, uint32_t num_points,
            uint32_t num_queries, uint32_t *indices, void *stream) {
     if (num_points < 32) return fail(SDF_E_INVALID, "number of points must be at least 32");
+    if (num_points > kMaxTreePoints)
+        return fail(SDF_E_INVALID, "at most %u points (got %u)", kMaxTreePoints, num_points);
     if (!points || !aabb_tree || (num_queries > 0 && (!queries || !indices)))
         return fail(SDF_E_INVALID, "NULL pointer argument");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -815,6 +822,8 @@ int sdf_start_points(const float *rays, uint32_t num_rays, const float *points,
                      uint32_t num_points, const float *aabb_tree, uint32_t *start, void *scratch,
                      size_t scratch_bytes, void *stream) {
     if (num_points < 32) return fail(SDF_E_INVALID, "number of points must be at least 32");
+    if (num_points > kMaxTreePoints)
+        return fail(SDF_E_INVALID, "at most %u points (got %u)", kMaxTreePoints, num_points);
     if (!points || !aabb_tree || (num_rays > 0 && (!rays || !start)))
         return fail(SDF_E_INVALID, "NULL pointer argument");
     const size_t need = sdf_start_points_scratch_bytes(num_rays);

@@ -189,6 +189,15 @@ def test_start_points_sizes_and_errors():
     assert b"scratch must hold" in L.sdf_last_error()
     assert L.sdf_start_points(p, 10, p, 40, p, p, aligned + 8, need, None) == 1
     assert b"256-byte aligned" in L.sdf_last_error()
+    # the tree has pow2(N) boxes in 32 bits: more than 2^31 points is refused
+    # before any work, by the start lookup, nn and the tree build alike
+    big = (1 << 31) + 1
+    assert L.sdf_start_points(p, 10, p, big, p, p, aligned, need, None) == 1
+    assert b"at most 2147483648 points" in L.sdf_last_error()
+    assert L.sdf_nn(p, p, p, big, 10, p, None) == 1
+    assert b"at most 2147483648 points" in L.sdf_last_error()
+    assert L.sdf_build_aabb_tree(p, big, p, None) == 1
+    assert b"at most 2147483648 points" in L.sdf_last_error()
 
 
 def test_triangulation_table_argument_errors():
