@@ -492,6 +492,27 @@ __device__ __forceinline__ void cell_isect_grad(const float *p, const float *q, 
     g[2] = (num * ray.dz + dp * (ray.oz - p[2])) / dp2;
 }
 
+// cell_isect_grad(p, q) and cell_isect_grad(q, p) together.  Swapping p and
+// q negates the face normal q - p exactly, and with it num and dp (every
+// product and fused sum of the dots changes sign only), while (p + q) / 2
+// and dp^2 stay the same; so both come from one set of them, bit for bit
+// what the two separate calls give.
+__device__ __forceinline__ void cell_isect_grad_pair(const float *p, const float *q,
+                                                     const RayF &ray, float *g_pq, float *g_qp) {
+    const float fo0 = (p[0] + q[0]) / 2.0f, fo1 = (p[1] + q[1]) / 2.0f, fo2 = (p[2] + q[2]) / 2.0f;
+    const float fn0 = q[0] - p[0], fn1 = q[1] - p[1], fn2 = q[2] - p[2];
+    const float num = sdf_dot3(fo0 - ray.ox, fo1 - ray.oy, fo2 - ray.oz, fn0, fn1, fn2);
+    const float dp = sdf_dot3(fn0, fn1, fn2, ray.dx, ray.dy, ray.dz);
+    const float dp2 = dp * dp;
+    g_pq[0] = (num * ray.dx + dp * (ray.ox - p[0])) / dp2;
+    g_pq[1] = (num * ray.dy + dp * (ray.oy - p[1])) / dp2;
+    g_pq[2] = (num * ray.dz + dp * (ray.oz - p[2])) / dp2;
+    const float nnum = -num, ndp = -dp;
+    g_qp[0] = (nnum * ray.dx + ndp * (ray.ox - q[0])) / dp2;
+    g_qp[1] = (nnum * ray.dy + ndp * (ray.oy - q[1])) / dp2;
+    g_qp[2] = (nnum * ray.dz + ndp * (ray.oz - q[2])) / dp2;
+}
+
 __device__ __forceinline__ uint64_t fnv_step(uint64_t h, uint32_t cell) {
     return (h ^ (uint64_t)cell) * 0x100000001b3ull;
 }

@@ -373,30 +373,51 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
 // gets a face against the world origin (prev = 0) and the last two pending
 // gradients are never flushed -- all as the reference does.  Returns whether
 // a flush of (flush_idx, flush_g) is due.
+//
+// A step takes the face gradients of two faces: (prev, cur) as dprev and
+// dt0_cur, and (cur, next) as dt1_cur and dt1_next.  The second face of a
+// step is the first face of the next stepped step whenever that step's cell
+// is this step's next (the usual case: t1 > t0 at every step), so its two
+// gradients are kept (face_to, face_pq, face_qp) and the next step takes
+// them instead of forming them again: the same inputs, so the same bits.
 struct GeomState {
     uint32_t prev_idx;
     float prev_pt[3];
     float prev_g[3], cur_g[3], next_g[3];
+    uint32_t face_to;   // cell the kept face leads to (kNoIndex: none kept)
+    float face_pq[3];   // cell_isect_grad(prev_pt, x of face_to)
+    float face_qp[3];   // cell_isect_grad(x of face_to, prev_pt)
 };
 
 __device__ __forceinline__ void geom_init(GeomState &gs) {
     gs.prev_idx = kNoIndex;
+    gs.face_to = kNoIndex;
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         gs.prev_pt[i] = 0.0f;
         gs.prev_g[i] = gs.cur_g[i] = gs.next_g[i] = 0.0f;
+        gs.face_pq[i] = gs.face_qp[i] = 0.0f;
     }
 }
 
 __device__ __forceinline__ bool geom_step(GeomState &gs, uint32_t cell, const float *xc,
-                                          const float *xn, float dL_dt0, float dL_dt1,
-                                          const RayF &ray, uint32_t &flush_idx, float *flush_g) {
+                                          uint32_t next, const float *xn, float dL_dt0,
+                                          float dL_dt1, const RayF &ray, uint32_t &flush_idx,
+                                          float *flush_g) {
     float dprev[3] = {0.0f, 0.0f, 0.0f};
-    if (gs.prev_idx != kNoIndex) cell_isect_grad(gs.prev_pt, xc, ray, dprev);
     float dt1_cur[3], dt0_cur[3], dt1_next[3];
-    cell_isect_grad(xc, xn, ray, dt1_cur);
-    cell_isect_grad(xc, gs.prev_pt, ray, dt0_cur);
-    cell_isect_grad(xn, xc, ray, dt1_next);
+    if (gs.prev_idx != kNoIndex && cell == gs.face_to) {
+        // the previous step's (cur, next) face: prev_pt and xc are its points
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            dprev[i] = gs.face_pq[i];
+            dt0_cur[i] = gs.face_qp[i];
+        }
+    } else {
+        if (gs.prev_idx != kNoIndex) cell_isect_grad(gs.prev_pt, xc, ray, dprev);
+        cell_isect_grad(xc, gs.prev_pt, ray, dt0_cur);
+    }
+    cell_isect_grad_pair(xc, xn, ray, dt1_cur, dt1_next);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         gs.prev_g[i] = fmaf(dL_dt0, dprev[i], gs.prev_g[i]);
@@ -412,8 +433,11 @@ __device__ __forceinline__ bool geom_step(GeomState &gs, uint32_t cell, const fl
         gs.prev_g[i] = gs.cur_g[i];
         gs.cur_g[i] = gs.next_g[i];
         gs.next_g[i] = 0.0f;
+        gs.face_pq[i] = dt1_cur[i];
+        gs.face_qp[i] = dt1_next[i];
     }
     gs.prev_idx = cell;
+    gs.face_to = next;
     return flush;
 }
 
@@ -921,7 +945,7 @@ backward_sdf_kernel(BwdArgs a) {
                         }
                     }
                 }
-                flush = geom_step(gs, cell, ws.xc, si.xn, units - dL_ddelta, dL_ddelta, ray,
+                flush = geom_step(gs, cell, ws.xc, si.next, si.xn, units - dL_ddelta, dL_ddelta, ray,
                                   flush_idx, flush_g);
                 const float dphi_dd = -sha * phi * (1.0f - phi);
                 const float ds_dd = sha * (1.0f - 2.0f * phi) * dphi_dd;
@@ -1158,7 +1182,8 @@ backward_density_kernel(BwdArgs a) {
                     dL_ddt = fmaf(-s, cur_dg, dL_ddt);
                 }
                 dL_dt0 = dL_dt0 + -dL_ddt;
-                flush = geom_step(gs, cell, ws.xc, si.xn, dL_dt0, dL_ddt, ray, flush_idx, flush_g);
+                flush = geom_step(gs, cell, ws.xc, si.next, si.xn, dL_dt0, dL_ddt, ray, flush_idx,
+                                  flush_g);
                 dds = dL_ds;
                 if (r == 0.0f) dr = 0.0f;
                 if (g == 0.0f) dg = 0.0f;
