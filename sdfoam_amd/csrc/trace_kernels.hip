@@ -94,70 +94,74 @@ __device__ inline uint32_t record_claim(const WalkRecordArgs &r, uint32_t *tab, 
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)got);
 }
 
-// Groups of lanes per forward slot round.
-constexpr int kSlots = 16;
+// The forward's per-cell updates, `contribution[cell] += w` per step and
+// `alpha[cell] = a visiting step's alpha` (src/tracing/pipeline.cu:159-163;
+// the reference's alpha store is a last-writer race), go through a per-wave
+// hash table in LDS: a stepped lane claims its cell's slot by a
+// compare-and-swap of the slot's tag (equal cells share it, others probe
+// on), adds its weight there and stores its alpha, and every kContribTrips
+// trips each lane flushes kContribSlots / 64 slots: one contribution atomic
+// and one alpha store per distinct cell of those trips.  A flush follows at
+// most 64 * kContribTrips = kContribSlots claims, so a probe always ends at
+// its cell's slot or a free one.  The lanes' claims run side by side (a
+// serial round per distinct cell costs more), and one global atomic per step
+// costs far more (same-address adds serialise in L2).
+constexpr uint32_t kContribTrips = 4;
+constexpr uint32_t kContribSlots = 64 * kContribTrips;
+constexpr uint32_t kContribFree = 0xffffffffu;
 
-// Per-wave LDS slots of the forward's grouped contribution updates.
-struct FwdSlots {
-    float w[kSlots];
-    float alpha[kSlots];
+struct ContribTable {
+    uint32_t tag[kContribSlots];
+    float w[kContribSlots];
+    float alpha[kContribSlots];
 };
 
-// A lane's step for the contribution updates: its cell, weight and alpha.
-struct FwdEntry {
-    uint32_t cell;
-    float w, alpha;
-    bool valid;
-};
-
-// Contribution updates of two entries per lane (all 64 lanes active):
-// `contribution[cell] += sum of the weights` and `alpha[cell] = one entry's
-// alpha` (the reference's last-writer store, src/tracing/pipeline.cu:159-163)
-// for every distinct cell among the entries.  Up to kSlots cells per round:
-// the entries of group k add their weights into LDS slot k (ds_add), then
-// lane k issues group k's contribution atomic and alpha store.  The pending
-// entries stay per-lane predicates (scalar lane masks) and each group costs
-// one compare per entry.
-template <typename AT>
-__device__ __forceinline__ void contribution_pass(FwdSlots &fs, const FwdEntry &ea,
-                                                  const FwdEntry &eb, void *contribution,
-                                                  float *alpha_out) {
+__device__ __forceinline__ void contrib_clear(ContribTable &ct) {
     const uint32_t lane = lane_id();
-    bool pa = ea.valid, pb = eb.valid;
-    uint64_t ta = lane_mask(pa), tb = lane_mask(pb);
-    while (ta | tb) {
-        int n = 0, sa = -1, sb = -1;
-        uint32_t cells = 0u;
-        while ((ta | tb) && n < kSlots) {
-            const uint32_t c =
-                ta ? readlane_u(ea.cell, first_lane(ta)) : readlane_u(eb.cell, first_lane(tb));
-            const bool qa = ea.cell == c, qb = eb.cell == c;
-            if (pa && qa) sa = n;
-            if (pb && qb) sb = n;
-            pa = pa && !qa;
-            pb = pb && !qb;
-            ta &= ~lane_mask(qa);
-            tb &= ~lane_mask(qb);
-            if (lane == (uint32_t)n) cells = c;
-            ++n;
-        }
-        if (sa >= 0) {
-            atomicAdd(fs.w + sa, ea.w);
-            fs.alpha[sa] = ea.alpha;
-        }
-        if (sb >= 0) {
-            atomicAdd(fs.w + sb, eb.w);
-            fs.alpha[sb] = eb.alpha;
-        }
-        __builtin_amdgcn_wave_barrier();
-        if ((int)lane < n) {
-            const float sum = fs.w[lane];
-            fs.w[lane] = 0.0f;
-            if (contribution) atomic_add_elem<AT>(contribution, cells, sum);
-            if (alpha_out) alpha_out[cells] = fs.alpha[lane];
-        }
-        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (uint32_t k = 0; k < kContribSlots / 64; ++k) {
+        ct.tag[lane + 64u * k] = kContribFree;
+        ct.w[lane + 64u * k] = 0.0f;
     }
+    __builtin_amdgcn_wave_barrier();
+}
+
+// One lane's step (any subset of the wave's lanes).
+template <typename AT>
+__device__ __forceinline__ void contrib_add(ContribTable &ct, uint32_t cell, float w, float alpha,
+                                            void *contribution) {
+    uint32_t h = (cell * 0x9e3779b1u) >> 24; // 8 bits: kContribSlots == 256
+    for (uint32_t probe = 0; probe < kContribSlots; ++probe) {
+        const uint32_t old = atomicCAS(&ct.tag[h], kContribFree, cell);
+        if (old == kContribFree || old == cell) {
+            atomicAdd(&ct.w[h], w);
+            ct.alpha[h] = alpha;
+            return;
+        }
+        h = (h + 1u) & (kContribSlots - 1u);
+    }
+    // not reached: the table has room for every claim between flushes
+    if (contribution) atomic_add_elem<AT>(contribution, cell, w);
+}
+
+// The wave's pending sums (all 64 lanes).
+template <typename AT>
+__device__ __forceinline__ void contrib_flush(ContribTable &ct, void *contribution, float *alpha_out) {
+    __builtin_amdgcn_wave_barrier();
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (uint32_t k = 0; k < kContribSlots / 64; ++k) {
+        const uint32_t s = lane + 64u * k;
+        const uint32_t c = ct.tag[s];
+        if (c != kContribFree) {
+            const float v = ct.w[s];
+            ct.tag[s] = kContribFree;
+            ct.w[s] = 0.0f;
+            if (contribution) atomic_add_elem<AT>(contribution, c, v);
+            if (alpha_out) alpha_out[c] = ct.alpha[s];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
 }
 
 // ---------------------------------------------------------------------------
@@ -171,10 +175,9 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     constexpr int D = 1 + 3 * nsh;
     // SH basis of each lane's ray, in LDS (frees nsh VGPRs)
     __shared__ float sh_all[kBlock * nsh];
-    __shared__ FwdSlots fwd_slots[STATS ? 1 : kBlock / 64];
-    if constexpr (!STATS) {
-        if ((threadIdx.x & 63u) < (uint32_t)kSlots) fwd_slots[threadIdx.x >> 6].w[threadIdx.x & 63u] = 0.0f;
-    }
+    __shared__ ContribTable contrib_tables[STATS ? 1 : kBlock / 64];
+    ContribTable &ct = contrib_tables[STATS ? 0 : threadIdx.x >> 6];
+    if constexpr (!STATS) contrib_clear(ct);
     bool valid;
     const uint32_t ray_idx =
         ray_for_lane<kForwardChunk>(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid,
@@ -215,7 +218,6 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     uint64_t wslot = ~0ull;
     if (!STATS && a.record.entries) wtab = walk_record_table<kForwardChunk>(a.record);
     uint32_t trip = 0;
-    FwdEntry held = {0u, 0.0f, 0.0f, false}; // step waiting for the next contribution pass
 
     while (__ballot(ws.alive) != 0ull) {
         StepInfo si;
@@ -318,19 +320,12 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         }
 
         if constexpr (!STATS) {
-            // per cell: contribution += sum of the weights, alpha = one
-            // visiting step's alpha; a step waits one trip in `held` so each
-            // pass covers two trips (fewer distinct cells than two passes)
-            if (a.contribution || a.alpha_out) {
-                const FwdEntry cur = {ws.cell, w, alpha, si.stepped};
-                if (trip % 2u == 0u) {
-                    contribution_pass<AT>(fwd_slots[threadIdx.x >> 6], held, cur, a.contribution,
-                                          a.alpha_out);
-                    held.valid = false;
-                } else {
-                    held = cur;
-                }
-            }
+            // per cell: contribution += the weights, alpha = a visiting
+            // step's alpha, through the wave's table
+            if (si.stepped && (a.contribution || a.alpha_out))
+                contrib_add<AT>(ct, ws.cell, w, alpha, a.contribution);
+            if ((a.contribution || a.alpha_out) && trip % kContribTrips == 0u)
+                contrib_flush<AT>(ct, a.contribution, a.alpha_out);
         }
         if (si.stepped && !keep) ws.alive = false;
         if (ws.alive && si.found) walk_move(ws, si);
@@ -342,11 +337,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         record_store(a.record.entries + wslot + (trip % kChunkTrips) * 64u,
                      make_uint2(kWalkUnrecorded, 0u));
     if constexpr (!STATS) {
-        if (a.contribution || a.alpha_out) {
-            const FwdEntry none = {0u, 0.0f, 0.0f, false};
-            contribution_pass<AT>(fwd_slots[threadIdx.x >> 6], held, none, a.contribution,
-                                  a.alpha_out);
-        }
+        if (a.contribution || a.alpha_out) contrib_flush<AT>(ct, a.contribution, a.alpha_out);
     }
 
     if (!valid) return;
