@@ -535,6 +535,9 @@ def triangulate_bench(args, dev) -> int:
                      "open_points_qhull": float(np.mean([s["open_points_qhull_s"] for s in stats])),
                      "merge": float(np.mean([s["merge_s"] for s in stats]))},
         "open_points": last["open"],
+        "open_levels": last.get("open_levels", []),
+        "qhull_points": last.get("open_points_qhull"),
+        "open_phase_s": {"levels": last.get("open_levels_s"), "qhull": last.get("open_qhull_s")},
         "roofline": {"kernel": "certify_kernel", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": load_traffic(f"traffic_certify_C{args.config}.json")},

@@ -165,11 +165,98 @@ class _Undecided(RuntimeError):
     """The GPU tetrahedralisation met a sign it could not decide."""
 
 
+def _certify(L, pts: torch.Tensor, gptr: int, gbytes: int, stream):
+    """sdf_delaunay_certify over CUDA float32 points [n, 3]: (reports [nr, 4]
+    int32 rows (point, a, b, c), open points [nu] int32 in index order,
+    counts).  Raises _Undecided where the GPU cannot decide."""
+    dev = pts.device
+    n = pts.numel() // 3
+    open_pts = torch.empty(n, dtype=torch.int32, device=dev)
+    counts = (C.c_uint64 * 5)()
+    cap = 28 * n + 4096
+    for _ in range(2):
+        reports = torch.empty((cap, 4), dtype=torch.int32, device=dev)
+        rc = L.sdf_delaunay_certify(ptr(pts), n, ptr(reports), cap, ptr(open_pts), counts, gptr,
+                                    gbytes, stream)
+        if rc == _lib.SDF_E_INVALID:
+            # no volume or non-finite points: Qhull on every point decides
+            raise _Undecided(L.sdf_last_error().decode())
+        check(rc)
+        if counts[0] <= cap:
+            break
+        cap = int(counts[0])
+    if counts[4]:
+        raise TriangulationFailedError("duplicate points found")
+    nr, nu = int(counts[0]), int(counts[1])
+    return reports[:nr], torch.sort(open_pts[:nu])[0], counts
+
+
+# Open points are certified again among themselves while at least 256 of them
+# remain and a level leaves at most this share of them open (a level costs a
+# few ms; at C3 the first one halves the open points, a second one takes
+# little more).
+_LEVEL_SHRINK = 0.7
+
+
+def _open_candidates(L, pts: torch.Tensor, U: torch.Tensor, stream, stats: dict):
+    """Candidate tetrahedra [m, 4] (global indices, int32 on the points'
+    device) for the Delaunay tetrahedra of `pts` whose four vertices are all
+    in the open set U, and the hull's face count.  Such a tetrahedron's
+    circumsphere holds no point of U either, so it is one of U's own Delaunay
+    tetrahedra: of those, the ones with a vertex whose cell certifies among U
+    alone come from that certification, the rest have four vertices open
+    again and come from the next level; the last level's open points go
+    through Qhull on the host.  Every level's tetrahedra are candidates (the
+    merge keeps a candidate only if no point of `pts` lies in its
+    circumsphere), and the hull points stay open at every level, so Qhull's
+    hull is the whole set's."""
+    parts = []
+    t = time.perf_counter()
+    while U.numel() >= 256:
+        sub = pts[U.long()].contiguous()
+        gb = int(L.sdf_delaunay_certify_scratch_bytes(U.numel()))
+        if gb == 0:
+            break
+        gbuf, gp = _aligned(gb, pts.device)
+        try:
+            rep, U2, _ = _certify(L, sub, gp, gb, stream)
+        except (_Undecided, TriangulationFailedError):
+            break
+        del gbuf
+        if U2.numel() > _LEVEL_SHRINK * U.numel():
+            break
+        if rep.shape[0]:
+            parts.append(U[rep.long()])
+        stats.setdefault("open_levels", []).append(int(U2.numel()))
+        U = U[U2.long()]
+    t_levels = time.perf_counter()
+    u_np = U.cpu().numpy()
+    try:
+        simplices, nbr_u = qhull_tetrahedra(pts[U.long()].cpu().numpy())
+    except TriangulationFailedError as e:
+        # a degenerate open subset: Qhull on every point decides
+        raise _Undecided(str(e)) from None
+    t_qhull = time.perf_counter()
+    stats["open_points_qhull"] = int(u_np.size)
+    q = torch.from_numpy(np.ascontiguousarray(u_np[simplices], dtype=np.int32)).to(pts.device)
+    if parts:
+        # a tetrahedron comes once from each of its certified vertices and
+        # possibly from Qhull as well
+        cand = torch.cat(parts + [q])
+        cand = torch.unique(torch.sort(cand, dim=1)[0], dim=0)
+    else:
+        cand = q
+    stats["open_levels_s"] = t_levels - t
+    stats["open_qhull_s"] = t_qhull - t_levels
+    return cand.to(torch.int32).contiguous(), int((nbr_u < 0).sum())
+
+
 def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, dict]:
     """Delaunay tetrahedra of CUDA float32 points [N, 3] by certified
     Voronoi cells (sdf_delaunay_certify / sdf_delaunay_merge): the points
     whose cells the GPU cannot certify (the hull and the layer under it) are
-    triangulated by Qhull on the host, and their tetrahedra kept where no
+    certified again among themselves, and what stays open at the last level
+    is triangulated by Qhull on the host; their tetrahedra are kept where no
     point lies in the circumsphere.  Returns (tets [T, 4] int32, neighbors
     [T, 4] int32, -1 on the hull, stats) on the points' device."""
     pts = points.contiguous()
@@ -181,36 +268,13 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
     if gbytes == 0:
         raise RuntimeError("sdf_delaunay_certify_scratch_bytes failed")
     gbuf, gptr = _aligned(gbytes, dev)
-    open_pts = torch.empty(n, dtype=torch.int32, device=dev)
-    counts = (C.c_uint64 * 5)()
-    cap = 28 * n + 4096
+    stats = {}
     t0 = time.perf_counter()
     with torch.cuda.device(dev):
-        for _ in range(2):
-            reports = torch.empty((cap, 4), dtype=torch.int32, device=dev)
-            rc = L.sdf_delaunay_certify(ptr(pts), n, ptr(reports), cap, ptr(open_pts), counts,
-                                        gptr, gbytes, stream)
-            if rc == _lib.SDF_E_INVALID:
-                # no volume or non-finite points: Qhull on every point decides
-                raise _Undecided(L.sdf_last_error().decode())
-            check(rc)
-            if counts[0] <= cap:
-                break
-            cap = int(counts[0])
-        nr, nu = int(counts[0]), int(counts[1])
-        if counts[4]:
-            raise TriangulationFailedError("duplicate points found")
+        reports, U, counts = _certify(L, pts, gptr, gbytes, stream)
+        nr, nu = int(reports.shape[0]), int(U.numel())
         t1 = time.perf_counter()
-        # the open points, in index order, through Qhull on the host
-        U = torch.sort(open_pts[:nu])[0]
-        u_np = U.cpu().numpy()
-        try:
-            simplices, nbr_u = qhull_tetrahedra(pts[U.long()].cpu().numpy())
-        except TriangulationFailedError as e:
-            # a degenerate open subset: Qhull on every point decides
-            raise _Undecided(str(e)) from None
-        hull_faces = int((nbr_u < 0).sum())
-        cand = torch.from_numpy(np.ascontiguousarray(u_np[simplices], dtype=np.int32)).to(dev)
+        cand, hull_faces = _open_candidates(L, pts, U, stream, stats)
         m = int(cand.shape[0])
         t2 = time.perf_counter()
         result = (C.c_uint64 * 4)()
@@ -239,9 +303,9 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
     if int(result[1]) != hull_faces:
         raise _Undecided(f"{int(result[1])} faces without a neighbour, the hull has {hull_faces}")
     t3 = time.perf_counter()
-    stats = {"open": nu, "reports": nr, "candidates": m, "tets": T,
-             "undecided_cells": int(counts[2]), "overflow_cells": int(counts[3]),
-             "certify_s": t1 - t0, "open_points_qhull_s": t2 - t1, "merge_s": t3 - t2}
+    stats.update({"open": nu, "reports": nr, "candidates": m, "tets": T,
+                  "undecided_cells": int(counts[2]), "overflow_cells": int(counts[3]),
+                  "certify_s": t1 - t0, "open_points_qhull_s": t2 - t1, "merge_s": t3 - t2})
     return tets[:T], nbr[:T], stats
 
 
