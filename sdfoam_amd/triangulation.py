@@ -191,10 +191,10 @@ def _certify(L, pts: torch.Tensor, gptr: int, gbytes: int, stream):
     return reports[:nr], torch.sort(open_pts[:nu])[0], counts
 
 
-# Open points are certified again among themselves while at least 256 of them
-# remain and a level leaves at most this share of them open (a level costs a
-# few ms; at C3 the first one halves the open points, a second one takes
-# little more).
+# The open points are certified once more among themselves when there are at
+# least 256 of them, and that level's stars are used when it leaves at most
+# this share of them open (at C3 it halves them in a few ms; a further level
+# would remove another ~12% only, for about the same time again).
 _LEVEL_SHRINK = 0.7
 
 
@@ -204,31 +204,26 @@ def _open_candidates(L, pts: torch.Tensor, U: torch.Tensor, stream, stats: dict)
     in the open set U, and the hull's face count.  Such a tetrahedron's
     circumsphere holds no point of U either, so it is one of U's own Delaunay
     tetrahedra: of those, the ones with a vertex whose cell certifies among U
-    alone come from that certification, the rest have four vertices open
-    again and come from the next level; the last level's open points go
-    through Qhull on the host.  Every level's tetrahedra are candidates (the
-    merge keeps a candidate only if no point of `pts` lies in its
-    circumsphere), and the hull points stay open at every level, so Qhull's
+    alone come from that certification, and the rest have four vertices that
+    stay open there and come from Qhull on those on the host.  All of these
+    are candidates (the merge keeps a candidate only if no point of `pts`
+    lies in its circumsphere), and the hull points stay open, so Qhull's
     hull is the whole set's."""
     parts = []
     t = time.perf_counter()
-    while U.numel() >= 256:
-        sub = pts[U.long()].contiguous()
-        gb = int(L.sdf_delaunay_certify_scratch_bytes(U.numel()))
-        if gb == 0:
-            break
+    gb = int(L.sdf_delaunay_certify_scratch_bytes(U.numel())) if U.numel() >= 256 else 0
+    if gb:
         gbuf, gp = _aligned(gb, pts.device)
         try:
-            rep, U2, _ = _certify(L, sub, gp, gb, stream)
+            rep, U2, _ = _certify(L, pts[U.long()].contiguous(), gp, gb, stream)
         except (_Undecided, TriangulationFailedError):
-            break
+            rep = None
         del gbuf
-        if U2.numel() > _LEVEL_SHRINK * U.numel():
-            break
-        if rep.shape[0]:
-            parts.append(U[rep.long()])
-        stats.setdefault("open_levels", []).append(int(U2.numel()))
-        U = U[U2.long()]
+        if rep is not None and U2.numel() <= _LEVEL_SHRINK * U.numel():
+            if rep.shape[0]:
+                parts.append(U[rep.long()])
+            stats["open_levels"] = [int(U2.numel())]
+            U = U[U2.long()]
     t_levels = time.perf_counter()
     u_np = U.cpu().numpy()
     try:
