@@ -253,6 +253,24 @@ __device__ __forceinline__ void sh_rgb(const float *sh, int sh_stride, const AT 
     b = fmaxf(a2, 0.0f);
 }
 
+// sh_rgb with the basis in registers (sh[j], fully unrolled): the same fused
+// products in the same order per channel, so the same bits.
+template <int L, typename AT>
+__device__ __forceinline__ void sh_rgb_regs(const float *sh, const AT *__restrict__ row, float &r,
+                                            float &g, float &b) {
+    constexpr int nsh = (L + 1) * (L + 1);
+    float a0 = 0.5f, a1 = 0.5f, a2 = 0.5f;
+#pragma unroll
+    for (int j = 0; j < nsh; ++j) {
+        a0 = fmaf(sh[j], (float)row[3 * j + 0], a0);
+        a1 = fmaf(sh[j], (float)row[3 * j + 1], a1);
+        a2 = fmaf(sh[j], (float)row[3 * j + 2], a2);
+    }
+    r = fmaxf(a0, 0.0f);
+    g = fmaxf(a1, 0.0f);
+    b = fmaxf(a2, 0.0f);
+}
+
 // Cell table (optional; the forward builds it from the caller's arrays before
 // it walks): one record per cell holding what a step of the forward reads of
 // that cell: words 0-2 the position (fp32 bits), word 3 the CSR row begin,

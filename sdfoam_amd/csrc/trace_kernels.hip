@@ -173,8 +173,6 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     constexpr uint32_t RB = CT ? cell_record_bytes(L, sizeof(AT)) : 0u;
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
-    // SH basis of each lane's ray, in LDS (frees nsh VGPRs)
-    __shared__ float sh_all[kBlock * nsh];
     __shared__ ContribTable contrib_tables[STATS ? 1 : kBlock / 64];
     ContribTable &ct = contrib_tables[STATS ? 0 : threadIdx.x >> 6];
     if constexpr (!STATS) contrib_clear(ct);
@@ -186,13 +184,11 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
 
     RayF ray = {};
     if (valid) ray = load_ray(a.rays, ray_idx);
-    float *sh = sh_all + threadIdx.x; // basis function k at sh[k * kBlock]
-    {
-        float sh0[nsh];
-        sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
-#pragma unroll
-        for (int k = 0; k < nsh; ++k) sh[k * kBlock] = sh0[k];
-    }
+    // SH basis of the lane's ray, in registers (the kernel's LDS goes to the
+    // contribution table; in LDS the basis cost 16 reads per step and
+    // limited the blocks per CU)
+    float sh[nsh];
+    sh_basis<L>(ray.dx, ray.dy, ray.dz, sh);
     const float sha = a.sharpness[0];
     const int32_t sdf_ch = a.settings.sdf_channel;
     const bool neus_alpha = NEUS && sdf_ch >= 0;
@@ -281,7 +277,7 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
             if constexpr (!STATS) {
                 float r, g, b;
                 if (NEUS || (float)row[D - 1] > 1e-6f) {
-                    sh_rgb<L>(sh, kBlock, row, r, g, b);
+                    sh_rgb_regs<L>(sh, row, r, g, b);
                 } else {
                     r = g = b = 0.0f;
                 }
