@@ -419,11 +419,12 @@ def trace_benchmark(sh_degree, points, attributes, adjacency, offsets, adjacent_
 
 def _mix32(x: np.ndarray) -> np.ndarray:
     """The reference's 32-bit integer hash (src/utils/random.h:11-20,
-    C. Wellons' hash-prospector "triple32").  Parity unpinned for its
-    constants: the reference's header cannot be built here (it includes
-    cuda_fp16.h) and no published output vectors are at hand, so the tests
-    pin only what the constants do not decide (0 -> 0, uniform rows, rows
-    depending on position alone); a wrong multiplier or shift would pass."""
+    C. Wellons' hash-prospector "triple32").  Pinned by the inverse that
+    hash-prospector publishes beside it (other multipliers: the inverses of
+    these modulo 2^32): composed with it the hash gives back every input
+    tried, which a multiplier or shift off by one step does not.  The
+    reference's header itself cannot be built here (it includes
+    cuda_fp16.h)."""
     x = x.astype(np.uint32)
     with np.errstate(over="ignore"):
         x ^= x >> np.uint32(17)
