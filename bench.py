@@ -130,6 +130,10 @@ def main() -> int:
                     help="time Triangulation.rebuild (sort, GPU Delaunay with Qhull on the "
                          "open points, tables) on C3's 1M points, with Qhull on every point "
                          "beside it")
+    ap.add_argument("--perturb", type=float, default=0.02,
+                    help="--triangulate: the incremental rebuilds move each point by this "
+                         "share of its cell radius (farthest Delaunay neighbour) times N(0, 1) "
+                         "per coordinate")
     ap.add_argument("--render", action="store_true",
                     help="time the inference render (Pipeline.trace_benchmark, the reference's "
                          "benchmark.py) on the config's camera instead of the training step")
@@ -510,7 +514,29 @@ def triangulate_bench(args, dev) -> int:
         raise RuntimeError("the GPU tetrahedralisation fell back to Qhull")
     last = stats[-1]
     certify = float(np.mean([s["certify_s"] for s in stats]))
-    sorted_pts = pts[tri.permutation().view(torch.int32).long()].cpu().numpy()
+    # incremental rebuilds (the reference's rebuild(points, true) between
+    # full ones): the sorted points moved by --perturb of their cell radius
+    base = pts[tri.permutation().view(torch.int32).long()].contiguous()
+    _, radius = sdfoam_amd.farthest_neighbor(base, tri.point_adjacency(),
+                                             tri.point_adjacency_offsets())
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    inc = []
+    for i in range(args.warmup + args.steps):
+        moved = base + args.perturb * radius[:, None] * torch.randn(
+            base.shape, generator=gen, device=dev)
+        if i == args.warmup:
+            torch.cuda.synchronize()
+            t_inc = time.perf_counter()
+        tri.rebuild(moved, incremental=True)
+        if i >= args.warmup:
+            inc.append(tri.last_stats)
+    torch.cuda.synchronize()
+    dt_inc = (time.perf_counter() - t_inc) / args.steps
+    if tri.last_method != "gpu":
+        raise RuntimeError("the GPU tetrahedralisation fell back to Qhull")
+    inc_done = [s for s in inc if s.get("incremental")]
+    sorted_pts = base.cpu().numpy()
     tq = time.perf_counter()
     qhull_tetrahedra(sorted_pts)
     t_qhull = time.perf_counter() - tq
@@ -538,6 +564,16 @@ def triangulate_bench(args, dev) -> int:
         "open_levels": last.get("open_levels", []),
         "qhull_points": last.get("open_points_qhull"),
         "open_phase_s": {"levels": last.get("open_levels_s"), "qhull": last.get("open_qhull_s")},
+        "incremental": {
+            "ms_per_rebuild": dt_inc * 1e3, "perturb": args.perturb,
+            "rebuilds": len(inc), "incremental": len(inc_done),
+            "fallback": [s["incremental_fallback"] for s in inc if "incremental_fallback" in s][:1],
+            "dirty_points": int(np.mean([s["dirty"] for s in inc_done])) if inc_done else None,
+            "kept_old_tets": int(np.mean([s["kept_old"] for s in inc_done])) if inc_done else None,
+            "open_points": int(np.mean([s["open"] for s in inc_done])) if inc_done else None,
+            "phases_s": {k: float(np.mean([s[k + "_s"] for s in inc_done]))
+                         for k in ("check", "certify", "open_points_qhull", "merge")}
+            if inc_done else None},
         "roofline": {"kernel": "certify_kernel", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": load_traffic(f"traffic_certify_C{args.config}.json")},

@@ -483,6 +483,53 @@ int sdf_delaunay_merge(const float *points, uint32_t num_points,
                        uint64_t *result, void *scratch, size_t scratch_bytes,
                        void *stream);
 
+/* Incremental rebuild over moved points, the same tetrahedra count
+ * (replaces delete_delaunay_violations, src/delaunay/delete_violations.cu:
+ * 7-178, and the regrowth from its frontier, src/delaunay/delaunay.cu:
+ * 288-345).
+ *
+ * sdf_delaunay_check: the grid over the moved points into certify_scratch
+ * (sdf_delaunay_certify_scratch_bytes), then each old tetrahedron [T, 4]
+ * (neighbors [T, 4], -1 on the hull, as sdf_delaunay_merge writes them):
+ * keep[t] = 1 when no point lies strictly inside its circumsphere (every
+ * sign decided), else 0.  dirty[N] = 1 for the vertices of tetrahedra not
+ * kept and of hull faces, else 0.  A tetrahedron with a clean vertex is a
+ * Delaunay tetrahedron of the moved points exactly when it is one of the
+ * kept old ones; the others all have four dirty vertices.  Fails on a
+ * vertex id >= N.  Synchronizes the stream. */
+int sdf_delaunay_check(const float *points, uint32_t num_points,
+                       const uint32_t *tets, const int32_t *neighbors,
+                       uint64_t num_tets, uint32_t *keep, uint32_t *dirty,
+                       void *certify_scratch, size_t certify_scratch_bytes,
+                       void *stream);
+
+/* sdf_delaunay_certify_points: sdf_delaunay_certify for the listed points
+ * only (query [Q], ids below N; reports, open_points and counts as there),
+ * on the grid an sdf_delaunay_check call over the same points left in the
+ * scratch; the other points count as clean.  Then sdf_delaunay_merge_verified
+ * merges its reports, the open points' candidates and the kept old
+ * tetrahedra that have a clean vertex and no certified one.
+ * Synchronizes the stream. */
+int sdf_delaunay_certify_points(const float *points, uint32_t num_points,
+                                const uint32_t *query, uint32_t num_query,
+                                uint32_t *reports, uint64_t report_capacity,
+                                uint32_t *open_points, uint64_t *counts,
+                                void *certify_scratch, size_t certify_scratch_bytes,
+                                void *stream);
+
+/* sdf_delaunay_merge with verified rows [V, 4] kept as they are (their
+ * circumspheres already checked).  scratch:
+ * sdf_delaunay_merge_scratch_bytes(N, num_reports, num_candidates + V,
+ * tet_capacity). */
+int sdf_delaunay_merge_verified(const float *points, uint32_t num_points,
+                                void *certify_scratch, size_t certify_scratch_bytes,
+                                const uint32_t *reports, uint64_t num_reports,
+                                const uint32_t *candidates, uint64_t num_candidates,
+                                const uint32_t *verified, uint64_t num_verified,
+                                uint32_t *tets, int32_t *neighbors, uint64_t tet_capacity,
+                                uint64_t *result, void *scratch, size_t scratch_bytes,
+                                void *stream);
+
 /* ---- measurement and test hooks (no counterpart in the reference) ----- */
 
 /* Per-ray walk statistics of the forward (backward = 0) or backward

@@ -58,6 +58,9 @@ EXPORTS = (
     "sdf_delaunay_certify",
     "sdf_delaunay_merge_scratch_bytes",
     "sdf_delaunay_merge",
+    "sdf_delaunay_check",
+    "sdf_delaunay_certify_points",
+    "sdf_delaunay_merge_verified",
     "sdf_nn",
     "sdf_trace_walk_stats",
     "sdf_debug_fpmath",
@@ -227,6 +230,13 @@ def lib() -> C.CDLL:
     L.sdf_delaunay_merge.restype = C.c_int
     L.sdf_delaunay_merge.argtypes = [P, U32, P, SZ, P, C.c_uint64, P, C.c_uint64, P, P,
                                      C.c_uint64, P, P, SZ, P]
+    L.sdf_delaunay_check.restype = C.c_int
+    L.sdf_delaunay_check.argtypes = [P, U32, P, P, C.c_uint64, P, P, P, SZ, P]
+    L.sdf_delaunay_certify_points.restype = C.c_int
+    L.sdf_delaunay_certify_points.argtypes = [P, U32, P, U32, P, C.c_uint64, P, P, P, SZ, P]
+    L.sdf_delaunay_merge_verified.restype = C.c_int
+    L.sdf_delaunay_merge_verified.argtypes = [P, U32, P, SZ, P, C.c_uint64, P, C.c_uint64, P,
+                                              C.c_uint64, P, P, C.c_uint64, P, P, SZ, P]
     L.sdf_nn.restype = C.c_int
     L.sdf_nn.argtypes = [P, P, P, U32, U32, P, P]
     L.sdf_trace_walk_stats.restype = C.c_int

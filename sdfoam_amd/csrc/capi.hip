@@ -754,28 +754,30 @@ size_t sdf_delaunay_merge_scratch_bytes(uint32_t num_points, uint64_t num_report
     return delaunay_merge_scratch_bytes(num_points, num_reports, num_candidates, tet_capacity);
 }
 
-int sdf_delaunay_merge(const float *points, uint32_t num_points, void *certify_scratch,
-                       size_t certify_scratch_bytes, const uint32_t *reports,
-                       uint64_t num_reports, const uint32_t *candidates, uint64_t num_candidates,
-                       uint32_t *tets, int32_t *neighbors, uint64_t tet_capacity,
-                       uint64_t *result, void *scratch, size_t scratch_bytes, void *stream) {
+static int delaunay_merge_common(const char *name, const float *points, uint32_t num_points,
+                                 void *certify_scratch, size_t certify_scratch_bytes,
+                                 const uint32_t *reports, uint64_t num_reports,
+                                 const uint32_t *candidates, uint64_t num_candidates,
+                                 const uint32_t *verified, uint64_t num_verified, uint32_t *tets,
+                                 int32_t *neighbors, uint64_t tet_capacity, uint64_t *result,
+                                 void *scratch, size_t scratch_bytes, void *stream) {
     if (!points || !certify_scratch || !result || !scratch || (num_reports > 0 && !reports) ||
-        (num_candidates > 0 && !candidates) || (tet_capacity > 0 && (!tets || !neighbors)))
+        (num_candidates > 0 && !candidates) || (num_verified > 0 && !verified) ||
+        (tet_capacity > 0 && (!tets || !neighbors)))
         return fail(SDF_E_INVALID, "NULL pointer argument");
     if ((reinterpret_cast<uintptr_t>(scratch) & 255u) != 0 ||
         (reinterpret_cast<uintptr_t>(certify_scratch) & 255u) != 0)
         return fail(SDF_E_INVALID, "scratch must be 256-byte aligned");
     if (num_points < 32)
         return fail(SDF_E_INVALID, "Delaunay triangulation does not support less than 32 points");
-    if (num_reports + num_candidates >= 0xffffffffull)
+    if (num_reports + num_candidates + num_verified >= 0xffffffffull)
         return fail(SDF_E_INVALID, "too many reports and candidates");
     if (num_points > (1u << 26) || num_candidates > (1ull << 26))
-        return fail(SDF_E_INVALID, "sdf_delaunay_merge takes at most 2^26 points and candidates");
+        return fail(SDF_E_INVALID, "%s takes at most 2^26 points and candidates", name);
     const size_t gneed = delaunay_certify_scratch_bytes(num_points);
-    const size_t need =
-        delaunay_merge_scratch_bytes(num_points, num_reports, num_candidates, tet_capacity);
-    if (gneed == 0 || need == 0)
-        return fail(SDF_E_HIP, "delaunay_merge: no device to size the scans for");
+    const size_t need = delaunay_merge_scratch_bytes(num_points, num_reports,
+                                                     num_candidates + num_verified, tet_capacity);
+    if (gneed == 0 || need == 0) return fail(SDF_E_HIP, "%s: no device to size the scans for", name);
     if (certify_scratch_bytes < gneed)
         return fail(SDF_E_INVALID, "certify_scratch must hold %zu bytes (got %zu)", gneed,
                     certify_scratch_bytes);
@@ -783,10 +785,10 @@ int sdf_delaunay_merge(const float *points, uint32_t num_points, void *certify_s
         return fail(SDF_E_INVALID, "scratch must hold %zu bytes (got %zu)", need, scratch_bytes);
     hipError_t e = launch_delaunay_merge(points, num_points, certify_scratch,
                                          certify_scratch_bytes, reports, num_reports, candidates,
-                                         num_candidates, tets, neighbors, tet_capacity, result,
-                                         scratch, scratch_bytes,
+                                         num_candidates, verified, num_verified, tets, neighbors,
+                                         tet_capacity, result, scratch, scratch_bytes,
                                          static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return hip_fail(e, "delaunay_merge");
+    if (e != hipSuccess) return hip_fail(e, name);
     if (result[2] != 0)
         return fail(SDF_E_INVALID, "%llu reports or candidates were invalid or undecided",
                     (unsigned long long)result[2]);
@@ -796,6 +798,89 @@ int sdf_delaunay_merge(const float *points, uint32_t num_points, void *certify_s
     if (result[3] != 0)
         return fail(SDF_E_INVALID, "%llu faces are shared by more than two tets",
                     (unsigned long long)result[3]);
+    return SDF_OK;
+}
+
+int sdf_delaunay_merge(const float *points, uint32_t num_points, void *certify_scratch,
+                       size_t certify_scratch_bytes, const uint32_t *reports,
+                       uint64_t num_reports, const uint32_t *candidates, uint64_t num_candidates,
+                       uint32_t *tets, int32_t *neighbors, uint64_t tet_capacity,
+                       uint64_t *result, void *scratch, size_t scratch_bytes, void *stream) {
+    return delaunay_merge_common("delaunay_merge", points, num_points, certify_scratch,
+                                 certify_scratch_bytes, reports, num_reports, candidates,
+                                 num_candidates, nullptr, 0, tets, neighbors, tet_capacity, result,
+                                 scratch, scratch_bytes, stream);
+}
+
+int sdf_delaunay_merge_verified(const float *points, uint32_t num_points, void *certify_scratch,
+                                size_t certify_scratch_bytes, const uint32_t *reports,
+                                uint64_t num_reports, const uint32_t *candidates,
+                                uint64_t num_candidates, const uint32_t *verified,
+                                uint64_t num_verified, uint32_t *tets, int32_t *neighbors,
+                                uint64_t tet_capacity, uint64_t *result, void *scratch,
+                                size_t scratch_bytes, void *stream) {
+    return delaunay_merge_common("delaunay_merge_verified", points, num_points, certify_scratch,
+                                 certify_scratch_bytes, reports, num_reports, candidates,
+                                 num_candidates, verified, num_verified, tets, neighbors,
+                                 tet_capacity, result, scratch, scratch_bytes, stream);
+}
+
+static int delaunay_scratch_ok(const char *name, uint32_t num_points, const void *scratch,
+                               size_t scratch_bytes) {
+    if ((reinterpret_cast<uintptr_t>(scratch) & 255u) != 0)
+        return fail(SDF_E_INVALID, "scratch must be 256-byte aligned");
+    if (num_points < 32)
+        return fail(SDF_E_INVALID, "Delaunay triangulation does not support less than 32 points");
+    if (num_points > (1u << 26)) return fail(SDF_E_INVALID, "%s takes at most 2^26 points", name);
+    const size_t need = delaunay_certify_scratch_bytes(num_points);
+    if (need == 0) return fail(SDF_E_HIP, "%s: no device to size the sorts for", name);
+    if (scratch_bytes < need)
+        return fail(SDF_E_INVALID, "scratch must hold %zu bytes (got %zu)", need, scratch_bytes);
+    return SDF_OK;
+}
+
+int sdf_delaunay_check(const float *points, uint32_t num_points, const uint32_t *tets,
+                       const int32_t *neighbors, uint64_t num_tets, uint32_t *keep,
+                       uint32_t *dirty, void *certify_scratch, size_t certify_scratch_bytes,
+                       void *stream) {
+    if (!points || !dirty || !certify_scratch || (num_tets > 0 && (!tets || !neighbors || !keep)))
+        return fail(SDF_E_INVALID, "NULL pointer argument");
+    const int rc = delaunay_scratch_ok("sdf_delaunay_check", num_points, certify_scratch,
+                                       certify_scratch_bytes);
+    if (rc != SDF_OK) return rc;
+    uint64_t errors = 0;
+    hipError_t e = launch_delaunay_check(points, num_points, tets, neighbors, num_tets, keep,
+                                         dirty, &errors, certify_scratch, certify_scratch_bytes,
+                                         static_cast<hipStream_t>(stream));
+    if (e == hipErrorInvalidValue)
+        return fail(SDF_E_INVALID, "points must be finite and span a volume");
+    if (e != hipSuccess) return hip_fail(e, "delaunay_check");
+    if (errors != 0)
+        return fail(SDF_E_INVALID, "%llu tets have a vertex id >= num_points",
+                    (unsigned long long)errors);
+    return SDF_OK;
+}
+
+int sdf_delaunay_certify_points(const float *points, uint32_t num_points, const uint32_t *query,
+                                uint32_t num_query, uint32_t *reports, uint64_t report_capacity,
+                                uint32_t *open_points, uint64_t *counts, void *certify_scratch,
+                                size_t certify_scratch_bytes, void *stream) {
+    if (!points || !open_points || !counts || !certify_scratch || (num_query > 0 && !query) ||
+        (report_capacity > 0 && !reports))
+        return fail(SDF_E_INVALID, "NULL pointer argument");
+    const int rc = delaunay_scratch_ok("sdf_delaunay_certify_points", num_points,
+                                       certify_scratch, certify_scratch_bytes);
+    if (rc != SDF_OK) return rc;
+    if (num_query > num_points)
+        return fail(SDF_E_INVALID, "at most num_points query points (got %u)", num_query);
+    hipError_t e = launch_delaunay_certify_points(points, num_points, query, num_query, reports,
+                                                  report_capacity, open_points, counts,
+                                                  certify_scratch, certify_scratch_bytes,
+                                                  static_cast<hipStream_t>(stream));
+    if (e == hipErrorNotReady)
+        return fail(SDF_E_INVALID, "certify_scratch holds no grid of these points "
+                                   "(call sdf_delaunay_check first)");
+    if (e != hipSuccess) return hip_fail(e, "delaunay_certify_points");
     return SDF_OK;
 }
 

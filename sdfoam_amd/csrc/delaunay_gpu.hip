@@ -38,6 +38,7 @@ using dgrid::GridView;
 
 struct GridScratch {
     GridGeom *geom;
+    uint64_t *tag; // kGridTag and the point count, once the grid is built
     unsigned long long *counters;
     uint32_t *mm, *index, *status;
     uint64_t *keys, *keys_sorted;
@@ -58,6 +59,7 @@ GridScratch carve_grid(void *base, uint32_t n, size_t temp_bytes) {
         return q;
     };
     s.geom = reinterpret_cast<GridGeom *>(take(sizeof(GridGeom)));
+    s.tag = reinterpret_cast<uint64_t *>(take(2 * 8));
     s.counters = reinterpret_cast<unsigned long long *>(take(8 * 8));
     s.mm = reinterpret_cast<uint32_t *>(take(6 * 4));
     for (int l = 0; l < dgrid::kLevels; ++l) {
@@ -95,6 +97,16 @@ float unordered(uint32_t k) {
     float f;
     std::memcpy(&f, &u, 4);
     return f;
+}
+
+constexpr uint64_t kGridTag = 0x5344464f414d4752ull;
+
+__global__ __launch_bounds__(64) void tag_kernel(uint64_t *__restrict__ tag, uint64_t a,
+                                                 uint64_t b) {
+    if (threadIdx.x == 0) {
+        tag[0] = a;
+        tag[1] = b;
+    }
 }
 
 __global__ __launch_bounds__(64) void init_kernel(uint32_t *__restrict__ mm,
@@ -507,7 +519,7 @@ __device__ bool wave_touches_box(const WaveCell &c, const WaveShared &sh) {
 
 // counters: 0 report rows asked for, 1 open points, 2 undecided cells,
 // 3 cells over the fixed capacity, 4 coincident point pairs seen (twice).
-// One 64-thread block per point.  Four waves per SIMD (128 VGPRs, 200 bytes
+// One 64-thread block per point (per entry of `query` when it is given).  Four waves per SIMD (128 VGPRs, 200 bytes
 // of spills per lane) run it ~20% faster than the two its natural register
 // count (203) allows; three (168 VGPRs, 40 bytes) run it ~10% slower than
 // four.  What is uniform over the wave and indexed at run time (the grid
@@ -518,13 +530,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                                                      uint64_t report_capacity,
                                                      unsigned long long *__restrict__ counters,
                                                      uint32_t *__restrict__ open,
-                                                     uint32_t *__restrict__ status_out) {
+                                                     uint32_t *__restrict__ status_out,
+                                                     const uint32_t *__restrict__ query) {
     __shared__ WaveShared sh;
     // the point's grid cell and searched rings per level (uniform over the
     // wave; indexed by level, so kept in LDS rather than scratch memory)
     __shared__ int hc[dgrid::kLevels][3];
     __shared__ int rings[dgrid::kLevels];
-    const uint32_t i = blockIdx.x;
+    const uint32_t i = query ? query[blockIdx.x] : blockIdx.x;
     if (i >= n) return;
     const uint32_t l = wlane();
     const GridGeom &g = gv.g;
@@ -735,18 +748,68 @@ __global__ __launch_bounds__(64) void keep_empty_kernel(const float *__restrict_
     if (l == 0) keep[t] = inside ? 0u : (undecided ? 2u : 1u);
 }
 
-// Row t of [reports; candidates] survives: a report (i, a, b, c) when i is
-// its lowest certified vertex, a candidate when keep says so.
+// Incremental rebuild, one lane per tetrahedron t of the previous
+// tetrahedralisation over the moved points: keep[t] = 1 when no point lies
+// strictly inside its circumsphere and every sign is decided (status: every
+// point clean), else 0.  The vertices of a tetrahedron not kept and the three
+// vertices of each face without a neighbour (the hull) are marked dirty.
+// The sphere is scanned on the finest level where it spans at most 6 x 6
+// columns (at C3's 1M points 29.5 ms for 6.7M tetrahedra, against 55 ms at
+// 3 x 3, 43 ms at 4 x 4 and 53 ms at 8 x 8).  errors[0]: rows with a vertex
+// out of range.
+__global__ __launch_bounds__(256) void check_kernel(const float *__restrict__ p, uint32_t n,
+                                                    GridView gv,
+                                                    const uint32_t *__restrict__ status,
+                                                    const uint32_t *__restrict__ tets,
+                                                    const int32_t *__restrict__ nbr, uint64_t T,
+                                                    uint32_t *__restrict__ keep,
+                                                    uint32_t *__restrict__ dirty,
+                                                    unsigned long long *__restrict__ errors) {
+    const uint64_t t = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (t >= T) return;
+    uint32_t v[4];
+    bool valid = true;
+    for (int k = 0; k < 4; ++k) {
+        v[k] = tets[4 * t + k];
+        valid = valid && v[k] < n;
+    }
+    if (!valid) {
+        keep[t] = 0u;
+        atomicAdd(errors, 1ull);
+        return;
+    }
+    // a sphere still wider than 8 x 8 columns of the coarsest level (the
+    // huge spheres of flat tetrahedra at the hull) is not scanned: its
+    // tetrahedron is not kept, which only adds dirty points
+    dgrid::Sphere S;
+    bool kept = dgrid::sphere_setup(p, v, gv, S, 36.0);
+    const uint32_t cols = kept ? dgrid::sphere_columns(S) : 0u;
+    kept = kept && cols <= 64u;
+    for (uint32_t c = 0; kept && c < cols; ++c)
+        kept = dgrid::sphere_scan_column(p, v, gv, status, S, c) == 1u;
+    keep[t] = kept ? 1u : 0u;
+    for (int j = 0; j < 4; ++j) {
+        const bool hull = nbr[4 * t + j] < 0;
+        for (int k = 0; k < 4; ++k)
+            if (!kept || (hull && k != j)) dirty[v[k]] = 1u;
+    }
+}
+
+// Row t of [reports; candidates; verified] survives: a report (i, a, b, c)
+// when i is its lowest certified vertex, a candidate when keep says so, a
+// verified tetrahedron always.
 // errors: 0 a report index out of range, 1 an undecided candidate.
 __global__ __launch_bounds__(256) void select_kernel(const uint32_t *__restrict__ reports,
                                                      uint64_t nr,
                                                      const uint32_t *__restrict__ keep,
                                                      uint64_t m,
+                                                     const uint32_t *__restrict__ verified,
+                                                     uint64_t nv,
                                                      const uint32_t *__restrict__ status,
                                                      uint32_t n, uint32_t *__restrict__ flag,
                                                      unsigned long long *__restrict__ errors) {
     const uint64_t t = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-    if (t >= nr + m) return;
+    if (t >= nr + m + nv) return;
     uint32_t f = 0;
     if (t < nr) {
         const uint32_t i = reports[4 * t];
@@ -758,10 +821,15 @@ __global__ __launch_bounds__(256) void select_kernel(const uint32_t *__restrict_
         }
         if (f == 0u) atomicAdd(errors, 1ull);
         f = f == 1u ? 1u : 0u;
-    } else {
+    } else if (t < nr + m) {
         const uint32_t k = keep[t - nr];
         f = k == 1u ? 1u : 0u;
         if (k == 2u) atomicAdd(errors + 1, 1ull);
+    } else {
+        f = 1u;
+        for (int k = 0; k < 4; ++k)
+            if (verified[4 * (t - nr - m) + k] >= n) f = 0u;
+        if (f == 0u) atomicAdd(errors, 1ull);
     }
     flag[t] = f;
 }
@@ -770,15 +838,19 @@ __global__ __launch_bounds__(256) void compact_kernel(const uint32_t *__restrict
                                                       uint64_t nr,
                                                       const uint32_t *__restrict__ cand,
                                                       uint64_t m,
+                                                      const uint32_t *__restrict__ verified,
+                                                      uint64_t nv,
                                                       const uint32_t *__restrict__ flag,
                                                       const uint32_t *__restrict__ pos,
                                                       uint32_t *__restrict__ out,
                                                       uint64_t capacity) {
     const uint64_t t = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-    if (t >= nr + m || !flag[t]) return;
+    if (t >= nr + m + nv || !flag[t]) return;
     const uint64_t w = pos[t];
     if (w >= capacity) return;
-    const uint32_t *src = t < nr ? reports + 4 * t : cand + 4 * (t - nr);
+    const uint32_t *src = t < nr       ? reports + 4 * t
+                          : t < nr + m ? cand + 4 * (t - nr)
+                                       : verified + 4 * (t - nr - m);
     for (int k = 0; k < 4; ++k) out[4 * w + k] = src[k];
 }
 
@@ -889,20 +961,20 @@ size_t delaunay_certify_scratch_bytes(uint32_t num_points) {
     return carve_grid(nullptr, num_points, temp).total;
 }
 
-hipError_t launch_delaunay_certify(const float *points, uint32_t n, uint32_t *reports,
-                                   uint64_t report_capacity, uint32_t *open, uint64_t counts[5],
-                                   void *scratch, size_t bytes, hipStream_t stream) {
-    for (int k = 0; k < 5; ++k) counts[k] = 0;
-    const size_t temp = grid_temp_bytes(n);
-    GridScratch s = carve_grid(scratch, n, temp);
-    if (n == 0 || temp == 0 || s.total > bytes) return hipErrorInvalidValue;
+namespace {
+
+// The grid levels over the points into the scratch, its geometry kept there
+// for the calls that follow; `g` receives it too and must live until the
+// caller's next synchronisation of the stream (the copy reads it).
+hipError_t build_grid(const float *points, uint32_t n, const GridScratch &s, GridGeom &g,
+                      hipStream_t stream) {
+    hipLaunchKernelGGL(tag_kernel, dim3(1), dim3(64), 0, stream, s.tag, 0ull, 0ull);
     hipLaunchKernelGGL(init_kernel, dim3(1), dim3(64), 0, stream, s.mm, s.counters);
     hipLaunchKernelGGL(bbox_kernel, grid1(n), dim3(256), 0, stream, points, n, s.mm);
     uint32_t hm[6];
     hipError_t e = hipMemcpyAsync(hm, s.mm, sizeof(hm), hipMemcpyDeviceToHost, stream);
     if (e != hipSuccess) return e;
     if ((e = hipStreamSynchronize(stream)) != hipSuccess) return e;
-    GridGeom g{};
     double lo[3], hi[3];
     for (int k = 0; k < 3; ++k) {
         lo[k] = (double)unordered(hm[k]);
@@ -927,19 +999,34 @@ hipError_t launch_delaunay_certify(const float *points, uint32_t n, uint32_t *re
                            s.table[l], g.table_mask);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    // the geometry stays in the scratch for the merge (`g` lives until the
-    // synchronisation below)
     if ((e = hipMemcpyAsync(s.geom, &g, sizeof(g), hipMemcpyHostToDevice, stream)) != hipSuccess)
         return e;
+    hipLaunchKernelGGL(tag_kernel, dim3(1), dim3(64), 0, stream, s.tag, kGridTag, (uint64_t)n);
+    return hipGetLastError();
+}
+
+GridView grid_view(const GridScratch &s, const GridGeom &g) {
     GridView gv{};
     gv.g = g;
     for (int l = 0; l < dgrid::kLevels; ++l) {
         gv.table[l] = s.table[l];
         gv.sorted[l] = s.sorted[l];
     }
-    hipLaunchKernelGGL(certify_kernel, dim3(n), dim3(64), 0, stream, points, n, gv,
-                       reports, report_capacity, s.counters, open, s.status);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    return gv;
+}
+
+// certify_kernel over all points (query == nullptr) or the nq listed ones,
+// then the counters to the host.
+hipError_t run_certify(const float *points, uint32_t n, const uint32_t *query, uint32_t nq,
+                       const GridView &gv, const GridScratch &s, uint32_t *reports,
+                       uint64_t report_capacity, uint32_t *open, uint64_t counts[5],
+                       hipStream_t stream) {
+    hipError_t e;
+    if (nq > 0) {
+        hipLaunchKernelGGL(certify_kernel, dim3(nq), dim3(64), 0, stream, points, n, gv, reports,
+                           report_capacity, s.counters, open, s.status, query);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     unsigned long long hc[8];
     if ((e = hipMemcpyAsync(hc, s.counters, sizeof(hc), hipMemcpyDeviceToHost, stream)) !=
             hipSuccess ||
@@ -947,6 +1034,73 @@ hipError_t launch_delaunay_certify(const float *points, uint32_t n, uint32_t *re
         return e;
     for (int k = 0; k < 5; ++k) counts[k] = hc[k];
     return hipSuccess;
+}
+
+} // namespace
+
+hipError_t launch_delaunay_certify(const float *points, uint32_t n, uint32_t *reports,
+                                   uint64_t report_capacity, uint32_t *open, uint64_t counts[5],
+                                   void *scratch, size_t bytes, hipStream_t stream) {
+    for (int k = 0; k < 5; ++k) counts[k] = 0;
+    const size_t temp = grid_temp_bytes(n);
+    GridScratch s = carve_grid(scratch, n, temp);
+    if (n == 0 || temp == 0 || s.total > bytes) return hipErrorInvalidValue;
+    GridGeom g{};
+    hipError_t e = build_grid(points, n, s, g, stream);
+    if (e != hipSuccess) return e;
+    return run_certify(points, n, nullptr, n, grid_view(s, g), s, reports, report_capacity, open,
+                       counts, stream);
+}
+
+hipError_t launch_delaunay_check(const float *points, uint32_t n, const uint32_t *tets,
+                                 const int32_t *nbr, uint64_t T, uint32_t *keep, uint32_t *dirty,
+                                 uint64_t *errors, void *scratch, size_t bytes,
+                                 hipStream_t stream) {
+    *errors = 0;
+    const size_t temp = grid_temp_bytes(n);
+    GridScratch s = carve_grid(scratch, n, temp);
+    if (n == 0 || temp == 0 || s.total > bytes) return hipErrorInvalidValue;
+    GridGeom g{};
+    hipError_t e = build_grid(points, n, s, g, stream);
+    if (e != hipSuccess) return e;
+    // every point clean until certify_points certifies or opens it
+    hipLaunchKernelGGL(fill_kernel, grid1(n), dim3(256), 0, stream, s.status, (uint64_t)n,
+                       dgrid::kStatusClean);
+    hipLaunchKernelGGL(fill_kernel, grid1(n), dim3(256), 0, stream, dirty, (uint64_t)n, 0u);
+    if (T > 0)
+        hipLaunchKernelGGL(check_kernel, grid1(T), dim3(256), 0, stream, points, n,
+                           grid_view(s, g), s.status, tets, nbr, T, keep, dirty, s.counters + 5);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    unsigned long long hc[8];
+    if ((e = hipMemcpyAsync(hc, s.counters, sizeof(hc), hipMemcpyDeviceToHost, stream)) !=
+            hipSuccess ||
+        (e = hipStreamSynchronize(stream)) != hipSuccess)
+        return e;
+    *errors = hc[5];
+    return hipSuccess;
+}
+
+hipError_t launch_delaunay_certify_points(const float *points, uint32_t n, const uint32_t *query,
+                                          uint32_t nq, uint32_t *reports,
+                                          uint64_t report_capacity, uint32_t *open,
+                                          uint64_t counts[5], void *scratch, size_t bytes,
+                                          hipStream_t stream) {
+    for (int k = 0; k < 5; ++k) counts[k] = 0;
+    const size_t temp = grid_temp_bytes(n);
+    GridScratch s = carve_grid(scratch, n, temp);
+    if (n == 0 || temp == 0 || s.total > bytes) return hipErrorInvalidValue;
+    GridGeom g{};
+    uint64_t tag[2] = {0, 0};
+    hipError_t e = hipMemcpyAsync(&g, s.geom, sizeof(g), hipMemcpyDeviceToHost, stream);
+    if (e != hipSuccess) return e;
+    if ((e = hipMemcpyAsync(tag, s.tag, sizeof(tag), hipMemcpyDeviceToHost, stream)) != hipSuccess)
+        return e;
+    if ((e = hipStreamSynchronize(stream)) != hipSuccess) return e;
+    // the grid must come from a check call over these points
+    if (tag[0] != kGridTag || tag[1] != (uint64_t)n) return hipErrorNotReady;
+    hipLaunchKernelGGL(init_kernel, dim3(1), dim3(64), 0, stream, nullptr, s.counters);
+    return run_certify(points, n, query, nq, grid_view(s, g), s, reports, report_capacity, open,
+                       counts, stream);
 }
 
 size_t delaunay_merge_scratch_bytes(uint32_t n, uint64_t nr, uint64_t m, uint64_t tcap) {
@@ -957,17 +1111,20 @@ size_t delaunay_merge_scratch_bytes(uint32_t n, uint64_t nr, uint64_t m, uint64_
 
 hipError_t launch_delaunay_merge(const float *points, uint32_t n, void *grid_scratch,
                                  size_t grid_bytes, const uint32_t *reports, uint64_t nr,
-                                 const uint32_t *cand, uint64_t m, uint32_t *tets, int32_t *nbr,
-                                 uint64_t tcap, uint64_t result[4], void *scratch, size_t bytes,
+                                 const uint32_t *cand, uint64_t m, const uint32_t *verified,
+                                 uint64_t nv, uint32_t *tets, int32_t *nbr, uint64_t tcap,
+                                 uint64_t result[4], void *scratch, size_t bytes,
                                  hipStream_t stream) {
     for (int k = 0; k < 4; ++k) result[k] = 0;
     const size_t gtemp = grid_temp_bytes(n);
     const GridScratch gs = carve_grid(grid_scratch, n, gtemp);
-    const size_t temp = merge_temp_bytes(n, nr + m);
-    const MergeScratch s = carve_merge(scratch, n, nr, m, tcap, temp);
+    // the scratch is sized for nr reports and m + nv candidates (keep holds
+    // m + nv entries, of which the verified rows use none)
+    const size_t temp = merge_temp_bytes(n, nr + m + nv);
+    const MergeScratch s = carve_merge(scratch, n, nr, m + nv, tcap, temp);
     if (n == 0 || gtemp == 0 || gs.total > grid_bytes || temp == 0 || s.total > bytes)
         return hipErrorInvalidValue;
-    if (nr + m >= 0xffffffffull) return hipErrorInvalidValue;
+    if (nr + m + nv >= 0xffffffffull) return hipErrorInvalidValue;
     GridView gv{};
     hipError_t e =
         hipMemcpyAsync(&gv.g, gs.geom, sizeof(GridGeom), hipMemcpyDeviceToHost, stream);
@@ -981,17 +1138,17 @@ hipError_t launch_delaunay_merge(const float *points, uint32_t n, void *grid_scr
     if (m > 0)
         hipLaunchKernelGGL(keep_empty_kernel, dim3((unsigned)m), dim3(64), 0, stream, points, n,
                            gv, cand, (uint32_t)m, gs.status, s.keep);
-    const uint64_t rows = nr + m;
+    const uint64_t rows = nr + m + nv;
     uint32_t last[2] = {0, 0};
     if (rows > 0) {
         hipLaunchKernelGGL(select_kernel, grid1(rows), dim3(256), 0, stream, reports, nr, s.keep,
-                           m, gs.status, n, s.flag, s.acc + 2);
+                           m, verified, nv, gs.status, n, s.flag, s.acc + 2);
         size_t tb = s.temp_bytes;
         e = rocprim::exclusive_scan(s.temp, tb, s.flag, s.pos, 0u, (size_t)rows,
                                     rocprim::plus<uint32_t>(), stream);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(compact_kernel, grid1(rows), dim3(256), 0, stream, reports, nr, cand,
-                           m, s.flag, s.pos, tets, tcap);
+                           m, verified, nv, s.flag, s.pos, tets, tcap);
         if ((e = hipMemcpyAsync(last, s.pos + (rows - 1), 4, hipMemcpyDeviceToHost, stream)) !=
                 hipSuccess ||
             (e = hipMemcpyAsync(last + 1, s.flag + (rows - 1), 4, hipMemcpyDeviceToHost,

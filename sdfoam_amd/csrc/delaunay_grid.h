@@ -336,8 +336,12 @@ struct Sphere {
     int lo_c[3], hi_c[3];
 };
 
-// False if the tetrahedron is flat (no circumcentre).
-SDF_HD bool sphere_setup(const float *p, const uint32_t *v, const GridView &gv, Sphere &S) {
+// False if the tetrahedron is flat (no circumcentre).  The level is the
+// finest on which the sphere's box spans at most `max_cols` (y, z) columns:
+// many small cells for a wavefront that scans the columns in parallel, a
+// few cells of about the sphere's size for one lane that scans them all.
+SDF_HD bool sphere_setup(const float *p, const uint32_t *v, const GridView &gv, Sphere &S,
+                         double max_cols = 256.0) {
     const GridGeom &g = gv.g;
     for (int k = 0; k < 3; ++k) S.o[k] = (double)p[3ull * v[0] + k];
     for (int s = 0; s < 3; ++s) {
@@ -363,7 +367,7 @@ SDF_HD bool sphere_setup(const float *p, const uint32_t *v, const GridView &gv, 
         }
         const double cols =
             (double)(S.hi_c[1] - S.lo_c[1] + 1) * (double)(S.hi_c[2] - S.lo_c[2] + 1);
-        if (cols <= 256.0 || S.l == kLevels - 1) break;
+        if (cols <= max_cols || S.l == kLevels - 1) break;
     }
     return true;
 }
@@ -372,9 +376,14 @@ SDF_HD uint32_t sphere_columns(const Sphere &S) {
     return (uint32_t)(S.hi_c[1] - S.lo_c[1] + 1) * (uint32_t)(S.hi_c[2] - S.lo_c[2] + 1);
 }
 
+// Status of a point an incremental rebuild neither certifies nor lists as
+// open (its old tetrahedra are kept): like a certified point, its sign on a
+// sphere must be decided.
+constexpr uint32_t kStatusClean = 4u;
+
 // Points of column `col` against the sphere: 0 if one lies strictly inside,
-// 2 if none does but one's sign is undecided and it is certified (an open
-// point exactly on the sphere is passed over: the candidates' own
+// 2 if none does but one's sign is undecided and it is certified or clean (an
+// open point exactly on the sphere is passed over: the candidates' own
 // triangulation of the open points already chose among such points), 1
 // otherwise.
 SDF_HD uint32_t sphere_scan_column(const float *p, const uint32_t *v, const GridView &gv,
@@ -411,7 +420,7 @@ SDF_HD uint32_t sphere_scan_column(const float *p, const uint32_t *v, const Grid
             if (e0 * e0 + e1 * e1 + e2 * e2 > S.r * S.r) continue; // clearly outside
             const int s = vcell::in_sphere(S.pl[0].n, S.pl[1].n, S.pl[2].n, q);
             if (s > 0) return 0u;
-            if (s == 0 && status[j] == vcell::kCertified) res = 2u;
+            if (s == 0 && (status[j] == vcell::kCertified || status[j] == kStatusClean)) res = 2u;
         }
     }
     return res;
@@ -419,11 +428,11 @@ SDF_HD uint32_t sphere_scan_column(const float *p, const uint32_t *v, const Grid
 
 // Candidate tetrahedron v[4] (ids below n): 1 if no point lies strictly
 // inside its circumsphere, 0 if one does, 2 if it is flat or, with none
-// inside, a certified point's sign could not be decided.
+// inside, a certified or clean point's sign could not be decided.
 SDF_HD uint32_t sphere_empty(const float *p, const uint32_t *v, const GridView &gv,
-                             const uint32_t *status) {
+                             const uint32_t *status, double max_cols = 256.0) {
     Sphere S;
-    if (!sphere_setup(p, v, gv, S)) return 2u;
+    if (!sphere_setup(p, v, gv, S, max_cols)) return 2u;
     uint32_t res = 1u;
     const uint32_t cols = sphere_columns(S);
     for (uint32_t c = 0; c < cols; ++c) {

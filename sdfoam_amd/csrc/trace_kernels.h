@@ -271,12 +271,29 @@ hipError_t launch_delaunay_certify(const float *points, uint32_t num_points, uin
 size_t delaunay_merge_scratch_bytes(uint32_t num_points, uint64_t num_reports,
                                     uint64_t num_candidates, uint64_t tet_capacity);
 // result: tets, hull faces, invalid or undecided rows, faces of three tets.
+// The verified rows (num_verified of them) are kept as they are; the scratch
+// is sized for num_candidates + num_verified candidates.
 hipError_t launch_delaunay_merge(const float *points, uint32_t num_points, void *grid_scratch,
                                  size_t grid_bytes, const uint32_t *reports, uint64_t num_reports,
                                  const uint32_t *candidates, uint64_t num_candidates,
+                                 const uint32_t *verified, uint64_t num_verified,
                                  uint32_t *tets, int32_t *neighbors, uint64_t tet_capacity,
                                  uint64_t result[4], void *scratch, size_t scratch_bytes,
                                  hipStream_t stream);
+// Incremental rebuild: the grid over the moved points into the certify
+// scratch, every point clean, then one lane per old tetrahedron (keep, dirty
+// marks).  errors: rows with a vertex out of range.  Synchronizes `stream`.
+hipError_t launch_delaunay_check(const float *points, uint32_t num_points, const uint32_t *tets,
+                                 const int32_t *neighbors, uint64_t num_tets, uint32_t *keep,
+                                 uint32_t *dirty, uint64_t *errors, void *scratch,
+                                 size_t scratch_bytes, hipStream_t stream);
+// certify_kernel over the listed points on the grid a launch_delaunay_check
+// call over the same points left in the scratch (hipErrorNotReady if none).
+hipError_t launch_delaunay_certify_points(const float *points, uint32_t num_points,
+                                          const uint32_t *query, uint32_t num_query,
+                                          uint32_t *reports, uint64_t report_capacity,
+                                          uint32_t *open, uint64_t counts[5], void *scratch,
+                                          size_t scratch_bytes, hipStream_t stream);
 
 hipError_t launch_build_aabb_tree(const float *points, uint32_t num_points, float *tree,
                                   hipStream_t stream);

@@ -7,7 +7,9 @@ src/delaunay/delaunay.h:9-44).
 ``sort_points`` order (``permutation()``: sorted = points[perm]) and
 triangulates them; ``rebuild(points, incremental)`` re-triangulates, sorting
 again unless ``incremental`` and the point count is unchanged, and returns
-whether it sorted (the caller then permutes its arrays).  Outputs are CUDA
+whether it sorted (the caller then permutes its arrays).  An incremental
+rebuild starts from the previous tetrahedra: those whose circumspheres stay
+empty are kept, and only the points of the others are certified again.  Outputs are CUDA
 uint32 tensors indexing the sorted points:
 
 * ``tets()`` [T, 4], ordered by their sorted vertex sets, each listing its
@@ -165,19 +167,26 @@ class _Undecided(RuntimeError):
     """The GPU tetrahedralisation met a sign it could not decide."""
 
 
-def _certify(L, pts: torch.Tensor, gptr: int, gbytes: int, stream):
-    """sdf_delaunay_certify over CUDA float32 points [n, 3]: (reports [nr, 4]
-    int32 rows (point, a, b, c), open points [nu] int32 in index order,
-    counts).  Raises _Undecided where the GPU cannot decide."""
+def _certify(L, pts: torch.Tensor, gptr: int, gbytes: int, stream, query=None):
+    """sdf_delaunay_certify over CUDA float32 points [n, 3], or with `query`
+    (int32 ids) sdf_delaunay_certify_points over those on the grid of an
+    sdf_delaunay_check call: (reports [nr, 4] int32 rows (point, a, b, c),
+    open points [nu] int32 in index order, counts).  Raises _Undecided where
+    the GPU cannot decide."""
     dev = pts.device
     n = pts.numel() // 3
-    open_pts = torch.empty(n, dtype=torch.int32, device=dev)
+    nq = n if query is None else int(query.numel())
+    open_pts = torch.empty(max(nq, 1), dtype=torch.int32, device=dev)
     counts = (C.c_uint64 * 5)()
-    cap = 28 * n + 4096
+    cap = 28 * nq + 4096
     for _ in range(2):
         reports = torch.empty((cap, 4), dtype=torch.int32, device=dev)
-        rc = L.sdf_delaunay_certify(ptr(pts), n, ptr(reports), cap, ptr(open_pts), counts, gptr,
-                                    gbytes, stream)
+        if query is None:
+            rc = L.sdf_delaunay_certify(ptr(pts), n, ptr(reports), cap, ptr(open_pts), counts,
+                                        gptr, gbytes, stream)
+        else:
+            rc = L.sdf_delaunay_certify_points(ptr(pts), n, ptr(query), nq, ptr(reports), cap,
+                                               ptr(open_pts), counts, gptr, gbytes, stream)
         if rc == _lib.SDF_E_INVALID:
             # no volume or non-finite points: Qhull on every point decides
             raise _Undecided(L.sdf_last_error().decode())
@@ -246,6 +255,49 @@ def _open_candidates(L, pts: torch.Tensor, U: torch.Tensor, stream, stats: dict)
     return cand.to(torch.int32).contiguous(), int((nbr_u < 0).sum())
 
 
+def _merge(L, pts: torch.Tensor, gptr: int, gbytes: int, reports, cand, verified,
+           hull_faces: int, stream, tcap: int | None = None):
+    """sdf_delaunay_merge (sdf_delaunay_merge_verified with `verified`
+    rows): (tets, neighbors, T); raises _Undecided when a candidate is
+    undecided or the union is inconsistent (Qhull on every point decides).
+    `tcap`: the tets to make room for (a second merge runs if more come)."""
+    dev = pts.device
+    n = pts.numel() // 3
+    nr, m = int(reports.shape[0]), int(cand.shape[0])
+    nv = 0 if verified is None else int(verified.shape[0])
+    result = (C.c_uint64 * 4)()
+    if tcap is None:
+        # every certified vertex of a tetrahedron reports it (~4 rows per tet)
+        tcap = nr // 3 + m + nv + 4096
+    for _ in range(2):
+        tets = torch.empty((tcap, 4), dtype=torch.int32, device=dev)
+        nbr = torch.empty((tcap, 4), dtype=torch.int32, device=dev)
+        mbytes = int(L.sdf_delaunay_merge_scratch_bytes(n, nr, m + nv, tcap))
+        if mbytes == 0:
+            raise RuntimeError("sdf_delaunay_merge_scratch_bytes failed")
+        mbuf, mptr = _aligned(mbytes, dev)
+        if verified is None:
+            rc = L.sdf_delaunay_merge(ptr(pts), n, gptr, gbytes, ptr(reports), nr, ptr(cand), m,
+                                      ptr(tets), ptr(nbr), tcap, result, mptr, mbytes, stream)
+        else:
+            rc = L.sdf_delaunay_merge_verified(ptr(pts), n, gptr, gbytes, ptr(reports), nr,
+                                               ptr(cand), m, ptr(verified), nv, ptr(tets),
+                                               ptr(nbr), tcap, result, mptr, mbytes, stream)
+        if rc == _lib.SDF_E_INVALID and result[0] > tcap and result[2] == 0:
+            tcap = int(result[0])
+            continue
+        if rc == _lib.SDF_E_INVALID:
+            raise _Undecided(L.sdf_last_error().decode())
+        check(rc)
+        break
+    else:
+        raise _Undecided("tets did not fit the merge's capacity")
+    T = int(result[0])
+    if int(result[1]) != hull_faces:
+        raise _Undecided(f"{int(result[1])} faces without a neighbour, the hull has {hull_faces}")
+    return tets, nbr, T
+
+
 def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, dict]:
     """Delaunay tetrahedra of CUDA float32 points [N, 3] by certified
     Voronoi cells (sdf_delaunay_certify / sdf_delaunay_merge): the points
@@ -272,35 +324,92 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
         cand, hull_faces = _open_candidates(L, pts, U, stream, stats)
         m = int(cand.shape[0])
         t2 = time.perf_counter()
-        result = (C.c_uint64 * 4)()
-        tcap = nr // 3 + m + 4096
-        for _ in range(2):
-            tets = torch.empty((tcap, 4), dtype=torch.int32, device=dev)
-            nbr = torch.empty((tcap, 4), dtype=torch.int32, device=dev)
-            mbytes = int(L.sdf_delaunay_merge_scratch_bytes(n, nr, m, tcap))
-            if mbytes == 0:
-                raise RuntimeError("sdf_delaunay_merge_scratch_bytes failed")
-            mbuf, mptr = _aligned(mbytes, dev)
-            rc = L.sdf_delaunay_merge(ptr(pts), n, gptr, gbytes, ptr(reports), nr, ptr(cand), m,
-                                      ptr(tets), ptr(nbr), tcap, result, mptr, mbytes, stream)
-            if rc == _lib.SDF_E_INVALID and result[0] > tcap and result[2] == 0:
-                tcap = int(result[0])
-                continue
-            if rc == _lib.SDF_E_INVALID:
-                # an undecided candidate or an inconsistent union: Qhull on
-                # every point decides
-                raise _Undecided(L.sdf_last_error().decode())
-            check(rc)
-            break
-        else:
-            raise _Undecided("tets did not fit the merge's capacity")
-    T = int(result[0])
-    if int(result[1]) != hull_faces:
-        raise _Undecided(f"{int(result[1])} faces without a neighbour, the hull has {hull_faces}")
+        tets, nbr, T = _merge(L, pts, gptr, gbytes, reports, cand, None, hull_faces, stream)
     t3 = time.perf_counter()
     stats.update({"open": nu, "reports": nr, "candidates": m, "tets": T,
                   "undecided_cells": int(counts[2]), "overflow_cells": int(counts[3]),
                   "certify_s": t1 - t0, "open_points_qhull_s": t2 - t1, "merge_s": t3 - t2})
+    return tets[:T], nbr[:T], stats
+
+
+# An incremental rebuild re-certifies the dirty points only; past this share
+# of dirty points the full rebuild is used instead (at C3's 1M points the two
+# take about as long at ~40% dirty: the check costs ~30 ms, certifying the
+# dirty points ~40-50 ms per 100k-300k of them).
+_INCREMENTAL_MAX_DIRTY = 0.4
+
+
+def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
+                               nbr_old: torch.Tensor):
+    """The Delaunay tetrahedra of moved CUDA float32 points [N, 3] from the
+    previous tetrahedralisation of the same points (tets_old, nbr_old: int32
+    [T, 4] on the points' device, -1 on the hull), in place of
+    delete_delaunay_violations and the regrowth from its frontier
+    (src/delaunay/delete_violations.cu:7-178, src/delaunay/delaunay.cu:
+    288-345).  sdf_delaunay_check keeps the old tetrahedra whose circumsphere
+    is still empty and marks the vertices of the others, and of the hull
+    faces, dirty; the dirty points alone are certified (the open ones go
+    through the open points' path of the full rebuild), and the merge takes
+    their reports and candidates and the kept old tetrahedra with a clean
+    vertex and no certified one.  A Delaunay tetrahedron of the moved points
+    with a clean vertex v is one of v's old ones (those are all kept, so they
+    still fill a neighbourhood of v, and Delaunay tetrahedra do not
+    overlap); all other Delaunay tetrahedra have four dirty vertices.
+    Returns (tets, neighbors, stats); raises _Undecided like gpu_tetrahedra,
+    and when more than half the points are dirty (the caller then rebuilds in
+    full)."""
+    pts = points.contiguous()
+    dev = pts.device
+    n = pts.numel() // 3
+    T_old = int(tets_old.shape[0])
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    gbytes = int(L.sdf_delaunay_certify_scratch_bytes(n))
+    if gbytes == 0:
+        raise RuntimeError("sdf_delaunay_certify_scratch_bytes failed")
+    gbuf, gptr = _aligned(gbytes, dev)
+    tets_old = tets_old.to(dev, torch.int32).contiguous()
+    nbr_old = nbr_old.to(dev, torch.int32).contiguous()
+    keep = torch.empty(max(T_old, 1), dtype=torch.int32, device=dev)
+    dirty = torch.empty(n, dtype=torch.int32, device=dev)
+    stats = {"incremental": True}
+    t0 = time.perf_counter()
+    with torch.cuda.device(dev):
+        rc = L.sdf_delaunay_check(ptr(pts), n, ptr(tets_old), ptr(nbr_old), T_old, ptr(keep),
+                                  ptr(dirty), gptr, gbytes, stream)
+        if rc == _lib.SDF_E_INVALID:
+            raise _Undecided(L.sdf_last_error().decode())
+        check(rc)
+        D = torch.nonzero(dirty).view(-1).to(torch.int32)
+        nd = int(D.numel())
+        stats.update({"dirty": nd, "kept_old": int(keep[:T_old].sum().item())})
+        if nd > _INCREMENTAL_MAX_DIRTY * n:
+            raise _Undecided(f"{nd} of {n} points dirty")
+        t1 = time.perf_counter()
+        reports, U, counts = _certify(L, pts, gptr, gbytes, stream, query=D)
+        nr, nu = int(reports.shape[0]), int(U.numel())
+        t2 = time.perf_counter()
+        cand, hull_faces = _open_candidates(L, pts, U, stream, stats)
+        m = int(cand.shape[0])
+        t3 = time.perf_counter()
+        # 0 clean, 1 dirty and certified, 2 dirty and open
+        state = torch.zeros(n, dtype=torch.int8, device=dev)
+        if nd:
+            state[D.long()] = 1
+        if nu:
+            state[U.long()] = 2
+        sv = state[tets_old.long()]
+        sel = (keep[:T_old] == 1) & (sv != 1).all(dim=1) & (sv == 0).any(dim=1)
+        verified = tets_old[sel].contiguous()
+        # about as many tetrahedra as before (a tet may have one certified
+        # vertex only, so the reports do not bound them as in a full rebuild)
+        tets, nbr, T = _merge(L, pts, gptr, gbytes, reports, cand, verified, hull_faces, stream,
+                              tcap=T_old + T_old // 16 + m + 4096)
+    t4 = time.perf_counter()
+    stats.update({"open": nu, "reports": nr, "candidates": m, "verified": int(verified.shape[0]),
+                  "tets": T, "undecided_cells": int(counts[2]),
+                  "overflow_cells": int(counts[3]), "check_s": t1 - t0, "certify_s": t2 - t1,
+                  "open_points_qhull_s": t3 - t2, "merge_s": t4 - t3})
     return tets[:T], nbr[:T], stats
 
 
@@ -365,6 +474,8 @@ class Triangulation:
         self.last_stats = None
         self._num_points = 0
         self._perm_t = None
+        self._tets_prev = None  # the last tetrahedra (int32 [T, 4] on the device)
+        self._nbr_prev = None
         self.rebuild(points, incremental=False)
 
     def rebuild(self, points: torch.Tensor, incremental: bool = False) -> bool:
@@ -382,9 +493,21 @@ class Triangulation:
             self._num_points = n
             sorted_now = True
         if self.method == "gpu":
+            got = None
+            why = None
+            if not sorted_now and self._tets_prev is not None:
+                try:
+                    got = gpu_tetrahedra_incremental(pts_dev, self._tets_prev, self._nbr_prev)
+                except _Undecided as e:
+                    why = str(e)
             try:
-                simplices, neighbors, self.last_stats = gpu_tetrahedra(pts_dev)
+                if got is None:
+                    got = gpu_tetrahedra(pts_dev)
+                    if why is not None:
+                        got[2]["incremental_fallback"] = why
+                simplices, neighbors, self.last_stats = got
                 self.last_method = "gpu"
+                self._keep(simplices, neighbors)
                 self._tables = device_tables(pts_dev, simplices, neighbors)
                 return sorted_now
             except _Undecided:
@@ -395,8 +518,19 @@ class Triangulation:
         simplices, neighbors = qhull_tetrahedra(pts)
         self.last_method = "qhull"
         self.last_stats = None
+        self._keep(simplices, neighbors)
         self._tables = device_tables(pts_dev, simplices, neighbors)
         return sorted_now
+
+    def _keep(self, simplices, neighbors) -> None:
+        """The tetrahedra an incremental rebuild starts from."""
+        dev = self._perm_t.device
+        if isinstance(simplices, torch.Tensor):
+            self._tets_prev = simplices.to(dev, torch.int32).contiguous()
+            self._nbr_prev = neighbors.to(dev, torch.int32).contiguous()
+        else:
+            self._tets_prev = torch.from_numpy(np.ascontiguousarray(simplices, np.int32)).to(dev)
+            self._nbr_prev = torch.from_numpy(np.ascontiguousarray(neighbors, np.int32)).to(dev)
 
     def permutation(self) -> torch.Tensor:
         return self._perm_t

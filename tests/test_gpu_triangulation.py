@@ -234,6 +234,65 @@ def test_gpu_tetrahedra_match_qhull(dev, name):
         assert np.array_equal(_np(mine[k]).reshape(v.shape), v), k
 
 
+@pytest.mark.parametrize("name,scale", [("gaussian", 0.0), ("gaussian", 1e-3), ("clustered", 1e-3),
+                                        ("shell", 1e-3), ("C2", 3e-4), ("C2", 1e-3)])
+def test_incremental_rebuild_matches_qhull(dev, name, scale):
+    """rebuild(incremental=True) over moved points (each coordinate moved by
+    `scale` times the point's cell radius, N(0, 1)): the old tetrahedra whose
+    circumspheres stay empty are kept, the dirty points re-certified, and
+    every table equals Qhull's on the moved points."""
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd.triangulation import triangulate_host
+
+    raw = np.ascontiguousarray(_gpu_sets()[name](), dtype=np.float32)
+    n = raw.shape[0]
+    print(f"incremental {name} n={n} scale={scale}", flush=True)
+    tri = sdfoam_amd.Triangulation(torch.from_numpy(raw).to(dev))
+    assert tri.last_method == "gpu"
+    pts = raw[tri.permutation().view(torch.int32).cpu().numpy()]
+    _, radius = sdfoam_amd.farthest_neighbor(torch.from_numpy(pts).to(dev), tri.point_adjacency(),
+                                             tri.point_adjacency_offsets())
+    r = radius.cpu().numpy()[:, None]
+    rng = np.random.default_rng(5)
+    moved = (pts + scale * r * rng.normal(size=pts.shape)).astype(np.float32)
+    assert tri.rebuild(torch.from_numpy(moved).to(dev), incremental=True) is False
+    st = tri.last_stats
+    print({k: v for k, v in st.items() if not k.endswith("_s")}, flush=True)
+    assert tri.last_method == "gpu" and st.get("incremental"), st
+    assert st["verified"] > 0 and st["dirty"] < 0.5 * n, st
+    host = triangulate_host(moved)
+    for k in ("tets", "tet_adjacency", "vert_to_tet", "point_adjacency", "point_adjacency_offsets"):
+        assert np.array_equal(_np(getattr(tri, k)()).reshape(host[k].shape), host[k]), k
+    # and again from the incremental result
+    moved2 = (moved + scale * r * rng.normal(size=pts.shape)).astype(np.float32)
+    tri.rebuild(torch.from_numpy(moved2).to(dev), incremental=True)
+    assert tri.last_stats.get("incremental"), tri.last_stats
+    host2 = triangulate_host(moved2)
+    for k in ("tets", "point_adjacency", "point_adjacency_offsets"):
+        assert np.array_equal(_np(getattr(tri, k)()).reshape(host2[k].shape), host2[k]), k
+
+
+def test_incremental_rebuild_falls_back_when_most_points_move(dev):
+    """Points moved by about their spacing leave most of them dirty: the
+    rebuild is a full one, with the same tables as Qhull's."""
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd.triangulation import triangulate_host
+
+    raw = np.ascontiguousarray(_gpu_sets()["gaussian"](), dtype=np.float32)
+    tri = sdfoam_amd.Triangulation(torch.from_numpy(raw).to(dev))
+    pts = raw[tri.permutation().view(torch.int32).cpu().numpy()]
+    rng = np.random.default_rng(6)
+    moved = rng.normal(size=pts.shape).astype(np.float32)
+    tri.rebuild(torch.from_numpy(moved).to(dev), incremental=True)
+    assert tri.last_method == "gpu" and not tri.last_stats.get("incremental"), tri.last_stats
+    host = triangulate_host(moved)
+    assert np.array_equal(_np(tri.point_adjacency()), host["point_adjacency"])
+
+
 def test_triangulation_methods_agree(dev):
     import torch
 
