@@ -572,7 +572,7 @@ def triangulate_bench(args, dev) -> int:
             "kept_old_tets": int(np.mean([s["kept_old"] for s in inc_done])) if inc_done else None,
             "open_points": int(np.mean([s["open"] for s in inc_done])) if inc_done else None,
             "phases_s": {k: float(np.mean([s[k + "_s"] for s in inc_done]))
-                         for k in ("check", "certify", "open_points_qhull", "merge")}
+                         for k in ("check", "certify", "open_points_qhull", "merge", "select")}
             if inc_done else None},
         "roofline": {"kernel": "certify_kernel", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,

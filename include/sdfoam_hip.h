@@ -492,8 +492,10 @@ int sdf_delaunay_merge(const float *points, uint32_t num_points,
  * (sdf_delaunay_certify_scratch_bytes), then each old tetrahedron [T, 4]
  * (neighbors [T, 4], -1 on the hull, as sdf_delaunay_merge writes them):
  * keep[t] = 1 when no point lies strictly inside its circumsphere (every
- * sign decided), else 0.  dirty[N] = 1 for the vertices of tetrahedra not
- * kept and of hull faces, else 0.  A tetrahedron with a clean vertex is a
+ * sign decided), else 0.  dirty[N]: 2 for the vertices of hull faces, 1 for
+ * the other vertices of tetrahedra not kept, else 0 (the hull's vertices
+ * need not be certified: their cells are unbounded, they go straight to the
+ * open points).  A tetrahedron with a clean vertex is a
  * Delaunay tetrahedron of the moved points exactly when it is one of the
  * kept old ones; the others all have four dirty vertices.  Fails on a
  * vertex id >= N.  Synchronizes the stream. */

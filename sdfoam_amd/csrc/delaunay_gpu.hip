@@ -751,8 +751,9 @@ __global__ __launch_bounds__(64) void keep_empty_kernel(const float *__restrict_
 // Incremental rebuild, one lane per tetrahedron t of the previous
 // tetrahedralisation over the moved points: keep[t] = 1 when no point lies
 // strictly inside its circumsphere and every sign is decided (status: every
-// point clean), else 0.  The vertices of a tetrahedron not kept and the three
-// vertices of each face without a neighbour (the hull) are marked dirty.
+// point clean), else 0.  The vertices of a tetrahedron not kept are marked
+// dirty (1), the three vertices of each face without a neighbour (the old
+// hull) dirty and on the hull (2).
 // The sphere is scanned on the finest level where it spans at most 6 x 6
 // columns (at C3's 1M points 29.5 ms for 6.7M tetrahedra, against 55 ms at
 // 3 x 3, 43 ms at 4 x 4 and 53 ms at 8 x 8).  errors[0]: rows with a vertex
@@ -788,10 +789,12 @@ __global__ __launch_bounds__(256) void check_kernel(const float *__restrict__ p,
     for (uint32_t c = 0; kept && c < cols; ++c)
         kept = dgrid::sphere_scan_column(p, v, gv, status, S, c) == 1u;
     keep[t] = kept ? 1u : 0u;
+    if (!kept)
+        for (int k = 0; k < 4; ++k) atomicMax(dirty + v[k], 1u);
     for (int j = 0; j < 4; ++j) {
-        const bool hull = nbr[4 * t + j] < 0;
+        if (nbr[4 * t + j] >= 0) continue;
         for (int k = 0; k < 4; ++k)
-            if (!kept || (hull && k != j)) dirty[v[k]] = 1u;
+            if (k != j) atomicMax(dirty + v[k], 2u);
     }
 }
 

@@ -386,7 +386,14 @@ def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
         if nd > _INCREMENTAL_MAX_DIRTY * n:
             raise _Undecided(f"{nd} of {n} points dirty")
         t1 = time.perf_counter()
-        reports, U, counts = _certify(L, pts, gptr, gbytes, stream, query=D)
+        # the old hull's vertices (2) go to the open points uncertified: their
+        # cells are unbounded (or, if one moved inside, its tetrahedra still
+        # come from the other sources), and certifying them is the costliest
+        # part of the dirty points' certification
+        hull_pts = torch.nonzero(dirty == 2).view(-1).to(torch.int32)
+        inner = torch.nonzero(dirty == 1).view(-1).to(torch.int32)
+        reports, U, counts = _certify(L, pts, gptr, gbytes, stream, query=inner)
+        U = torch.sort(torch.cat([U, hull_pts]))[0]
         nr, nu = int(reports.shape[0]), int(U.numel())
         t2 = time.perf_counter()
         cand, hull_faces = _open_candidates(L, pts, U, stream, stats)
@@ -401,6 +408,7 @@ def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
         sv = state[tets_old.long()]
         sel = (keep[:T_old] == 1) & (sv != 1).all(dim=1) & (sv == 0).any(dim=1)
         verified = tets_old[sel].contiguous()
+        t_sel = time.perf_counter()
         # about as many tetrahedra as before (a tet may have one certified
         # vertex only, so the reports do not bound them as in a full rebuild)
         tets, nbr, T = _merge(L, pts, gptr, gbytes, reports, cand, verified, hull_faces, stream,
@@ -409,7 +417,8 @@ def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
     stats.update({"open": nu, "reports": nr, "candidates": m, "verified": int(verified.shape[0]),
                   "tets": T, "undecided_cells": int(counts[2]),
                   "overflow_cells": int(counts[3]), "check_s": t1 - t0, "certify_s": t2 - t1,
-                  "open_points_qhull_s": t3 - t2, "merge_s": t4 - t3})
+                  "open_points_qhull_s": t3 - t2, "merge_s": t4 - t3,
+                  "select_s": t_sel - t3})
     return tets[:T], nbr[:T], stats
 
 
