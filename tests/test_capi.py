@@ -250,6 +250,24 @@ def test_gpu_delaunay_argument_errors():
     rc = L.sdf_delaunay_merge(p, 100, aligned, 1 << 20, p, 5, p, (1 << 26) + 1, p, p, 10,
                               result, aligned, 1 << 20, None)
     assert rc == 1 and b"at most 2^26 points and candidates" in L.sdf_last_error()
+    # the incremental rebuild's calls
+    rc = L.sdf_delaunay_check(p, 100, p, p, 10, None, p, aligned, 1 << 20, None)
+    assert rc == 1 and b"NULL pointer" in L.sdf_last_error()
+    rc = L.sdf_delaunay_check(p, 100, p, p, 10, p, p, aligned + 64, 1 << 20, None)
+    assert rc == 1 and b"256-byte aligned" in L.sdf_last_error()
+    rc = L.sdf_delaunay_check(p, 31, p, p, 10, p, p, aligned, 1 << 20, None)
+    assert rc == 1 and b"less than 32 points" in L.sdf_last_error()
+    rc = L.sdf_delaunay_certify_points(p, 100, None, 5, p, 10, p, counts, aligned, 1 << 20, None)
+    assert rc == 1 and b"NULL pointer" in L.sdf_last_error()
+    rc = L.sdf_delaunay_certify_points(p, (1 << 26) + 1, p, 5, p, 10, p, counts, aligned,
+                                       1 << 20, None)
+    assert rc == 1 and b"at most 2^26 points" in L.sdf_last_error()
+    rc = L.sdf_delaunay_merge_verified(p, 100, aligned, 1 << 20, p, 5, p, 1, None, 3, p, p, 10,
+                                       result, aligned, 1 << 20, None)
+    assert rc == 1 and b"NULL pointer" in L.sdf_last_error()
+    rc = L.sdf_delaunay_merge_verified(p, 100, aligned, 1 << 20, p, 1 << 31, p, 1 << 30, p,
+                                       1 << 30, p, p, 10, result, aligned, 1 << 20, None)
+    assert rc == 1 and b"too many reports" in L.sdf_last_error()
 
 
 def test_ray_order_and_plan_errors():
