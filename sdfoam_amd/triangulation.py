@@ -356,8 +356,8 @@ def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
     still fill a neighbourhood of v, and Delaunay tetrahedra do not
     overlap); all other Delaunay tetrahedra have four dirty vertices.
     Returns (tets, neighbors, stats); raises _Undecided like gpu_tetrahedra,
-    and when more than half the points are dirty (the caller then rebuilds in
-    full)."""
+    and when more than _INCREMENTAL_MAX_DIRTY of the points are dirty (the
+    caller then rebuilds in full)."""
     pts = points.contiguous()
     dev = pts.device
     n = pts.numel() // 3
@@ -387,9 +387,9 @@ def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
             raise _Undecided(f"{nd} of {n} points dirty")
         t1 = time.perf_counter()
         # the old hull's vertices (2) go to the open points uncertified: their
-        # cells are unbounded (or, if one moved inside, its tetrahedra still
-        # come from the other sources), and certifying them is the costliest
-        # part of the dirty points' certification
+        # cells are unbounded, so certifying them would only list them as
+        # open (and if one moved inside, its tetrahedra still come from the
+        # open points' candidates, the reports and the kept ones)
         hull_pts = torch.nonzero(dirty == 2).view(-1).to(torch.int32)
         inner = torch.nonzero(dirty == 1).view(-1).to(torch.int32)
         reports, U, counts = _certify(L, pts, gptr, gbytes, stream, query=inner)
