@@ -130,10 +130,11 @@ def main() -> int:
                     help="time Triangulation.rebuild (sort, GPU Delaunay with Qhull on the "
                          "open points, tables) on C3's 1M points, with Qhull on every point "
                          "beside it")
-    ap.add_argument("--perturb", type=float, default=0.02,
+    ap.add_argument("--perturb", type=float, default=0.001,
                     help="--triangulate: the incremental rebuilds move each point by this "
                          "share of its cell radius (farthest Delaunay neighbour) times N(0, 1) "
-                         "per coordinate")
+                         "per coordinate (past ~0.005 most points are dirty and the rebuild "
+                         "is a full one)")
     ap.add_argument("--render", action="store_true",
                     help="time the inference render (Pipeline.trace_benchmark, the reference's "
                          "benchmark.py) on the config's camera instead of the training step")
