@@ -380,7 +380,12 @@ __device__ __forceinline__ void walk_init(const SceneView &sc, uint32_t start, W
 // such t is <= t0 (then it lies outside the safe set, or the safe set is
 // empty while the unsafe one is not); sets si.agrees.
 // RB: walk over a cell table of RB-byte records (0: the scene's arrays).
-template <bool SAFE, bool COUNT, bool GUARD = false, bool DUAL = false, uint32_t RB = 0>
+// HALF: a batch's second pair of entries is loaded only by the lanes whose
+// row reaches it (fewer bytes for memory-bound walks of incoherent rays; one
+// more branch per batch, which costs more than it saves where a wavefront's
+// rays share their cells).
+template <bool SAFE, bool COUNT, bool GUARD = false, bool DUAL = false, uint32_t RB = 0,
+          bool HALF = false>
 __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ray,
                                              uint32_t max_steps, WalkState &ws, StepInfo &si,
                                              WalkCounters &wc) {
@@ -422,8 +427,19 @@ __device__ __forceinline__ void walk_advance(const SceneView &sc, const RayF &ra
     // batches of 4: the table is padded, so the last batch may over-read
     for (uint32_t k0 = 0; k0 < nf; k0 += 4) {
         uint2 h[4];
+        if constexpr (HALF && !GUARD) {
+            h[0] = row[k0];
+            h[1] = row[k0 + 1];
+            if (k0 + 2 < nf) {
+                h[2] = row[k0 + 2];
+                h[3] = row[k0 + 3];
+            } else {
+                h[2] = h[3] = make_uint2(0u, 0u); // past the row: dropped by k < nf
+            }
+        } else {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) h[u] = row[GUARD ? min(k0 + u, nf - 1) : k0 + u];
+            for (int u = 0; u < 4; ++u) h[u] = row[GUARD ? min(k0 + u, nf - 1) : k0 + u];
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const uint32_t k = k0 + u;

@@ -168,7 +168,9 @@ __device__ __forceinline__ void contrib_flush(ContribTable &ct, void *contributi
 // forward (src/tracing/pipeline.cu:36-264)
 
 // CT: walk over the cell table (a.scene.cells) and read attribute rows from it.
-template <int L, bool NEUS, bool STATS, typename AT, bool CT = false>
+// HALF: the face scan's half-batch loads (walk_advance), for rays in an
+// explicit launch order (incoherent batches such as random training pixels).
+template <int L, bool NEUS, bool STATS, typename AT, bool CT = false, bool HALF = false>
 __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
     constexpr uint32_t RB = CT ? cell_record_bytes(L, sizeof(AT)) : 0u;
     constexpr int nsh = (L + 1) * (L + 1);
@@ -222,14 +224,14 @@ __global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
         uint2 entry = make_uint2(kWalkUnrecorded, 0u);
         if (ws.alive) {
             if constexpr (NEUS || STATS) {
-                walk_advance<true, STATS, false, false, RB>(a.scene, ray, max_steps, ws, si, wc);
+                walk_advance<true, STATS, false, false, RB, HALF>(a.scene, ray, max_steps, ws, si, wc);
                 entry = make_uint2(si.found ? si.next : kNoIndex,
                                    __builtin_bit_cast(uint32_t, si.t1));
             } else {
                 // the density backward walks in the unsafe mode: a step is
                 // recorded while that walk takes the same exit; from the first
                 // step where it would not, the backward scans for itself
-                walk_advance<true, false, false, true, RB>(a.scene, ray, max_steps, ws, si, wc);
+                walk_advance<true, false, false, true, RB, HALF>(a.scene, ray, max_steps, ws, si, wc);
                 if (si.agrees)
                     entry = make_uint2(si.found ? si.next : kNoIndex,
                                        __builtin_bit_cast(uint32_t, si.t1));
@@ -1233,9 +1235,14 @@ template <int L, typename AT>
 static hipError_t launch_forward_L(const FwdArgs &a, bool neus, bool stats, hipStream_t stream) {
     const dim3 grid(grid_blocks_for_tiles(a.num_tiles));
     const bool ct = a.scene.cells != nullptr;
+    // rays in an explicit order are an incoherent batch: half-batch face loads
+    const bool half = a.order != nullptr;
     if (neus) {
         if (stats) {
             hipLaunchKernelGGL((forward_kernel<L, true, true, AT>), grid, dim3(kBlock), 0, stream, a);
+        } else if (ct && half) {
+            hipLaunchKernelGGL((forward_kernel<L, true, false, AT, true, true>), grid, dim3(kBlock),
+                               0, stream, a);
         } else if (ct) {
             hipLaunchKernelGGL((forward_kernel<L, true, false, AT, true>), grid, dim3(kBlock), 0,
                                stream, a);
@@ -1245,6 +1252,9 @@ static hipError_t launch_forward_L(const FwdArgs &a, bool neus, bool stats, hipS
     } else {
         if (stats) {
             hipLaunchKernelGGL((forward_kernel<L, false, true, AT>), grid, dim3(kBlock), 0, stream, a);
+        } else if (ct && half) {
+            hipLaunchKernelGGL((forward_kernel<L, false, false, AT, true, true>), grid,
+                               dim3(kBlock), 0, stream, a);
         } else if (ct) {
             hipLaunchKernelGGL((forward_kernel<L, false, false, AT, true>), grid, dim3(kBlock), 0,
                                stream, a);
