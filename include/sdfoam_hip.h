@@ -80,6 +80,11 @@ size_t sdf_trace_scratch_bytes(uint32_t num_points, uint32_t adjacency_size);
 /* adjacent_diff[k] = fp16(points[adjacency[k]] - points[i]) for every CSR
  * entry k of row i, 4 halves per entry (w = 0); rows with out-of-range
  * neighbours get NaN planes.  `adjacent_diff` holds (E + 32) x 4 halves.
+ * Offsets are expected non-decreasing (a CSR row array, as the reference's
+ * triangulation writes them).  With others the entries are unspecified, as
+ * in the reference (its one-thread-per-row kernel writes overlapping rows
+ * racily and leaves entries outside every row unwritten); every read and
+ * write stays within the table. */
  * Replaces prefetch_adjacent_diff (src/tracing/pipeline.h:70-77,
  * src/tracing/pipeline.cu:1202-1242). */
 int sdf_prefetch_adjacent_diff(const float *points, uint32_t num_points,

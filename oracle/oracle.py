@@ -47,6 +47,7 @@ class _Visits(C.Structure):
         ("faces", C.c_void_p),
         ("faces_stepped", C.c_void_p),
         ("t_exit", C.c_void_p),
+        ("point_visits", C.c_void_p),
     ]
 
 
@@ -220,6 +221,7 @@ class ForwardResult:
     cells: np.ndarray | None
     cell_alphas: np.ndarray | None
     t_exit: np.ndarray | None
+    point_visits: np.ndarray | None = None  # [N] u32: steps into each point
 
 
 def _settings(alpha_mode, weight_threshold, max_intersections, sdf_channel, D):
@@ -237,7 +239,11 @@ def _settings(alpha_mode, weight_threshold, max_intersections, sdf_channel, D):
 def trace_forward(sh_degree, points, attributes, adjacency, offsets, rays, start_point,
                   depth_quantiles=None, *, alpha_mode="sdfoam", inv_s=1.0,
                   weight_threshold=None, max_intersections=None, sdf_channel=None,
-                  return_contribution=True, record=0, threads=1) -> ForwardResult:
+                  return_contribution=True, record=0, threads=1,
+                  point_visits=False) -> ForwardResult:
+    """point_visits=True also counts each point's cell steps over all rays
+    (`ForwardResult.point_visits`: the number K of terms of its contribution
+    sum, for the summation bound of the parity tests)."""
     points = _c(points, np.float32)
     attributes = _c(attributes, np.float32)
     adjacency = _c(adjacency, np.uint32)
@@ -265,8 +271,9 @@ def trace_forward(sh_degree, points, attributes, adjacency, offsets, rays, start
     cells = np.zeros((R, record), dtype=np.uint32) if record else None
     calpha = np.zeros((R, record), dtype=np.float32) if record else None
     texit = np.zeros((R, record), dtype=np.float32) if record else None
+    pvis = np.zeros(N, dtype=np.uint32) if point_visits else None
     vis = _Visits(_p(vh), _p(cells), _p(calpha), record, _p(steps), _p(faces), _p(faces_st),
-                  _p(texit))
+                  _p(texit), _p(pvis))
     rc = lib().oracle_trace_forward(
         C.byref(st), sh_degree, N, _p(points), _p(attributes), adjacency.size, _p(adjacency),
         _p(offsets), R, _p(rays), _p(start), Q, _p(quant), _p(sharp), _p(rgba), _p(depth),
@@ -281,7 +288,7 @@ def trace_forward(sh_degree, points, attributes, adjacency, offsets, rays, start
         None if contrib is None else contrib.reshape(N, 1),
         alpha.reshape(N, 1),
         vh.reshape(lead), steps.reshape(lead), faces.reshape(lead), faces_st.reshape(lead),
-        cells, calpha, texit)
+        cells, calpha, texit, pvis)
 
 
 @dataclass
@@ -337,7 +344,7 @@ def trace_backward(sh_degree, points, attributes, adjacency, offsets, rays, star
     g = _Grads(_p(pg), _p(ag), _p(sg), _p(pe), _p(pga), _p(aga), _p(sga), _p(pgk), _p(agk), _p(sgk))
     vh = np.zeros(R, dtype=np.uint64)
     steps = np.zeros(R, dtype=np.uint32)
-    vis = _Visits(_p(vh), None, None, 0, _p(steps), None, None, None)
+    vis = _Visits(_p(vh), None, None, 0, _p(steps), None, None, None, None)
     rc = lib().oracle_trace_backward(
         C.byref(st), sh_degree, N, _p(points), _p(attributes), adjacency.size, _p(adjacency),
         _p(offsets), R, _p(rays), _p(start), Q, _p(quant), _p(didx), _p(rgba), _p(grad_rgba),

@@ -272,6 +272,8 @@ typedef struct {
 static void visit_push(visit_rec *vr, uint32_t cell, float alpha, float t1) {
     vr->hash ^= (uint64_t)cell;
     vr->hash *= 0x100000001b3ull;
+    if (vr->v && vr->v->point_visits)
+        __atomic_fetch_add(&vr->v->point_visits[cell], 1u, __ATOMIC_RELAXED);
     if (vr->v && vr->count < vr->v->stride) {
         if (vr->v->cells) vr->v->cells[vr->ray * vr->v->stride + vr->count] = cell;
         if (vr->v->alphas) vr->v->alphas[vr->ray * vr->v->stride + vr->count] = alpha;

@@ -45,7 +45,9 @@ typedef struct {
  * hash: FNV-1a 64 over the cell index of every cell step (functor call);
  * cells/alphas: the first `stride` steps of each ray, row-major [R, stride];
  * steps: number of cell steps of each ray;
- * faces: number of faces scanned by each ray (all loop iterations). */
+ * faces: number of faces scanned by each ray (all loop iterations);
+ * point_visits: per point, the number of cell steps into it (the count K of
+ * terms in its contribution sum). */
 typedef struct {
     uint64_t *hash;
     uint32_t *cells;
@@ -55,6 +57,7 @@ typedef struct {
     uint64_t *faces;
     uint64_t *faces_stepped; /* faces of the cells that got a functor call */
     float *t_exit;           /* [R, stride]: t1 of each recorded step */
+    uint32_t *point_visits;  /* [N]: cell steps into each point over all rays */
 } oracle_visits;
 
 const char *oracle_version(void);

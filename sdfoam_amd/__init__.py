@@ -11,7 +11,7 @@ calling the tracer does.
 """
 
 from .fetch import BatchFetcher
-from .pipeline import Pipeline, create_pipeline, prefetch_adjacent_diff
+from .pipeline import Pipeline, create_pipeline, prefetch_adjacent_diff, release_trace_plan
 from .render import ErrorBox, TraceRays
 from .spatial import build_aabb_tree, get_starting_point, nn
 from .triangulation import Triangulation, TriangulationFailedError, farthest_neighbor
@@ -20,6 +20,7 @@ __all__ = [
     "Pipeline",
     "create_pipeline",
     "prefetch_adjacent_diff",
+    "release_trace_plan",
     "TraceRays",
     "ErrorBox",
     "build_aabb_tree",

@@ -276,6 +276,15 @@ def _backward_can_follow(points, attributes, inv_s) -> bool:
 _PLAN_ATTR = "_sdfoam_trace_plan"
 
 
+def release_trace_plan(rgba: torch.Tensor) -> None:
+    """Drop the trace plan (walk record, ray order, offset table) that a
+    forward attached to its ``rgba``, for an ``rgba`` kept without a backward
+    over it (no counterpart in the reference).  A later backward over that
+    ``rgba`` scans for itself, with the same results."""
+    if hasattr(rgba, _PLAN_ATTR):
+        delattr(rgba, _PLAN_ATTR)
+
+
 def _auto_sort(sort_rays, settings, num_rays: int) -> bool:
     if sort_rays is None:
         return int(settings.ray_image_width) == 0 and num_rays >= AUTO_SORT_MIN_RAYS

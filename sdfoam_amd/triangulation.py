@@ -225,8 +225,10 @@ def _open_candidates(L, pts: torch.Tensor, U: torch.Tensor, stream, stats: dict)
         gbuf, gp = _aligned(gb, pts.device)
         try:
             rep, U2, _ = _certify(L, pts[U.long()].contiguous(), gp, gb, stream)
-        except (_Undecided, TriangulationFailedError):
+        except _Undecided:
             rep = None
+        # a TriangulationFailedError (coincident open points) propagates: the
+        # points coincide in the whole set too
         del gbuf
         if rep is not None and U2.numel() <= _LEVEL_SHRINK * U.numel():
             if rep.shape[0]:
@@ -253,6 +255,21 @@ def _open_candidates(L, pts: torch.Tensor, U: torch.Tensor, stream, stats: dict)
     stats["open_levels_s"] = t_levels - t
     stats["open_qhull_s"] = t_qhull - t_levels
     return cand.to(torch.int32).contiguous(), int((nbr_u < 0).sum())
+
+
+def has_coincident_points(pts: torch.Tensor) -> bool:
+    """Whether two of the CUDA float32 points [n, 3] are equal (+0 equals
+    -0): the coordinates' bit patterns sorted lexicographically by three
+    stable sorts, then neighbouring rows compared.  Exact, ~1 ms at 1M
+    points."""
+    if pts.shape[0] < 2:
+        return False
+    b = (pts + 0.0).view(torch.int32)  # -0 + 0 = +0
+    order = torch.sort(b[:, 2], stable=True)[1]
+    order = order[torch.sort(b[order, 1], stable=True)[1]]
+    order = order[torch.sort(b[order, 0], stable=True)[1]]
+    s = b[order]
+    return bool((s[1:] == s[:-1]).all(dim=1).any().item())
 
 
 def _merge(L, pts: torch.Tensor, gptr: int, gbytes: int, reports, cand, verified,
@@ -380,6 +397,12 @@ def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
         if rc == _lib.SDF_E_INVALID:
             raise _Undecided(L.sdf_last_error().decode())
         check(rc)
+        # the certification finds a point equal to the one it certifies; the
+        # points it does not certify here (clean ones, the old hull's) are
+        # checked for coincidence over the whole set, as the reference's
+        # incremental rebuild does (src/delaunay/delaunay.cu:291-294)
+        if has_coincident_points(pts):
+            raise TriangulationFailedError("duplicate points found")
         D = torch.nonzero(dirty).view(-1).to(torch.int32)
         nd = int(D.numel())
         stats.update({"dirty": nd, "kept_old": int(keep[:T_old].sum().item())})

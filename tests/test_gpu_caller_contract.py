@@ -24,7 +24,7 @@ import numpy as np
 import pytest
 
 from conftest import scene
-from test_gpu_parity import U, assert_close_model, gamma, to_dev, u32, _threads
+from test_gpu_parity import U, assert_close_model, gamma, sum_depth, to_dev, u32, _threads
 
 pytestmark = pytest.mark.gpu
 
@@ -144,7 +144,7 @@ def _check(w, st, mode, oracle_lib):
         sa = ref.sharpness_abs if np.isfinite(ref.sharpness_grad) else 0.0
         expect = sg * w.inv_s
         got = float(st["variance"].grad.cpu())
-        tol = 1e-5 + 1e-4 * abs(expect) + gamma(ref.sharpness_k) * sa * w.inv_s + 4 * U * abs(expect)
+        tol = 1e-5 + 1e-4 * abs(expect) + gamma(min(ref.sharpness_k, sum_depth(w, ref))) * sa * w.inv_s + 4 * U * abs(expect)
         assert abs(got - expect) <= tol, (got, expect, tol)
     else:
         # softplus_beta10'(x) = sigmoid(10 x): the tracer's density gradient times it

@@ -37,6 +37,8 @@ def _threads():
 def gamma(k):
     k = np.maximum(np.asarray(k, dtype=np.float64) - 1.0, 0.0)
     ku = k * U
+    # the bound holds for n u < 1 only; a count past that must not pass silently
+    assert np.all(ku < 0.5), f"summation bound vacuous for K up to {int(k.max()) + 1}"
     return ku / (1.0 - ku)
 
 
@@ -271,7 +273,8 @@ def _forward_both(w, dev, oracle_lib, mode, record=0, inv_s=None, sort_rays=None
     torch.cuda.synchronize()
     ref = oracle_lib.trace_forward(
         w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets, w.rays, w.extra["start"],
-        w.quantiles, alpha_mode=mode, inv_s=inv, record=record, threads=_threads())
+        w.quantiles, alpha_mode=mode, inv_s=inv, record=record, threads=_threads(),
+        point_visits=True)
     return out, st, ref
 
 
@@ -295,7 +298,11 @@ def _check_forward(out, st, ref, w, record):
     assert_close("depth", out["depth"].cpu().numpy().reshape(R, -1), ref.depth.reshape(R, -1))
     contrib = out["contribution"].cpu().numpy().reshape(-1)
     cref = ref.contribution.reshape(-1)
-    assert_close_model("contribution", contrib, cref, np.abs(cref), R)
+    # each point's sum has K = its number of cell steps over all rays of
+    # fp32 weights (>= 0, the same bits on both sides); unvisited points stay 0
+    k = ref.point_visits
+    assert np.all(contrib[k == 0] == 0.0), "contribution of unvisited points"
+    assert_close_model("contribution", contrib, cref, np.abs(cref), k)
     # alpha: some visiting step's value; unvisited points untouched
     alpha = out["alpha"].cpu().numpy().reshape(-1)
     visited = np.zeros(w.num_points, dtype=bool)
@@ -402,6 +409,22 @@ def record_rows(plan):
     return E, Cc, np.repeat(have, 16, axis=1)
 
 
+def sum_depth(w, ref):
+    """Depth of the backward's summation tree for the sharpness scalar: the
+    most steps one lane takes (from the oracle backward `ref`, same walks),
+    six wave-reduction levels and one atomic per wavefront of the launch
+    (16x16-pixel tiles of four wavefronts for image-shaped rays, 256-ray
+    blocks otherwise; the tile count is also an upper bound for the same rays
+    launched flat, ceil(W H / 256) <= ceil(W / 16) ceil(H / 16))."""
+    steps = int(ref.steps.max()) if w.num_rays else 0
+    if w.rays.ndim >= 3:
+        h, wd = w.rays.shape[-3], w.rays.shape[-2]
+        waves = 4 * (-(-wd // 16)) * (-(-(w.num_rays // wd) // 16))
+    else:
+        waves = 4 * (-(-w.num_rays // 256))
+    return steps + 6 + waves
+
+
 def _check_backward(bwd, st, ref, w):
     R = w.num_rays
     vh = st["visit_hash"].cpu().numpy().view(np.uint64)
@@ -411,8 +434,13 @@ def _check_backward(bwd, st, ref, w):
     assert_close_model("attr_grad", bwd["attr_grad"].cpu().numpy(), ref.attr_grad,
                        ref.attr_grad_abs, ref.attr_grad_k)
     sg = float(bwd["sharpness_grad"].cpu().numpy().reshape(-1)[0])
+    # the kernel sums a lane's steps in order, reduces the wave in 6 levels
+    # and adds one value per wavefront to the scalar: no term passes through
+    # more than (steps of a lane) + 6 + (wavefronts) additions, the depth of
+    # that summation tree, which bounds the error as K does for a chain
     assert_close_model("sharpness_grad", np.array([sg]), np.array([ref.sharpness_grad]),
-                       np.array([ref.sharpness_abs]), np.array([ref.sharpness_k]))
+                       np.array([ref.sharpness_abs]),
+                       np.array([min(ref.sharpness_k, sum_depth(w, ref))]))
     print(f"sharpness: gpu {sg!r} ref {ref.sharpness_grad!r} |d| {abs(sg - ref.sharpness_grad):.3e} "
           f"sqrt(K) u A {np.sqrt(max(ref.sharpness_k, 1)) * U * ref.sharpness_abs:.3e}")
     if "point_error" in bwd:

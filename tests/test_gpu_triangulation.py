@@ -293,6 +293,35 @@ def test_incremental_rebuild_falls_back_when_most_points_move(dev):
     assert np.array_equal(_np(tri.point_adjacency()), host["point_adjacency"])
 
 
+@pytest.mark.parametrize("where", ["hull", "interior"])
+def test_incremental_rebuild_rejects_coincident_points(dev, where):
+    """An incremental rebuild over points where one was moved onto another
+    raises TriangulationFailedError, as the reference's does
+    (src/delaunay/delaunay.cu:291-294): for two vertices of the old hull
+    (which the rebuild sends to the open points without certifying them) and
+    for two interior points; the triangulation stays usable afterwards."""
+    import torch
+
+    import sdfoam_amd
+
+    raw = np.ascontiguousarray(_gpu_sets()["gaussian"](), dtype=np.float32)
+    tri = sdfoam_amd.Triangulation(torch.from_numpy(raw).to(dev))
+    pts = raw[tri.permutation().view(torch.int32).cpu().numpy()]
+    tets = _np(tri.tets()).reshape(-1, 4)
+    adj = _np(tri.tet_adjacency()).reshape(-1, 4)
+    on_hull = np.zeros(pts.shape[0], dtype=bool)
+    for t, j in zip(*np.nonzero(adj == 0xFFFFFFFF)):
+        on_hull[np.delete(tets[t], j)] = True
+    pick = np.nonzero(on_hull if where == "hull" else ~on_hull)[0]
+    a, b = int(pick[0]), int(pick[len(pick) // 2])
+    moved = pts.copy()
+    moved[a] = moved[b]
+    with pytest.raises(sdfoam_amd.TriangulationFailedError, match="duplicate points"):
+        tri.rebuild(torch.from_numpy(moved).to(dev), incremental=True)
+    assert tri.rebuild(torch.from_numpy(pts).to(dev), incremental=True) is False
+    assert tri.last_method == "gpu"
+
+
 def test_triangulation_methods_agree(dev):
     import torch
 

@@ -137,3 +137,20 @@ def test_record_walk_default_follows_autograd():
     with torch.no_grad():
         assert _backward_can_follow(pts, frozen, inv)
     assert not _backward_can_follow(pts.detach(), frozen, 50.0)
+
+
+def test_release_trace_plan_drops_the_record():
+    """release_trace_plan removes the plan a forward attached to its rgba
+    (a kept rgba then holds no walk record); a tensor without one is left as
+    it is."""
+    import torch
+
+    import sdfoam_amd
+    from sdfoam_amd import pipeline
+
+    rgba = torch.zeros(4, 4)
+    setattr(rgba, pipeline._PLAN_ATTR, object())
+    sdfoam_amd.release_trace_plan(rgba)
+    assert not hasattr(rgba, pipeline._PLAN_ATTR)
+    sdfoam_amd.release_trace_plan(rgba)
+    sdfoam_amd.release_trace_plan(torch.zeros(2))

@@ -25,8 +25,23 @@ def c1_fwd(oracle_lib):
     w = scene(1)
     f = oracle_lib.trace_forward(w.sh_degree, w.points, w.attributes, w.adjacency, w.offsets,
                                  w.rays, w.extra["start"], w.quantiles, inv_s=w.inv_s, record=64,
-                                 threads=4)
+                                 threads=4, point_visits=True)
     return w, f
+
+
+def test_point_visits_count_the_steps(c1_fwd):
+    """The oracle's per-point visit counts (the K of the contribution sums'
+    tolerance) equal the occurrences of each point in the recorded visit
+    sequences, and a point is visited iff its contribution is nonzero or a
+    zero-weight step reached it."""
+    w, f = c1_fwd
+    R = w.num_rays
+    steps = f.steps.reshape(R)
+    mask = np.arange(64)[None, :] < steps[:, None]
+    want = np.bincount(f.cells[mask], minlength=w.num_points)
+    assert np.array_equal(f.point_visits, want)
+    assert int(f.point_visits.sum()) == int(steps.sum())
+    assert np.all(f.contribution.reshape(-1)[f.point_visits == 0] == 0.0)
 
 
 def test_visits_are_paths(c1_fwd):

@@ -115,3 +115,32 @@ def test_farthest_neighbor_oracle_against_float64():
     i2, r2 = oracle.farthest_neighbor(pts2, np.array([1], dtype=np.uint32),
                                       np.array([0, 1, 1, 1], dtype=np.uint32))
     assert i2[0] == 0xFFFFFFFF and r2[0] == 0.0 and np.isnan(r2[1])
+
+
+def test_has_coincident_points():
+    """The incremental rebuild's duplicate check (exact: equal bit patterns
+    after +0 / -0 are made equal), on host tensors: planted duplicates are
+    found wherever they sit in the order, points one ulp apart and equal
+    coordinates in other rows are not."""
+    import torch
+
+    from sdfoam_amd.triangulation import has_coincident_points
+
+    rng = np.random.default_rng(3)
+    pts = rng.normal(size=(5000, 3)).astype(np.float32)
+    # rows sharing one or two coordinates with another row are not duplicates
+    pts[10, :2] = pts[20, :2]
+    pts[30, 0] = pts[40, 0]
+    assert not has_coincident_points(torch.from_numpy(pts))
+    for i, j in [(0, 1), (0, 4999), (1234, 17), (4998, 4999)]:
+        q = pts.copy()
+        q[i] = q[j]
+        assert has_coincident_points(torch.from_numpy(q)), (i, j)
+    q = pts.copy()
+    q[5] = np.nextafter(q[6], np.float32(np.inf))
+    assert not has_coincident_points(torch.from_numpy(q))
+    q = pts.copy()
+    q[7] = [0.0, 1.5, -2.0]
+    q[8] = [-0.0, 1.5, -2.0]
+    assert has_coincident_points(torch.from_numpy(q))
+    assert not has_coincident_points(torch.from_numpy(pts[:1]))
