@@ -114,8 +114,8 @@ def main() -> int:
                          "2^20 rays and looks up their start cells)")
     ap.add_argument("--cpu-stride", type=int, default=-1,
                     help="CPU baseline traces every n-th ray (0 skips it; default: the "
-                         "smallest n >= 3 that keeps the sample to about 640k rays, "
-                         "10-20 s on 16 threads)")
+                         "smallest n that keeps the sample to at most 1.92M rays: every ray "
+                         "of C3, about 30 s on 16 threads)")
     ap.add_argument("--alpha-mode", default="sdfoam", choices=["sdfoam", "standard"],
                     help="sdfoam (NeuS alpha, backward_sdf; the headline) or standard "
                          "(density alpha, the density backward; the scene's last channel is a "
@@ -430,7 +430,7 @@ def main() -> int:
     if args.cpu_stride != 0:
         b0 = batches[0]
         n_rays = b0["rays_np"].size // 6
-        stride = args.cpu_stride if args.cpu_stride > 0 else max(3, -(-n_rays // CPU_SAMPLE_RAYS))
+        stride = args.cpu_stride if args.cpu_stride > 0 else max(1, -(-n_rays // CPU_SAMPLE_RAYS))
         result["cpu_baseline"] = cpu_baseline(
             w, b0["rays_np"], host_start, b0["q"].cpu().numpy(),
             b0["g"].float().cpu().numpy(), b0["dg"].cpu().numpy(), stride, args.alpha_mode)
@@ -440,7 +440,7 @@ def main() -> int:
     return 0
 
 
-CPU_SAMPLE_RAYS = 640_000
+CPU_SAMPLE_RAYS = 1_920_000
 
 
 def load_counters(name):
@@ -824,14 +824,16 @@ def cpu_baseline(w, rays, start, quantiles, grad_rgba, depth_grad, stride: int,
         return r.shape[0], int(np.sum(f.steps)), dt
 
     n, steps, dt = run(stride, threads)
-    # one thread on a sample a sixteenth the size (about as long)
-    n1, steps1, dt1 = run(stride * 16, 1)
+    # one thread on 1 ray in 48 or fewer (a few seconds)
+    stride1 = max(stride * 16, 48)
+    n1, steps1, dt1 = run(stride1, 1)
     return {
         "value": n / dt / 1e6,
         "unit": "Mrays/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"1 ray in {stride} of the same workload ({n} rays, {steps} cell steps), "
+        "sample": (f"every ray of the same workload ({n} rays" if stride == 1 else
+                   f"1 ray in {stride} of the same workload ({n} rays") + f", {steps} cell steps), "
                   f"forward + backward, {dt:.1f}s on {threads} threads (every CPU the process "
                   f"may use) of {cpu_model()}",
         "cell_steps_per_s": steps / dt,
@@ -840,7 +842,7 @@ def cpu_baseline(w, rays, start, quantiles, grad_rgba, depth_grad, stride: int,
         "cgroup_cpu_quota": cpu_quota(),
         "single_thread": {"value": n1 / dt1 / 1e6, "unit": "Mrays/s", "cores": 1,
                           "cell_steps_per_s": steps1 / dt1,
-                          "sample": f"1 ray in {stride * 16} ({n1} rays, {steps1} cell steps), "
+                          "sample": f"1 ray in {stride1} ({n1} rays, {steps1} cell steps), "
                                     f"{dt1:.1f}s on one thread"},
     }
 

@@ -84,7 +84,7 @@ size_t sdf_trace_scratch_bytes(uint32_t num_points, uint32_t adjacency_size);
  * triangulation writes them).  With others the entries are unspecified, as
  * in the reference (its one-thread-per-row kernel writes overlapping rows
  * racily and leaves entries outside every row unwritten); every read and
- * write stays within the table. */
+ * write stays within the table.
  * Replaces prefetch_adjacent_diff (src/tracing/pipeline.h:70-77,
  * src/tracing/pipeline.cu:1202-1242). */
 int sdf_prefetch_adjacent_diff(const float *points, uint32_t num_points,
