@@ -71,6 +71,19 @@ __device__ inline void record_store(float4 *p, float4 v) {
     __builtin_nontemporal_store(w, reinterpret_cast<f4v *>(p));
 }
 
+// Loads from the walk record (the backward reads each entry once): also
+// non-temporal, so the stream of record rows does not displace the cells'
+// points and gradient rows from L2.
+__device__ inline uint2 record_load(const uint2 *p) {
+    const uint64_t v = __builtin_nontemporal_load(reinterpret_cast<const uint64_t *>(p));
+    return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+}
+__device__ inline float4 record_load(const float4 *p) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v w = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(p));
+    return make_float4(w.x, w.y, w.z, w.w);
+}
+
 // wavefronts of the launch grid, the padding blocks included (they write
 // their "unrecorded" row)
 __host__ inline uint64_t walk_record_waves(uint32_t num_tiles) {

@@ -439,24 +439,28 @@ constexpr int kPitch = 65;
 
 // Trips per grouping pass.  A lane's steps wait in kWindow LDS entry slots
 // and are applied together every kWindow trips: rays of a wavefront enter
-// the cells that others of it have just left, so a pass over two trips'
-// steps meets about a third fewer distinct cells than two passes do.
-constexpr int kWindow = 2;
+// the cells that others of it have just left, so a pass over several trips'
+// steps meets fewer distinct cells than that many passes do (from oracle
+// walks of C3 tiles: 64% of the groups over two trips, 49% over three).
+// Three trips keep four blocks of 256 lanes per CU within its 160 KB of LDS
+// (L = 3 without point error: 39.5 KB per block).
+constexpr int kWindow = 3;
 
-template <int L>
+// PE: entries carry a point error (the caller asked for point_error).
+template <int L, bool PE>
 struct WaveTables {
     static constexpr int nsh = (L + 1) * (L + 1);
     static constexpr int kOnes = kPitch * nsh;      // offset of the row of ones
     static constexpr int kRec = kOnes + kPitch;     // offset of rec
-    static constexpr int kSlot = kPitch * 8;        // floats per entry slot
-    static constexpr int kZeros = kRec + kSlot * kWindow; // offset of the row of zeros
+    static constexpr int kComp = PE ? 8 : 7;        // components per entry
+    static constexpr int kSlot = kPitch * kComp;    // floats per entry slot
+    static constexpr int kEnd = kRec + kSlot * kWindow;
     // y [0, kOnes): SH basis function k of lane l at k * kPitch + l;
     // ones: the multiplier of the non-SH components;
-    // rec [kRec, kZeros): kWindow entry slots; in slot s, component c of
+    // rec [kRec, kEnd): kWindow entry slots; in slot s, component c of
     //   lane l's entry at s * kSlot + c * kPitch + l: dL/d(r, g, b, last
-    //   channel), flushed position gradient (x, y, z), point error;
-    // zeros: what the idle owner lanes read
-    float buf[kZeros + kPitch];
+    //   channel), flushed position gradient (x, y, z), point error (PE)
+    float buf[kEnd];
     __device__ float *y() { return buf; }
     __device__ float *rec() { return buf + kRec; }
 };
@@ -476,11 +480,11 @@ __device__ __forceinline__ uint32_t pop_member(uint64_t &mm) {
 //   i < 3 nsh (SH):      Y_{i/3}(m) * dL/drgb_{i%3}(m)   (sh_utils.cuh:85-92)
 //   i == last_ch:        1 * dL/dlast(m)
 //   i == 60, 61, 62:     1 * flushed position gradient x, y, z (m)
-//   i == 63:             1 * point error(m)
-//   others:              1 * 0 (the zero row)
+//   i == 63 (PE):        1 * point error(m)
+//   others:              a live component whose sum the lane never writes
 struct OwnerLane {
     int y_base, g_base; // member m of slot 0: y = buf[y_base + m], g = buf[g_base + m]
-    int g_slot;         // g of slot s is s * g_slot further (0 on the zero row)
+    int g_slot;         // g of slot s is s * g_slot further
     bool also_last;     // last_ch is an SH component too: add dL/dlast as well
     // gradient accumulator row: this lane's float in a cell's row, and whether
     // the lane adds to it (attribute and position components; the point
@@ -489,16 +493,16 @@ struct OwnerLane {
     bool row_active;
 };
 
-template <int L>
-__device__ __forceinline__ OwnerLane owner_lane(int last_ch, bool point_error) {
-    using T = WaveTables<L>;
+template <int L, bool PE>
+__device__ __forceinline__ OwnerLane owner_lane(int last_ch) {
+    using T = WaveTables<L, PE>;
     constexpr int nsh = (L + 1) * (L + 1);
     const int lane = (int)lane_id();
     constexpr int D = 1 + 3 * nsh;
     OwnerLane o;
     o.also_last = false;
     o.row_off = lane < D ? (uint32_t)lane : lane >= 60 ? (uint32_t)(D + lane - 60) : 0u;
-    o.row_active = lane < D || (lane >= 60 && lane < 63) || (lane == 63 && point_error);
+    o.row_active = lane < D || (lane >= 60 && lane < 63) || (lane == 63 && PE);
     if (lane < 3 * nsh) {
         o.y_base = (lane / 3) * kPitch;
         o.g_base = T::kRec + (lane % 3) * kPitch;
@@ -509,13 +513,13 @@ __device__ __forceinline__ OwnerLane owner_lane(int last_ch, bool point_error) {
             o.g_base = T::kRec + 3 * kPitch;
         } else if (lane >= 60 && lane < 63) {
             o.g_base = T::kRec + (4 + (lane - 60)) * kPitch;
-        } else if (lane == 63) {
+        } else if (lane == 63 && PE) {
             o.g_base = T::kRec + 7 * kPitch;
         } else {
-            o.g_base = T::kZeros;
+            o.g_base = T::kRec; // read, summed, never written (row_active is false)
         }
     }
-    o.g_slot = o.g_base == T::kZeros ? 0 : T::kSlot;
+    o.g_slot = T::kSlot;
     return o;
 }
 
@@ -560,7 +564,7 @@ struct StepEntries {
     uint32_t key[kWindow]; // cell of the complete entry in slot s
     uint32_t ready;        // bit s: slot s holds a complete entry not yet applied
     uint32_t flushed;      // bit s: that entry carries a flushed position gradient
-    uint32_t count;        // entries published so far
+    uint32_t next_slot;    // slot of the next entry published (entries go round)
     uint32_t pend_slot;    // slot of the pending entry
     uint32_t pend_cell;    // its cell
     bool pend;             // an entry waits for its position flush
@@ -571,7 +575,7 @@ __device__ __forceinline__ void entries_init(StepEntries &e) {
     for (int s = 0; s < kWindow; ++s) e.key[s] = 0u;
     e.ready = 0u;
     e.flushed = 0u;
-    e.count = 0u;
+    e.next_slot = 0u;
     e.pend_slot = 0u;
     e.pend_cell = 0u;
     e.pend = false;
@@ -579,10 +583,10 @@ __device__ __forceinline__ void entries_init(StepEntries &e) {
 
 // Attaches the flushed position gradient (flush) or zeros to the pending
 // entry and marks it complete.
-template <int L>
+template <int L, bool PE>
 __device__ __forceinline__ void complete_entry(StepEntries &e, bool flush, const float *flush_g,
-                                               WaveTables<L> &tb) {
-    float *r = tb.rec() + e.pend_slot * WaveTables<L>::kSlot + lane_id();
+                                               WaveTables<L, PE> &tb) {
+    float *r = tb.rec() + e.pend_slot * WaveTables<L, PE>::kSlot + lane_id();
     r[4 * kPitch] = flush ? flush_g[0] : 0.0f;
     r[5 * kPitch] = flush ? flush_g[1] : 0.0f;
     r[6 * kPitch] = flush ? flush_g[2] : 0.0f;
@@ -595,23 +599,23 @@ __device__ __forceinline__ void complete_entry(StepEntries &e, bool flush, const
     e.pend = false;
 }
 
-// Publishes a lane's step (components 0..3, 7 of its entry) as the pending
-// entry.
-template <int L>
-__device__ __forceinline__ void publish_step(WaveTables<L> &tb, StepEntries &e, uint32_t cell,
+// Publishes a lane's step (components 0..3, and 7 with PE, of its entry) as
+// the pending entry.
+template <int L, bool PE>
+__device__ __forceinline__ void publish_step(WaveTables<L, PE> &tb, StepEntries &e, uint32_t cell,
                                              float gr, float gg, float gb, float g_last,
                                              float perr) {
-    const uint32_t slot = e.count % (uint32_t)kWindow;
-    float *r = tb.rec() + slot * WaveTables<L>::kSlot + lane_id();
+    const uint32_t slot = e.next_slot;
+    float *r = tb.rec() + slot * WaveTables<L, PE>::kSlot + lane_id();
     r[0] = gr;
     r[kPitch] = gg;
     r[2 * kPitch] = gb;
     r[3 * kPitch] = g_last;
-    r[7 * kPitch] = perr;
+    if constexpr (PE) r[7 * kPitch] = perr;
     e.pend_slot = slot;
     e.pend_cell = cell;
     e.pend = true;
-    ++e.count;
+    e.next_slot = slot + 1u == (uint32_t)kWindow ? 0u : slot + 1u;
 }
 
 // Grouped gradient updates of the wave's complete entries (all 64 lanes
@@ -632,9 +636,9 @@ __device__ __forceinline__ void publish_step(WaveTables<L> &tb, StepEntries &e, 
 // !ACC: straight into attr_grad, points_grad (only when an entry of the
 // group flushed a position) and point_error.
 // ALSO_LAST: the last channel is an SH component too (sdf_channel < 3 nsh).
-template <int L, typename AT, bool ACC, bool ALSO_LAST>
+template <int L, bool PE, typename AT, bool ACC, bool ALSO_LAST>
 __device__ __forceinline__ void grouped_pass_impl(StepEntries &e, const OwnerLane &ow,
-                                                  WaveTables<L> &tb, void *__restrict__ attr_grad,
+                                                  WaveTables<L, PE> &tb, void *__restrict__ attr_grad,
                                                   void *__restrict__ point_error,
                                                   float *__restrict__ points_grad,
                                                   float *__restrict__ row) {
@@ -647,12 +651,17 @@ __device__ __forceinline__ void grouped_pass_impl(StepEntries &e, const OwnerLan
         todo[s] = __ballot((e.ready >> s) & 1u);
         flushing[s] = ACC ? 0ull : __ballot((e.flushed >> s) & 1u);
     }
-    static_assert(kWindow == 2, "the leader selection below takes two slots");
     while (true) {
         // leader: the first entry left, in slot order (selects, no branches)
-        const uint64_t lead = todo[0] ? todo[0] : todo[1];
+        uint64_t lead = todo[kWindow - 1];
+        uint32_t lead_key = e.key[kWindow - 1];
+#pragma unroll
+        for (int s = kWindow - 2; s >= 0; --s) {
+            lead_key = todo[s] ? e.key[s] : lead_key;
+            lead = todo[s] ? todo[s] : lead;
+        }
         if (!lead) break;
-        const uint32_t c = readlane_u(todo[0] ? e.key[0] : e.key[1], first_lane(lead));
+        const uint32_t c = readlane_u(lead_key, first_lane(lead));
         // every ready entry of cell c is still in todo[s]
         uint64_t grp[kWindow];
         uint64_t flush_any = 0ull;
@@ -667,7 +676,7 @@ __device__ __forceinline__ void grouped_pass_impl(StepEntries &e, const OwnerLan
         float acc = 0.0f;
 #pragma unroll
         for (int s = 0; s < kWindow; ++s) {
-            const float *ls = last + s * WaveTables<L>::kSlot;
+            const float *ls = last + s * WaveTables<L, PE>::kSlot;
             acc = acc + sum_members<ALSO_LAST>(grp[s], tb.buf, ow, s, ls);
         }
         if constexpr (ACC) {
@@ -681,13 +690,13 @@ __device__ __forceinline__ void grouped_pass_impl(StepEntries &e, const OwnerLan
                     dst = static_cast<float *>(attr_grad) + (uint64_t)c * D + lane;
                 } else if (lane >= 60u && lane < 63u) {
                     if (pos) dst = points_grad + 3ull * c + (lane - 60u);
-                } else if (lane == 63u && point_error) {
+                } else if (PE && lane == 63u) {
                     dst = static_cast<float *>(point_error) + c;
                 }
                 if (dst) atomicAdd(dst, acc);
             } else {
                 atomic_add_row<AT>(attr_grad, c, lane, (uint32_t)D, acc);
-                if (point_error && lane == 63u) atomic_add_elem<AT>(point_error, c, acc);
+                if (PE && lane == 63u) atomic_add_elem<AT>(point_error, c, acc);
                 if (pos && lane >= 60u && lane < 63u)
                     atomicAdd(points_grad + 3ull * c + (lane - 60u), acc);
             }
@@ -706,24 +715,24 @@ struct PassTarget {
     bool also_last;     // some owner lane adds the last channel to an SH component
 };
 
-template <int L, typename AT>
+template <int L, bool PE, typename AT>
 __device__ __forceinline__ void grouped_pass(StepEntries &e, const OwnerLane &ow,
-                                             WaveTables<L> &tb, const PassTarget &t) {
+                                             WaveTables<L, PE> &tb, const PassTarget &t) {
     __builtin_amdgcn_wave_barrier();
     if (t.row) {
         if (t.also_last)
-            grouped_pass_impl<L, AT, true, true>(e, ow, tb, t.attr_grad, t.point_error,
-                                                 t.points_grad, t.row);
+            grouped_pass_impl<L, PE, AT, true, true>(e, ow, tb, t.attr_grad, t.point_error,
+                                                     t.points_grad, t.row);
         else
-            grouped_pass_impl<L, AT, true, false>(e, ow, tb, t.attr_grad, t.point_error,
-                                                  t.points_grad, t.row);
+            grouped_pass_impl<L, PE, AT, true, false>(e, ow, tb, t.attr_grad, t.point_error,
+                                                      t.points_grad, t.row);
     } else {
         if (t.also_last)
-            grouped_pass_impl<L, AT, false, true>(e, ow, tb, t.attr_grad, t.point_error,
-                                                  t.points_grad, t.row);
+            grouped_pass_impl<L, PE, AT, false, true>(e, ow, tb, t.attr_grad, t.point_error,
+                                                      t.points_grad, t.row);
         else
-            grouped_pass_impl<L, AT, false, false>(e, ow, tb, t.attr_grad, t.point_error,
-                                                   t.points_grad, t.row);
+            grouped_pass_impl<L, PE, AT, false, false>(e, ow, tb, t.attr_grad, t.point_error,
+                                                       t.points_grad, t.row);
     }
     __builtin_amdgcn_wave_barrier();
 }
@@ -739,53 +748,51 @@ __device__ __forceinline__ PassTarget pass_target(const BwdArgs &a, const OwnerL
     return t;
 }
 
-template <int L>
-__device__ __forceinline__ void tables_init(WaveTables<L> &tb, const float *sh) {
+template <int L, bool PE>
+__device__ __forceinline__ void tables_init(WaveTables<L, PE> &tb, const float *sh) {
+    using T = WaveTables<L, PE>;
     constexpr int nsh = (L + 1) * (L + 1);
+    static_assert(T::kComp * kWindow <= 64, "one lane per padding row");
     const uint32_t lane = lane_id();
 #pragma unroll
     for (int k = 0; k < nsh; ++k) tb.y()[k * kPitch + lane] = sh[k];
     // the padding member (lane 64): zero basis and zero record
     if (lane < (uint32_t)nsh) tb.y()[lane * kPitch + 64] = 0.0f;
-    if (lane < 8u * kWindow) tb.rec()[lane * kPitch + 64] = 0.0f;
-    tb.buf[WaveTables<L>::kOnes + lane] = 1.0f;
-    tb.buf[WaveTables<L>::kZeros + lane] = 0.0f;
-    if (lane == 0) {
-        tb.buf[WaveTables<L>::kOnes + 64] = 1.0f;
-        tb.buf[WaveTables<L>::kZeros + 64] = 0.0f;
-    }
+    if (lane < (uint32_t)(T::kComp * kWindow)) tb.rec()[lane * kPitch + 64] = 0.0f;
+    tb.buf[T::kOnes + lane] = 1.0f;
+    if (lane == 0) tb.buf[T::kOnes + 64] = 1.0f;
     __builtin_amdgcn_wave_barrier();
 }
 
 // ---------------------------------------------------------------------------
 // backward_sdf (src/tracing/pipeline.cu:267-550)
 
-template <int L, bool STATS, typename AT>
+template <int L, bool STATS, typename AT, bool PE = false>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 backward_sdf_kernel(BwdArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
-    __shared__ WaveTables<L> tables[kBlock / 64];
+    __shared__ WaveTables<L, PE> tables[kBlock / 64];
     bool valid;
     const uint32_t ray_idx =
         ray_for_lane<kBackwardChunk>(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid,
                                      a.order);
     const uint32_t lane = lane_id();
-    WaveTables<L> &tb = tables[threadIdx.x >> 6];
+    WaveTables<L, PE> &tb = tables[threadIdx.x >> 6];
 
     RayF ray = {};
     if (valid) ray = load_ray(a.rays, ray_idx);
     {
         float sh0[nsh];
         sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
-        tables_init<L>(tb, sh0);
+        tables_init<L, PE>(tb, sh0);
     }
     const float *sh = tb.y() + lane; // this ray's SH basis, in LDS (stride kPitch)
 
     const float sha = a.sharpness[0];
     const int32_t sdf_ch = a.settings.sdf_channel >= 0 ? a.settings.sdf_channel : D - 1;
     const bool write_sdf = a.settings.sdf_channel >= 0;
-    const OwnerLane owner = owner_lane<L>(write_sdf ? sdf_ch : -1, a.point_error != nullptr);
+    const OwnerLane owner = owner_lane<L, PE>(write_sdf ? sdf_ch : -1);
     const PassTarget target = pass_target<L>(a, owner);
     const float thr = a.settings.weight_threshold;
     const uint32_t Q = a.num_quantiles;
@@ -845,8 +852,8 @@ backward_sdf_kernel(BwdArgs a) {
             uint2 e = make_uint2(kWalkUnrecorded, 0u);
             if (replaying && trip < a.record.budget && wslot != ~0ull) {
                 const uint64_t i = wslot + (trip % kChunkTrips) * 64u;
-                e = a.record.entries[i];
-                rc4 = a.record.colors[i];
+                e = record_load(a.record.entries + i);
+                rc4 = record_load(a.record.colors + i);
             }
             if (e.x == kNoIndex) {
                 ++ws.n;
@@ -954,17 +961,17 @@ backward_sdf_kernel(BwdArgs a) {
             // the flush of the same cell) or when its walk ends; complete
             // steps go out every kWindow trips
             if (ents.pend && (si.stepped || !ws.alive))
-                complete_entry<L>(ents, si.stepped && flush, flush_g, tb);
-            if (trip % kWindow == 0) grouped_pass<L, AT>(ents, owner, tb, target);
-            if (si.stepped) publish_step<L>(tb, ents, ws.cell, dr, dg, db, dsdf, pe);
+                complete_entry<L, PE>(ents, si.stepped && flush, flush_g, tb);
+            if (trip % kWindow == 0) grouped_pass<L, PE, AT>(ents, owner, tb, target);
+            if (si.stepped) publish_step<L, PE>(tb, ents, ws.cell, dr, dg, db, dsdf, pe);
         }
         if (ws.alive && si.found) walk_move(ws, si);
     }
     if constexpr (!STATS) {
         // steps not applied when the walks ended
         const float zero3[3] = {0.0f, 0.0f, 0.0f};
-        if (ents.pend) complete_entry<L>(ents, false, zero3, tb);
-        grouped_pass<L, AT>(ents, owner, tb, target);
+        if (ents.pend) complete_entry<L, PE>(ents, false, zero3, tb);
+        grouped_pass<L, PE, AT>(ents, owner, tb, target);
     }
 
     if constexpr (STATS) {
@@ -984,29 +991,29 @@ backward_sdf_kernel(BwdArgs a) {
 
 // backward, density mode (src/tracing/pipeline.cu:553-791); the walk runs in
 // the reference's unsafe mode (no t > t0 test, :782-790).
-template <int L, bool STATS, typename AT>
+template <int L, bool STATS, typename AT, bool PE = false>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 backward_density_kernel(BwdArgs a) {
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
-    __shared__ WaveTables<L> tables[kBlock / 64];
+    __shared__ WaveTables<L, PE> tables[kBlock / 64];
     bool valid;
     const uint32_t ray_idx =
         ray_for_lane<kBackwardChunk>(a.num_rays, a.settings.ray_image_width, a.num_tiles, valid,
                                      a.order);
     const uint32_t lane = lane_id();
-    WaveTables<L> &tb = tables[threadIdx.x >> 6];
+    WaveTables<L, PE> &tb = tables[threadIdx.x >> 6];
 
     RayF ray = {};
     if (valid) ray = load_ray(a.rays, ray_idx);
     {
         float sh0[nsh];
         sh_basis<L>(ray.dx, ray.dy, ray.dz, sh0);
-        tables_init<L>(tb, sh0);
+        tables_init<L, PE>(tb, sh0);
     }
     const float *sh = tb.y() + lane; // this ray's SH basis, in LDS (stride kPitch)
 
-    const OwnerLane owner = owner_lane<L>(D - 1, a.point_error != nullptr);
+    const OwnerLane owner = owner_lane<L, PE>(D - 1);
     const PassTarget target = pass_target<L>(a, owner);
     const float thr = a.settings.weight_threshold;
     const uint32_t Q = a.num_quantiles;
@@ -1074,8 +1081,8 @@ backward_density_kernel(BwdArgs a) {
             if (replaying && !seeking && ridx < a.record.budget) {
                 const uint64_t i = record_slot(a.record, wtab, ridx, lane);
                 if (i != ~0ull) {
-                    e = a.record.entries[i];
-                    rc4 = a.record.colors[i];
+                    e = record_load(a.record.entries + i);
+                    rc4 = record_load(a.record.colors + i);
                 }
                 ++ridx;
             }
@@ -1184,9 +1191,9 @@ backward_density_kernel(BwdArgs a) {
         if (si.stepped && !keep) ws.alive = false;
         if constexpr (!STATS) {
             if (ents.pend && (si.stepped || !ws.alive))
-                complete_entry<L>(ents, si.stepped && flush, flush_g, tb);
-            if (trip % kWindow == 0) grouped_pass<L, AT>(ents, owner, tb, target);
-            if (si.stepped) publish_step<L>(tb, ents, ws.cell, dr, dg, db, dds, pe);
+                complete_entry<L, PE>(ents, si.stepped && flush, flush_g, tb);
+            if (trip % kWindow == 0) grouped_pass<L, PE, AT>(ents, owner, tb, target);
+            if (si.stepped) publish_step<L, PE>(tb, ents, ws.cell, dr, dg, db, dds, pe);
         }
         if (ws.alive && si.found) walk_move(ws, si);
         if (seeking && ws.alive) {
@@ -1198,7 +1205,7 @@ backward_density_kernel(BwdArgs a) {
                 if (f >= a.record.budget) break;
                 const uint64_t i = record_slot(a.record, wtab, f, lane);
                 if (i == ~0ull) break;
-                const uint2 fe = a.record.entries[i];
+                const uint2 fe = record_load(a.record.entries + i);
                 if (fe.x == kNoIndex || fe.x == kWalkUnrecorded) break;
                 if ((fe.x & ~kWalkDiffers) == ws.cell &&
                     fe.y == __builtin_bit_cast(uint32_t, ws.t0)) {
@@ -1211,8 +1218,8 @@ backward_density_kernel(BwdArgs a) {
     }
     if constexpr (!STATS) {
         const float zero3[3] = {0.0f, 0.0f, 0.0f};
-        if (ents.pend) complete_entry<L>(ents, false, zero3, tb);
-        grouped_pass<L, AT>(ents, owner, tb, target);
+        if (ents.pend) complete_entry<L, PE>(ents, false, zero3, tb);
+        grouped_pass<L, PE, AT>(ents, owner, tb, target);
     }
 
     if constexpr (STATS) {
@@ -1434,9 +1441,14 @@ hipError_t launch_forward(int L, const FwdArgs &a, bool neus, bool stats, bool h
 template <int L, typename AT>
 static hipError_t launch_backward_L(const BwdArgs &a, bool neus, bool stats, hipStream_t stream) {
     const dim3 grid(grid_blocks_for_tiles(a.num_tiles));
+    // PE: entries carry the point error (a larger LDS table per wave)
+    const bool pe = !stats && a.point_error != nullptr;
     if (neus) {
         if (stats) {
             hipLaunchKernelGGL((backward_sdf_kernel<L, true, AT>), grid, dim3(kBlock), 0, stream, a);
+        } else if (pe) {
+            hipLaunchKernelGGL((backward_sdf_kernel<L, false, AT, true>), grid, dim3(kBlock), 0,
+                               stream, a);
         } else {
             hipLaunchKernelGGL((backward_sdf_kernel<L, false, AT>), grid, dim3(kBlock), 0, stream, a);
         }
@@ -1444,6 +1456,9 @@ static hipError_t launch_backward_L(const BwdArgs &a, bool neus, bool stats, hip
         if (stats) {
             hipLaunchKernelGGL((backward_density_kernel<L, true, AT>), grid, dim3(kBlock), 0, stream,
                                a);
+        } else if (pe) {
+            hipLaunchKernelGGL((backward_density_kernel<L, false, AT, true>), grid, dim3(kBlock), 0,
+                               stream, a);
         } else {
             hipLaunchKernelGGL((backward_density_kernel<L, false, AT>), grid, dim3(kBlock), 0,
                                stream, a);

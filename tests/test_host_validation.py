@@ -154,3 +154,4 @@ def test_release_trace_plan_drops_the_record():
     assert not hasattr(rgba, pipeline._PLAN_ATTR)
     sdfoam_amd.release_trace_plan(rgba)
     sdfoam_amd.release_trace_plan(torch.zeros(2))
+
