@@ -364,7 +364,10 @@ def main() -> int:
         # calibrated) over its live duration
         achieved, basis = traffic / kernel_s / 1e9, "rocprof HBM bytes per launch / live kernel time"
     else:
-        achieved, basis = model_gbps, "gather model (no rocprof counters for this workload)"
+        why = STALE_COUNTERS.get(f"traffic_{dominant}{variant}_C{args.config}.json")
+        achieved, basis = model_gbps, ("gather model (" + (
+            f"rocprof counters stale: {why}" if why else "no rocprof counters for this workload")
+            + ")")
 
     if args.config == 5:
         rays_desc = f"{R} rays per step sampled from 64 cameras 960x640 (10 seeded batches)"
@@ -443,19 +446,42 @@ def main() -> int:
 CPU_SAMPLE_RAYS = 1_920_000
 
 
+def file_sha256(path):
+    import hashlib
+
+    with open(path, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
+STALE_COUNTERS = {}  # profile name -> why its counters were not used
+
+
 def load_counters(name):
     """A committed rocprofv3 counter summary of one kernel (profiles/<name>):
-    HBM bytes per launch, L2 hit rate, source table; or None."""
+    HBM bytes per launch, L2 hit rate, source table; or None.  The summary
+    lists the kernel sources it was measured on with their SHA-256; if any
+    of them has changed since (or the list is missing) the summary is stale
+    and None is returned (the reason goes to STALE_COUNTERS)."""
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f)
+        c = json.load(f)
+    srcs = c.get("sources")
+    if not srcs:
+        STALE_COUNTERS[name] = "no source hashes"
+        return None
+    for rel, sha in srcs.items():
+        p = os.path.join(ROOT, rel)
+        if not os.path.exists(p) or file_sha256(p) != sha:
+            STALE_COUNTERS[name] = f"{rel} changed since the profile"
+            return None
+    return c
 
 
 def load_traffic(name):
     """HBM bytes per launch that a committed rocprofv3 counter summary
-    (profiles/<name>) records, or None."""
+    (profiles/<name>) records, or None (missing or stale)."""
     c = load_counters(name)
     return c.get("hbm_bytes_per_launch") if c else None
 

@@ -167,11 +167,17 @@ __device__ __forceinline__ void contrib_flush(ContribTable &ct, void *contributi
 // ---------------------------------------------------------------------------
 // forward (src/tracing/pipeline.cu:36-264)
 
+// Waves per SIMD asked of the forward over the cell table for image rays
+// (the compiler then keeps it to 512 / kForwardWaves VGPRs).
+constexpr int kForwardWaves = 6;
+
 // CT: walk over the cell table (a.scene.cells) and read attribute rows from it.
 // HALF: the face scan's half-batch loads (walk_advance), for rays in an
 // explicit launch order (incoherent batches such as random training pixels).
 template <int L, bool NEUS, bool STATS, typename AT, bool CT = false, bool HALF = false>
-__global__ __launch_bounds__(kBlock) void forward_kernel(FwdArgs a) {
+__global__ __launch_bounds__(kBlock)
+__attribute__((amdgpu_waves_per_eu(CT && !HALF && !STATS ? kForwardWaves : 1))) void
+forward_kernel(FwdArgs a) {
     constexpr uint32_t RB = CT ? cell_record_bytes(L, sizeof(AT)) : 0u;
     constexpr int nsh = (L + 1) * (L + 1);
     constexpr int D = 1 + 3 * nsh;
