@@ -408,13 +408,14 @@ def test_c3_triangulation_matches_qhull(dev, say):
         assert np.array_equal(got.reshape(v.shape), v), k
 
 
-def test_c3_standard_record_replays_the_unsafe_walk(dev, say):
+def test_c3_standard_record_replays_the_unsafe_walk(dev, oracle_lib, say):
     """Standard mode at C3 (1M points, 1600x1200 rays): the backward that
     replays the forward's record, leaving it where the unsafe walk differs and
     taking it up again where the walks meet, gives the gradients of the
-    backward that scans every step (itself checked against the oracle on the
-    smaller configs).  A lane replaying from a wrong place would follow other
-    cells and move the sums far outside this tolerance."""
+    backward that scans every step.  A lane replaying from a wrong place would
+    follow other cells and move the sums far outside this tolerance.  Both,
+    and the standard-mode forward, also meet the oracle's parity bars on an
+    image-shaped subset of the same workload."""
     import torch
 
     import sdfoam_amd
@@ -448,3 +449,18 @@ def test_c3_standard_record_replays_the_unsafe_walk(dev, say):
         scale = float(np.abs(b).max())
         assert scale > 0, k
         np.testing.assert_allclose(a, b, rtol=1e-3, atol=1e-5 * scale, err_msg=k)
+    del b_rec, b_scan, fwd
+    # and both paths against the oracle (density mode) on the image subset of
+    # every 4th row and column (120k rays through the tile path)
+    from test_gpu_parity import _backward_both, _check_backward, _check_forward, _forward_both
+
+    host_start = start.view(torch.int32).cpu().numpy().view(np.uint32).reshape(w.rays.shape[:-1])
+    sl = (slice(None, None, 4), slice(None, None, 4))
+    sub = _subset(w, w.rays[sl], w.quantiles[sl], w.grad_rgba[sl], w.depth_grad[sl],
+                  host_start[sl])
+    out, st, ref = _forward_both(sub, dev, oracle_lib, "standard", record=0)
+    _check_forward(out, st, ref, sub, 0)
+    for walk in (True, False):
+        bwd, st, ref = _backward_both(sub, dev, oracle_lib, "standard", walk=walk)
+        _check_backward(bwd, st, ref, sub)
+    say(f"C3 standard forward and backward (record and scan) parity on {sub.num_rays} rays")
