@@ -106,7 +106,7 @@ __device__ inline uint32_t record_claim(const WalkRecordArgs &r, uint32_t *tab, 
 // its cell's slot or a free one.  The lanes' claims run side by side (a
 // serial round per distinct cell costs more), and one global atomic per step
 // costs far more (same-address adds serialise in L2).
-constexpr uint32_t kContribTrips = 4;
+constexpr uint32_t kContribTrips = 8;
 constexpr uint32_t kContribSlots = 64 * kContribTrips;
 constexpr uint32_t kContribFree = 0xffffffffu;
 
@@ -130,7 +130,9 @@ __device__ __forceinline__ void contrib_clear(ContribTable &ct) {
 template <typename AT>
 __device__ __forceinline__ void contrib_add(ContribTable &ct, uint32_t cell, float w, float alpha,
                                             void *contribution) {
-    uint32_t h = (cell * 0x9e3779b1u) >> 24; // 8 bits: kContribSlots == 256
+    static_assert((kContribSlots & (kContribSlots - 1u)) == 0u, "a power of two");
+    constexpr uint32_t kBits = __builtin_ctz(kContribSlots);
+    uint32_t h = (cell * 0x9e3779b1u) >> (32u - kBits);
     for (uint32_t probe = 0; probe < kContribSlots; ++probe) {
         const uint32_t old = atomicCAS(&ct.tag[h], kContribFree, cell);
         if (old == kContribFree || old == cell) {
