@@ -146,16 +146,25 @@ __device__ __forceinline__ void contrib_add(ContribTable &ct, uint32_t cell, flo
     if (contribution) atomic_add_elem<AT>(contribution, cell, w);
 }
 
-// The wave's pending sums (all 64 lanes).
+// The wave's pending sums (all 64 lanes).  Lane l holds slots l + 64 k; it
+// flushes its occupied ones one per round, so the wave issues as many
+// atomic and store instructions as its busiest lane has occupied slots
+// (a few at C3) rather than one per slot position.
 template <typename AT>
 __device__ __forceinline__ void contrib_flush(ContribTable &ct, void *contribution, float *alpha_out) {
+    static_assert(kContribSlots / 64 <= 32, "one bit per slot of a lane");
     __builtin_amdgcn_wave_barrier();
     const uint32_t lane = lane_id();
+    uint32_t occ = 0u;
 #pragma unroll
-    for (uint32_t k = 0; k < kContribSlots / 64; ++k) {
-        const uint32_t s = lane + 64u * k;
-        const uint32_t c = ct.tag[s];
-        if (c != kContribFree) {
+    for (uint32_t k = 0; k < kContribSlots / 64; ++k)
+        occ |= (ct.tag[lane + 64u * k] != kContribFree ? 1u : 0u) << k;
+    while (__ballot(occ != 0u)) {
+        if (occ) {
+            const uint32_t k = (uint32_t)__builtin_ctz(occ);
+            occ &= occ - 1u;
+            const uint32_t s = lane + 64u * k;
+            const uint32_t c = ct.tag[s];
             const float v = ct.w[s];
             ct.tag[s] = kContribFree;
             ct.w[s] = 0.0f;
