@@ -220,6 +220,11 @@ struct StagedVert {
     double x[3], e, r2;
 };
 
+// A cell vertex as the batch test reads it (position and error bound).
+struct TestVert {
+    double x[3], e;
+};
+
 struct WaveShared {
     double pn[kWavePlanes][3]; // plane normals
     double pc[kWavePlanes];    // plane offsets: x.n < c inside
@@ -227,7 +232,10 @@ struct WaveShared {
     uint32_t edges[kWavePlanes * kWavePlanes / 32];
     uint32_t used[2];
     uint8_t remap[kWavePlanes];
-    StagedVert stg[kWaveNew];
+    union {
+        StagedVert stg[kWaveNew];     // wave_clip's new vertices
+        TestVert tv[kWaveVerts];      // wave_may_cut's copy of the vertices
+    };
     double mr2, blo[3], bhi[3]; // max |v|^2 and the vertices' box (the cell's bounds)
 };
 
@@ -258,6 +266,15 @@ __device__ __forceinline__ uint32_t wsumu(uint32_t v) {
 }
 __device__ __forceinline__ uint32_t wmaxu(uint32_t v) {
     for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
+    return v;
+}
+// inclusive prefix sum over the lanes
+__device__ __forceinline__ uint32_t wscanu(uint32_t v) {
+    const uint32_t l = wlane();
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = (uint32_t)__shfl_up((int)v, off, 64);
+        if (l >= (uint32_t)off) v += y;
+    }
     return v;
 }
 
@@ -509,6 +526,50 @@ __device__ int wave_clip(WaveCell &c, WaveShared &sh, const double *q, double qc
     return 1;
 }
 
+// The lanes whose candidate plane (relative position q, qc = |q|^2 / 2;
+// `mine`: the lane holds one) may cut the cell: each lane tests its plane
+// against every vertex (copied to LDS), and a plane that leaves every
+// vertex inside by more than the bound wave_clip uses (the vertex's error
+// bound and the dot product's rounding) misses the cell, and every cell the
+// clips that follow make (they only shrink it).  One pass for a batch of
+// candidates in place of a wave_clip call each, most of which find no cut
+// where the cell is large.
+__device__ uint64_t wave_may_cut(const WaveCell &c, WaveShared &sh, bool mine, const double *q,
+                                 double qc) {
+    const uint64_t a0 = wballot(c.vp[0] != kFree), a1 = wballot(c.vp[1] != kFree);
+    const uint32_t n0 = (uint32_t)__popcll(a0), nv = n0 + (uint32_t)__popcll(a1);
+    for (int s = 0; s < 2; ++s) {
+        if (c.vp[s] == kFree) continue;
+        TestVert &t = sh.tv[s == 0 ? wbelow(a0) : n0 + wbelow(a1)];
+        t.x[0] = c.vx[s][0];
+        t.x[1] = c.vx[s][1];
+        t.x[2] = c.vx[s][2];
+        t.e = c.ve[s];
+    }
+    __syncthreads();
+    bool cut = false;
+    if (mine) {
+        const double qn = vcell::dabs(q[0]) + vcell::dabs(q[1]) + vcell::dabs(q[2]);
+        for (uint32_t v = 0; v < nv && !cut; ++v) {
+            const double *x = sh.tv[v].x;
+            const double sd = x[0] * q[0] + x[1] * q[1] + x[2] * q[2] - qc;
+            const double bound =
+                sh.tv[v].e * qn + 4.0 * vcell::kEps *
+                                      (vcell::dabs(x[0] * q[0]) + vcell::dabs(x[1] * q[1]) +
+                                       vcell::dabs(x[2] * q[2]) + qc);
+            cut = !(sd < -bound);
+        }
+    }
+    const uint64_t m = wballot(cut);
+    __syncthreads(); // the copy is read before wave_clip stages vertices there
+    return m;
+}
+
+// Candidates that survive the per-lane filters in a batch before the batch
+// test pays for itself (a wave_clip call that finds no cut costs about as
+// much as the test over a typical cell's vertices).
+constexpr int kBatchTestMin = 3;
+
 __device__ bool wave_touches_box(const WaveCell &c, const WaveShared &sh) {
     bool t = false;
     for (int s = 0; s < 2; ++s)
@@ -583,19 +644,31 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                         dgrid::cell_range(gv, lev, (uint32_t)cx, (uint32_t)cy, (uint32_t)cz, b,
                                           e);
                 }
+                // the batch's points, 64 at a time in cell order: lane l
+                // takes point f0 + l of the concatenated cell ranges (its
+                // cell: the first lane whose inclusive prefix exceeds it)
                 const uint32_t cnt = e - b;
-                examined += wsumu(cnt);
+                const uint32_t incl = wscanu(cnt);
+                const uint32_t total = (uint32_t)__shfl((int)incl, 63, 64);
+                examined += total;
                 if (examined > dgrid::kMaxCandidates) {
                     decided = true;
                     break;
                 }
-                const uint32_t rounds = wmaxu(cnt);
-                for (uint32_t k = 0; k < rounds && !decided; ++k) {
+                for (uint32_t f0 = 0; f0 < total && !decided; f0 += 64) {
+                    const uint32_t f = f0 + l;
+                    const uint32_t fc = f < total ? f : total - 1;
+                    uint32_t owner = 0;
+                    for (uint32_t step = 32; step > 0; step >>= 1)
+                        if ((uint32_t)__shfl((int)incl, (int)(owner + step - 1), 64) <= fc)
+                            owner += step;
+                    const uint32_t ob = (uint32_t)__shfl((int)b, (int)owner, 64);
+                    const uint32_t oex = (uint32_t)__shfl((int)(incl - cnt), (int)owner, 64);
                     bool surv = false, dup = false;
                     double q[3] = {0.0, 0.0, 0.0}, d2 = INFINITY;
                     uint32_t j = 0;
-                    if (k < cnt) {
-                        j = sorted[b + k];
+                    if (f < total) {
+                        j = sorted[ob + (f - oex)];
                         if (j != i) {
                             const double x[3] = {(double)p[3ull * j], (double)p[3ull * j + 1],
                                                  (double)p[3ull * j + 2]};
@@ -624,6 +697,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                         break;
                     }
                     uint64_t m = wballot(surv);
+                    if (__popcll(m) >= kBatchTestMin) m = wave_may_cut(c, sh, surv, q, 0.5 * d2);
                     while (m) {
                         // nearest first
                         const bool mine = (m >> l) & 1ull;

@@ -350,14 +350,16 @@ SDF_HD bool sphere_setup(const float *p, const uint32_t *v, const GridView &gv, 
                            S.pl[s].n[2] * S.pl[s].n[2]);
         S.pl[s].point = (int32_t)v[s + 1];
     }
-    // the circumcentre (relative to o) is where the three bisectors meet;
-    // its error grows with the conditioning of that system
-    if (!vcell::meet(S.pl[0], S.pl[1], S.pl[2], S.ctr)) return false;
-    double perm;
-    const double d = vcell::det3(S.pl[0].n, S.pl[1].n, S.pl[2].n, perm);
-    const double cond = perm / vcell::dabs(d);
+    // the circumcentre (relative to o) is where the three bisectors meet, to
+    // within err per coordinate (meet's bound); a point strictly inside the
+    // true sphere lies within |ctr| + 2 sqrt(3) err of the computed centre.
+    // The margin is absolute: a relative one would let the nearly flat
+    // tetrahedra on a planar face of the hull (radii ~1e6 times the scene)
+    // cover the whole scene.
+    double err = 0.0;
+    if (!vcell::meet(S.pl[0], S.pl[1], S.pl[2], S.ctr, &err)) return false;
     const double r2 = S.ctr[0] * S.ctr[0] + S.ctr[1] * S.ctr[1] + S.ctr[2] * S.ctr[2];
-    S.r = sqrt(r2) * (1.0 + 1e-6 + 1e-13 * cond) + g.slack;
+    S.r = sqrt(r2) * (1.0 + 1e-12) + 4.0 * err + g.slack;
     // the finest level whose cells cover the sphere's box in few columns
     for (S.l = 0;; ++S.l) {
         const GridLevel &lv = g.level[S.l];

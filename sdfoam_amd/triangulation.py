@@ -178,7 +178,10 @@ def _certify(L, pts: torch.Tensor, gptr: int, gbytes: int, stream, query=None):
     nq = n if query is None else int(query.numel())
     open_pts = torch.empty(max(nq, 1), dtype=torch.int32, device=dev)
     counts = (C.c_uint64 * 5)()
-    cap = 28 * nq + 4096
+    # report rows: ~27 per certified cell over a whole point set (the mean
+    # tetrahedra per vertex); more per cell among the dirty points of an
+    # incremental rebuild, where a second pass would double the time
+    cap = (28 if query is None else 40) * nq + 4096
     for _ in range(2):
         reports = torch.empty((cap, 4), dtype=torch.int32, device=dev)
         if query is None:
@@ -345,7 +348,8 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
     t3 = time.perf_counter()
     stats.update({"open": nu, "reports": nr, "candidates": m, "tets": T,
                   "undecided_cells": int(counts[2]), "overflow_cells": int(counts[3]),
-                  "certify_s": t1 - t0, "open_points_qhull_s": t2 - t1, "merge_s": t3 - t2})
+                  "certify_s": t1 - t0, "open_points_qhull_s": t2 - t1, "merge_s": t3 - t2,
+                  "open_ids": U})
     return tets[:T], nbr[:T], stats
 
 
@@ -357,7 +361,7 @@ _INCREMENTAL_MAX_DIRTY = 0.4
 
 
 def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
-                               nbr_old: torch.Tensor):
+                               nbr_old: torch.Tensor, open_old: torch.Tensor | None = None):
     """The Delaunay tetrahedra of moved CUDA float32 points [N, 3] from the
     previous tetrahedralisation of the same points (tets_old, nbr_old: int32
     [T, 4] on the points' device, -1 on the hull), in place of
@@ -372,7 +376,15 @@ def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
     with a clean vertex v is one of v's old ones (those are all kept, so they
     still fill a neighbourhood of v, and Delaunay tetrahedra do not
     overlap); all other Delaunay tetrahedra have four dirty vertices.
-    Returns (tets, neighbors, stats); raises _Undecided like gpu_tetrahedra,
+    `open_old` (int32 ids on the device, optional): the points the previous
+    tetrahedralisation left open; those of them that are dirty join the open
+    points without a certification, like the old hull's vertices (their
+    cells, next to the hull or to large empty regions, rarely certify and
+    take the longest to try: ~20-40 ms for one at C3, against ~0.3 ms for
+    the median dirty point).  Any split of the dirty points into certified
+    and open ones gives the same tetrahedra.
+    Returns (tets, neighbors, stats), stats["open_ids"] the points left open;
+    raises _Undecided like gpu_tetrahedra,
     and when more than _INCREMENTAL_MAX_DIRTY of the points are dirty (the
     caller then rebuilds in full)."""
     pts = points.contiguous()
@@ -412,11 +424,19 @@ def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
         # the old hull's vertices (2) go to the open points uncertified: their
         # cells are unbounded, so certifying them would only list them as
         # open (and if one moved inside, its tetrahedra still come from the
-        # open points' candidates, the reports and the kept ones)
-        hull_pts = torch.nonzero(dirty == 2).view(-1).to(torch.int32)
+        # open points' candidates, the reports and the kept ones); so do the
+        # dirty points the previous tetrahedralisation left open
+        direct = torch.nonzero(dirty == 2).view(-1).to(torch.int32)
         inner = torch.nonzero(dirty == 1).view(-1).to(torch.int32)
+        if open_old is not None and open_old.numel():
+            was_open = torch.zeros(n, dtype=torch.bool, device=dev)
+            was_open[open_old.to(dev).long()] = True
+            again = was_open[inner.long()]
+            direct = torch.cat([direct, inner[again]])
+            inner = inner[~again]
+            stats["open_again"] = int(again.sum().item())
         reports, U, counts = _certify(L, pts, gptr, gbytes, stream, query=inner)
-        U = torch.sort(torch.cat([U, hull_pts]))[0]
+        U = torch.sort(torch.cat([U, direct]))[0]
         nr, nu = int(reports.shape[0]), int(U.numel())
         t2 = time.perf_counter()
         cand, hull_faces = _open_candidates(L, pts, U, stream, stats)
@@ -441,7 +461,7 @@ def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
                   "tets": T, "undecided_cells": int(counts[2]),
                   "overflow_cells": int(counts[3]), "check_s": t1 - t0, "certify_s": t2 - t1,
                   "open_points_qhull_s": t3 - t2, "merge_s": t4 - t3,
-                  "select_s": t_sel - t3})
+                  "select_s": t_sel - t3, "open_ids": U})
     return tets[:T], nbr[:T], stats
 
 
@@ -508,6 +528,7 @@ class Triangulation:
         self._perm_t = None
         self._tets_prev = None  # the last tetrahedra (int32 [T, 4] on the device)
         self._nbr_prev = None
+        self._open_prev = None  # the points they left open (int32 ids), if from the GPU
         self.rebuild(points, incremental=False)
 
     def rebuild(self, points: torch.Tensor, incremental: bool = False) -> bool:
@@ -529,7 +550,8 @@ class Triangulation:
             why = None
             if not sorted_now and self._tets_prev is not None:
                 try:
-                    got = gpu_tetrahedra_incremental(pts_dev, self._tets_prev, self._nbr_prev)
+                    got = gpu_tetrahedra_incremental(pts_dev, self._tets_prev, self._nbr_prev,
+                                                     self._open_prev)
                 except _Undecided as e:
                     why = str(e)
             try:
@@ -539,7 +561,7 @@ class Triangulation:
                         got[2]["incremental_fallback"] = why
                 simplices, neighbors, self.last_stats = got
                 self.last_method = "gpu"
-                self._keep(simplices, neighbors)
+                self._keep(simplices, neighbors, self.last_stats["open_ids"])
                 self._tables = device_tables(pts_dev, simplices, neighbors)
                 return sorted_now
             except _Undecided:
@@ -554,9 +576,11 @@ class Triangulation:
         self._tables = device_tables(pts_dev, simplices, neighbors)
         return sorted_now
 
-    def _keep(self, simplices, neighbors) -> None:
-        """The tetrahedra an incremental rebuild starts from."""
+    def _keep(self, simplices, neighbors, open_ids=None) -> None:
+        """The tetrahedra an incremental rebuild starts from, and the points
+        the GPU tetrahedralisation left open (None after Qhull)."""
         dev = self._perm_t.device
+        self._open_prev = open_ids
         if isinstance(simplices, torch.Tensor):
             self._tets_prev = simplices.to(dev, torch.int32).contiguous()
             self._nbr_prev = neighbors.to(dev, torch.int32).contiguous()
