@@ -822,16 +822,20 @@ __global__ __launch_bounds__(64) void keep_empty_kernel(const float *__restrict_
     if (l == 0) keep[t] = inside ? 0u : (undecided ? 2u : 1u);
 }
 
-// Incremental rebuild, one lane per tetrahedron t of the previous
+// Incremental rebuild, kCheckLanes lanes per tetrahedron t of the previous
 // tetrahedralisation over the moved points: keep[t] = 1 when no point lies
 // strictly inside its circumsphere and every sign is decided (status: every
 // point clean), else 0.  The vertices of a tetrahedron not kept are marked
 // dirty (1), the three vertices of each face without a neighbour (the old
 // hull) dirty and on the hull (2).
 // The sphere is scanned on the finest level where it spans at most 6 x 6
-// columns (at C3's 1M points 29.5 ms for 6.7M tetrahedra, against 55 ms at
-// 3 x 3, 43 ms at 4 x 4 and 53 ms at 8 x 8).  errors[0]: rows with a vertex
-// out of range.
+// columns (at C3's 1M points, with one lane per tetrahedron, 29.5 ms for
+// 6.7M tetrahedra, against 55 ms at 3 x 3, 43 ms at 4 x 4 and 53 ms at
+// 8 x 8); the group's lanes take its columns in turn (2-8 lanes a group
+// ~19 ms, one lane 25 ms, 16 lanes 21 ms, 64 lanes 33 ms).  errors[0]: rows
+// with a vertex out of range.
+constexpr uint32_t kCheckLanes = 4;
+
 __global__ __launch_bounds__(256) void check_kernel(const float *__restrict__ p, uint32_t n,
                                                     GridView gv,
                                                     const uint32_t *__restrict__ status,
@@ -840,28 +844,38 @@ __global__ __launch_bounds__(256) void check_kernel(const float *__restrict__ p,
                                                     uint32_t *__restrict__ keep,
                                                     uint32_t *__restrict__ dirty,
                                                     unsigned long long *__restrict__ errors) {
-    const uint64_t t = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-    if (t >= T) return;
-    uint32_t v[4];
-    bool valid = true;
-    for (int k = 0; k < 4; ++k) {
-        v[k] = tets[4 * t + k];
-        valid = valid && v[k] < n;
-    }
+    static_assert(64u % kCheckLanes == 0u, "groups within a wavefront");
+    const uint64_t t = ((uint64_t)blockIdx.x * 256u + threadIdx.x) / kCheckLanes;
+    const uint32_t sub = threadIdx.x % kCheckLanes;
+    const bool live = t < T;
+    uint32_t v[4] = {0u, 0u, 0u, 0u};
+    bool valid = live;
+    if (live)
+        for (int k = 0; k < 4; ++k) {
+            v[k] = tets[4 * t + k];
+            valid = valid && v[k] < n;
+        }
+    // a sphere still wider than 8 x 8 columns of the coarsest level (the
+    // huge spheres of flat tetrahedra at the hull) is not scanned: its
+    // tetrahedron is not kept, which only adds dirty points
+    dgrid::Sphere S;
+    bool kept = valid && dgrid::sphere_setup(p, v, gv, S, 36.0);
+    const uint32_t cols = kept ? dgrid::sphere_columns(S) : 0u;
+    kept = kept && cols <= 64u;
+    bool hit = false;
+    for (uint32_t c = sub; kept && !hit && c < cols; c += kCheckLanes)
+        hit = dgrid::sphere_scan_column(p, v, gv, status, S, c) != 1u;
+    // the group's lanes are consecutive bits of the wavefront's ballot
+    const uint64_t hits = __builtin_amdgcn_ballot_w64(hit);
+    const uint32_t first = (threadIdx.x & 63u) & ~(kCheckLanes - 1u);
+    const uint64_t group = kCheckLanes == 64u ? ~0ull : ((1ull << kCheckLanes) - 1ull) << first;
+    kept = kept && (hits & group) == 0ull;
+    if (!live || sub != 0u) return;
     if (!valid) {
         keep[t] = 0u;
         atomicAdd(errors, 1ull);
         return;
     }
-    // a sphere still wider than 8 x 8 columns of the coarsest level (the
-    // huge spheres of flat tetrahedra at the hull) is not scanned: its
-    // tetrahedron is not kept, which only adds dirty points
-    dgrid::Sphere S;
-    bool kept = dgrid::sphere_setup(p, v, gv, S, 36.0);
-    const uint32_t cols = kept ? dgrid::sphere_columns(S) : 0u;
-    kept = kept && cols <= 64u;
-    for (uint32_t c = 0; kept && c < cols; ++c)
-        kept = dgrid::sphere_scan_column(p, v, gv, status, S, c) == 1u;
     keep[t] = kept ? 1u : 0u;
     if (!kept)
         for (int k = 0; k < 4; ++k) atomicMax(dirty + v[k], 1u);
@@ -1145,7 +1159,7 @@ hipError_t launch_delaunay_check(const float *points, uint32_t n, const uint32_t
                        dgrid::kStatusClean);
     hipLaunchKernelGGL(fill_kernel, grid1(n), dim3(256), 0, stream, dirty, (uint64_t)n, 0u);
     if (T > 0)
-        hipLaunchKernelGGL(check_kernel, grid1(T), dim3(256), 0, stream, points, n,
+        hipLaunchKernelGGL(check_kernel, grid1(T * kCheckLanes), dim3(256), 0, stream, points, n,
                            grid_view(s, g), s.status, tets, nbr, T, keep, dirty, s.counters + 5);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     unsigned long long hc[8];
