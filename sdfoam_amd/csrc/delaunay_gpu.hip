@@ -20,6 +20,7 @@
 #include <rocprim/device/device_radix_sort.hpp>
 #include <rocprim/device/device_scan.hpp>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -62,10 +63,11 @@ GridScratch carve_grid(void *base, uint32_t n, size_t temp_bytes) {
     s.tag = reinterpret_cast<uint64_t *>(take(2 * 8));
     s.counters = reinterpret_cast<unsigned long long *>(take(8 * 8));
     s.mm = reinterpret_cast<uint32_t *>(take(6 * 4));
-    for (int l = 0; l < dgrid::kLevels; ++l) {
+    for (int l = 0; l < dgrid::kLevels; ++l)
         s.table[l] = reinterpret_cast<dgrid::CellEntry *>(take(sizeof(dgrid::CellEntry) * slots));
-        s.sorted[l] = reinterpret_cast<uint32_t *>(take(4ull * n));
-    }
+    // one order serves every level
+    uint32_t *sorted = reinterpret_cast<uint32_t *>(take(4ull * n));
+    for (int l = 0; l < dgrid::kLevels; ++l) s.sorted[l] = sorted;
     s.keys = reinterpret_cast<uint64_t *>(take(8ull * n));
     s.keys_sorted = reinterpret_cast<uint64_t *>(take(8ull * n));
     s.index = reinterpret_cast<uint32_t *>(take(4ull * n));
@@ -118,33 +120,60 @@ __global__ __launch_bounds__(64) void init_kernel(uint32_t *__restrict__ mm,
     if (threadIdx.x < 8) counters[threadIdx.x] = 0ull;
 }
 
+// Bounds of the points as orderable bits: a grid-stride pass (kBboxBlocks
+// blocks), a block reduction, then one atomic per block and bound (one per
+// wavefront serialised ~15k same-address atomics: ~1 ms at 1M points).
+constexpr uint32_t kBboxBlocks = 1024;
+
 __global__ __launch_bounds__(256) void bbox_kernel(const float *__restrict__ p, uint32_t n,
                                                    uint32_t *__restrict__ mm) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    __shared__ uint32_t red[4][6];
     uint32_t lo[3] = {0xffffffffu, 0xffffffffu, 0xffffffffu}, hi[3] = {0u, 0u, 0u};
-    if (i < n)
-        for (int k = 0; k < 3; ++k) lo[k] = hi[k] = ordered(p[3ull * i + k]);
-    // wave reduction, then one atomic per wave and bound
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u)
+        for (int k = 0; k < 3; ++k) {
+            const uint32_t o = ordered(p[3ull * i + k]);
+            lo[k] = min(lo[k], o);
+            hi[k] = max(hi[k], o);
+        }
     for (int off = 32; off > 0; off >>= 1)
         for (int k = 0; k < 3; ++k) {
             lo[k] = min(lo[k], (uint32_t)__shfl_xor((int)lo[k], off));
             hi[k] = max(hi[k], (uint32_t)__shfl_xor((int)hi[k], off));
         }
+    const uint32_t w = threadIdx.x >> 6;
     if ((threadIdx.x & 63u) == 0)
         for (int k = 0; k < 3; ++k) {
-            atomicMin(mm + k, lo[k]);
-            atomicMax(mm + 3 + k, hi[k]);
+            red[w][k] = lo[k];
+            red[w][3 + k] = hi[k];
         }
+    __syncthreads();
+    if (threadIdx.x < 3) {
+        const uint32_t k = threadIdx.x;
+        atomicMin(mm + k, min(min(red[0][k], red[1][k]), min(red[2][k], red[3][k])));
+        atomicMax(mm + 3 + k, max(max(red[0][3 + k], red[1][3 + k]), max(red[2][3 + k], red[3][3 + k])));
+    }
 }
 
-__global__ __launch_bounds__(256) void cell_keys_kernel(const float *__restrict__ p, uint32_t n,
-                                                        GridGeom g, int level,
-                                                        uint64_t *__restrict__ keys,
-                                                        uint32_t *__restrict__ index) {
+// Morton code of each point's finest-level cell.
+__global__ __launch_bounds__(256) void morton_keys_kernel(const float *__restrict__ p, uint32_t n,
+                                                          GridGeom g, uint64_t *__restrict__ keys,
+                                                          uint32_t *__restrict__ index) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
     if (i >= n) return;
-    keys[i] = dgrid::point_key(g, level, p[3ull * i], p[3ull * i + 1], p[3ull * i + 2]);
+    const dgrid::GridLevel &lv = g.level[0];
+    keys[i] = dgrid::morton_key(
+        (uint32_t)dgrid::axis_cell((double)p[3ull * i], g.lo[0], lv.inv_h, lv.dims[0]),
+        (uint32_t)dgrid::axis_cell((double)p[3ull * i + 1], g.lo[1], lv.inv_h, lv.dims[1]),
+        (uint32_t)dgrid::axis_cell((double)p[3ull * i + 2], g.lo[2], lv.inv_h, lv.dims[2]));
     index[i] = i;
+}
+
+// Level-l cell keys of the points in Morton order.
+__global__ __launch_bounds__(256) void level_keys_kernel(const uint64_t *__restrict__ morton,
+                                                         uint32_t n, int level,
+                                                         uint64_t *__restrict__ keys) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < n) keys[i] = dgrid::level_key(morton[i], level);
 }
 
 __global__ __launch_bounds__(256) void fill_kernel(uint32_t *__restrict__ v, uint64_t n,
@@ -1061,7 +1090,8 @@ hipError_t build_grid(const float *points, uint32_t n, const GridScratch &s, Gri
                       hipStream_t stream) {
     hipLaunchKernelGGL(tag_kernel, dim3(1), dim3(64), 0, stream, s.tag, 0ull, 0ull);
     hipLaunchKernelGGL(init_kernel, dim3(1), dim3(64), 0, stream, s.mm, s.counters);
-    hipLaunchKernelGGL(bbox_kernel, grid1(n), dim3(256), 0, stream, points, n, s.mm);
+    hipLaunchKernelGGL(bbox_kernel, dim3(std::min<uint32_t>(grid1(n).x, kBboxBlocks)), dim3(256), 0,
+                       stream, points, n, s.mm);
     uint32_t hm[6];
     hipError_t e = hipMemcpyAsync(hm, s.mm, sizeof(hm), hipMemcpyDeviceToHost, stream);
     if (e != hipSuccess) return e;
@@ -1072,21 +1102,25 @@ hipError_t build_grid(const float *points, uint32_t n, const GridScratch &s, Gri
         hi[k] = (double)unordered(hm[3 + k]);
     }
     if (!dgrid::grid_geometry(lo, hi, n, g)) return hipErrorInvalidValue;
-    // each level: points sorted by cell key, then the table of occupied cells
+    // the points sorted once by the Morton code of their finest cell (one
+    // radix sort in place of one per level; 11 at ~0.25 ms each at 1M
+    // points), then per level the table of occupied cells over that order
+    hipLaunchKernelGGL(morton_keys_kernel, grid1(n), dim3(256), 0, stream, points, n, g, s.keys,
+                       s.index);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    size_t tb = s.temp_bytes;
+    e = rocprim::radix_sort_pairs(s.temp, tb, s.keys, s.keys_sorted, s.index, s.sorted[0],
+                                  (size_t)n, 0u, 63u, stream);
+    if (e != hipSuccess) return e;
     const uint64_t slots = g.table_mask + 1;
     for (int l = 0; l < dgrid::kLevels; ++l) {
-        hipLaunchKernelGGL(cell_keys_kernel, grid1(n), dim3(256), 0, stream, points, n, g, l,
-                           s.keys, s.index);
+        hipLaunchKernelGGL(level_keys_kernel, grid1(n), dim3(256), 0, stream, s.keys_sorted, n, l,
+                           s.keys);
         hipLaunchKernelGGL(table_clear_kernel, grid1(slots), dim3(256), 0, stream, s.table[l],
                            slots);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        size_t tb = s.temp_bytes;
-        e = rocprim::radix_sort_pairs(s.temp, tb, s.keys, s.keys_sorted, s.index, s.sorted[l],
-                                      (size_t)n, 0u, 63u, stream);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(table_insert_kernel, grid1(n), dim3(256), 0, stream, s.keys_sorted, n,
+        hipLaunchKernelGGL(table_insert_kernel, grid1(n), dim3(256), 0, stream, s.keys, n,
                            s.table[l], g.table_mask);
-        hipLaunchKernelGGL(table_end_kernel, grid1(n), dim3(256), 0, stream, s.keys_sorted, n,
+        hipLaunchKernelGGL(table_end_kernel, grid1(n), dim3(256), 0, stream, s.keys, n,
                            s.table[l], g.table_mask);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }

@@ -19,8 +19,12 @@ namespace dgrid {
 // twice the mean point spacing over the bounding box, the finest is
 // kLevelRatio^(kLevels-1) times finer, so that regions a million times denser
 // than the mean still have a level with a few points per cell.  Only
-// occupied cells are stored: a level is its points sorted by cell and an
-// open-addressing hash table from cell key to the cell's range of them.  A
+// occupied cells are stored: the points are sorted once by the Morton code
+// of their finest-level cell, which also orders them by their cell on every
+// coarser level (a level-l cell is the finest cell's coordinates shifted
+// right by l, exactly, since the cell edges are the finest one's times
+// powers of two), and each level is an open-addressing hash table from cell
+// key to the cell's run of that one order.  A
 // cell starts on the finest level where its point's own grid cell holds
 // another point, is clipped ring by ring there, and moves up a level when
 // the rings it would still need exceed kMaxRing.
@@ -59,7 +63,7 @@ struct GridGeom {
 struct GridView {
     GridGeom g;
     const CellEntry *table[kLevels];
-    const uint32_t *sorted[kLevels]; // point ids by cell
+    const uint32_t *sorted[kLevels]; // point ids by cell (one array: the Morton order)
 };
 
 // Hash table slots: a power of two of at least twice the points, so that
@@ -119,6 +123,33 @@ SDF_HD int axis_cell(double x, double lo, double inv_h, uint32_t dim) {
 
 SDF_HD uint64_t cell_key(uint32_t cx, uint32_t cy, uint32_t cz) {
     return (uint64_t)cx | ((uint64_t)cy << 21) | ((uint64_t)cz << 42);
+}
+
+// Morton code of a cell (21 bits per axis, x lowest) and back.
+SDF_HD uint64_t spread3(uint32_t v) {
+    uint64_t x = v & 0x1fffffull;
+    x = (x | x << 32) & 0x1f00000000ffffull;
+    x = (x | x << 16) & 0x1f0000ff0000ffull;
+    x = (x | x << 8) & 0x100f00f00f00f00full;
+    x = (x | x << 4) & 0x10c30c30c30c30c3ull;
+    x = (x | x << 2) & 0x1249249249249249ull;
+    return x;
+}
+SDF_HD uint32_t compact3(uint64_t x) {
+    x &= 0x1249249249249249ull;
+    x = (x | x >> 2) & 0x10c30c30c30c30c3ull;
+    x = (x | x >> 4) & 0x100f00f00f00f00full;
+    x = (x | x >> 8) & 0x1f0000ff0000ffull;
+    x = (x | x >> 16) & 0x1f00000000ffffull;
+    x = (x | x >> 32) & 0x1fffffull;
+    return (uint32_t)x;
+}
+SDF_HD uint64_t morton_key(uint32_t cx, uint32_t cy, uint32_t cz) {
+    return spread3(cx) | spread3(cy) << 1 | spread3(cz) << 2;
+}
+// The level-l cell key of the finest cell with Morton code m.
+SDF_HD uint64_t level_key(uint64_t m, int l) {
+    return cell_key(compact3(m) >> l, compact3(m >> 1) >> l, compact3(m >> 2) >> l);
 }
 
 SDF_HD uint64_t point_key(const GridGeom &g, int l, double x, double y, double z) {

@@ -32,6 +32,8 @@ def vc(tmp_path_factory):
     L.vc_box_unpaired.restype = C.c_int
     L.vc_insphere.argtypes = [P, P, P, P]
     L.vc_insphere.restype = C.c_int
+    L.vc_grid_mismatches.argtypes = [P, C.c_uint32]
+    L.vc_grid_mismatches.restype = C.c_longlong
     return L
 
 
@@ -198,3 +200,34 @@ def test_assert_delaunay_rejects_the_other_triangulation():
         assert _tet_set(_delaunay(pts).simplices) == _tet_set(good)
         with pytest.raises(AssertionError):
             assert_delaunay(pts, good[1:], vol)
+
+
+@pytest.mark.parametrize("kind", ["uniform", "shell", "clustered", "flat", "offset"])
+def test_one_morton_order_serves_every_level(vc, kind):
+    """The grids sort the points once, by the Morton code of their finest
+    cell: every level's cell (from a position, as a lookup computes it) is the
+    finest cell shifted right by the level, and every level's cells are
+    contiguous runs of that one order.  Includes points on the bounding
+    box's far faces (clamped to the last cell) and a flat set (one cell
+    across an axis)."""
+    rng = np.random.default_rng(11)
+    n = 20000
+    if kind == "uniform":
+        pts = rng.uniform(-1, 1, (n, 3))
+    elif kind == "shell":
+        v = rng.normal(size=(n, 3))
+        pts = v / np.linalg.norm(v, axis=1, keepdims=True) * (1 + 1e-3 * rng.normal(size=(n, 1)))
+    elif kind == "clustered":
+        c = rng.uniform(-5, 5, (20, 3))
+        pts = c[rng.integers(0, 20, n)] + 10.0 ** rng.uniform(-4, -1, (n, 1)) * rng.normal(size=(n, 3))
+    elif kind == "flat":
+        pts = np.c_[rng.uniform(0, 1, (n, 2)), np.zeros(n)]
+    else:
+        pts = 1000.0 + rng.uniform(0, 1e-2, (n, 3))
+    # points exactly on the box's faces and corners
+    pts[:8] = np.array([[a, b, c] for a in (0, 1) for b in (0, 1) for c in (0, 1)]) * (
+        pts.max(0) - pts.min(0)) + pts.min(0)
+    pts = np.ascontiguousarray(pts, dtype=np.float32)
+    dims = np.zeros(3, dtype=np.uint32)
+    assert vc.vc_grid(_p(pts), n, _p(dims)) > 0
+    assert vc.vc_grid_mismatches(_p(pts), n) == 0

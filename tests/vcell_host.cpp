@@ -88,10 +88,11 @@ int vc_insphere(const double *a, const double *b, const double *c, const double 
     return in_sphere(a, b, c, q);
 }
 
-// The device's grids over n points (bounding box of the floats; each
-// level's points stably sorted by cell key, and the hash table of occupied
-// cells, filled by the same probing); returns the number of occupied cells
-// of level 0 (dims: its dimensions), 0 if the box is degenerate.
+// The device's grids over n points (bounding box of the floats; the points
+// stably sorted once by the Morton code of their finest cell, and per level
+// the hash table of occupied cells over that order, filled by the same
+// probing); returns the number of occupied cells of level 0 (dims: its
+// dimensions), 0 if the box is degenerate.
 int vc_grid(const float *points, uint32_t n, uint32_t *dims) {
     double lo[3] = {INFINITY, INFINITY, INFINITY}, hi[3] = {-INFINITY, -INFINITY, -INFINITY};
     for (uint32_t i = 0; i < n; ++i)
@@ -101,33 +102,77 @@ int vc_grid(const float *points, uint32_t n, uint32_t *dims) {
         }
     if (!dgrid::grid_geometry(lo, hi, n, g_geom)) return 0;
     const uint64_t slots = g_geom.table_mask + 1;
+    const dgrid::GridLevel &l0 = g_geom.level[0];
     std::vector<std::pair<uint64_t, uint32_t>> keyed(n);
+    for (uint32_t i = 0; i < n; ++i)
+        keyed[i] = {dgrid::morton_key(
+                        (uint32_t)dgrid::axis_cell(points[3 * i], g_geom.lo[0], l0.inv_h, l0.dims[0]),
+                        (uint32_t)dgrid::axis_cell(points[3 * i + 1], g_geom.lo[1], l0.inv_h, l0.dims[1]),
+                        (uint32_t)dgrid::axis_cell(points[3 * i + 2], g_geom.lo[2], l0.inv_h, l0.dims[2])),
+                    i};
+    std::stable_sort(keyed.begin(), keyed.end(),
+                     [](const auto &a, const auto &b) { return a.first < b.first; });
     int occupied0 = 0;
+    std::vector<uint64_t> key(n);
     for (int l = 0; l < dgrid::kLevels; ++l) {
-        for (uint32_t i = 0; i < n; ++i)
-            keyed[i] = {dgrid::point_key(g_geom, l, points[3 * i], points[3 * i + 1],
-                                         points[3 * i + 2]),
-                        i};
-        std::stable_sort(keyed.begin(), keyed.end(),
-                         [](const auto &a, const auto &b) { return a.first < b.first; });
         g_sorted[l].resize(n);
-        for (uint32_t t = 0; t < n; ++t) g_sorted[l][t] = keyed[t].second;
+        for (uint32_t t = 0; t < n; ++t) {
+            g_sorted[l][t] = keyed[t].second;
+            key[t] = dgrid::level_key(keyed[t].first, l);
+        }
         std::vector<dgrid::CellEntry> &table = g_table[l];
         table.assign(slots, dgrid::CellEntry{dgrid::kEmptyKey, 0u, 0u});
         int occupied = 0;
         for (uint32_t t = 0; t < n; ++t) {
-            if (t > 0 && keyed[t].first == keyed[t - 1].first) continue;
+            if (t > 0 && key[t] == key[t - 1]) continue;
             uint32_t e = t + 1;
-            while (e < n && keyed[e].first == keyed[t].first) ++e;
-            uint64_t sl = dgrid::key_hash(keyed[t].first) & g_geom.table_mask;
+            while (e < n && key[e] == key[t]) ++e;
+            uint64_t sl = dgrid::key_hash(key[t]) & g_geom.table_mask;
             while (table[sl].key != dgrid::kEmptyKey) sl = (sl + 1) & g_geom.table_mask;
-            table[sl] = dgrid::CellEntry{keyed[t].first, t, e};
+            table[sl] = dgrid::CellEntry{key[t], t, e};
             ++occupied;
         }
         if (l == 0) occupied0 = occupied;
     }
     for (int k = 0; k < 3; ++k) dims[k] = g_geom.level[0].dims[k];
     return occupied0;
+}
+
+// On the last grid: points whose level-l cell (from their position, as a
+// lookup computes it) differs from their finest cell's coordinates shifted
+// right by l (as the single Morton order assumes), over every level, plus
+// cells whose run in the Morton order is not contiguous (a key met again
+// after another one).
+long long vc_grid_mismatches(const float *points, uint32_t n) {
+    long long bad = 0;
+    const dgrid::GridLevel &l0 = g_geom.level[0];
+    for (uint32_t i = 0; i < n; ++i) {
+        uint32_t f[3];
+        for (int k = 0; k < 3; ++k)
+            f[k] = (uint32_t)dgrid::axis_cell(points[3 * i + k], g_geom.lo[k], l0.inv_h, l0.dims[k]);
+        const uint64_t m = dgrid::morton_key(f[0], f[1], f[2]);
+        for (int l = 0; l < dgrid::kLevels; ++l) {
+            const uint64_t want = dgrid::point_key(g_geom, l, points[3 * i], points[3 * i + 1],
+                                                   points[3 * i + 2]);
+            bad += dgrid::level_key(m, l) != want ? 1 : 0;
+        }
+    }
+    for (int l = 0; l < dgrid::kLevels; ++l) {
+        std::vector<uint64_t> seen;
+        uint64_t prev = dgrid::kEmptyKey;
+        for (uint32_t t = 0; t < n; ++t) {
+            const uint32_t i = g_sorted[l][t];
+            const uint64_t k = dgrid::point_key(g_geom, l, points[3 * i], points[3 * i + 1],
+                                                points[3 * i + 2]);
+            if (k != prev) {
+                seen.push_back(k);
+                prev = k;
+            }
+        }
+        std::sort(seen.begin(), seen.end());
+        bad += (long long)(seen.size() - (size_t)(std::unique(seen.begin(), seen.end()) - seen.begin()));
+    }
+    return bad;
 }
 
 // certify_cell for every point on the last grid: status [n], coincident
