@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void orient_kernel(
     const float *__restrict__ points, uint32_t num_points, const uint32_t *__restrict__ tets_in,
     const int32_t *__restrict__ nbr_in, uint32_t num_tets, uint32_t *__restrict__ tets_o,
     int32_t *__restrict__ nbr_o, uint64_t *__restrict__ key_hi, uint64_t *__restrict__ key_lo,
-    uint32_t *__restrict__ index, uint32_t *__restrict__ error) {
+    uint32_t *__restrict__ index, uint32_t *__restrict__ error, uint32_t kb) {
     const uint32_t t = blockIdx.x * 256u + threadIdx.x;
     if (t >= num_tets) return;
     uint32_t s[4];
@@ -154,8 +154,8 @@ __global__ __launch_bounds__(256) void orient_kernel(
     }
     SDF_CSWAP(0, 1) SDF_CSWAP(2, 3) SDF_CSWAP(0, 2) SDF_CSWAP(1, 3) SDF_CSWAP(1, 2)
 #undef SDF_CSWAP
-    key_hi[t] = ((uint64_t)v[0] << 32) | v[1];
-    key_lo[t] = ((uint64_t)v[2] << 32) | v[3];
+    key_hi[t] = ((uint64_t)v[0] << kb) | v[1];
+    key_lo[t] = ((uint64_t)v[2] << kb) | v[3];
     index[t] = t;
 }
 
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void emit_kernel(
     const uint32_t *__restrict__ order, const uint32_t *__restrict__ rank,
     const uint32_t *__restrict__ tets_o, const int32_t *__restrict__ nbr_o, uint32_t num_tets,
     uint32_t *__restrict__ tets_out, uint32_t *__restrict__ tet_adj,
-    uint32_t *__restrict__ vert_to_tet, uint64_t *__restrict__ edges) {
+    uint32_t *__restrict__ vert_to_tet, uint64_t *__restrict__ edges, uint32_t kb) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
     if (i >= num_tets) return;
     const uint32_t t = order[i];
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void emit_kernel(
 #pragma unroll
         for (int q = p + 1; q < 4; ++q) {
             const uint32_t lo = min(s[p], s[q]), hi = max(s[p], s[q]);
-            edges[6ull * i + e] = ((uint64_t)lo << 32) | hi;
+            edges[6ull * i + e] = ((uint64_t)lo << kb) | hi;
             ++e;
         }
     }
@@ -226,7 +226,8 @@ __global__ __launch_bounds__(256) void both_dirs_kernel(const uint64_t *__restri
                                                         uint64_t capacity,
                                                         uint64_t *__restrict__ dirs,
                                                         uint32_t *__restrict__ counts,
-                                                        uint32_t *__restrict__ error) {
+                                                        uint32_t *__restrict__ error,
+                                                        uint32_t kb) {
     const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
     const uint64_t u = *num_unique;
     if (i >= u) return;
@@ -235,9 +236,9 @@ __global__ __launch_bounds__(256) void both_dirs_kernel(const uint64_t *__restri
         return;
     }
     const uint64_t k = uniq[i];
-    const uint32_t lo = (uint32_t)(k >> 32), hi = (uint32_t)k;
+    const uint32_t lo = (uint32_t)(k >> kb), hi = (uint32_t)(k & ((1ull << kb) - 1ull));
     dirs[2 * i] = k;
-    dirs[2 * i + 1] = ((uint64_t)hi << 32) | lo;
+    dirs[2 * i + 1] = ((uint64_t)hi << kb) | lo;
     atomicAdd(counts + lo, 1u);
     atomicAdd(counts + hi, 1u);
 }
@@ -245,10 +246,10 @@ __global__ __launch_bounds__(256) void both_dirs_kernel(const uint64_t *__restri
 __global__ __launch_bounds__(256) void low_words_kernel(const uint64_t *__restrict__ keys,
                                                         const uint64_t *__restrict__ num_unique,
                                                         uint64_t capacity,
-                                                        uint32_t *__restrict__ out) {
+                                                        uint32_t *__restrict__ out, uint32_t kb) {
     const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
     const uint64_t n = 2 * *num_unique;
-    if (i < n && n <= capacity) out[i] = (uint32_t)keys[i];
+    if (i < n && n <= capacity) out[i] = (uint32_t)(keys[i] & ((1ull << kb) - 1ull));
 }
 
 struct TablesScratch {
@@ -270,12 +271,22 @@ size_t tables_temp_bytes(uint32_t num_points, uint32_t num_tets, uint64_t capaci
     const uint32_t *v = nullptr;
     uint32_t *vo = nullptr;
     const uint64_t ne = 6ull * num_tets;
-    if (rocprim::radix_sort_pairs(nullptr, a, k, ko, v, vo, num_tets, 0u, 64u) != hipSuccess)
-        return 0;
-    if (rocprim::radix_sort_keys(nullptr, b, k, ko, (size_t)ne, 0u, 64u) != hipSuccess) return 0;
+    // the sorts run over 2 kb bits (launch_delaunay_tables); the size for
+    // 64 bits is asked as well and the larger kept
+    const uint32_t kb = num_points > 1u ? 32u - (uint32_t)__builtin_clz(num_points - 1u) : 1u;
+    for (const uint32_t bits : {64u, 2u * kb}) {
+        size_t a1 = 0, b1 = 0, d1 = 0;
+        if (rocprim::radix_sort_pairs(nullptr, a1, k, ko, v, vo, num_tets, 0u, bits) !=
+                hipSuccess ||
+            rocprim::radix_sort_keys(nullptr, b1, k, ko, (size_t)ne, 0u, bits) != hipSuccess ||
+            rocprim::radix_sort_keys(nullptr, d1, k, ko, (size_t)capacity, 0u, bits) !=
+                hipSuccess)
+            return 0;
+        a = std::max(a, a1);
+        b = std::max(b, b1);
+        d = std::max(d, d1);
+    }
     if (rocprim::unique(nullptr, c, k, ko, (uint64_t *)nullptr, (size_t)ne) != hipSuccess) return 0;
-    if (rocprim::radix_sort_keys(nullptr, d, k, ko, (size_t)capacity, 0u, 64u) != hipSuccess)
-        return 0;
     size_t e = 0;
     if (rocprim::exclusive_scan(nullptr, e, v, vo, 0u, (size_t)num_points + 1,
                                 rocprim::plus<uint32_t>()) != hipSuccess)
@@ -418,6 +429,9 @@ hipError_t launch_delaunay_tables(const float *points, uint32_t num_points,
     TablesScratch s;
     if (!carve(scratch, scratch_bytes, num_points, num_tets, cap, s)) return hipErrorInvalidValue;
     const uint32_t T = num_tets;
+    // keys pack two point ids of kb bits each, so the radix sorts run over 2 kb
+    // bits (40 at 1M points) instead of 64
+    const uint32_t kb = num_points > 1u ? 32u - (uint32_t)__builtin_clz(num_points - 1u) : 1u;
     hipLaunchKernelGGL(fill_u32_kernel, grid1(1), dim3(256), 0, stream, s.error, (uint64_t)1, 0u);
     hipLaunchKernelGGL(fill_u32_kernel, grid1(num_points), dim3(256), 0, stream, vert_to_tet,
                        (uint64_t)num_points, kNoIndex);
@@ -429,26 +443,26 @@ hipError_t launch_delaunay_tables(const float *points, uint32_t num_points,
     if (T > 0) {
         hipLaunchKernelGGL(orient_kernel, grid1(T), dim3(256), 0, stream, points, num_points,
                            tets_in, nbr_in, T, s.tets_o, s.nbr_o, s.key_hi, s.key_lo, s.idx_a,
-                           s.error);
+                           s.error, kb);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // lexicographic order of (key_hi, key_lo): stable sort by key_lo, then by key_hi
         size_t t = s.temp_bytes;
         e = rocprim::radix_sort_pairs(s.temp, t, s.key_lo, s.key_sorted, s.idx_a, s.idx_b, T, 0u,
-                                      64u, stream);
+                                      2u * kb, stream);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(gather_u64_kernel, grid1(T), dim3(256), 0, stream, s.key_hi, s.idx_b,
                            T, s.key_tmp);
         t = s.temp_bytes;
         e = rocprim::radix_sort_pairs(s.temp, t, s.key_tmp, s.key_sorted, s.idx_b, s.idx_a, T, 0u,
-                                      64u, stream);
+                                      2u * kb, stream);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(rank_kernel, grid1(T), dim3(256), 0, stream, s.idx_a, T, s.rank);
         hipLaunchKernelGGL(emit_kernel, grid1(T), dim3(256), 0, stream, s.idx_a, s.rank, s.tets_o,
-                           s.nbr_o, T, tets_out, tet_adj, vert_to_tet, s.edges);
+                           s.nbr_o, T, tets_out, tet_adj, vert_to_tet, s.edges, kb);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         const uint64_t ne = 6ull * T;
         t = s.temp_bytes;
-        e = rocprim::radix_sort_keys(s.temp, t, s.edges, s.edges_sorted, (size_t)ne, 0u, 64u,
+        e = rocprim::radix_sort_keys(s.temp, t, s.edges, s.edges_sorted, (size_t)ne, 0u, 2u * kb,
                                      stream);
         if (e != hipSuccess) return e;
         t = s.temp_bytes;
@@ -456,7 +470,7 @@ hipError_t launch_delaunay_tables(const float *points, uint32_t num_points,
                             rocprim::equal_to<uint64_t>(), stream);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(both_dirs_kernel, grid1(ne), dim3(256), 0, stream, s.uniq,
-                           s.num_unique, cap, s.dirs, s.counts, s.error);
+                           s.num_unique, cap, s.dirs, s.counts, s.error, kb);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // the edge count decides the size of the last sort: read it (and the
         // input checks) on the host
@@ -474,11 +488,11 @@ hipError_t launch_delaunay_tables(const float *points, uint32_t num_points,
         }
         const uint64_t n2 = 2 * num_unique;
         t = s.temp_bytes;
-        e = rocprim::radix_sort_keys(s.temp, t, s.dirs, s.dirs_sorted, (size_t)n2, 0u, 64u,
+        e = rocprim::radix_sort_keys(s.temp, t, s.dirs, s.dirs_sorted, (size_t)n2, 0u, 2u * kb,
                                      stream);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(low_words_kernel, grid1(n2), dim3(256), 0, stream, s.dirs_sorted,
-                           s.num_unique, cap, adjacency);
+                           s.num_unique, cap, adjacency, kb);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     size_t t = s.temp_bytes;
