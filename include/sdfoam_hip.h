@@ -468,6 +468,22 @@ int sdf_delaunay_certify(const float *points, uint32_t num_points,
                          uint32_t *open_points, uint64_t *counts, void *scratch,
                          size_t scratch_bytes, void *stream);
 
+/* sdf_delaunay_certify_exhaustive: sdf_delaunay_certify for a small set
+ * (the points the full certification leaves open, certified among
+ * themselves), with a clipping box 1e8 extents wide and every cell the grid
+ * search leaves open clipped by every point of the set.  A cell then closed
+ * certifies as above; a cell still reaching the box (a hull point of the
+ * set) is listed in open_points and its vertices off the box faces are
+ * reported as well: with the certified ones, every Delaunay tetrahedron of
+ * the set whose circumcentre lies within the box.  counts as for
+ * sdf_delaunay_certify.  32 to 2^20 points.  Synchronizes the stream.
+ * No counterpart in the reference: it replaces the host triangulation of
+ * the open points between the two calls above. */
+int sdf_delaunay_certify_exhaustive(const float *points, uint32_t num_points,
+                                    uint32_t *reports, uint64_t report_capacity,
+                                    uint32_t *open_points, uint64_t *counts,
+                                    void *scratch, size_t scratch_bytes, void *stream);
+
 /* sdf_delaunay_merge: candidates [M, 4] (the Delaunay tetrahedra of the open
  * points, as global point ids) are kept where their circumsphere holds no
  * point; each certified tetrahedron is kept once.  Writes tets [T, 4] (any

@@ -56,6 +56,7 @@ EXPORTS = (
     "sdf_delaunay_tables",
     "sdf_delaunay_certify_scratch_bytes",
     "sdf_delaunay_certify",
+    "sdf_delaunay_certify_exhaustive",
     "sdf_delaunay_merge_scratch_bytes",
     "sdf_delaunay_merge",
     "sdf_delaunay_check",
@@ -225,6 +226,8 @@ def lib() -> C.CDLL:
     L.sdf_delaunay_certify_scratch_bytes.argtypes = [U32]
     L.sdf_delaunay_certify.restype = C.c_int
     L.sdf_delaunay_certify.argtypes = [P, U32, P, C.c_uint64, P, P, P, SZ, P]
+    L.sdf_delaunay_certify_exhaustive.restype = C.c_int
+    L.sdf_delaunay_certify_exhaustive.argtypes = [P, U32, P, C.c_uint64, P, P, P, SZ, P]
     L.sdf_delaunay_merge_scratch_bytes.restype = SZ
     L.sdf_delaunay_merge_scratch_bytes.argtypes = [U32, C.c_uint64, C.c_uint64, C.c_uint64]
     L.sdf_delaunay_merge.restype = C.c_int

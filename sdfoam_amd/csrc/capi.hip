@@ -6,6 +6,7 @@
 #include <cstring>
 #include <mutex>
 
+#include "delaunay_gpu.h"
 #include "trace_kernels.h"
 
 using namespace sdfoam_hip;
@@ -746,6 +747,32 @@ int sdf_delaunay_certify(const float *points, uint32_t num_points, uint32_t *rep
     if (e == hipErrorInvalidValue)
         return fail(SDF_E_INVALID, "points must be finite and span a volume");
     if (e != hipSuccess) return hip_fail(e, "delaunay_certify");
+    return SDF_OK;
+}
+
+int sdf_delaunay_certify_exhaustive(const float *points, uint32_t num_points, uint32_t *reports,
+                                    uint64_t report_capacity, uint32_t *open_points,
+                                    uint64_t *counts, void *scratch, size_t scratch_bytes,
+                                    void *stream) {
+    if (!points || !open_points || !counts || !scratch || (report_capacity > 0 && !reports))
+        return fail(SDF_E_INVALID, "NULL pointer argument");
+    if ((reinterpret_cast<uintptr_t>(scratch) & 255u) != 0)
+        return fail(SDF_E_INVALID, "scratch must be 256-byte aligned");
+    if (num_points < 32)
+        return fail(SDF_E_INVALID, "Delaunay triangulation does not support less than 32 points");
+    if (num_points > (1u << 20))
+        return fail(SDF_E_INVALID, "sdf_delaunay_certify_exhaustive takes at most 2^20 points");
+    const size_t need = delaunay_certify_scratch_bytes(num_points);
+    if (need == 0) return fail(SDF_E_HIP, "delaunay_certify: no device to size the sorts for");
+    if (scratch_bytes < need)
+        return fail(SDF_E_INVALID, "scratch must hold %zu bytes (got %zu)", need, scratch_bytes);
+    hipError_t e = launch_delaunay_certify_exhaustive(points, num_points, reports,
+                                                      report_capacity, open_points, counts,
+                                                      scratch, scratch_bytes,
+                                                      static_cast<hipStream_t>(stream));
+    if (e == hipErrorInvalidValue)
+        return fail(SDF_E_INVALID, "points must be finite and span a volume");
+    if (e != hipSuccess) return hip_fail(e, "delaunay_certify_exhaustive");
     return SDF_OK;
 }
 

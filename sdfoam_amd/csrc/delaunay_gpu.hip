@@ -25,6 +25,7 @@
 #include <cstring>
 
 #include "delaunay_grid.h"
+#include "delaunay_gpu.h"
 #include "trace_kernels.h"
 
 namespace sdfoam_hip {
@@ -594,6 +595,12 @@ __device__ uint64_t wave_may_cut(const WaveCell &c, WaveShared &sh, bool mine, c
     return m;
 }
 
+// The clipping box of an exhaustive certification: the bounding box grown by
+// this many times its extent, so that the hull cells' Voronoi vertices
+// (circumcentres of Delaunay tetrahedra on the hull, some ~1e6 extents away
+// for nearly flat ones) lie inside it.
+constexpr double kExhaustiveBox = 1e8;
+
 // Candidates that survive the per-lane filters in a batch before the batch
 // test pays for itself (a wave_clip call that finds no cut costs about as
 // much as the test over a typical cell's vertices).
@@ -615,6 +622,7 @@ __device__ bool wave_touches_box(const WaveCell &c, const WaveShared &sh) {
 // four.  What is uniform over the wave and indexed at run time (the grid
 // cell and searched rings per level) or needed by every lane (the cell's
 // bounds) lives in LDS, not in per-lane registers or scratch.
+template <bool EXHAUSTIVE>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void certify_kernel(const float *__restrict__ p, uint32_t n,
                                                      GridView gv, uint32_t *__restrict__ reports,
                                                      uint64_t report_capacity,
@@ -781,11 +789,99 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                 break;
         }
     }
+    // exhaustive: a cell the grid search leaves open is clipped by every point
+    // of the set (the batch test drops the planes that miss it); it is then
+    // exact, certified if no box face is left, else a hull cell whose
+    // vertices off the box faces (circumcentres inside the box) are reported
+    // as well
+    bool hull_cell = false;
+    if (EXHAUSTIVE && st == vcell::kOpen && !coincident) {
+        bool failed = false;
+        for (uint32_t base = 0; base < n && !failed; base += 64u) {
+            const uint32_t j = base + l;
+            bool surv = false, dup = false;
+            double q[3] = {0.0, 0.0, 0.0}, d2 = INFINITY;
+            if (j < n && j != i) {
+                q[0] = (double)p[3ull * j] - o[0];
+                q[1] = (double)p[3ull * j + 1] - o[1];
+                q[2] = (double)p[3ull * j + 2] - o[2];
+                d2 = q[0] * q[0] + q[1] * q[1] + q[2] * q[2];
+                if (d2 == 0.0) {
+                    dup = true;
+                } else if (d2 <= 4.0 * sh.mr2 * (1.0 + 1e-9)) {
+                    double reach_q = 0.0, mag = d2;
+                    for (int mm = 0; mm < 3; ++mm) {
+                        const double bb = q[mm] > 0.0 ? sh.bhi[mm] : sh.blo[mm];
+                        reach_q += bb * q[mm];
+                        mag += vcell::dabs(bb * q[mm]);
+                    }
+                    surv = !(reach_q < 0.5 * d2 - 1e-14 * mag);
+                }
+            }
+            if (wballot(dup)) {
+                coincident = true;
+                st = vcell::kUncertain;
+                failed = true;
+                break;
+            }
+            uint64_t m = wballot(surv);
+            if (__popcll(m) >= kBatchTestMin) m = wave_may_cut(c, sh, surv, q, 0.5 * d2);
+            while (m) {
+                const bool mine = (m >> l) & 1ull;
+                const double dm = wmind(mine ? d2 : INFINITY);
+                const uint64_t hit = wballot(mine && d2 == dm);
+                const int src = __builtin_ctzll(hit);
+                m &= ~(1ull << src);
+                const double qq[3] = {__shfl(q[0], src, 64), __shfl(q[1], src, 64),
+                                      __shfl(q[2], src, 64)};
+                const double dd = __shfl(d2, src, 64);
+                const int32_t jj = __shfl((int)j, src, 64);
+                // a point the grid search clipped by already: its plane holds
+                // vertices of the cell, which the exact test cannot place
+                if (wballot((int)l < c.np && sh.pp[l] == jj)) continue;
+                const int rc = wave_clip(c, sh, qq, 0.5 * dd, jj);
+                if (rc >= 2) {
+                    st = rc == 2 ? vcell::kUncertain : vcell::kOverflow;
+                    failed = true;
+                    break;
+                }
+            }
+        }
+        if (!failed) {
+            hull_cell = wave_touches_box(c, sh);
+            st = hull_cell ? vcell::kOpen : vcell::kCertified;
+        }
+    }
     if (l == 0) {
         status_out[i] = st;
         if (coincident) atomicAdd(counters + 4, 1ull);
     }
-    if (st == vcell::kCertified) {
+    if (hull_cell) {
+        // the vertices of three bisectors: Delaunay tetrahedra of the set
+        bool fin[2] = {false, false};
+        for (int s = 0; s < 2; ++s)
+            fin[s] = c.vp[s] != kFree && sh.pp[plane_of(c.vp[s], 0)] >= 0 &&
+                     sh.pp[plane_of(c.vp[s], 1)] >= 0 && sh.pp[plane_of(c.vp[s], 2)] >= 0;
+        const uint64_t a0 = wballot(fin[0]), a1 = wballot(fin[1]);
+        const unsigned long long nv = (unsigned long long)(__popcll(a0) + __popcll(a1));
+        unsigned long long at = 0;
+        if (l == 0) at = atomicAdd(counters, nv);
+        at = __shfl(at, 0, 64);
+        if (at + nv <= report_capacity)
+            for (int s = 0; s < 2; ++s) {
+                if (!fin[s]) continue;
+                const uint32_t idx = s == 0 ? wbelow(a0) : (uint32_t)__popcll(a0) + wbelow(a1);
+                uint32_t *row = reports + 4ull * (at + idx);
+                row[0] = i;
+                row[1] = (uint32_t)sh.pp[plane_of(c.vp[s], 0)];
+                row[2] = (uint32_t)sh.pp[plane_of(c.vp[s], 1)];
+                row[3] = (uint32_t)sh.pp[plane_of(c.vp[s], 2)];
+            }
+        if (l == 0) {
+            const unsigned long long at2 = atomicAdd(counters + 1, 1ull);
+            open[at2] = i;
+        }
+    } else if (st == vcell::kCertified) {
         const uint64_t a0 = wballot(c.vp[0] != kFree), a1 = wballot(c.vp[1] != kFree);
         const unsigned long long nv = (unsigned long long)(__popcll(a0) + __popcll(a1));
         unsigned long long at = 0;
@@ -1113,7 +1209,7 @@ namespace {
 // for the calls that follow; `g` receives it too and must live until the
 // caller's next synchronisation of the stream (the copy reads it).
 hipError_t build_grid(const float *points, uint32_t n, const GridScratch &s, GridGeom &g,
-                      hipStream_t stream) {
+                      hipStream_t stream, double box_scale = 1.0) {
     hipLaunchKernelGGL(tag_kernel, dim3(1), dim3(64), 0, stream, s.tag, 0ull, 0ull);
     hipLaunchKernelGGL(init_kernel, dim3(1), dim3(64), 0, stream, s.mm, s.counters);
     hipLaunchKernelGGL(bbox_kernel, dim3(std::min<uint32_t>(grid1(n).x, kBboxBlocks)), dim3(256), 0,
@@ -1127,7 +1223,7 @@ hipError_t build_grid(const float *points, uint32_t n, const GridScratch &s, Gri
         lo[k] = (double)unordered(hm[k]);
         hi[k] = (double)unordered(hm[3 + k]);
     }
-    if (!dgrid::grid_geometry(lo, hi, n, g)) return hipErrorInvalidValue;
+    if (!dgrid::grid_geometry(lo, hi, n, g, box_scale)) return hipErrorInvalidValue;
     // the points sorted once by the Morton code of their finest cell (one
     // radix sort in place of one per level; 11 at ~0.25 ms each at 1M
     // points), then per level the table of occupied cells over that order
@@ -1171,11 +1267,15 @@ GridView grid_view(const GridScratch &s, const GridGeom &g) {
 hipError_t run_certify(const float *points, uint32_t n, const uint32_t *query, uint32_t nq,
                        const GridView &gv, const GridScratch &s, uint32_t *reports,
                        uint64_t report_capacity, uint32_t *open, uint64_t counts[5],
-                       hipStream_t stream) {
+                       hipStream_t stream, bool exhaustive = false) {
     hipError_t e;
     if (nq > 0) {
-        hipLaunchKernelGGL(certify_kernel, dim3(nq), dim3(64), 0, stream, points, n, gv, reports,
-                           report_capacity, s.counters, open, s.status, query);
+        if (exhaustive)
+            hipLaunchKernelGGL(certify_kernel<true>, dim3(nq), dim3(64), 0, stream, points, n, gv,
+                               reports, report_capacity, s.counters, open, s.status, query);
+        else
+            hipLaunchKernelGGL(certify_kernel<false>, dim3(nq), dim3(64), 0, stream, points, n, gv,
+                               reports, report_capacity, s.counters, open, s.status, query);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     unsigned long long hc[8];
@@ -1189,18 +1289,37 @@ hipError_t run_certify(const float *points, uint32_t n, const uint32_t *query, u
 
 } // namespace
 
-hipError_t launch_delaunay_certify(const float *points, uint32_t n, uint32_t *reports,
-                                   uint64_t report_capacity, uint32_t *open, uint64_t counts[5],
-                                   void *scratch, size_t bytes, hipStream_t stream) {
+namespace {
+
+hipError_t certify_all(const float *points, uint32_t n, uint32_t *reports,
+                       uint64_t report_capacity, uint32_t *open, uint64_t counts[5],
+                       void *scratch, size_t bytes, hipStream_t stream, bool exhaustive) {
     for (int k = 0; k < 5; ++k) counts[k] = 0;
     const size_t temp = grid_temp_bytes(n);
     GridScratch s = carve_grid(scratch, n, temp);
     if (n == 0 || temp == 0 || s.total > bytes) return hipErrorInvalidValue;
     GridGeom g{};
-    hipError_t e = build_grid(points, n, s, g, stream);
+    hipError_t e = build_grid(points, n, s, g, stream, exhaustive ? kExhaustiveBox : 1.0);
     if (e != hipSuccess) return e;
     return run_certify(points, n, nullptr, n, grid_view(s, g), s, reports, report_capacity, open,
-                       counts, stream);
+                       counts, stream, exhaustive);
+}
+
+} // namespace
+
+hipError_t launch_delaunay_certify(const float *points, uint32_t n, uint32_t *reports,
+                                   uint64_t report_capacity, uint32_t *open, uint64_t counts[5],
+                                   void *scratch, size_t bytes, hipStream_t stream) {
+    return certify_all(points, n, reports, report_capacity, open, counts, scratch, bytes, stream,
+                       false);
+}
+
+hipError_t launch_delaunay_certify_exhaustive(const float *points, uint32_t n, uint32_t *reports,
+                                              uint64_t report_capacity, uint32_t *open,
+                                              uint64_t counts[5], void *scratch, size_t bytes,
+                                              hipStream_t stream) {
+    return certify_all(points, n, reports, report_capacity, open, counts, scratch, bytes, stream,
+                       true);
 }
 
 hipError_t launch_delaunay_check(const float *points, uint32_t n, const uint32_t *tets,

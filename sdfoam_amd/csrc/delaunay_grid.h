@@ -76,9 +76,11 @@ inline uint64_t table_slots(uint32_t n) {
     return c;
 }
 
-// The grids over the bounding box [lo, hi] of n points.  False if the box
-// is not finite or has no extent.
-inline bool grid_geometry(const double *lo, const double *hi, uint32_t n, GridGeom &g) {
+// The grids over the bounding box [lo, hi] of n points, and the clipping box:
+// the bounding box grown by box_scale times its extent.  False if the box is
+// not finite or has no extent.
+inline bool grid_geometry(const double *lo, const double *hi, uint32_t n, GridGeom &g,
+                          double box_scale = 1.0) {
     double ext = 0.0, mag = 0.0;
     for (int k = 0; k < 3; ++k) {
         if (!std::isfinite(lo[k]) || !std::isfinite(hi[k]) || !(hi[k] >= lo[k])) return false;
@@ -110,8 +112,8 @@ inline bool grid_geometry(const double *lo, const double *hi, uint32_t n, GridGe
     g.table_mask = table_slots(n) - 1;
     for (int k = 0; k < 3; ++k) {
         g.lo[k] = lo[k];
-        g.box_lo[k] = lo[k] - ext;
-        g.box_hi[k] = hi[k] + ext;
+        g.box_lo[k] = lo[k] - box_scale * ext;
+        g.box_hi[k] = hi[k] + box_scale * ext;
     }
     return true;
 }

@@ -167,12 +167,14 @@ class _Undecided(RuntimeError):
     """The GPU tetrahedralisation met a sign it could not decide."""
 
 
-def _certify(L, pts: torch.Tensor, gptr: int, gbytes: int, stream, query=None):
+def _certify(L, pts: torch.Tensor, gptr: int, gbytes: int, stream, query=None,
+             exhaustive: bool = False):
     """sdf_delaunay_certify over CUDA float32 points [n, 3], or with `query`
     (int32 ids) sdf_delaunay_certify_points over those on the grid of an
-    sdf_delaunay_check call: (reports [nr, 4] int32 rows (point, a, b, c),
-    open points [nu] int32 in index order, counts).  Raises _Undecided where
-    the GPU cannot decide."""
+    sdf_delaunay_check call, or with `exhaustive` sdf_delaunay_certify_exhaustive
+    (a small set: hull cells' finite vertices reported too): (reports [nr, 4]
+    int32 rows (point, a, b, c), open points [nu] int32 in index order,
+    counts).  Raises _Undecided where the GPU cannot decide."""
     dev = pts.device
     n = pts.numel() // 3
     nq = n if query is None else int(query.numel())
@@ -184,7 +186,10 @@ def _certify(L, pts: torch.Tensor, gptr: int, gbytes: int, stream, query=None):
     cap = (28 if query is None else 40) * nq + 4096
     for _ in range(2):
         reports = torch.empty((cap, 4), dtype=torch.int32, device=dev)
-        if query is None:
+        if exhaustive:
+            rc = L.sdf_delaunay_certify_exhaustive(ptr(pts), n, ptr(reports), cap, ptr(open_pts),
+                                                   counts, gptr, gbytes, stream)
+        elif query is None:
             rc = L.sdf_delaunay_certify(ptr(pts), n, ptr(reports), cap, ptr(open_pts), counts,
                                         gptr, gbytes, stream)
         else:
@@ -208,6 +213,99 @@ def _certify(L, pts: torch.Tensor, gptr: int, gbytes: int, stream, query=None):
 # this share of them open (at C3 it halves them in a few ms; a further level
 # would remove another ~12% only, for about the same time again).
 _LEVEL_SHRINK = 0.7
+
+
+class _OpenRetry(RuntimeError):
+    """The open points' tetrahedra from the GPU left a face without a
+    neighbour off the convex hull (a circumcentre beyond the exhaustive
+    certification's box, or a fault): they are made again with Qhull."""
+
+
+def _open_candidates_gpu(L, pts: torch.Tensor, U: torch.Tensor, stream, stats: dict):
+    """Candidates [m, 4] for the Delaunay tetrahedra with four open vertices
+    from sdf_delaunay_certify_exhaustive over the open points U: every
+    Delaunay tetrahedron of the whole set with four vertices in U is one of
+    U's own (its circumsphere holds no point at all), which the exhaustive
+    certification reports from each of its vertices' cells, hull cells
+    included, as long as its circumcentre lies within the 1e8-extent box.
+    None when a cell is undecided (Qhull then decides)."""
+    if U.numel() < 32 or U.numel() > (1 << 20):
+        return None
+    t = time.perf_counter()
+    gb = int(L.sdf_delaunay_certify_scratch_bytes(U.numel()))
+    if gb == 0:
+        return None
+    gbuf, gp = _aligned(gb, pts.device)
+    try:
+        rep, U2, counts = _certify(L, pts[U.long()].contiguous(), gp, gb, stream, exhaustive=True)
+    except _Undecided:
+        return None
+    finally:
+        del gbuf
+    # a cell over the fixed capacity reports nothing, but each of its
+    # tetrahedra comes from its other vertices' cells as well (one whose four
+    # vertices all overflow leaves a hole, which the hull check finds); an
+    # undecided sign means cospherical points, which Qhull decides
+    if counts[2] or rep.shape[0] == 0:
+        return None
+    cand = U[rep.long()]
+    # a tetrahedron comes once from each of its vertices
+    cand = torch.unique(torch.sort(cand, dim=1)[0], dim=0)
+    stats["open_levels"] = [int(U2.numel())]
+    stats["open_points_qhull"] = 0
+    stats["open_levels_s"] = time.perf_counter() - t
+    stats["open_qhull_s"] = 0.0
+    return cand.to(torch.int32).contiguous()
+
+
+def _hull_is_convex(pts: torch.Tensor, tets: torch.Tensor, nbr: torch.Tensor, T: int,
+                    U: torch.Tensor) -> bool:
+    """Whether every face of the merged tetrahedra without a neighbour is a
+    facet of the convex hull: every point of U (the open points, among which
+    are the hull's vertices and the far vertex of any tetrahedron missing
+    behind such a face) lies strictly on the face's inner side, the sign of
+    each float64 orientation determinant decided against a bound of 1e-14
+    times its permanent (Shewchuk's static bound for orient3d is 7.8e-16).
+    Then the merged tetrahedra, all Delaunay, cover the hull: no face
+    without a neighbour lies inside it."""
+    dev = pts.device
+    nb = nbr[:T]
+    tt, jj = torch.nonzero(nb < 0, as_tuple=True)
+    F = int(tt.numel())
+    if F == 0:
+        return False
+    tv = tets[:T][tt].long()
+    keep = torch.arange(4, device=dev)[None, :] != jj[:, None]
+    fv = tv[keep].view(F, 3)
+    far = tv[torch.arange(F, device=dev), jj]
+    P = pts.double()
+    X = P[U.long()]
+    uid = U.long()
+    # faces in chunks of up to 2^23 face-point pairs; one host read at the end
+    step = max(1, (1 << 23) // max(1, int(uid.numel())))
+    ok = torch.ones((), dtype=torch.bool, device=dev)
+    for f0 in range(0, F, step):
+        f1 = min(F, f0 + step)
+        a, b, c, d = P[fv[f0:f1, 0]], P[fv[f0:f1, 1]], P[fv[f0:f1, 2]], P[far[f0:f1]]
+        e1, e2 = b - a, c - a
+        n = torch.cross(e1, e2, dim=1)
+        na = torch.stack([(e1[:, 1] * e2[:, 2]).abs() + (e1[:, 2] * e2[:, 1]).abs(),
+                          (e1[:, 2] * e2[:, 0]).abs() + (e1[:, 0] * e2[:, 2]).abs(),
+                          (e1[:, 0] * e2[:, 1]).abs() + (e1[:, 1] * e2[:, 0]).abs()], dim=1)
+        dd = d - a
+        sd = (dd * n).sum(1)
+        ok &= (sd.abs() > 1e-14 * (dd.abs() * na).sum(1)).all()
+        sx = torch.zeros((f1 - f0, X.shape[0]), dtype=torch.float64, device=dev)
+        bx = torch.zeros_like(sx)
+        for k in range(3):
+            xk = X[None, :, k] - a[:, k:k + 1]
+            sx += xk * n[:, k:k + 1]
+            bx += xk.abs() * na[:, k:k + 1]
+        on_face = (uid[None, :] == fv[f0:f1, 0:1]) | (uid[None, :] == fv[f0:f1, 1:2]) | \
+            (uid[None, :] == fv[f0:f1, 2:3])
+        inner = (torch.sign(sx) == torch.sign(sd)[:, None]) & (sx.abs() > 1e-14 * bx)
+        ok &= (inner | on_face).all()
+    return bool(ok.item())
 
 
 def _open_candidates(L, pts: torch.Tensor, U: torch.Tensor, stream, stats: dict):
@@ -276,11 +374,14 @@ def has_coincident_points(pts: torch.Tensor) -> bool:
 
 
 def _merge(L, pts: torch.Tensor, gptr: int, gbytes: int, reports, cand, verified,
-           hull_faces: int, stream, tcap: int | None = None):
+           hull_faces, stream, tcap: int | None = None, open_ids=None):
     """sdf_delaunay_merge (sdf_delaunay_merge_verified with `verified`
     rows): (tets, neighbors, T); raises _Undecided when a candidate is
     undecided or the union is inconsistent (Qhull on every point decides).
-    `tcap`: the tets to make room for (a second merge runs if more come)."""
+    `tcap`: the tets to make room for (a second merge runs if more come).
+    hull_faces None (the candidates came from the GPU, not Qhull): instead
+    of Qhull's hull face count, every face without a neighbour must be a
+    convex-hull facet (_hull_is_convex over `open_ids`), else _OpenRetry."""
     dev = pts.device
     n = pts.numel() // 3
     nr, m = int(reports.shape[0]), int(cand.shape[0])
@@ -307,25 +408,57 @@ def _merge(L, pts: torch.Tensor, gptr: int, gbytes: int, reports, cand, verified
             tcap = int(result[0])
             continue
         if rc == _lib.SDF_E_INVALID:
+            if hull_faces is None:
+                raise _OpenRetry(L.sdf_last_error().decode())
             raise _Undecided(L.sdf_last_error().decode())
         check(rc)
         break
     else:
         raise _Undecided("tets did not fit the merge's capacity")
     T = int(result[0])
-    if int(result[1]) != hull_faces:
+    if hull_faces is None:
+        if not _hull_is_convex(pts, tets, nbr, T, open_ids):
+            raise _OpenRetry("a face without a neighbour is not on the convex hull")
+    elif int(result[1]) != hull_faces:
         raise _Undecided(f"{int(result[1])} faces without a neighbour, the hull has {hull_faces}")
     return tets, nbr, T
+
+
+def _open_and_merge(L, pts, U, gptr, gbytes, reports, verified, stream, stats, tcap=None):
+    """The open points' candidates (from the GPU's exhaustive certification,
+    else Qhull) and the merge: (tets, neighbors, T, candidates)."""
+    t = time.perf_counter()
+    cand = _open_candidates_gpu(L, pts, U, stream, stats)
+    t_open = time.perf_counter()
+    if cand is not None:
+        try:
+            tets, nbr, T = _merge(L, pts, gptr, gbytes, reports, cand, verified, None, stream,
+                                  tcap, open_ids=U)
+            stats["open_points_qhull_s"] = t_open - t
+            stats["merge_s"] = time.perf_counter() - t_open
+            return tets, nbr, T, cand
+        except _OpenRetry as e:
+            stats["open_gpu_retry"] = str(e)
+    t = time.perf_counter()
+    cand, hull_faces = _open_candidates(L, pts, U, stream, stats)
+    t_open = time.perf_counter()
+    tets, nbr, T = _merge(L, pts, gptr, gbytes, reports, cand, verified, hull_faces, stream, tcap)
+    stats["open_points_qhull_s"] = t_open - t
+    stats["merge_s"] = time.perf_counter() - t_open
+    return tets, nbr, T, cand
 
 
 def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, dict]:
     """Delaunay tetrahedra of CUDA float32 points [N, 3] by certified
     Voronoi cells (sdf_delaunay_certify / sdf_delaunay_merge): the points
     whose cells the GPU cannot certify (the hull and the layer under it) are
-    certified again among themselves, and what stays open at the last level
-    is triangulated by Qhull on the host; their tetrahedra are kept where no
-    point lies in the circumsphere.  Returns (tets [T, 4] int32, neighbors
-    [T, 4] int32, -1 on the hull, stats) on the points' device."""
+    certified again among themselves, exhaustively (hull cells' finite
+    vertices included); their tetrahedra are kept where no point lies in the
+    circumsphere, and the hull's faces are checked convex.  Where that
+    certification cannot decide or the check fails, the open points'
+    tetrahedra come from Qhull on the host instead.  Returns (tets [T, 4]
+    int32, neighbors [T, 4] int32, -1 on the hull, stats) on the points'
+    device."""
     pts = points.contiguous()
     dev = pts.device
     n = pts.numel() // 3
@@ -341,15 +474,11 @@ def gpu_tetrahedra(points: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, di
         reports, U, counts = _certify(L, pts, gptr, gbytes, stream)
         nr, nu = int(reports.shape[0]), int(U.numel())
         t1 = time.perf_counter()
-        cand, hull_faces = _open_candidates(L, pts, U, stream, stats)
-        m = int(cand.shape[0])
-        t2 = time.perf_counter()
-        tets, nbr, T = _merge(L, pts, gptr, gbytes, reports, cand, None, hull_faces, stream)
-    t3 = time.perf_counter()
-    stats.update({"open": nu, "reports": nr, "candidates": m, "tets": T,
+        tets, nbr, T, cand = _open_and_merge(L, pts, U, gptr, gbytes, reports, None, stream,
+                                             stats)
+    stats.update({"open": nu, "reports": nr, "candidates": int(cand.shape[0]), "tets": T,
                   "undecided_cells": int(counts[2]), "overflow_cells": int(counts[3]),
-                  "certify_s": t1 - t0, "open_points_qhull_s": t2 - t1, "merge_s": t3 - t2,
-                  "open_ids": U})
+                  "certify_s": t1 - t0, "open_ids": U})
     return tets[:T], nbr[:T], stats
 
 
@@ -439,9 +568,6 @@ def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
         U = torch.sort(torch.cat([U, direct]))[0]
         nr, nu = int(reports.shape[0]), int(U.numel())
         t2 = time.perf_counter()
-        cand, hull_faces = _open_candidates(L, pts, U, stream, stats)
-        m = int(cand.shape[0])
-        t3 = time.perf_counter()
         # 0 clean, 1 dirty and certified, 2 dirty and open
         state = torch.zeros(n, dtype=torch.int8, device=dev)
         if nd:
@@ -453,15 +579,15 @@ def gpu_tetrahedra_incremental(points: torch.Tensor, tets_old: torch.Tensor,
         verified = tets_old[sel].contiguous()
         t_sel = time.perf_counter()
         # about as many tetrahedra as before (a tet may have one certified
-        # vertex only, so the reports do not bound them as in a full rebuild)
-        tets, nbr, T = _merge(L, pts, gptr, gbytes, reports, cand, verified, hull_faces, stream,
-                              tcap=T_old + T_old // 16 + m + 4096)
-    t4 = time.perf_counter()
-    stats.update({"open": nu, "reports": nr, "candidates": m, "verified": int(verified.shape[0]),
-                  "tets": T, "undecided_cells": int(counts[2]),
-                  "overflow_cells": int(counts[3]), "check_s": t1 - t0, "certify_s": t2 - t1,
-                  "open_points_qhull_s": t3 - t2, "merge_s": t4 - t3,
-                  "select_s": t_sel - t3, "open_ids": U})
+        # vertex only, so the reports do not bound them as in a full rebuild),
+        # plus the open points' candidates
+        tets, nbr, T, cand = _open_and_merge(L, pts, U, gptr, gbytes, reports, verified, stream,
+                                             stats, tcap=T_old + T_old // 16 + 8 * nu + 4096)
+    stats.update({"open": nu, "reports": nr, "candidates": int(cand.shape[0]),
+                  "verified": int(verified.shape[0]), "tets": T,
+                  "undecided_cells": int(counts[2]), "overflow_cells": int(counts[3]),
+                  "check_s": t1 - t0, "certify_s": t2 - t1, "select_s": t_sel - t2,
+                  "open_ids": U})
     return tets[:T], nbr[:T], stats
 
 

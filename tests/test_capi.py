@@ -237,6 +237,13 @@ def test_gpu_delaunay_argument_errors():
     assert rc == 1 and b"NULL pointer" in L.sdf_last_error()
     rc = L.sdf_delaunay_certify(p, 100, p, 10, p, counts, aligned + 8, 1 << 20, None)
     assert rc == 1 and b"256-byte aligned" in L.sdf_last_error()
+    rc = L.sdf_delaunay_certify_exhaustive(p, 31, p, 10, p, counts, aligned, 1 << 20, None)
+    assert rc == 1 and b"less than 32 points" in L.sdf_last_error()
+    rc = L.sdf_delaunay_certify_exhaustive(p, (1 << 20) + 1, p, 10, p, counts, aligned, 1 << 20,
+                                           None)
+    assert rc == 1 and b"at most 2^20 points" in L.sdf_last_error()
+    rc = L.sdf_delaunay_certify_exhaustive(p, 100, p, 10, None, counts, aligned, 1 << 20, None)
+    assert rc == 1 and b"NULL pointer" in L.sdf_last_error()
     result = (C.c_uint64 * 4)()
     rc = L.sdf_delaunay_merge(p, 100, aligned, 1 << 20, None, 5, p, 1, p, p, 10, result,
                               aligned, 1 << 20, None)

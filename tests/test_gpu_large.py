@@ -378,10 +378,10 @@ def test_c4_render_full_camera(dev, oracle_lib, say):
 
 def test_c3_triangulation_matches_qhull(dev, say):
     """Triangulation.rebuild at C3's 1M points: every table the GPU path
-    (certified cells, the open points certified again among themselves, Qhull
-    on those that stay open, merge) produces equals the tables of Qhull's
-    tetrahedralisation of all points, bit for bit; the open points' own
-    certification ran and left fewer points to Qhull."""
+    (certified cells, the open points certified again among themselves,
+    exhaustively, hull cells included, merge) produces equals the tables of
+    Qhull's tetrahedralisation of all points, bit for bit; no point went to
+    Qhull."""
     import torch
 
     import sdfoam_amd
@@ -397,7 +397,8 @@ def test_c3_triangulation_matches_qhull(dev, say):
         f"{tri.last_stats['open']} open points")
     assert tri.last_method == "gpu"
     st = tri.last_stats
-    assert st.get("open_levels") and st["open_points_qhull"] < 0.7 * st["open"], st
+    assert st.get("open_levels") and st["open_points_qhull"] == 0, st
+    assert "open_gpu_retry" not in st, st
     sorted_pts = pts[tri.permutation().to(torch.long)].cpu().numpy()
     t = time.time()
     simplices, neighbors = qhull_tetrahedra(sorted_pts)

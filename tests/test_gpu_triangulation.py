@@ -179,9 +179,10 @@ def _face_neighbors(tets):
 
 @pytest.mark.parametrize("name", list(_gpu_sets()))
 def test_gpu_tetrahedra_match_qhull(dev, name):
-    """sdf_delaunay_certify + Qhull of the open points + sdf_delaunay_merge:
-    the same tetrahedra as Qhull on every point, and (through
-    sdf_delaunay_tables) every derived table bit-exact."""
+    """sdf_delaunay_certify + the open points' exhaustive certification
+    (sdf_delaunay_certify_exhaustive; Qhull of them where it cannot decide) +
+    sdf_delaunay_merge: the same tetrahedra as Qhull on every point, and
+    (through sdf_delaunay_tables) every derived table bit-exact."""
     import torch
 
     from sdfoam_amd.triangulation import device_tables, gpu_tetrahedra, host_tables, qhull_tetrahedra
@@ -228,6 +229,10 @@ def test_gpu_tetrahedra_match_qhull(dev, name):
     if name not in ("shell",):
         # the hull layer is a larger share of a small set
         assert stats["open"] < (0.2 if pts.shape[0] < 10_000 else 0.12) * pts.shape[0], stats
+    print({k: v for k, v in stats.items() if k.startswith("open") and k != "open_ids"}, flush=True)
+    if name != "C1":
+        # the open points' tetrahedra came from the GPU, not Qhull
+        assert stats["open_points_qhull"] == 0 and "open_gpu_retry" not in stats, stats
     mine = device_tables(pd, tets, nbr)
     host = host_tables(pts, simplices, neighbors)
     for k, v in host.items():
@@ -262,6 +267,7 @@ def test_incremental_rebuild_matches_qhull(dev, name, scale):
     print({k: v for k, v in st.items() if not k.endswith("_s")}, flush=True)
     assert tri.last_method == "gpu" and st.get("incremental"), st
     assert st["verified"] > 0 and st["dirty"] < 0.5 * n, st
+    assert st["open_points_qhull"] == 0 and "open_gpu_retry" not in st, st
     host = triangulate_host(moved)
     for k in ("tets", "tet_adjacency", "vert_to_tet", "point_adjacency", "point_adjacency_offsets"):
         assert np.array_equal(_np(getattr(tri, k)()).reshape(host[k].shape), host[k]), k
@@ -396,3 +402,26 @@ def test_gpu_delaunay_far_from_the_origin(dev):
     # volumes relative to the cloud's corner, in double
     local = (pts.astype(np.float64) - 1000.0).astype(np.float64)
     assert_delaunay(local, t, ConvexHull(local).volume)
+
+
+@pytest.mark.parametrize("name", ["gaussian", "shell", "C2"])
+def test_open_points_by_qhull_when_the_gpu_cannot(dev, name, monkeypatch):
+    """The open points' fallback: with the exhaustive certification made to
+    give up, Qhull triangulates them (as when a cell is undecided or a face
+    without a neighbour is off the hull), and the tetrahedra are the same."""
+    import torch
+
+    from sdfoam_amd import triangulation as tr
+
+    pts = np.ascontiguousarray(_gpu_sets()[name](), dtype=np.float32)
+    pd = torch.from_numpy(pts).to(dev)
+    tets_gpu, _, st_gpu = tr.gpu_tetrahedra(pd)
+    monkeypatch.setattr(tr, "_open_candidates_gpu", lambda *a, **k: None)
+    tets_q, _, st_q = tr.gpu_tetrahedra(pd)
+    assert st_gpu["open_points_qhull"] == 0 and st_q["open_points_qhull"] > 0, (st_gpu, st_q)
+
+    def canon(t):
+        t = np.sort(t.cpu().numpy(), axis=1)
+        return t[np.lexsort(t[:, ::-1].T)]
+
+    assert np.array_equal(canon(tets_gpu), canon(tets_q))

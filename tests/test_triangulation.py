@@ -144,3 +144,50 @@ def test_has_coincident_points():
     q[8] = [-0.0, 1.5, -2.0]
     assert has_coincident_points(torch.from_numpy(q))
     assert not has_coincident_points(torch.from_numpy(pts[:1]))
+
+
+def test_hull_check_finds_missing_tetrahedra():
+    """_hull_is_convex, the check the GPU path's merge makes in place of
+    Qhull's hull face count: a Delaunay tetrahedralisation passes; removing
+    any one tetrahedron (interior, or on the hull: its inner faces are then
+    exposed) leaves a face without a neighbour off the hull, which fails;
+    and a face on the hull with an open point beyond it (a planted
+    inconsistency) fails too."""
+    import torch
+    from scipy.spatial import Delaunay
+
+    from sdfoam_amd.triangulation import _hull_is_convex
+
+    rng = np.random.default_rng(21)
+    pts_np = rng.normal(size=(400, 3)).astype(np.float32)
+    d = Delaunay(pts_np.astype(np.float64))
+    pts = torch.from_numpy(pts_np)
+    tets = torch.from_numpy(d.simplices.astype(np.int32))
+    nbr = torch.from_numpy(d.neighbors.astype(np.int32))
+    T = tets.shape[0]
+    U = torch.arange(pts_np.shape[0], dtype=torch.int32)
+    assert _hull_is_convex(pts, tets, nbr, T, U)
+
+    def without(t):
+        keep = torch.ones(T, dtype=torch.bool)
+        keep[t] = False
+        remap = torch.cumsum(keep.int(), 0) - 1
+        nb = nbr.clone()
+        nb[nb == t] = -1
+        nb = torch.where(nb >= 0, remap[nb.clamp(min=0).long()].int(), nb)
+        return tets[keep].contiguous(), nb[keep].contiguous()
+
+    hull_tet = int(np.nonzero((d.neighbors < 0).any(1))[0][0])
+    inner_tet = int(np.nonzero((d.neighbors >= 0).all(1))[0][0])
+    for t in (hull_tet, inner_tet):
+        tt, nn = without(t)
+        assert not _hull_is_convex(pts, tt, nn, T - 1, U), t
+    # a point moved beyond a hull face: the face stays neighbourless but is
+    # no longer a hull facet
+    f_t, f_j = np.argwhere(d.neighbors < 0)[0]
+    face = [d.simplices[f_t][k] for k in range(4) if k != f_j]
+    far = d.simplices[f_t][f_j]
+    c = pts_np[face].mean(0)
+    out = pts_np.copy()
+    out[far] = c + 3.0 * (c - pts_np[far])
+    assert not _hull_is_convex(torch.from_numpy(out), tets, nbr, T, U)
