@@ -46,6 +46,7 @@ struct GridScratch {
     uint64_t *keys, *keys_sorted;
     dgrid::CellEntry *table[dgrid::kLevels];
     uint32_t *sorted[dgrid::kLevels];
+    float *spts; // coordinates in the sorted order, 4 floats a point
     void *temp;
     size_t temp_bytes;
     size_t total;
@@ -69,6 +70,7 @@ GridScratch carve_grid(void *base, uint32_t n, size_t temp_bytes) {
     // one order serves every level
     uint32_t *sorted = reinterpret_cast<uint32_t *>(take(4ull * n));
     for (int l = 0; l < dgrid::kLevels; ++l) s.sorted[l] = sorted;
+    s.spts = reinterpret_cast<float *>(take(16ull * n));
     s.keys = reinterpret_cast<uint64_t *>(take(8ull * n));
     s.keys_sorted = reinterpret_cast<uint64_t *>(take(8ull * n));
     s.index = reinterpret_cast<uint32_t *>(take(4ull * n));
@@ -167,6 +169,16 @@ __global__ __launch_bounds__(256) void morton_keys_kernel(const float *__restric
         (uint32_t)dgrid::axis_cell((double)p[3ull * i + 1], g.lo[1], lv.inv_h, lv.dims[1]),
         (uint32_t)dgrid::axis_cell((double)p[3ull * i + 2], g.lo[2], lv.inv_h, lv.dims[2]));
     index[i] = i;
+}
+
+// The points' coordinates in the sorted order (x, y, z, 0).
+__global__ __launch_bounds__(256) void gather_points_kernel(const float *__restrict__ p,
+                                                            const uint32_t *__restrict__ order,
+                                                            uint32_t n, float4 *__restrict__ out) {
+    const uint32_t k = blockIdx.x * 256u + threadIdx.x;
+    if (k >= n) return;
+    const uint32_t j = order[k];
+    out[k] = make_float4(p[3ull * j], p[3ull * j + 1], p[3ull * j + 2], 0.0f);
 }
 
 // Level-l cell keys of the points in Morton order.
@@ -707,8 +719,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                     if (f < total) {
                         j = sorted[ob + (f - oex)];
                         if (j != i) {
-                            const double x[3] = {(double)p[3ull * j], (double)p[3ull * j + 1],
-                                                 (double)p[3ull * j + 2]};
+                            const float4 sp =
+                                reinterpret_cast<const float4 *>(gv.spts)[ob + (f - oex)];
+                            const double x[3] = {(double)sp.x, (double)sp.y, (double)sp.z};
                             q[0] = x[0] - o[0];
                             q[1] = x[1] - o[1];
                             q[2] = x[2] - o[2];
@@ -797,14 +810,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
     bool hull_cell = false;
     if (EXHAUSTIVE && st == vcell::kOpen && !coincident) {
         bool failed = false;
+        const uint32_t *order = gv.sorted[0];
         for (uint32_t base = 0; base < n && !failed; base += 64u) {
-            const uint32_t j = base + l;
+            // the points in the grid's (Morton) order
+            const uint32_t k = base + l;
+            const uint32_t j = k < n ? order[k] : i;
             bool surv = false, dup = false;
             double q[3] = {0.0, 0.0, 0.0}, d2 = INFINITY;
-            if (j < n && j != i) {
-                q[0] = (double)p[3ull * j] - o[0];
-                q[1] = (double)p[3ull * j + 1] - o[1];
-                q[2] = (double)p[3ull * j + 2] - o[2];
+            if (j != i) {
+                const float4 sp = reinterpret_cast<const float4 *>(gv.spts)[k];
+                q[0] = (double)sp.x - o[0];
+                q[1] = (double)sp.y - o[1];
+                q[2] = (double)sp.z - o[2];
                 d2 = q[0] * q[0] + q[1] * q[1] + q[2] * q[2];
                 if (d2 == 0.0) {
                     dup = true;
@@ -987,7 +1004,7 @@ __global__ __launch_bounds__(64) void keep_empty_kernel(const float *__restrict_
 // with a vertex out of range.
 constexpr uint32_t kCheckLanes = 4;
 
-__global__ __launch_bounds__(256) void check_kernel(const float *__restrict__ p, uint32_t n,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void check_kernel(const float *__restrict__ p, uint32_t n,
                                                     GridView gv,
                                                     const uint32_t *__restrict__ status,
                                                     const uint32_t *__restrict__ tets,
@@ -1234,6 +1251,8 @@ hipError_t build_grid(const float *points, uint32_t n, const GridScratch &s, Gri
     e = rocprim::radix_sort_pairs(s.temp, tb, s.keys, s.keys_sorted, s.index, s.sorted[0],
                                   (size_t)n, 0u, 63u, stream);
     if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(gather_points_kernel, grid1(n), dim3(256), 0, stream, points, s.sorted[0],
+                       n, reinterpret_cast<float4 *>(s.spts));
     const uint64_t slots = g.table_mask + 1;
     for (int l = 0; l < dgrid::kLevels; ++l) {
         hipLaunchKernelGGL(level_keys_kernel, grid1(n), dim3(256), 0, stream, s.keys_sorted, n, l,
@@ -1259,6 +1278,7 @@ GridView grid_view(const GridScratch &s, const GridGeom &g) {
         gv.table[l] = s.table[l];
         gv.sorted[l] = s.sorted[l];
     }
+    gv.spts = s.spts;
     return gv;
 }
 
@@ -1404,6 +1424,7 @@ hipError_t launch_delaunay_merge(const float *points, uint32_t n, void *grid_scr
         gv.table[l] = gs.table[l];
         gv.sorted[l] = gs.sorted[l];
     }
+    gv.spts = gs.spts;
     hipLaunchKernelGGL(init_kernel, dim3(1), dim3(64), 0, stream, nullptr, s.acc);
     if (m > 0)
         hipLaunchKernelGGL(keep_empty_kernel, dim3((unsigned)m), dim3(64), 0, stream, points, n,

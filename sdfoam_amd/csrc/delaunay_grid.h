@@ -66,6 +66,9 @@ struct GridView {
     GridGeom g;
     const CellEntry *table[kLevels];
     const uint32_t *sorted[kLevels]; // point ids by cell (one array: the Morton order)
+    // the points' coordinates in that order (x, y, z, 0 per point): a run of
+    // a cell's candidates is a run of memory, not one cache line per point
+    const float *spts;
 };
 
 // Hash table slots: a power of two of at least twice the points, so that
@@ -307,8 +310,8 @@ SDF_HD uint32_t certify_cell(const float *p, uint32_t i, const GridView &gv, vce
                         for (uint32_t k = begin; k < end; ++k) {
                             const uint32_t j = sorted[k];
                             if (j == i) continue;
-                            const double x[3] = {(double)p[3ull * j], (double)p[3ull * j + 1],
-                                                 (double)p[3ull * j + 2]};
+                            const float *sp = gv.spts + 4ull * k;
+                            const double x[3] = {(double)sp[0], (double)sp[1], (double)sp[2]};
                             const double q[3] = {x[0] - o[0], x[1] - o[1], x[2] - o[2]};
                             const double d2 = q[0] * q[0] + q[1] * q[1] + q[2] * q[2];
                             if (d2 == 0.0) {
@@ -451,8 +454,9 @@ SDF_HD uint32_t sphere_scan_column(const float *p, const uint32_t *v, const Grid
         for (uint32_t k = begin; k < end; ++k) {
             const uint32_t j = sorted[k];
             if (j == v[0] || j == v[1] || j == v[2] || j == v[3]) continue;
+            const float *sp = gv.spts + 4ull * k;
             double q[3];
-            for (int m = 0; m < 3; ++m) q[m] = (double)p[3ull * j + m] - S.o[m];
+            for (int m = 0; m < 3; ++m) q[m] = (double)sp[m] - S.o[m];
             const double e0 = q[0] - S.ctr[0], e1 = q[1] - S.ctr[1], e2 = q[2] - S.ctr[2];
             if (e0 * e0 + e1 * e1 + e2 * e2 > S.r * S.r) continue; // clearly outside
             const int s = vcell::in_sphere(S.pl[0].n, S.pl[1].n, S.pl[2].n, q);

@@ -17,6 +17,7 @@ namespace {
 dgrid::GridGeom g_geom;
 std::vector<dgrid::CellEntry> g_table[dgrid::kLevels];
 std::vector<uint32_t> g_sorted[dgrid::kLevels];
+std::vector<float> g_spts; // coordinates in the sorted order, 4 floats a point
 
 dgrid::GridView view() {
     dgrid::GridView v{};
@@ -25,6 +26,7 @@ dgrid::GridView view() {
         v.table[l] = g_table[l].data();
         v.sorted[l] = g_sorted[l].data();
     }
+    v.spts = g_spts.data();
     return v;
 }
 } // namespace
@@ -112,6 +114,9 @@ int vc_grid(const float *points, uint32_t n, uint32_t *dims) {
                     i};
     std::stable_sort(keyed.begin(), keyed.end(),
                      [](const auto &a, const auto &b) { return a.first < b.first; });
+    g_spts.assign(4ull * n, 0.0f);
+    for (uint32_t t = 0; t < n; ++t)
+        for (int k = 0; k < 3; ++k) g_spts[4ull * t + k] = points[3ull * keyed[t].second + k];
     int occupied0 = 0;
     std::vector<uint64_t> key(n);
     for (int l = 0; l < dgrid::kLevels; ++l) {
