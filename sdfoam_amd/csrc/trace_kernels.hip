@@ -1514,31 +1514,38 @@ __global__ __launch_bounds__(kBlock) void grad_clear_kernel(float4 *__restrict__
         rows[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
-// One thread per row element; an element that is exactly zero (a cell no
-// ray reached) leaves its output untouched.  fp16 outputs (attribute
-// gradients, point error) get the fp32 sum added and rounded once.
+// One thread per 16 bytes of a row (the row's padding past D + 4 floats
+// skipped); an element that is exactly zero (a cell no ray reached) leaves
+// its output untouched.  fp16 outputs (attribute gradients, point error) get
+// the fp32 sum added and rounded once.
 template <int L, typename AT>
 __global__ __launch_bounds__(kBlock) void grad_finalize_kernel(
-    const float *__restrict__ rows, uint32_t num_points, AT *__restrict__ attr_grad,
+    const float4 *__restrict__ rows, uint32_t num_points, AT *__restrict__ attr_grad,
     float *__restrict__ points_grad, AT *__restrict__ point_error) {
-    constexpr uint32_t S = accum_stride(L);
+    constexpr uint32_t S4 = accum_stride(L) / 4;
     constexpr uint32_t D = 1 + 3 * (L + 1) * (L + 1);
-    const uint64_t total = (uint64_t)num_points * S;
+    constexpr uint32_t Q = (D + 4 + 3) / 4; // quads of a row that hold data
+    const uint64_t total = (uint64_t)num_points * S4;
     const uint64_t step = (uint64_t)gridDim.x * kBlock;
     for (uint64_t t = (uint64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += step) {
-        const uint32_t j = (uint32_t)(t % S);
-        if (j >= D + 4) continue;
-        const float v = rows[t];
-        if (v == 0.0f) continue;
-        const uint64_t c = t / S;
-        if (j < D) {
-            AT &o = attr_grad[c * D + j];
-            o = (AT)((float)o + v);
-        } else if (j < D + 3) {
-            points_grad[c * 3 + (j - D)] += v;
-        } else if (point_error) {
-            AT &o = point_error[c];
-            o = (AT)((float)o + v);
+        const uint32_t q = (uint32_t)(t % S4);
+        if (q >= Q) continue;
+        const float4 v4 = rows[t];
+        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        const uint64_t c = t / S4;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) {
+            const uint32_t j = 4u * q + k;
+            if (v[k] == 0.0f) continue;
+            if (j < D) {
+                AT &o = attr_grad[c * D + j];
+                o = (AT)((float)o + v[k]);
+            } else if (j < D + 3) {
+                points_grad[c * 3 + (j - D)] += v[k];
+            } else if (j == D + 3 && point_error) {
+                AT &o = point_error[c];
+                o = (AT)((float)o + v[k]);
+            }
         }
     }
 }
@@ -1560,24 +1567,25 @@ template <typename AT>
 static hipError_t launch_grad_finalize_T(int L, const float *accum, uint32_t num_points,
                                         void *attr_grad, float *points_grad, void *point_error,
                                         hipStream_t stream) {
-    const dim3 grid = accum_grid((uint64_t)num_points * accum_stride(L));
+    const dim3 grid = accum_grid((uint64_t)num_points * accum_stride(L) / 4);
+    const float4 *rows = reinterpret_cast<const float4 *>(accum);
     AT *ag = static_cast<AT *>(attr_grad);
     AT *pe = static_cast<AT *>(point_error);
     switch (L) {
     case 0:
-        hipLaunchKernelGGL((grad_finalize_kernel<0, AT>), grid, dim3(kBlock), 0, stream, accum,
+        hipLaunchKernelGGL((grad_finalize_kernel<0, AT>), grid, dim3(kBlock), 0, stream, rows,
                            num_points, ag, points_grad, pe);
         break;
     case 1:
-        hipLaunchKernelGGL((grad_finalize_kernel<1, AT>), grid, dim3(kBlock), 0, stream, accum,
+        hipLaunchKernelGGL((grad_finalize_kernel<1, AT>), grid, dim3(kBlock), 0, stream, rows,
                            num_points, ag, points_grad, pe);
         break;
     case 2:
-        hipLaunchKernelGGL((grad_finalize_kernel<2, AT>), grid, dim3(kBlock), 0, stream, accum,
+        hipLaunchKernelGGL((grad_finalize_kernel<2, AT>), grid, dim3(kBlock), 0, stream, rows,
                            num_points, ag, points_grad, pe);
         break;
     case 3:
-        hipLaunchKernelGGL((grad_finalize_kernel<3, AT>), grid, dim3(kBlock), 0, stream, accum,
+        hipLaunchKernelGGL((grad_finalize_kernel<3, AT>), grid, dim3(kBlock), 0, stream, rows,
                            num_points, ag, points_grad, pe);
         break;
     default:
