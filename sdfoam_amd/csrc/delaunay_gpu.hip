@@ -294,29 +294,65 @@ __device__ __forceinline__ uint32_t wbelow(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
+// Cross-lane moves without an LDS round trip.  A DPP move (`CTRL`:
+// row_shr:k = 0x110 + k, row_bcast:15 = 0x142, row_bcast:31 = 0x143) reads a
+// neighbouring lane's register in the same VALU instruction; lanes whose
+// source lies outside their row of 16, or whose row `ROWS` leaves out, get
+// `old`.  A read of one lane (`readlane`) gives a uniform value.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t old, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWS, 0xf, false);
+}
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)b, hi = (uint32_t)(b >> 32);
+    return __builtin_bit_cast(double, (uint64_t)dpp_u<CTRL, ROWS>(hi, hi) << 32 |
+                                          dpp_u<CTRL, ROWS>(lo, lo));
+}
+__device__ __forceinline__ uint32_t readlane_u(uint32_t v, int lane) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
+    return (uint64_t)readlane_u((uint32_t)(v >> 32), lane) << 32 | readlane_u((uint32_t)v, lane);
+}
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    return __builtin_bit_cast(double, (uint64_t)readlane_u((uint32_t)(b >> 32), lane) << 32 |
+                                          readlane_u((uint32_t)b, lane));
+}
+// Maximum / minimum over the wave (every lane active): lane 15 of each row
+// gathers its row by shifts of 1, 2, 4 and 8 (a lane without a source keeps
+// its own value, which max and min ignore), rows 1 and 3 take rows 0 and 2,
+// rows 2 and 3 take lane 31, and lane 63 holds the result.
 __device__ __forceinline__ double wmaxd(double v) {
-    for (int off = 32; off > 0; off >>= 1) v = fmax(v, __shfl_xor(v, off, 64));
-    return v;
+    v = fmax(v, dpp_d<0x111>(v));
+    v = fmax(v, dpp_d<0x112>(v));
+    v = fmax(v, dpp_d<0x114>(v));
+    v = fmax(v, dpp_d<0x118>(v));
+    v = fmax(v, dpp_d<0x142, 0xa>(v));
+    v = fmax(v, dpp_d<0x143, 0xc>(v));
+    return readlane_d(v, 63);
 }
 __device__ __forceinline__ double wmind(double v) {
-    for (int off = 32; off > 0; off >>= 1) v = fmin(v, __shfl_xor(v, off, 64));
-    return v;
+    v = fmin(v, dpp_d<0x111>(v));
+    v = fmin(v, dpp_d<0x112>(v));
+    v = fmin(v, dpp_d<0x114>(v));
+    v = fmin(v, dpp_d<0x118>(v));
+    v = fmin(v, dpp_d<0x142, 0xa>(v));
+    v = fmin(v, dpp_d<0x143, 0xc>(v));
+    return readlane_d(v, 63);
 }
-__device__ __forceinline__ uint32_t wsumu(uint32_t v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-__device__ __forceinline__ uint32_t wmaxu(uint32_t v) {
-    for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
-    return v;
-}
-// inclusive prefix sum over the lanes
+// inclusive prefix sum over the lanes (every lane active): within rows by
+// shifts of 1, 2, 4 and 8 (no source: 0), then rows 1 and 3 add the row
+// before, rows 2 and 3 add lane 31
 __device__ __forceinline__ uint32_t wscanu(uint32_t v) {
-    const uint32_t l = wlane();
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t y = (uint32_t)__shfl_up((int)v, off, 64);
-        if (l >= (uint32_t)off) v += y;
-    }
+    v += dpp_u<0x111>(0u, v);
+    v += dpp_u<0x112>(0u, v);
+    v += dpp_u<0x114>(0u, v);
+    v += dpp_u<0x118>(0u, v);
+    v += dpp_u<0x142, 0xa>(0u, v);
+    v += dpp_u<0x143, 0xc>(0u, v);
     return v;
 }
 
@@ -492,12 +528,8 @@ __device__ int wave_clip(WaveCell &c, WaveShared &sh, const double *q, double qc
                     ++nf;
                 }
             }
-    uint32_t incl = nf;
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t y = (uint32_t)__shfl_up((int)incl, off, 64);
-        if (l >= (uint32_t)off) incl += y;
-    }
-    const uint32_t total = (uint32_t)__shfl((int)incl, 63, 64);
+    const uint32_t incl = wscanu(nf);
+    const uint32_t total = readlane_u(incl, 63);
     const uint32_t base = incl - nf;
     const uint32_t kept = __popcll(a0 & ~o0) + __popcll(a1 & ~o1);
     if (total > (uint32_t)kWaveNew || kept + total > (uint32_t)kWaveVerts) return 3;
@@ -564,7 +596,6 @@ __device__ int wave_clip(WaveCell &c, WaveShared &sh, const double *q, double qc
         c.vr2[s] = v.r2;
     }
     __syncthreads();
-    wave_bounds(c, sh);
     return 1;
 }
 
@@ -606,6 +637,32 @@ __device__ uint64_t wave_may_cut(const WaveCell &c, WaveShared &sh, bool mine, c
     __syncthreads(); // the copy is read before wave_clip stages vertices there
     return m;
 }
+
+// The cells of the rings r = 0 .. kMaxRing around a grid cell, ring by ring
+// (ring r: the (2r+1)^3 - (2r-1)^3 cells at Chebyshev distance r, entries
+// (2r-1)^3 .. (2r+1)^3 - 1), each ring in z, y, x order; an entry packs
+// (dx + 8) | (dy + 8) << 4 | (dz + 8) << 8.  A pass over a ring's cells then
+// takes only its shell, not the whole cube around it (r = 3: 4 passes of 64
+// lanes instead of 6), and no lane divides by the ring's side.
+struct RingCells {
+    static constexpr int kSide = 2 * dgrid::kMaxRing + 1;
+    uint16_t v[kSide * kSide * kSide];
+    constexpr RingCells() : v() {
+        int k = 0;
+        for (int r = 0; r <= dgrid::kMaxRing; ++r)
+            for (int dz = -r; dz <= r; ++dz)
+                for (int dy = -r; dy <= r; ++dy)
+                    for (int dx = -r; dx <= r; ++dx) {
+                        const int ax = dx < 0 ? -dx : dx, ay = dy < 0 ? -dy : dy,
+                                  az = dz < 0 ? -dz : dz;
+                        const int m = ax > ay ? (ax > az ? ax : az) : (ay > az ? ay : az);
+                        if (m == r)
+                            v[k++] = (uint16_t)((dx + 8) | (dy + 8) << 4 | (dz + 8) << 8);
+                    }
+    }
+};
+static_assert(dgrid::kMaxRing < 8, "ring offsets fit 4 bits");
+__constant__ RingCells kRingCells = RingCells();
 
 // The clipping box of an exhaustive certification: the bounding box grown by
 // this many times its extent, so that the hull cells' Voronoi vertices
@@ -669,27 +726,34 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
     __syncthreads();
     uint32_t st = vcell::kOpen, examined = 0;
     bool decided = false, coincident = false;
-    const int l0 = dgrid::first_level(gv, o);
+    // dgrid::first_level with every level's lookup in flight at once: lane
+    // l < kLevels - 1 looks up the point's cell of level l
+    int l0 = dgrid::kLevels - 1;
+    {
+        uint32_t b = 0, e = 0;
+        if (l < (uint32_t)dgrid::kLevels - 1u)
+            dgrid::cell_range(gv, (int)l, (uint32_t)hc[l][0], (uint32_t)hc[l][1],
+                              (uint32_t)hc[l][2], b, e);
+        const uint64_t two = wballot(e - b >= 2u);
+        if (two) l0 = __builtin_ctzll(two);
+    }
     for (int lev = l0; lev < dgrid::kLevels && !decided; ++lev) {
         const dgrid::GridLevel &lv = g.level[lev];
         const uint32_t *sorted = gv.sorted[lev];
         const int *h = hc[lev];
         for (int r = 0; r <= dgrid::kMaxRing && !decided; ++r) {
-            const int side = 2 * r + 1;
-            const uint32_t cube = (uint32_t)(side * side * side);
-            for (uint32_t base = 0; base < cube && !decided; base += 64) {
+            const uint32_t first = r == 0 ? 0u : (uint32_t)((2 * r - 1) * (2 * r - 1) * (2 * r - 1));
+            const uint32_t cells = (uint32_t)((2 * r + 1) * (2 * r + 1) * (2 * r + 1)) - first;
+            for (uint32_t base = 0; base < cells && !decided; base += 64) {
                 // one grid cell of the ring's shell per lane
                 const uint32_t t = base + l;
                 uint32_t b = 0, e = 0;
-                if (t < cube) {
-                    const int dx = (int)(t % (uint32_t)side) - r;
-                    const int dy = (int)((t / (uint32_t)side) % (uint32_t)side) - r;
-                    const int dz = (int)(t / (uint32_t)(side * side)) - r;
-                    const int cx = h[0] + dx, cy = h[1] + dy, cz = h[2] + dz;
-                    const bool shell = dx == -r || dx == r || dy == -r || dy == r || dz == -r ||
-                                       dz == r;
-                    if (shell && cx >= 0 && cx < (int)lv.dims[0] && cy >= 0 &&
-                        cy < (int)lv.dims[1] && cz >= 0 && cz < (int)lv.dims[2])
+                if (t < cells) {
+                    const uint32_t d = kRingCells.v[first + t];
+                    const int cx = h[0] + (int)(d & 15u) - 8, cy = h[1] + (int)(d >> 4 & 15u) - 8,
+                              cz = h[2] + (int)(d >> 8) - 8;
+                    if (cx >= 0 && cx < (int)lv.dims[0] && cy >= 0 && cy < (int)lv.dims[1] &&
+                        cz >= 0 && cz < (int)lv.dims[2])
                         dgrid::cell_range(gv, lev, (uint32_t)cx, (uint32_t)cy, (uint32_t)cz, b,
                                           e);
                 }
@@ -698,7 +762,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                 // cell: the first lane whose inclusive prefix exceeds it)
                 const uint32_t cnt = e - b;
                 const uint32_t incl = wscanu(cnt);
-                const uint32_t total = (uint32_t)__shfl((int)incl, 63, 64);
+                const uint32_t total = readlane_u(incl, 63);
                 examined += total;
                 if (examined > dgrid::kMaxCandidates) {
                     decided = true;
@@ -748,6 +812,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                     }
                     uint64_t m = wballot(surv);
                     if (__popcll(m) >= kBatchTestMin) m = wave_may_cut(c, sh, surv, q, 0.5 * d2);
+                    bool clipped = false;
                     while (m) {
                         // nearest first
                         const bool mine = (m >> l) & 1ull;
@@ -755,10 +820,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                         const uint64_t hit = wballot(mine && d2 == dm);
                         const int src = __builtin_ctzll(hit);
                         m &= ~(1ull << src);
-                        const double qq[3] = {__shfl(q[0], src, 64), __shfl(q[1], src, 64),
-                                              __shfl(q[2], src, 64)};
-                        const double dd = __shfl(d2, src, 64);
-                        const int32_t jj = __shfl((int)j, src, 64);
+                        const double qq[3] = {readlane_d(q[0], src), readlane_d(q[1], src),
+                                              readlane_d(q[2], src)};
+                        const double dd = readlane_d(d2, src);
+                        const int32_t jj = (int32_t)readlane_u(j, src);
                         // the cell may have shrunk since the filter
                         if (dd > 4.0 * sh.mr2 * (1.0 + 1e-9)) continue;
                         double reach_q = 0.0, mag = dd;
@@ -774,7 +839,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                             decided = true;
                             break;
                         }
+                        clipped = clipped || rc == 1;
                     }
+                    // the batch's clips leave the bounds of the cell before them, which
+                    // still hold it (a clip only shrinks a cell); tightened once per batch
+                    if (clipped && !decided) wave_bounds(c, sh);
                 }
             }
             if (decided) break;
@@ -843,16 +912,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
             }
             uint64_t m = wballot(surv);
             if (__popcll(m) >= kBatchTestMin) m = wave_may_cut(c, sh, surv, q, 0.5 * d2);
+            bool clipped = false;
             while (m) {
                 const bool mine = (m >> l) & 1ull;
                 const double dm = wmind(mine ? d2 : INFINITY);
                 const uint64_t hit = wballot(mine && d2 == dm);
                 const int src = __builtin_ctzll(hit);
                 m &= ~(1ull << src);
-                const double qq[3] = {__shfl(q[0], src, 64), __shfl(q[1], src, 64),
-                                      __shfl(q[2], src, 64)};
-                const double dd = __shfl(d2, src, 64);
-                const int32_t jj = __shfl((int)j, src, 64);
+                const double qq[3] = {readlane_d(q[0], src), readlane_d(q[1], src),
+                                      readlane_d(q[2], src)};
+                const double dd = readlane_d(d2, src);
+                const int32_t jj = (int32_t)readlane_u(j, src);
                 // a point the grid search clipped by already: its plane holds
                 // vertices of the cell, which the exact test cannot place
                 if (wballot((int)l < c.np && sh.pp[l] == jj)) continue;
@@ -862,7 +932,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                     failed = true;
                     break;
                 }
+                clipped = clipped || rc == 1;
             }
+            // the batch's clips leave the bounds of the cell before them, which
+            // still hold it (a clip only shrinks a cell); tightened once per batch
+            if (clipped && !failed) wave_bounds(c, sh);
         }
         if (!failed) {
             hull_cell = wave_touches_box(c, sh);
@@ -883,7 +957,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
         const unsigned long long nv = (unsigned long long)(__popcll(a0) + __popcll(a1));
         unsigned long long at = 0;
         if (l == 0) at = atomicAdd(counters, nv);
-        at = __shfl(at, 0, 64);
+        at = readlane_u64(at, 0);
         if (at + nv <= report_capacity)
             for (int s = 0; s < 2; ++s) {
                 if (!fin[s]) continue;
@@ -903,7 +977,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
         const unsigned long long nv = (unsigned long long)(__popcll(a0) + __popcll(a1));
         unsigned long long at = 0;
         if (l == 0) at = atomicAdd(counters, nv);
-        at = __shfl(at, 0, 64);
+        at = readlane_u64(at, 0);
         if (at + nv <= report_capacity)
             for (int s = 0; s < 2; ++s) {
                 if (c.vp[s] == kFree) continue;

@@ -195,6 +195,40 @@ SDF_HD void cell_range(const GridView &gv, int l, uint32_t cx, uint32_t cy, uint
     }
 }
 
+// Probe of one table slot for `key`: true once the search ends there (the
+// key found: its run in b, e; or an empty slot: the cell holds no point).
+SDF_HD bool slot_ends(const CellEntry &en, uint64_t key, uint32_t &b, uint32_t &e) {
+    if (en.key == key) {
+        b = en.start;
+        e = en.end;
+        return true;
+    }
+    return en.key == kEmptyKey;
+}
+
+// cell_range probing a 64-byte group of four slots at a time: the group's
+// loads go out together, so a probe sequence within it (nearly all of them)
+// waits for one memory access.  For the circumsphere scans, which wait on
+// their lookups (check_kernel 20.9 -> 19.7 ms at C3); the certification,
+// which keeps more registers live, runs ~1% slower with it.
+SDF_HD void cell_range_grouped(const GridView &gv, int l, uint32_t cx, uint32_t cy,
+                               uint32_t cz, uint32_t &b, uint32_t &e) {
+    const uint64_t key = cell_key(cx, cy, cz);
+    const uint64_t mask = gv.g.table_mask;
+    const CellEntry *t = gv.table[l];
+    b = e = 0;
+    for (uint64_t s = key_hash(key) & mask;;) {
+        const uint64_t g0 = s & ~3ull; // the table has a power of two >= 4 slots
+        const uint32_t k0 = (uint32_t)(s - g0);
+        const CellEntry c0 = t[g0], c1 = t[g0 + 1], c2 = t[g0 + 2], c3 = t[g0 + 3];
+        if (k0 == 0u && slot_ends(c0, key, b, e)) return;
+        if (k0 <= 1u && slot_ends(c1, key, b, e)) return;
+        if (k0 <= 2u && slot_ends(c2, key, b, e)) return;
+        if (slot_ends(c3, key, b, e)) return;
+        s = (g0 + 4) & mask;
+    }
+}
+
 // The first level of point x: the finest whose grid cell around x holds
 // another point (the coarsest if none does).
 SDF_HD int first_level(const GridView &gv, const double *x) {
@@ -450,7 +484,7 @@ SDF_HD uint32_t sphere_scan_column(const float *p, const uint32_t *v, const Grid
     uint32_t res = 1u;
     for (int cx = x0 > S.lo_c[0] ? x0 : S.lo_c[0]; cx <= (x1 < S.hi_c[0] ? x1 : S.hi_c[0]); ++cx) {
         uint32_t begin, end;
-        cell_range(gv, S.l, (uint32_t)cx, (uint32_t)cy, (uint32_t)cz, begin, end);
+        cell_range_grouped(gv, S.l, (uint32_t)cx, (uint32_t)cy, (uint32_t)cz, begin, end);
         for (uint32_t k = begin; k < end; ++k) {
             const uint32_t j = sorted[k];
             if (j == v[0] || j == v[1] || j == v[2] || j == v[3]) continue;

@@ -207,7 +207,9 @@ def test_one_morton_order_serves_every_level(vc, kind):
     """The grids sort the points once, by the Morton code of their finest
     cell: every level's cell (from a position, as a lookup computes it) is the
     finest cell shifted right by the level, and every level's cells are
-    contiguous runs of that one order.  Includes points on the bounding
+    contiguous runs of that one order.  Both table lookups (one slot at a
+    time, and 64-byte groups of four) find each point's cell, holding it,
+    and agree on the cells beside it.  Includes points on the bounding
     box's far faces (clamped to the last cell) and a flat set (one cell
     across an axis)."""
     rng = np.random.default_rng(11)

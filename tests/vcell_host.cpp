@@ -177,6 +177,27 @@ long long vc_grid_mismatches(const float *points, uint32_t n) {
         std::sort(seen.begin(), seen.end());
         bad += (long long)(seen.size() - (size_t)(std::unique(seen.begin(), seen.end()) - seen.begin()));
     }
+    // the two table lookups agree, on every point's cell (found) and on the
+    // cells beside it (often empty)
+    const dgrid::GridView gv = view();
+    for (int l = 0; l < dgrid::kLevels; ++l) {
+        const dgrid::GridLevel &lv = g_geom.level[l];
+        for (uint32_t i = 0; i < n; ++i) {
+            int c[3];
+            for (int k = 0; k < 3; ++k)
+                c[k] = dgrid::axis_cell(points[3 * i + k], g_geom.lo[k], lv.inv_h, lv.dims[k]);
+            for (int d = 0; d < 3; ++d) {
+                const int cx = c[0] + d;
+                if (cx >= (int)lv.dims[0]) continue;
+                uint32_t b0, e0, b1, e1;
+                dgrid::cell_range(gv, l, (uint32_t)cx, (uint32_t)c[1], (uint32_t)c[2], b0, e0);
+                dgrid::cell_range_grouped(gv, l, (uint32_t)cx, (uint32_t)c[1], (uint32_t)c[2], b1,
+                                          e1);
+                bad += (b0 != b1 || e0 != e1) ? 1 : 0;
+                if (d == 0) bad += e0 > b0 ? 0 : 1; // the point's own cell holds it
+            }
+        }
+    }
     return bad;
 }
 
