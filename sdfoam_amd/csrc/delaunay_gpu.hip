@@ -274,6 +274,7 @@ struct WaveShared {
     uint32_t edges[kWavePlanes * kWavePlanes / 32];
     uint32_t used[2];
     uint8_t remap[kWavePlanes];
+    uint16_t fresh[kWaveNew];   // wave_clip's boundary edges, ea | eb << 6
     union {
         StagedVert stg[kWaveNew];     // wave_clip's new vertices
         TestVert tv[kWaveVerts];      // wave_may_cut's copy of the vertices
@@ -540,9 +541,15 @@ __device__ int wave_clip(WaveCell &c, WaveShared &sh, const double *q, double qc
     P.n[2] = q[2];
     P.c = qc;
     P.point = point;
+    // the boundary edges go to one lane each (lane t makes new vertex t), so
+    // the vertices are made side by side rather than up to six after another
+    // on the lanes that found them
+    for (uint32_t t = 0; t < nf; ++t)
+        sh.fresh[base + t] = (uint16_t)(t < 5 ? (uint32_t)(fresh >> (12u * t)) & 0xfffu : fresh5);
+    __syncthreads();
     bool bad = false;
-    for (uint32_t t = 0; t < nf; ++t) {
-        const uint32_t f = t < 5 ? (uint32_t)(fresh >> (12u * t)) & 0xfffu : fresh5;
+    if (l < total) {
+        const uint32_t f = sh.fresh[l];
         const uint32_t ea = f & 63u, eb = f >> 6;
         vcell::Plane A, B;
         for (int k = 0; k < 3; ++k) {
@@ -553,18 +560,18 @@ __device__ int wave_clip(WaveCell &c, WaveShared &sh, const double *q, double qc
         B.c = sh.pc[eb];
         A.point = sh.pp[ea];
         B.point = sh.pp[eb];
-        StagedVert &v = sh.stg[base + t];
+        StagedVert &v = sh.stg[l];
         double x[3], e = 0.0;
         if (!vcell::meet(A, B, P, x, &e)) {
             bad = true;
-            continue;
+        } else {
+            v.planes = ea | eb << 8 | np << 16;
+            v.x[0] = x[0];
+            v.x[1] = x[1];
+            v.x[2] = x[2];
+            v.e = e;
+            v.r2 = x[0] * x[0] + x[1] * x[1] + x[2] * x[2];
         }
-        v.planes = ea | eb << 8 | np << 16;
-        v.x[0] = x[0];
-        v.x[1] = x[1];
-        v.x[2] = x[2];
-        v.e = e;
-        v.r2 = x[0] * x[0] + x[1] * x[1] + x[2] * x[2];
     }
     if (wballot(bad)) {
         __syncthreads();

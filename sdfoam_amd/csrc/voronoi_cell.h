@@ -110,7 +110,9 @@ SDF_HD int in_sphere(const double *a, const double *b, const double *c, const do
 // Meeting point of three planes (Cramer's rule); false if they are (nearly)
 // dependent.  err: a bound on the rounding error of each coordinate (a few
 // times the first-order bound 9 eps sum|c| |minor| / |det| + 7 eps |x|
-// perm(det) / |det| of the rounded expressions below).
+// perm(det) / |det| of the rounded expressions below, plus 4 eps |x| for the
+// quotient: a product with the rounded reciprocal of det is within 2 eps of
+// the numerator over det; one reciprocal, not three fp64 divisions).
 SDF_HD bool meet(const Plane &A, const Plane &B, const Plane &C, double *x,
                  double *err = nullptr) {
     const double bc[3] = {B.n[1] * C.n[2] - B.n[2] * C.n[1], B.n[2] * C.n[0] - B.n[0] * C.n[2],
@@ -124,7 +126,8 @@ SDF_HD bool meet(const Plane &A, const Plane &B, const Plane &C, double *x,
     const double nb = dabs(B.n[0]) + dabs(B.n[1]) + dabs(B.n[2]);
     const double nc = dabs(C.n[0]) + dabs(C.n[1]) + dabs(C.n[2]);
     if (!(dabs(d) > 1e-12 * na * nb * nc)) return false;
-    for (int k = 0; k < 3; ++k) x[k] = (A.c * bc[k] + B.c * ca[k] + C.c * ab[k]) / d;
+    const double inv = 1.0 / d;
+    for (int k = 0; k < 3; ++k) x[k] = (A.c * bc[k] + B.c * ca[k] + C.c * ab[k]) * inv;
     if (err) {
         // permanents of the 2x2 minors
         const double pbc[3] = {dabs(B.n[1] * C.n[2]) + dabs(B.n[2] * C.n[1]),
@@ -137,11 +140,12 @@ SDF_HD bool meet(const Plane &A, const Plane &B, const Plane &C, double *x,
                                dabs(A.n[2] * B.n[0]) + dabs(A.n[0] * B.n[2]),
                                dabs(A.n[0] * B.n[1]) + dabs(A.n[1] * B.n[0])};
         const double pd = dabs(A.n[0]) * pbc[0] + dabs(A.n[1]) * pbc[1] + dabs(A.n[2]) * pbc[2];
-        const double ad = dabs(d);
+        const double inv_ad = dabs(inv);
         double e = 0.0;
         for (int k = 0; k < 3; ++k) {
             const double m = dabs(A.c) * pbc[k] + dabs(B.c) * pca[k] + dabs(C.c) * pab[k];
-            const double ek = 32.0 * kEps * (m + dabs(x[k]) * pd) / ad + 4.0 * kEps * dabs(x[k]);
+            const double ek =
+                32.0 * kEps * (m + dabs(x[k]) * pd) * inv_ad + 4.0 * kEps * dabs(x[k]);
             e = ek > e ? ek : e;
         }
         *err = e;
