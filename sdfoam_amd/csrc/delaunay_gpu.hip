@@ -275,6 +275,7 @@ struct WaveShared {
     uint32_t used[2];
     uint8_t remap[kWavePlanes];
     uint16_t fresh[kWaveNew];   // wave_clip's boundary edges, ea | eb << 6
+    uint8_t owner[64];          // a batch's lane whose cell range starts at each lane
     union {
         StagedVert stg[kWaveNew];     // wave_clip's new vertices
         TestVert tv[kWaveVerts];      // wave_may_cut's copy of the vertices
@@ -343,6 +344,16 @@ __device__ __forceinline__ double wmind(double v) {
     v = fmin(v, dpp_d<0x142, 0xa>(v));
     v = fmin(v, dpp_d<0x143, 0xc>(v));
     return readlane_d(v, 63);
+}
+// inclusive prefix maximum over the lanes (every lane active), as wscanu
+__device__ __forceinline__ uint32_t wscanmaxu(uint32_t v) {
+    v = max(v, dpp_u<0x111>(0u, v));
+    v = max(v, dpp_u<0x112>(0u, v));
+    v = max(v, dpp_u<0x114>(0u, v));
+    v = max(v, dpp_u<0x118>(0u, v));
+    v = max(v, dpp_u<0x142, 0xa>(0u, v));
+    v = max(v, dpp_u<0x143, 0xc>(0u, v));
+    return v;
 }
 // inclusive prefix sum over the lanes (every lane active): within rows by
 // shifts of 1, 2, 4 and 8 (no source: 0), then rows 1 and 3 add the row
@@ -748,8 +759,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
         const dgrid::GridLevel &lv = g.level[lev];
         const uint32_t *sorted = gv.sorted[lev];
         const int *h = hc[lev];
-        for (int r = 0; r <= dgrid::kMaxRing && !decided; ++r) {
-            const uint32_t first = r == 0 ? 0u : (uint32_t)((2 * r - 1) * (2 * r - 1) * (2 * r - 1));
+        // ring 1 takes ring 0 (the point's own cell) in with it: after ring 0
+        // alone the search always went on (no point lies beyond 0 cells yet,
+        // short of a grid of one cell, where ring 1 holds no cell)
+        for (int r = 1; r <= dgrid::kMaxRing && !decided; ++r) {
+            const uint32_t first = r == 1 ? 0u : (uint32_t)((2 * r - 1) * (2 * r - 1) * (2 * r - 1));
             const uint32_t cells = (uint32_t)((2 * r + 1) * (2 * r + 1) * (2 * r + 1)) - first;
             for (uint32_t base = 0; base < cells && !decided; base += 64) {
                 // one grid cell of the ring's shell per lane
@@ -777,11 +791,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                 }
                 for (uint32_t f0 = 0; f0 < total && !decided; f0 += 64) {
                     const uint32_t f = f0 + l;
-                    const uint32_t fc = f < total ? f : total - 1;
-                    uint32_t owner = 0;
-                    for (uint32_t step = 32; step > 0; step >>= 1)
-                        if ((uint32_t)__shfl((int)incl, (int)(owner + step - 1), 64) <= fc)
-                            owner += step;
+                    // each cell range starting in this window marks its first
+                    // lane with its own lane; a running maximum over the lanes
+                    // carries it on (the ranges follow one another in lane
+                    // order), from the range holding f0 (lanes whose ranges
+                    // end at or before f0 are below it); lanes past `total`
+                    // keep the last range
+                    sh.owner[l] = 0u;
+                    __syncthreads();
+                    const uint32_t ex = incl - cnt;
+                    if (cnt > 0u && ex > f0 && ex < f0 + 64u) sh.owner[ex - f0] = (uint8_t)l;
+                    __syncthreads();
+                    const uint32_t owner =
+                        wscanmaxu(max((uint32_t)sh.owner[l],
+                                      (uint32_t)__popcll(wballot(incl <= f0))));
                     const uint32_t ob = (uint32_t)__shfl((int)b, (int)owner, 64);
                     const uint32_t oex = (uint32_t)__shfl((int)(incl - cnt), (int)owner, 64);
                     bool surv = false, dup = false;
