@@ -215,6 +215,12 @@ def _certify(L, pts: torch.Tensor, gptr: int, gbytes: int, stream, query=None,
 _LEVEL_SHRINK = 0.7
 
 
+# The most open points the exhaustive certification takes (C3 leaves 7,935
+# open, C4 11,125; past some 60k, Qhull on those left open after a grid
+# level is faster).
+_EXHAUSTIVE_MAX = 1 << 16
+
+
 class _OpenRetry(RuntimeError):
     """The open points' tetrahedra from the GPU left a face without a
     neighbour off the convex hull (a circumcentre beyond the exhaustive
@@ -228,8 +234,12 @@ def _open_candidates_gpu(L, pts: torch.Tensor, U: torch.Tensor, stream, stats: d
     U's own (its circumsphere holds no point at all), which the exhaustive
     certification reports from each of its vertices' cells, hull cells
     included, as long as its circumcentre lies within the 1e8-extent box.
-    None when a cell is undecided (Qhull then decides)."""
-    if U.numel() < 32 or U.numel() > (1 << 20):
+    None when a cell is undecided (Qhull then decides), and for more than
+    _EXHAUSTIVE_MAX open points: a cell that the grid search among them
+    leaves open is clipped by every one of them, so the pass grows as the
+    square of their number (a plane of 300k points leaves 65.8k of them open:
+    the rebuild takes 0.78 s that way, 0.59 s with Qhull)."""
+    if U.numel() < 32 or U.numel() > _EXHAUSTIVE_MAX:
         return None
     t = time.perf_counter()
     gb = int(L.sdf_delaunay_certify_scratch_bytes(U.numel()))

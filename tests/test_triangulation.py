@@ -146,6 +146,18 @@ def test_has_coincident_points():
     assert not has_coincident_points(torch.from_numpy(pts[:1]))
 
 
+def test_exhaustive_open_pass_is_bounded():
+    """The open points' exhaustive certification grows as the square of
+    their number: past _EXHAUSTIVE_MAX of them (and below 32) the open points
+    go the Qhull way, before any GPU call."""
+    import torch
+    from sdfoam_amd import triangulation as T
+    assert T._EXHAUSTIVE_MAX == 1 << 16
+    for m in (31, T._EXHAUSTIVE_MAX + 1, 211286):
+        U = torch.arange(m, dtype=torch.int32)
+        assert T._open_candidates_gpu(None, None, U, None, {}) is None
+
+
 def test_hull_check_finds_missing_tetrahedra():
     """_hull_is_convex, the check the GPU path's merge makes in place of
     Qhull's hull face count: a Delaunay tetrahedralisation passes; removing
