@@ -716,7 +716,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                                                      unsigned long long *__restrict__ counters,
                                                      uint32_t *__restrict__ open,
                                                      uint32_t *__restrict__ status_out,
-                                                     const uint32_t *__restrict__ query) {
+                                                     const uint32_t *__restrict__ query,
+                                                     uint32_t max_candidates) {
     __shared__ WaveShared sh;
     // the point's grid cell and searched rings per level (uniform over the
     // wave; indexed by level, so kept in LDS rather than scratch memory)
@@ -785,7 +786,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void ce
                 const uint32_t incl = wscanu(cnt);
                 const uint32_t total = readlane_u(incl, 63);
                 examined += total;
-                if (examined > dgrid::kMaxCandidates) {
+                if (examined > max_candidates) {
                     decided = true;
                     break;
                 }
@@ -1386,6 +1387,16 @@ GridView grid_view(const GridScratch &s, const GridGeom &g) {
     return gv;
 }
 
+// Candidates a listed point's cell (an incremental rebuild's dirty point) may
+// examine before it is left open, a quarter of the whole set's cap: the few
+// cells that certify only after some 50k candidates (beside large empty
+// regions; 1,000-2,400 cuts and 3-6 ms each) set the length of the call, and
+// left open they go to the open points' exhaustive pass, and skip the next
+// rebuild's certification (C3 incremental rebuild 44.3 -> 42.0 ms; the whole
+// set's cap at 16,384 would leave 11.8k points open against 7.9k and take the
+// full rebuild 59.0 -> 59.8 ms).
+constexpr uint32_t kMaxCandidatesDirty = 16384;
+
 // certify_kernel over all points (query == nullptr) or the nq listed ones,
 // then the counters to the host.
 hipError_t run_certify(const float *points, uint32_t n, const uint32_t *query, uint32_t nq,
@@ -1394,12 +1405,13 @@ hipError_t run_certify(const float *points, uint32_t n, const uint32_t *query, u
                        hipStream_t stream, bool exhaustive = false) {
     hipError_t e;
     if (nq > 0) {
+        const uint32_t cap = query ? kMaxCandidatesDirty : dgrid::kMaxCandidates;
         if (exhaustive)
             hipLaunchKernelGGL(certify_kernel<true>, dim3(nq), dim3(64), 0, stream, points, n, gv,
-                               reports, report_capacity, s.counters, open, s.status, query);
+                               reports, report_capacity, s.counters, open, s.status, query, cap);
         else
             hipLaunchKernelGGL(certify_kernel<false>, dim3(nq), dim3(64), 0, stream, points, n, gv,
-                               reports, report_capacity, s.counters, open, s.status, query);
+                               reports, report_capacity, s.counters, open, s.status, query, cap);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     unsigned long long hc[8];
