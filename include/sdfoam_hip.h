@@ -476,7 +476,8 @@ int sdf_delaunay_certify(const float *points, uint32_t num_points,
  * set) is listed in open_points and its vertices off the box faces are
  * reported as well: with the certified ones, every Delaunay tetrahedron of
  * the set whose circumcentre lies within the box.  counts as for
- * sdf_delaunay_certify.  32 to 2^20 points.  Synchronizes the stream.
+ * sdf_delaunay_certify.  32 to 2^20 points (its time grows as the square
+ * of the number the grid search leaves open).  Synchronizes the stream.
  * No counterpart in the reference: it replaces the host triangulation of
  * the open points between the two calls above. */
 int sdf_delaunay_certify_exhaustive(const float *points, uint32_t num_points,
